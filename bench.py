@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Benchmark of the W8A8 linear-layer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra]
+
+A step is one launch of the W8A8 GEMM at the headline 4B shape (M = T = 4096 tokens, K = 2560,
+N = 9728, per-token x per-channel scale epilogue, bf16 out) on synthetic seeded inputs already
+resident in HBM; `value` is its throughput in TOPS (2 M N K int8 ops per launch).  The JSON line
+also carries the roofline of that kernel, the CPU baseline (the reference's CPU path: quant_act ->
+torch._int_mm -> scale epilogue, timed on this host's cores) and, unless --no-extra, the other hot
+path measurements: fused RMSNorm + quant GB/s (T = 4096, 32768), the GEMMs of the 4B layer and
+the per-layer hot path in tokens/s.
+
+Timing: W untimed warm-up launches, then exactly K launches bracketed by device synchronisation,
+HIP events recorded on the stream the kernels run on (torch's current stream), average per launch.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "W8A8 GEMM TOPS (% INT8 peak) + prefill tokens/s, 4B shapes, T=4096"
+PEAK_INT8_TOPS = 5000.0    # MI355X dense INT8 matrix peak, 5.0 POP/s (spec sheet; no sparsity)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
+HIDDEN, INTER, QKV_N, O_K, LAYERS = 2560, 9728, 6144, 4096, 36
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the current stream around a block of launches."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(steps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / steps  # ms per launch
+
+
+def gemm_launcher(torch, lib, qx, sx, qw, sw, out, residual=None, epilogue=0):
+    """A zero-allocation closure over the C ABI (what the drop-in mm_i8 calls, minus torch.empty)."""
+    M, K = qx.shape
+    N = qw.shape[0]
+    n_out = out.shape[1]
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (qx.data_ptr(), K, qw.data_ptr(), K, sx.data_ptr(), sw.data_ptr(), None,
+            None if residual is None else residual.data_ptr(), n_out, out.data_ptr(), n_out, 0, M, N, K, epilogue,
+            stream)
+    fn = lib.mica_mm_i8
+
+    def launch():
+        rc = fn(*args)
+        if rc != 0:
+            raise RuntimeError(f"mica_mm_i8 returned {rc}")
+    return launch
+
+
+def synthetic(torch, dev, M, K, N, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[:8]] *= 20.0
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.empty(N).uniform_(1e-3, 1e-2, generator=g)
+    return x.to(torch.bfloat16).to(dev), qw.to(dev), sw.to(dev)
+
+
+def cpu_baseline(torch, M, K, N):
+    """The reference's CPU path on the headline workload (oracle/cpu_path.qlinear), bounded to ~10 s."""
+    from oracle import cpu_path
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[:8]] *= 20.0
+    x = x.to(torch.bfloat16)
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.empty(N).uniform_(1e-3, 1e-2, generator=g)
+    cpu_path.qlinear(x, qw, sw)  # warm-up
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 30):
+        t0 = time.perf_counter()
+        cpu_path.qlinear(x, qw, sw)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(2.0 * M * N * K / med / 1e12, 4),
+        "unit": "TOPS",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"W8A8 linear M={M} K={K} N={N}: quant_act (round half even) + torch._int_mm + fp32 scale "
+                   f"epilogue -> bf16 (oracle/cpu_path.qlinear), median of {len(times)} runs, {med * 1e3:.1f} ms"),
+    }
+
+
+def traffic_from_profiles():
+    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, if one was recorded."""
+    p = ROOT / "profiles" / "gemm_i8_m4096_n9728_k2560_traffic.json"
+    if p.is_file():
+        try:
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the hot path is a single-GPU "
+              f"kernel set; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from mica_amd import _lib, fused_kernels, int8_kernels
+
+    ok, why = int8_kernels.available("cuda")
+    if not ok:
+        raise SystemExit(f"mica_amd kernels unavailable: {why}")
+    int8_kernels.STRICT = True
+    dev = torch.device("cuda", torch.cuda.current_device())
+    lib = _lib.load()
+    info = _lib.device_info(dev.index)
+    timer = Timer(torch)
+
+    # ---- headline: the W8A8 GEMM at M=4096, K=2560, N=9728 -------------------------------------
+    M, K, N = 4096, HIDDEN, INTER
+    x, qw, sw = synthetic(torch, dev, M, K, N, seed=0)
+    qx, sx = int8_kernels.act_quant(x)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ms = timer.run(gemm_launcher(torch, lib, qx, sx, qw, sw, out), args.steps, args.warmup)
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    result = {
+        "metric": METRIC,
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded: X bf16 ~N(0,1) with 8 outlier channels x20, quantized per token; "
+                "W int8 uniform [-127,127], per-channel scales ~U(1e-3,1e-2))",
+        "config": {"workload": "W8A8 GEMM M=4096 K=2560 N=9728 (4B MLP projection at T=4096), int8 x int8 -> "
+                               "int32 on MFMA, per-token x per-channel scale epilogue, bf16 out",
+                   "M": M, "K": K, "N": N, "T": M, "parallelism": "none (1 GPU)"},
+        "pct_int8_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(),
+                     "note": "INT8 TOP/s (2 M N K per launch / mean launch time); peak = MI355X dense INT8 5.0 "
+                             "POP/s"},
+        "device": {**info, "derived_int8_peak_tops": round(info["cu_count"] * info["clock_khz"] * 1e3 * 8192 / 1e12,
+                                                           1)},
+    }
+
+    if not args.no_extra:
+        extra = {}
+        # fused RMSNorm + quant (config 1): T * (2K + K + 4) + 2K algorithmic bytes
+        for T in (4096, 32768):
+            g = torch.Generator().manual_seed(T)
+            h = torch.randn(T, K, generator=g)
+            h[:, torch.randperm(K, generator=g)[:8]] *= 20
+            h = h.to(torch.bfloat16).to(dev)
+            w = (torch.randn(K, generator=g) * 0.1 + 1.0).to(torch.bfloat16).to(dev)
+            q = torch.empty(T, K, dtype=torch.int8, device=dev)
+            s = torch.empty(T, dtype=torch.float32, device=dev)
+            stream = torch.cuda.current_stream().cuda_stream
+            a = (h.data_ptr(), _lib.BF16, K, None, K, w.data_ptr(), _lib.BF16, 0.0, 1e-6, None, q.data_ptr(), K,
+                 s.data_ptr(), None, K, None, K, T, K, 0, stream)
+
+            def norm(a=a):
+                if lib.mica_rmsnorm_quant(*a) != 0:
+                    raise RuntimeError("mica_rmsnorm_quant failed")
+            ms_n = timer.run(norm, max(args.steps, 50), args.warmup)
+            nbytes = T * (2 * K + K + 4) + 2 * K
+            gbs = nbytes / (ms_n * 1e-3) / 1e9
+            extra[f"rmsnorm_quant_T{T}"] = {"us": round(ms_n * 1e3, 2), "GB/s": round(gbs, 1),
+                                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
+        # the 4B layer's GEMMs at T = 4096 and the per-layer W8A8 hot path
+        T = 4096
+        layer = {}
+        shapes = {"qkv": (QKV_N, HIDDEN), "o": (HIDDEN, O_K), "gate_up": (2 * INTER, HIDDEN), "down": (HIDDEN, INTER)}
+        bufs = {}
+        for name, (n, k) in shapes.items():
+            xx, ww, ss = synthetic(torch, dev, T, k, n, seed=n + k)
+            qa, sa = int8_kernels.act_quant(xx)
+            epi = 1 if name == "gate_up" else 0
+            o = torch.empty(T, n // 2 if epi else n, dtype=torch.bfloat16, device=dev)
+            res = torch.randn(T, n, device=dev).to(torch.bfloat16) if name in ("o", "down") else None
+            fn = gemm_launcher(torch, lib, qa, sa, ww, ss, o, residual=res, epilogue=epi)
+            ms_g = timer.run(fn, max(args.steps // 4, 20), args.warmup)
+            t = 2.0 * T * n * k / (ms_g * 1e-3) / 1e12
+            layer[name] = {"us": round(ms_g * 1e3, 2), "TOPS": round(t, 1), "pct_peak": round(100 * t / PEAK_INT8_TOPS, 1)}
+            bufs[name] = (qa, sa, ww, ss, o, res, fn)
+        # requant of h [T, 9728] between gate_up and down
+        hh = bufs["gate_up"][4]
+        qh = torch.empty(T, INTER, dtype=torch.int8, device=dev)
+        sh = torch.empty(T, dtype=torch.float32, device=dev)
+        st = torch.cuda.current_stream().cuda_stream
+        ra = (hh.data_ptr(), _lib.BF16, INTER, None, qh.data_ptr(), INTER, sh.data_ptr(), T, INTER, 0, st)
+
+        def requant():
+            if lib.mica_act_quant(*ra) != 0:
+                raise RuntimeError("mica_act_quant failed")
+        ms_r = timer.run(requant, 50, args.warmup)
+        rbytes = T * (2 * INTER + INTER + 4)
+        layer["requant_h"] = {"us": round(ms_r * 1e3, 2), "GB/s": round(rbytes / (ms_r * 1e-3) / 1e9, 1)}
+        ms_norm = extra["rmsnorm_quant_T4096"]["us"] / 1e3
+        per_layer_ms = 2 * ms_norm + ms_r + sum(layer[k]["us"] for k in shapes) / 1e3
+        layer["hot_path_us_per_layer"] = round(per_layer_ms * 1e3, 1)
+        layer["hot_path_tokens_per_s_36_layers"] = round(T / (LAYERS * per_layer_ms * 1e-3), 1)
+        layer["note"] = ("per 4B layer at T=4096: 2 fused RMSNorm+quant, QKV, O(+residual), fused gate+up with SiLU "
+                         "epilogue, requant of h, down(+residual); attention (a torch op) not included")
+        extra["layer_T4096"] = layer
+        result["extra"] = extra
+        result["prefill_tokens_per_s"] = layer["hot_path_tokens_per_s_36_layers"]
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, M, K, N)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

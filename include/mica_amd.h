@@ -1,0 +1,140 @@
+/*
+ * mica_amd.h -- C ABI of the MI355X (gfx950) W8A8 linear-layer hot path.
+ *
+ * Every entry point takes plain device pointers, element strides (in elements),
+ * int sizes and a HIP stream handle passed as void*.  Nothing here allocates or
+ * frees memory, synchronises the device or prints: the caller owns every buffer
+ * (inputs borrowed, outputs pre-allocated), and the launch is enqueued on the
+ * stream it is given, so the calls are safe inside HIP graph capture.
+ *
+ * Return value of every launcher:
+ *      0                launched (or nothing to do: M == 0)
+ *     >0  MICA_MISS_*   unsupported case, nothing launched; the Python layer turns
+ *                       this into the reference's "return None + count a fallback
+ *                       reason" convention (v0.5/serving/lib/int8_kernels.py:22-24)
+ *     <0                -(hipError_t) of a failed launch; Python raises RuntimeError,
+ *                       as the reference's driver check does (int8_kernels.py:60-64)
+ */
+#ifndef MICA_AMD_H
+#define MICA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *mica_stream_t; /* hipStream_t; NULL is the null stream */
+
+/* element types (the reference's DT table, int8_kernels.py:13, plus int8 / int32) */
+enum { MICA_BF16 = 0, MICA_FP16 = 1, MICA_FP32 = 2, MICA_INT8 = 3, MICA_INT32 = 4 };
+
+/* rounding of the activation quantizer:
+ *   EVEN  torch.round, half to even        (int8_quant.py:70, the CPU path)
+ *   AWAY  trunc(v +- 0.5), half away from 0 (kernel_src/kernels.py:35, the Triton kernel) */
+enum { MICA_ROUND_EVEN = 0, MICA_ROUND_AWAY = 1 };
+
+/* GEMM epilogues */
+enum {
+    MICA_EPI_SCALE = 0,    /* C = cvt((f32(acc) * sa[m]) * sb[n] (+ bias[n])) (kernels.py:63-68)          */
+    MICA_EPI_SILU_MUL = 1, /* gate/up interleaved in groups of 64 rows of B; C[m, n'] has N/2 columns:
+                              g = bf16(y_gate), u = bf16(y_up), C = bf16(bf16(silu(g)) * u)
+                              (fast_runtime.py:126-132 + fused_kernels.py:36-42, 85-87)                 */
+};
+
+/* reasons for a miss (>0 return) */
+enum {
+    MICA_MISS_SHAPE = 1,  /* a size is out of the supported range                 */
+    MICA_MISS_DTYPE = 2,  /* dtype code not supported for this argument           */
+    MICA_MISS_ALIGN = 3,  /* a pointer is not 16-byte aligned                      */
+    MICA_MISS_STRIDE = 4, /* a leading dimension is too small or not a multiple of 16 */
+    MICA_MISS_RANGE = 5,  /* an index product would overflow int32                 */
+    MICA_MISS_ARG = 6,    /* a required pointer is NULL / invalid flag            */
+    MICA_MISS_DEVICE = 7, /* the current device is not gfx950                       */
+};
+
+/* library version, (major << 16) | minor */
+int mica_version(void);
+
+/* short name of a miss code ("shape", "dtype", ...) or of an error */
+const char *mica_status_name(int rc);
+
+/* properties of a device that the rooflines are priced with:
+ * compute units, peak engine clock (kHz), LDS bytes per workgroup, gfx arch number (950). */
+int mica_device_info(int device, int *cu_count, int *clock_khz, int *lds_per_block, int *gfx_arch);
+
+/*
+ * Per-token symmetric INT8 activation quantizer.
+ * Replaces int8_kernels.act_quant (v0.5/serving/lib/int8_kernels.py:325-353), which launches the
+ * Triton act_quant (kernel_src/kernels.py:14-37); CPU semantics int8_quant.quant_act (int8_quant.py:64-73):
+ *   xf = f32(x[m, :]) (* inv_smooth[:]);  s[m] = max(max|xf|, 1e-8) / 127
+ *   q[m, k] = clamp(round(xf[k] / s[m]), -127, 127)
+ * x: [M, K] of x_dtype (bf16 / fp16 / fp32) with row stride ldx; q: [M, K] int8, row stride ldq;
+ * s: [M] fp32.  inv_smooth: [K] fp32 or NULL.
+ * Requires K % 8 == 0, 8 <= K <= 16384, 16-byte aligned rows.
+ */
+int mica_act_quant(const void *x, int x_dtype, int ldx, const float *inv_smooth, int8_t *q, int ldq, float *s,
+                   int M, int K, int rounding, mica_stream_t stream);
+
+/*
+ * Fused RMSNorm (+ optional residual add) + per-token INT8 quantizer, one read of x.
+ * Replaces fused_kernels.rms_norm (v0.5/serving/lib/fused_kernels.py:50-82, Triton norm :10-34)
+ * followed by int8_kernels.act_quant on its output (the QLinear call at int8_runtime.py:181):
+ *   v = residual ? bf16(x + residual) : x            (stored to sum if sum != NULL)   (:27-30, :52)
+ *   y = bf16((f32(v) * rsqrt(mean(f32(v)^2) + eps)) * (offset + f32(w)))           (:31-34, :54)
+ *   (q, s) = act_quant(y, inv_smooth)                 if q != NULL
+ *   y stored if y != NULL
+ * offset = 1.0 gives the Qwen3.5 zero-centred weight ((1 + w), fused_kernels.py:34);
+ * offset = 0.0 a plain gamma.  x, residual, y, sum: [M, K] of x_dtype (bf16 or fp16);
+ * w: [K] of w_dtype (bf16 / fp16 / fp32).  At least one of q, y must be non-NULL;
+ * with q != NULL, s must be non-NULL.
+ */
+int mica_rmsnorm_quant(const void *x, int x_dtype, int ldx, const void *residual, int ldr, const void *w, int w_dtype,
+                       float offset, float eps, const float *inv_smooth, int8_t *q, int ldq, float *s, void *y, int ldy,
+                       void *sum, int lds, int M, int K, int rounding, mica_stream_t stream);
+
+/*
+ * W8A8 GEMM on the gfx950 i8 matrix cores: acc[m, n] = sum_k A[m, k] * B[n, k] (exact int32),
+ * then the epilogue.  Replaces int8_kernels.mm_i8 (v0.5/serving/lib/int8_kernels.py:359-406),
+ * Triton mm_i8 (kernel_src/kernels.py:40-68); CPU fallback int8_runtime.py:186-192.
+ * A: [M, K] int8 (lda), B: [N, K] int8 (ldb, K-contiguous like QLinear.qweight), sa: [M] fp32,
+ * sb: [N] fp32, bias: [N] fp32 or NULL.  residual: NULL or [M, Nout] of out_dtype, added after the
+ * epilogue's rounding: C = cvt(f32(cvt(y)) + f32(residual)) (the "h + mlp(...)" of fork.py:419-422).
+ * C: [M, Nout] of out_dtype (bf16 / fp16 / fp32), Nout = N (SCALE) or N / 2 (SILU_MUL, bf16 only).
+ * out_dtype MICA_INT32 stores the raw accumulators acc[m, n] (SCALE only; scales, bias and
+ * residual are ignored) -- the int32 matmul of int8_quant.torch_int_mm (int8_quant.py:92-96).
+ * Requires K % 16 == 0, lda/ldb % 16 == 0, N % 128 == 0 for SILU_MUL.
+ */
+int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
+               const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M, int N, int K,
+               int epilogue, mica_stream_t stream);
+
+/*
+ * Elementwise SwiGLU y = bf16(bf16(silu(f32(g))) * f32(u)) over n elements of bf16.
+ * Replaces fused_kernels.swi_glu (v0.5/serving/lib/fused_kernels.py:85-96, Triton swiglu :36-42).
+ */
+int mica_swiglu(const void *g, const void *u, void *y, long long n, int dtype, mica_stream_t stream);
+
+/*
+ * Last-position readout over the allowed answer ids.
+ * Replaces the label-row readout of release_runtime.py:298-306 applied to
+ * body.norm(final_hidden(...)) (prefill_engine.py:280-304) and the slice + softmax of
+ * release_runtime.py:509-517, so no full-vocabulary projection is ever formed.
+ *   x_b    = h[rows[b], :]                                       (rows: int32 [B], the last token of request b)
+ *   x_b    = bf16(rms_norm(x_b, norm_w, eps, offset)) if norm_w != NULL  (the final norm)
+ *   logits[b, j] = sum_k f32(x_b[k]) * f32(W[ids ? ids[j] : j, k])      (fp32, j < L)
+ *   probs[b, i]  = softmax_i(logits[b, lo[b] + i]), i < cnt[b]          (lo/cnt NULL: over all L)
+ * h: [n_rows, K] bf16 (ldh); W: [w_rows, K] of w_dtype (fp32: the pre-gathered label rows, or bf16:
+ * the full output embedding indexed through ids); logits: [B, L] fp32; probs: [B, ldp] fp32 or NULL.
+ * rows / ids / lo / cnt live on the device: a row or id out of range gives NaN logits (and NaN probs
+ * for a bad row) instead of an access; the softmax slice is clipped to [0, L) and to ldp.
+ */
+int mica_gather_logits(const void *h, int ldh, int n_rows, const int *rows, int B, const void *norm_w, int norm_dtype,
+                       float offset, float eps, const void *W, int w_dtype, int ldw, int w_rows, const int *ids, int L,
+                       int K, float *logits, const int *lo, const int *cnt, float *probs, int ldp,
+                       mica_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MICA_AMD_H */

@@ -1,0 +1,389 @@
+// Row kernels of the W8A8 hot path on gfx950:
+//   * fused RMSNorm (+ residual add) + per-token INT8 quantizer  (mica_rmsnorm_quant)
+//   * standalone per-token INT8 quantizer                        (mica_act_quant)
+//   * elementwise SwiGLU                                          (mica_swiglu)
+//
+// Layout: one 64-lane wavefront owns one row at a time and keeps the whole row in registers,
+// so x is read from HBM once and q (int8) + s (fp32) are written once.  Lane l holds the
+// 8-element chunks [c * 512 + 8 l, c * 512 + 8 l + 8) for c < NCH = ceil(K / 512): every
+// load is a 16-byte vector and a wave's 64 lanes cover 1 KiB of contiguous bf16 per chunk.
+// The sum of squares and the absmax are wavefront reductions (no LDS, no barrier).
+// Waves walk rows with a grid stride; blocks are 256 threads (4 rows in flight per block).
+
+#include "common.h"
+
+namespace {
+
+constexpr int kChunk = 8;          // elements per lane per chunk
+constexpr int kRowStep = 64 * kChunk; // elements per chunk across the wave
+
+struct RowParams {
+    const void *x;
+    const void *res;
+    const void *w;
+    const float *inv;
+    int8_t *q;
+    float *s;
+    void *y;
+    void *sum;
+    int ldx, ldr, ldq, ldy, lds;
+    int M, K;
+    int w_dtype;
+    int rounding;
+    float offset, eps;
+};
+
+// 16-bit element j of a packed chunk as fp32
+template <int XT>
+MICA_DEVICE float elem16(const u32x4 &c, int j) {
+    uint32_t word = c[j >> 1];
+    uint16_t h = (j & 1) ? (uint16_t)(word >> 16) : (uint16_t)(word & 0xffffu);
+    if (XT == MICA_BF16) return bf16_to_f32(h);
+    return f16_to_f32(h);
+}
+
+template <int XT>
+MICA_DEVICE uint16_t to16(float f) {
+    if (XT == MICA_BF16) return f32_to_bf16(f);
+    return f32_to_f16(f);
+}
+
+template <int XT>
+MICA_DEVICE void unpack8(const u32x4 &c, float (&v)[kChunk]) {
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) v[j] = elem16<XT>(c, j);
+}
+
+template <int XT>
+MICA_DEVICE u32x4 pack8(const float (&v)[kChunk]) {
+    u32x4 c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = (uint32_t)to16<XT>(v[2 * j]) | ((uint32_t)to16<XT>(v[2 * j + 1]) << 16);
+    return c;
+}
+
+MICA_DEVICE void load_w8(const void *w, int w_dtype, int idx, float (&v)[kChunk]) {
+    if (w_dtype == MICA_FP32) {
+        const float4 *p = (const float4 *)((const float *)w + idx);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        u32x4 c = *(const u32x4 *)((const uint16_t *)w + idx);
+        if (w_dtype == MICA_BF16) unpack8<MICA_BF16>(c, v);
+        else unpack8<MICA_FP16>(c, v);
+    }
+}
+
+MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
+    const float4 *p = (const float4 *)(inv + idx);
+    float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// Quantize one chunk of 8 fp32 values with the row's scale and store 8 bytes.
+template <bool kFast>
+MICA_DEVICE void quant_store8(const float (&v)[kChunk], float s, float r, int rounding, int8_t *dst) {
+    int qv[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) qv[j] = quantize_one<kFast>(v[j], s, r, rounding);
+    u32x2 packed;
+    packed[0] = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
+    packed[1] = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
+    *(u32x2 *)dst = packed;
+}
+
+// XT: dtype of x / residual / y / sum (bf16 or fp16).  NORM: apply the RMSNorm first.
+// HAS_INV: multiply by inv_smooth before the absmax (forces the IEEE-division quotient).
+template <int NCH, int XT, bool NORM, bool HAS_INV>
+__global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
+    constexpr bool kFast = (XT == MICA_BF16) && !HAS_INV;
+    const int lane = threadIdx.x & 63;
+    const int nwaves = gridDim.x * (blockDim.x >> 6);
+    const int K = p.K;
+
+    // per-lane weight multipliers (offset + w), fp32, cached across the rows this wave visits
+    float w1[NORM ? NCH : 1][kChunk];
+    if (NORM) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            if (idx < K) {
+                load_w8(p.w, p.w_dtype, idx, w1[c]);
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) w1[c][j] = p.offset + w1[c][j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) w1[c][j] = 0.0f;
+            }
+        }
+    }
+
+    for (int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < p.M; row += nwaves) {
+        u32x4 raw[NCH];
+        const uint16_t *xr = (const uint16_t *)p.x + (long)row * p.ldx;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            raw[c] = idx < K ? *(const u32x4 *)(xr + idx) : u32x4{0u, 0u, 0u, 0u};
+        }
+        if (NORM && p.res != nullptr) {
+            // v = (x + r) rounded to the activation dtype (fused_kernels.py:27-30, :52)
+            const uint16_t *rr = (const uint16_t *)p.res + (long)row * p.ldr;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int idx = c * kRowStep + lane * kChunk;
+                if (idx < K) {
+                    u32x4 rc = *(const u32x4 *)(rr + idx);
+                    float a[kChunk], b[kChunk];
+                    unpack8<XT>(raw[c], a);
+                    unpack8<XT>(rc, b);
+#pragma unroll
+                    for (int j = 0; j < kChunk; ++j) a[j] = a[j] + b[j];
+                    raw[c] = pack8<XT>(a);
+                    if (p.sum != nullptr) *(u32x4 *)((uint16_t *)p.sum + (long)row * p.lds + idx) = raw[c];
+                }
+            }
+        }
+        if (NORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                float a[kChunk];
+                unpack8<XT>(raw[c], a);
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(a[j], a[j], ss);
+            }
+            ss = wave_sum(ss);
+            const float mean = ss / (float)K;
+            const float rstd = 1.0f / __builtin_sqrtf(mean + p.eps);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int idx = c * kRowStep + lane * kChunk;
+                float a[kChunk];
+                unpack8<XT>(raw[c], a);
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) a[j] = (a[j] * rstd) * w1[c][j];
+                raw[c] = pack8<XT>(a);
+                if (p.y != nullptr && idx < K) *(u32x4 *)((uint16_t *)p.y + (long)row * p.ldy + idx) = raw[c];
+            }
+        }
+        if (p.q == nullptr) continue;
+
+        // absmax of the (smoothed) row
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            float a[kChunk];
+            unpack8<XT>(raw[c], a);
+            if (HAS_INV) {
+                float iv[kChunk];
+                if (idx < K) load_inv8(p.inv, idx, iv);
+                else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) a[j] = a[j] * iv[j];
+            }
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(a[j]));
+        }
+        amax = wave_max(amax);
+        const float s = row_scale(amax);
+        const float r = 1.0f / s;
+        if (lane == 0) p.s[row] = s;
+        int8_t *qr = p.q + (long)row * p.ldq;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            if (idx >= K) continue;
+            float a[kChunk];
+            unpack8<XT>(raw[c], a);
+            if (HAS_INV) {
+                float iv[kChunk];
+                load_inv8(p.inv, idx, iv);
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) a[j] = a[j] * iv[j];
+            }
+            quant_store8<kFast>(a, s, r, p.rounding, qr + idx);
+        }
+    }
+}
+
+// fp32 activations (act_quant only): same structure, two 16-byte loads per chunk.
+template <int NCH, bool HAS_INV>
+__global__ __launch_bounds__(256) void row32_kernel(RowParams p) {
+    const int lane = threadIdx.x & 63;
+    const int nwaves = gridDim.x * (blockDim.x >> 6);
+    const int K = p.K;
+    for (int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < p.M; row += nwaves) {
+        float v[NCH][kChunk];
+        const float *xr = (const float *)p.x + (long)row * p.ldx;
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            if (idx < K) {
+                float4 a = *(const float4 *)(xr + idx), b = *(const float4 *)(xr + idx + 4);
+                v[c][0] = a.x; v[c][1] = a.y; v[c][2] = a.z; v[c][3] = a.w;
+                v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
+                if (HAS_INV) {
+                    float iv[kChunk];
+                    load_inv8(p.inv, idx, iv);
+#pragma unroll
+                    for (int j = 0; j < kChunk; ++j) v[c][j] = v[c][j] * iv[j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) v[c][j] = 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[c][j]));
+        }
+        amax = wave_max(amax);
+        const float s = row_scale(amax);
+        const float r = 1.0f / s;
+        if (lane == 0) p.s[row] = s;
+        int8_t *qr = p.q + (long)row * p.ldq;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            if (idx < K) quant_store8<false>(v[c], s, r, p.rounding, qr + idx);
+        }
+    }
+}
+
+// Elementwise SwiGLU on bf16: y = bf16(bf16(silu(g)) * u), 8 elements per thread.
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *g, const uint16_t *u, uint16_t *y, long long n) {
+    const long long i0 = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * kChunk;
+    if (i0 >= n) return;
+    if (i0 + kChunk <= n) {
+        u32x4 gc = *(const u32x4 *)(g + i0), uc = *(const u32x4 *)(u + i0);
+        float gv[kChunk], uv[kChunk], out[kChunk];
+        unpack8<MICA_BF16>(gc, gv);
+        unpack8<MICA_BF16>(uc, uv);
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const float act = round_bf16(gv[j] / (1.0f + expf(-gv[j])));
+            out[j] = act * uv[j];
+        }
+        *(u32x4 *)(y + i0) = pack8<MICA_BF16>(out);
+    } else {
+        for (long long i = i0; i < n; ++i) {
+            const float gv = bf16_to_f32(g[i]);
+            const float act = round_bf16(gv / (1.0f + expf(-gv)));
+            y[i] = f32_to_bf16(act * bf16_to_f32(u[i]));
+        }
+    }
+}
+
+int row_grid(int M) {
+    // enough waves to fill 256 CUs several times over; the row loop covers the rest
+    const int blocks = (M + 3) / 4;
+    return blocks < 4096 ? blocks : 4096;
+}
+
+template <int NCH>
+int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st) {
+    dim3 grid(row_grid(p.M)), block(256);
+#define MICA_ROW16(XT_, NORM_, INV_) \
+    hipLaunchKernelGGL((row16_kernel<NCH, XT_, NORM_, INV_>), grid, block, 0, st, p)
+    if (xt == MICA_BF16) {
+        if (norm) { if (has_inv) MICA_ROW16(MICA_BF16, true, true); else MICA_ROW16(MICA_BF16, true, false); }
+        else { if (has_inv) MICA_ROW16(MICA_BF16, false, true); else MICA_ROW16(MICA_BF16, false, false); }
+    } else {
+        if (norm) { if (has_inv) MICA_ROW16(MICA_FP16, true, true); else MICA_ROW16(MICA_FP16, true, false); }
+        else { if (has_inv) MICA_ROW16(MICA_FP16, false, true); else MICA_ROW16(MICA_FP16, false, false); }
+    }
+#undef MICA_ROW16
+    return mica_err(hipGetLastError());
+}
+
+template <int NCH>
+int launch32(const RowParams &p, bool has_inv, hipStream_t st) {
+    dim3 grid(row_grid(p.M)), block(256);
+    if (has_inv) hipLaunchKernelGGL((row32_kernel<NCH, true>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((row32_kernel<NCH, false>), grid, block, 0, st, p);
+    return mica_err(hipGetLastError());
+}
+
+// NCH = ceil(K / 512) in 1..32 (K <= 16384).  Widths of the hot shapes (K = 2560: 5,
+// 4096: 8, 9216: 18, 9728: 19) have their own instantiation; any other width runs on the next
+// larger one, whose surplus chunks are masked off.
+int dispatch_rows(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st) {
+    const int nch = (p.K + kRowStep - 1) / kRowStep;
+#define MICA_CASE(N_) \
+    if (nch <= N_) return xt == MICA_FP32 ? launch32<N_>(p, has_inv, st) : launch16<N_>(p, xt, norm, has_inv, st);
+    MICA_CASE(1) MICA_CASE(2) MICA_CASE(4) MICA_CASE(5) MICA_CASE(8) MICA_CASE(12) MICA_CASE(16) MICA_CASE(18)
+    MICA_CASE(19) MICA_CASE(24) MICA_CASE(32)
+#undef MICA_CASE
+    return MICA_MISS_SHAPE;
+}
+
+bool ld_ok(int ld, int K) { return ld >= K && ld % 8 == 0; }
+
+}  // namespace
+
+extern "C" int mica_act_quant(const void *x, int x_dtype, int ldx, const float *inv_smooth, int8_t *q, int ldq,
+                              float *s, int M, int K, int rounding, mica_stream_t stream) {
+    if (x == nullptr || q == nullptr || s == nullptr) return MICA_MISS_ARG;
+    if (x_dtype != MICA_BF16 && x_dtype != MICA_FP16 && x_dtype != MICA_FP32) return MICA_MISS_DTYPE;
+    if (rounding != MICA_ROUND_EVEN && rounding != MICA_ROUND_AWAY) return MICA_MISS_ARG;
+    if (M < 0 || K < 8 || K > 16384 || K % 8 != 0) return MICA_MISS_SHAPE;
+    if (!ld_ok(ldx, K) || !ld_ok(ldq, K)) return MICA_MISS_STRIDE;
+    if ((long long)M * ldx >= (1ll << 31) || (long long)M * ldq >= (1ll << 31)) return MICA_MISS_RANGE;
+    if (!mica_aligned16(x) || !mica_aligned16(q) || !mica_aligned16(s) ||
+        (inv_smooth != nullptr && !mica_aligned16(inv_smooth)))
+        return MICA_MISS_ALIGN;
+    if (M == 0) return 0;
+    RowParams p{};
+    p.x = x; p.inv = inv_smooth; p.q = q; p.s = s;
+    p.ldx = ldx; p.ldq = ldq; p.M = M; p.K = K; p.rounding = rounding;
+    return dispatch_rows(p, x_dtype, false, inv_smooth != nullptr, (hipStream_t)stream);
+}
+
+extern "C" int mica_rmsnorm_quant(const void *x, int x_dtype, int ldx, const void *residual, int ldr, const void *w,
+                                  int w_dtype, float offset, float eps, const float *inv_smooth, int8_t *q, int ldq,
+                                  float *s, void *y, int ldy, void *sum, int lds, int M, int K, int rounding,
+                                  mica_stream_t stream) {
+    if (x == nullptr || w == nullptr || (q == nullptr && y == nullptr)) return MICA_MISS_ARG;
+    if (q != nullptr && s == nullptr) return MICA_MISS_ARG;
+    if (sum != nullptr && residual == nullptr) return MICA_MISS_ARG;
+    if (x_dtype != MICA_BF16 && x_dtype != MICA_FP16) return MICA_MISS_DTYPE;
+    if (w_dtype != MICA_BF16 && w_dtype != MICA_FP16 && w_dtype != MICA_FP32) return MICA_MISS_DTYPE;
+    if (rounding != MICA_ROUND_EVEN && rounding != MICA_ROUND_AWAY) return MICA_MISS_ARG;
+    if (M < 0 || K < 8 || K > 16384 || K % 8 != 0) return MICA_MISS_SHAPE;
+    if (!ld_ok(ldx, K) || (residual && !ld_ok(ldr, K)) || (q && !ld_ok(ldq, K)) || (y && !ld_ok(ldy, K)) ||
+        (sum && !ld_ok(lds, K)))
+        return MICA_MISS_STRIDE;
+    long long maxld = ldx;
+    if (residual && ldr > maxld) maxld = ldr;
+    if (q && ldq > maxld) maxld = ldq;
+    if (y && ldy > maxld) maxld = ldy;
+    if (sum && lds > maxld) maxld = lds;
+    if ((long long)M * maxld >= (1ll << 31)) return MICA_MISS_RANGE;
+    if (!mica_aligned16(x) || !mica_aligned16(w) || (residual && !mica_aligned16(residual)) ||
+        (q && !mica_aligned16(q)) || (s && !mica_aligned16(s)) || (y && !mica_aligned16(y)) ||
+        (sum && !mica_aligned16(sum)) || (inv_smooth && !mica_aligned16(inv_smooth)))
+        return MICA_MISS_ALIGN;
+    if (M == 0) return 0;
+    RowParams p{};
+    p.x = x; p.res = residual; p.w = w; p.inv = inv_smooth; p.q = q; p.s = s; p.y = y; p.sum = sum;
+    p.ldx = ldx; p.ldr = ldr; p.ldq = ldq; p.ldy = ldy; p.lds = lds;
+    p.M = M; p.K = K; p.w_dtype = w_dtype; p.rounding = rounding; p.offset = offset; p.eps = eps;
+    return dispatch_rows(p, x_dtype, true, inv_smooth != nullptr && q != nullptr, (hipStream_t)stream);
+}
+
+extern "C" int mica_swiglu(const void *g, const void *u, void *y, long long n, int dtype, mica_stream_t stream) {
+    if (g == nullptr || u == nullptr || y == nullptr) return MICA_MISS_ARG;
+    if (dtype != MICA_BF16) return MICA_MISS_DTYPE;
+    if (n < 0) return MICA_MISS_SHAPE;
+    if (!mica_aligned16(g) || !mica_aligned16(u) || !mica_aligned16(y)) return MICA_MISS_ALIGN;
+    if (n == 0) return 0;
+    const long long threads = (n + kChunk - 1) / kChunk;
+    const long long blocks = (threads + 255) / 256;
+    if (blocks >= (1ll << 31)) return MICA_MISS_RANGE;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)g, (const uint16_t *)u, (uint16_t *)y, n);
+    return mica_err(hipGetLastError());
+}

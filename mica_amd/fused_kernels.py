@@ -1,0 +1,121 @@
+"""Drop-in replacement of the reference's ``fused_kernels`` (akivet/Mica v0.5/serving/lib/fused_kernels.py)
+plus the fused RMSNorm + INT8 quantizer of the W8A8 hot path, on the gfx950 HIP kernels.
+
+  rms_norm(x, weight, eps, residual=None)            fused_kernels.py:50-82
+  swi_glu(gate, up)                                  fused_kernels.py:85-96
+  rms_norm_quant(x, weight, eps, ...)                new: the norm and QLinear's act_quant in one pass
+
+The reference runs Triton here on a GPU and torch formulas on the CPU; this build has no CPU compute
+path: a CPU tensor raises ValueError (the reference raises ValueError for unsupported layouts, :57-58).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .int8_kernels import DT, ROUNDING, _aligned, _gpu_ok, _launched, _miss, _on, _stream
+
+NORM_DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
+
+
+def _check_row_input(x, weight, residual):
+    if not x.is_cuda:
+        raise ValueError("mica_amd RMSNorm runs on the GPU only (got a CPU tensor)")
+    if x.stride(-1) != 1:
+        raise ValueError("fused RMSNorm requires unit feature stride")
+    if x.dtype not in NORM_DT:
+        raise ValueError(f"fused RMSNorm supports bf16/fp16 activations, got {x.dtype}")
+    if weight.dtype not in DT or weight.numel() != x.shape[-1] or not weight.is_contiguous():
+        raise ValueError("RMSNorm weight must be a contiguous [K] bf16/fp16/fp32 tensor")
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype):
+        raise ValueError("residual must match x in shape and dtype")
+
+
+def _launch_norm(x, weight, eps, residual, offset, inv_smooth, want_q, want_y, rounding):
+    K = x.shape[-1]
+    flat = x.reshape(-1, K)
+    if flat.stride(0) != K:
+        flat = flat.contiguous()
+    M = flat.shape[0]
+    res = None
+    if residual is not None:
+        res = residual.reshape(-1, K)
+        if not res.is_contiguous():
+            res = res.contiguous()
+    dev = x.device
+    q = torch.empty((M, K), dtype=torch.int8, device=dev) if want_q else None
+    s = torch.empty((M,), dtype=torch.float32, device=dev) if want_q else None
+    y = torch.empty((M, K), dtype=x.dtype, device=dev) if want_y else None
+    summed = torch.empty((M, K), dtype=x.dtype, device=dev) if res is not None else None
+    tensors = [t for t in (flat, weight, res, q, s, y, summed, inv_smooth) if t is not None]
+    if not _aligned(*tensors):
+        raise ValueError("fused RMSNorm requires 16-byte aligned rows")
+    if not _gpu_ok(dev):
+        raise RuntimeError(f"mica_amd kernels need a gfx950 GPU (device {dev})")
+    L = _lib.load()
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = _lib.check(_on(dev, lambda: L.mica_rmsnorm_quant(
+        ptr(flat), NORM_DT[x.dtype], K, ptr(res), K, ptr(weight), DT[weight.dtype], float(offset), float(eps),
+        ptr(inv_smooth), ptr(q), K, ptr(s), ptr(y), K, ptr(summed), K, M, K, ROUNDING[rounding],
+        _stream(dev))), "mica_rmsnorm_quant")
+    if rc > 0:
+        reason = _lib.status_name(rc)
+        _miss("norm_" + reason)
+        raise ValueError(f"fused RMSNorm does not support this input ({reason})")
+    _launched()
+    shape = x.shape
+    return (q, s, None if y is None else y.view(shape), None if summed is None else summed.view(shape))
+
+
+def rms_norm(x, weight, eps, residual=None, offset=1.0):
+    """y = bf16((v * rsqrt(mean(v^2) + eps)) * (offset + w)), v = x (+ residual rounded to x's dtype).
+
+    Returns y, or (y, v) with a residual (fused_kernels.py:50-82).  offset=1.0 is the reference's
+    Qwen3.5 ``(1 + weight)``.
+    """
+    _check_row_input(x, weight, residual)
+    _, _, y, summed = _launch_norm(x, weight, eps, residual, offset, None, False, True, "even")
+    return y if residual is None else (y, summed)
+
+
+def rms_norm_quant(x, weight, eps, inv_smooth=None, residual=None, offset=1.0, rounding="even",
+                   return_normed=False):
+    """RMSNorm + per-token INT8 quantization in one read of x.
+
+    Equals ``int8_kernels.act_quant(rms_norm(x, weight, eps, residual), inv_smooth)``: q int8 [M, K]
+    and s fp32 [M] over the flattened rows.  Returns (q, s), plus the bf16 normed rows when
+    ``return_normed``, plus the summed input v when ``residual`` is given: (q, s[, y][, v]).
+    """
+    _check_row_input(x, weight, residual)
+    K = x.shape[-1]
+    if inv_smooth is not None and (inv_smooth.dtype != torch.float32 or inv_smooth.numel() != K
+                                   or not inv_smooth.is_contiguous() or inv_smooth.device != x.device):
+        raise ValueError("inv_smooth must be a contiguous fp32 [K] tensor on x's device")
+    q, s, y, summed = _launch_norm(x, weight, eps, residual, offset, inv_smooth, True, return_normed, rounding)
+    out = (q, s)
+    if return_normed:
+        out += (y,)
+    if residual is not None:
+        out += (summed,)
+    return out
+
+
+def swi_glu(gate, up):
+    """y = bf16(bf16(silu(gate)) * up), elementwise on bf16 (fused_kernels.py:85-96)."""
+    if not gate.is_cuda:
+        raise ValueError("mica_amd swi_glu runs on the GPU only (got a CPU tensor)")
+    if not gate.is_contiguous() or not up.is_contiguous():
+        raise ValueError("fused gate-up kernel requires dense projections")
+    if gate.dtype != torch.bfloat16 or up.dtype != torch.bfloat16 or gate.shape != up.shape:
+        raise ValueError("swi_glu takes two bf16 tensors of one shape")
+    y = torch.empty_like(gate)
+    if not _aligned(gate, up, y):
+        raise ValueError("swi_glu requires 16-byte aligned tensors")
+    L = _lib.load()
+    dev = gate.device
+    rc = _lib.check(_on(dev, lambda: L.mica_swiglu(gate.data_ptr(), up.data_ptr(), y.data_ptr(), gate.numel(),
+                                                   _lib.BF16, _stream(dev))), "mica_swiglu")
+    if rc > 0:
+        raise ValueError(f"swi_glu does not support this input ({_lib.status_name(rc)})")
+    _launched()
+    return y

@@ -1,0 +1,240 @@
+"""Drop-in replacement of the reference's kernel launcher module ``int8_kernels``
+(akivet/Mica v0.5/serving/lib/int8_kernels.py), backed by the gfx950 HIP kernels of libmica_amd.so.
+
+Same contract as the reference:
+  * ``act_quant(x, inv_smooth=None) -> (q, s) | None`` (int8_kernels.py:325-353)
+  * ``mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16) -> Tensor | None`` (:359-406)
+  * ``available(device=None) -> (bool, str)`` (:146-159), ``preload(device=None) -> int`` (:217-224),
+    ``kernel_dir()`` (:83-84), ``STATS`` (:19), ``ATTN`` / ``attn_keys`` / ``attn_fwd`` (:409-481)
+  * an unsupported input returns ``None`` and counts the reason in ``STATS['fallback']`` (:22-24);
+    every launch adds 1 to ``STATS['launch']`` (:310); a device error raises RuntimeError (:60-64).
+  * outputs are allocated with torch on the input's device; kernels run on torch's current stream
+    (:261-265); nothing synchronises, so the calls can be captured in a HIP graph.
+
+Extensions used by the fused hot path: ``rounding='away'`` (the Triton kernel's rounding,
+kernel_src/kernels.py:35), ``mm_i8(..., residual=, epilogue='silu_mul')``, ``mm_i8_int32`` (raw
+accumulators), and ``STRICT`` (env ``MICA_AMD_STRICT=1``) which turns a miss into an exception.
+
+Attention stays a torch op in this build: ``attn_fwd`` always misses with reason ``attn_unsupported``,
+exactly like the reference on a device whose container has no attention kernel.
+"""
+from __future__ import annotations
+
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+from . import _lib
+
+DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16, torch.float32: _lib.FP32}
+I32 = 2 ** 31
+STATS = {"launch": 0, "fallback": {}}
+STRICT = os.environ.get("MICA_AMD_STRICT", "") not in ("", "0")
+ROUNDING = {"even": _lib.ROUND_EVEN, "away": _lib.ROUND_AWAY}
+EPILOGUE = {"none": _lib.EPI_SCALE, "silu_mul": _lib.EPI_SILU_MUL}
+_STATS_LOCK = threading.Lock()
+
+
+class KernelMiss(RuntimeError):
+    """Raised instead of returning None when STRICT is set."""
+
+
+def _miss(reason):
+    with _STATS_LOCK:
+        STATS["fallback"][reason] = STATS["fallback"].get(reason, 0) + 1
+    if STRICT:
+        raise KernelMiss(f"mica_amd kernel miss: {reason}")
+    return None
+
+
+def _launched():
+    with _STATS_LOCK:
+        STATS["launch"] += 1
+
+
+def kernel_dir() -> Path:
+    """Directory holding libmica_amd.so (env MICA_AMD_LIB_DIR overrides)."""
+    return _lib.lib_path().parent
+
+
+_ARCH = {}
+
+
+def _dev(device):
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return dev
+
+
+def _gfx(dev) -> int:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _ARCH:
+        _ARCH[idx] = _lib.device_info(idx)["gfx_arch"]
+    return _ARCH[idx]
+
+
+def available(device=None):
+    """(True, description) when the kernels can run on ``device`` (a gfx950 GPU)."""
+    if not torch.cuda.is_available():
+        return (False, "no ROCm GPU available")
+    dev = _dev(device)
+    if dev.type != "cuda":
+        return (False, f"{dev} is not a GPU device")
+    try:
+        _lib.load()
+    except (OSError, RuntimeError) as exc:
+        return (False, f"library: {exc!r}"[:200])
+    arch = _gfx(dev)
+    if arch != 950:
+        return (False, f"gfx{arch} is not gfx950")
+    return (True, f"gfx950 kernels from {kernel_dir()}")
+
+
+def preload(device=None) -> int:
+    """Load the library (its code objects register with the HIP runtime at load); returns the number
+    of launchers it exports, or 0 when the device cannot run them."""
+    ok, _ = available(device)
+    if not ok:
+        return 0
+    return sum(1 for name in _lib.SIGNATURES if name not in ("mica_version", "mica_status_name",
+                                                            "mica_device_info"))
+
+
+def _stream(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _aligned(*ts):
+    return all(t.data_ptr() % 16 == 0 for t in ts)
+
+
+def _on(dev, call):
+    if dev.index is None or torch.cuda.current_device() == dev.index:
+        return call()
+    with torch.cuda.device(dev):
+        return call()
+
+
+def _run(dev, name, fn, *args):
+    """Launch through the C ABI on the current stream; returns True, or None on a miss."""
+    rc = _lib.check(_on(dev, lambda: fn(*args, _stream(dev))), name)
+    if rc > 0:
+        return _miss(_lib.status_name(rc))
+    _launched()
+    return True
+
+
+def _gpu_ok(dev):
+    return dev.type == "cuda" and _gfx(dev) == 950
+
+
+def act_quant(x, inv_smooth=None, rounding="even"):
+    """Per-token INT8 quantization of a 2-D activation (int8_kernels.py:325-353)."""
+    if x.dim() != 2 or x.device.type != "cuda" or x.dtype not in DT:
+        return _miss("act_input")
+    m, k = x.shape
+    if x.stride(1) != 1 or x.stride(0) != k:
+        return _miss("act_contiguous")
+    if not _gpu_ok(x.device):
+        return _miss("no_container")
+    if inv_smooth is not None and (inv_smooth.dtype != torch.float32 or not inv_smooth.is_contiguous()
+                                   or inv_smooth.numel() != k or inv_smooth.device != x.device):
+        return _miss("act_inv")
+    if m * k >= I32:
+        return _miss("i32_range")
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    if not _aligned(x, q, s, *(() if inv_smooth is None else (inv_smooth,))):
+        return _miss("align")
+    L = _lib.load()
+    ok = _run(x.device, "mica_act_quant", L.mica_act_quant, x.data_ptr(), DT[x.dtype], k,
+              None if inv_smooth is None else inv_smooth.data_ptr(), q.data_ptr(), k, s.data_ptr(), m, k,
+              ROUNDING[rounding])
+    return (q, s) if ok else None
+
+
+def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, epilogue="none"):
+    """C = (qx . qw^T)_i32 * sx[m] * sw[n] (+ bias[n]) -> out_dtype (int8_kernels.py:359-406).
+
+    Extensions: ``residual`` ([M, N] of out_dtype) is added after the output rounding;
+    ``epilogue='silu_mul'`` treats qw as gate/up rows interleaved in groups of 64
+    (int8_runtime.pack_gate_up) and returns bf16(bf16(silu(gate)) * up) of shape [M, N / 2].
+    """
+    if qx.dim() != 2 or qw.dim() != 2 or qx.dtype != torch.int8 or qw.dtype != torch.int8 or out_dtype not in DT:
+        return _miss("mm_input")
+    m, k = qx.shape
+    n = qw.shape[0]
+    if qw.shape[1] != k or qx.stride(1) != 1 or qw.stride(1) != 1 or qx.stride(0) != k or qw.stride(0) != k:
+        return _miss("mm_contiguous")
+    for t, size in ((sx, m), (sw, n)) + (((bias, n),) if bias is not None else ()):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != size or t.device != qx.device:
+            return _miss("mm_scales")
+    if qw.device != qx.device:
+        return _miss("mm_device")
+    if qx.device.type != "cuda" or not _gpu_ok(qx.device):
+        return _miss("no_container")
+    if epilogue not in EPILOGUE:
+        return _miss("mm_epilogue")
+    n_out = n // 2 if epilogue == "silu_mul" else n
+    if epilogue == "silu_mul" and (n % 128 or out_dtype != torch.bfloat16 or bias is not None
+                                   or residual is not None):
+        return _miss("mm_epilogue")
+    if residual is not None and (residual.shape != (m, n_out) or residual.dtype != out_dtype
+                                 or not residual.is_contiguous() or residual.device != qx.device):
+        return _miss("mm_residual")
+    if m * max(k, n) >= I32:
+        return _miss("i32_range")
+    if k % 16:
+        return _miss("div16:K")
+    out = torch.empty((m, n_out), dtype=out_dtype, device=qx.device)
+    extra = tuple(t for t in (bias, residual) if t is not None)
+    if not _aligned(qx, qw, sx, sw, out, *extra):
+        return _miss("align")
+    L = _lib.load()
+    ok = _run(qx.device, "mica_mm_i8", L.mica_mm_i8, qx.data_ptr(), k, qw.data_ptr(), k, sx.data_ptr(),
+              sw.data_ptr(), None if bias is None else bias.data_ptr(),
+              None if residual is None else residual.data_ptr(), n_out, out.data_ptr(), n_out, DT[out_dtype],
+              m, n, k, EPILOGUE[epilogue])
+    return out if ok else None
+
+
+def mm_i8_int32(qx, qw):
+    """Raw int32 accumulators qx . qw^T on the matrix cores (the int32 result of
+    int8_quant.torch_int_mm, int8_quant.py:92-96), or None on a miss."""
+    if qx.dim() != 2 or qw.dim() != 2 or qx.dtype != torch.int8 or qw.dtype != torch.int8:
+        return _miss("mm_input")
+    m, k = qx.shape
+    n = qw.shape[0]
+    if qw.shape[1] != k or not qx.is_contiguous() or not qw.is_contiguous() or qw.device != qx.device:
+        return _miss("mm_contiguous")
+    if qx.device.type != "cuda" or not _gpu_ok(qx.device):
+        return _miss("no_container")
+    if k % 16:
+        return _miss("div16:K")
+    if m * max(k, n) >= I32:
+        return _miss("i32_range")
+    out = torch.empty((m, n), dtype=torch.int32, device=qx.device)
+    dummy = torch.empty((max(m, n, 1),), dtype=torch.float32, device=qx.device)
+    if not _aligned(qx, qw, out):
+        return _miss("align")
+    L = _lib.load()
+    ok = _run(qx.device, "mica_mm_i8", L.mica_mm_i8, qx.data_ptr(), k, qw.data_ptr(), k, dummy.data_ptr(),
+              dummy.data_ptr(), None, None, n, out.data_ptr(), n, _lib.INT32, m, n, k, _lib.EPI_SCALE)
+    return out if ok else None
+
+
+ATTN = {"enabled": False}
+
+
+def attn_keys(device=None):
+    """No attention kernels ship in this build (attention runs as a torch op)."""
+    return []
+
+
+def attn_fwd(q, k, v, scale):
+    """Always a miss: the causal GQA attention of the reference (kernel_src/kernels.py:71-124) is outside
+    this build's scope and stays on torch's scaled_dot_product_attention."""
+    return _miss("attn_unsupported")

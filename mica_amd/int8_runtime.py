@@ -1,0 +1,319 @@
+"""W8A8 linear modules on the gfx950 kernels: a drop-in ``QLinear`` (akivet/Mica
+v0.5/serving/lib/int8_runtime.py:108-192), the fused gate+up projection of the gated MLP, and the
+reference's numerical self-test (int8_runtime.py:362-443).
+
+Buffers follow the reference (int8_runtime.py:124-127): ``qweight`` int8 [N, K] (K-contiguous),
+``wscale`` fp32 [N], ``inv_smooth`` fp32 [K] or None, ``bias`` fp32 [N] or None.
+"""
+from __future__ import annotations
+
+import time
+import types
+
+import torch
+from torch import nn
+
+from . import int8_kernels as aot
+from .fused_kernels import rms_norm_quant
+
+EPS = 1e-08              # int8_quant.py:13
+QMAX = 127.0             # int8_quant.py:11
+ALPHA = 0.5              # int8_runtime.py:10
+GATE_UP_GROUP = 64       # rows per gate / up group of the fused gate+up weight
+SELFTEST_ROWS = (3, 48, 200, 608, 1500)   # int8_runtime.py:288
+SELFTEST_TOL = 1.05                       # int8_runtime.py:289
+SELFTEST_SEED = 20261022                  # int8_runtime.py:290
+
+
+def quant_weight(w: torch.Tensor):
+    """Per-output-channel symmetric int8 (int8_quant.quant_weight, int8_quant.py:54-61); offline."""
+    wf = w.float()
+    s = wf.abs().amax(1).clamp_min(EPS) / QMAX
+    q = torch.round(wf / s[:, None]).clamp(-127, 127).to(torch.int8)
+    return q, s
+
+
+def smooth_factors(act_amax, w, alpha=ALPHA, lo=0.0001, hi=10000.0):
+    """SmoothQuant factors (int8_quant.smooth_factors, int8_quant.py:80-85); offline."""
+    a = act_amax.float().to(w.device)
+    wmax = w.float().abs().amax(0)
+    s = a.clamp_min(EPS).pow(alpha) / wmax.clamp_min(EPS).pow(1.0 - alpha)
+    s = torch.where((a > 0) & (wmax > 0), s, torch.ones_like(s))
+    return s.clamp(lo, hi)
+
+
+def _torch_quant_act(x, inv_smooth):
+    """The reference's fallback quantizer (int8_quant.quant_act, int8_quant.py:64-73) on the GPU."""
+    xf = x.float()
+    if inv_smooth is not None:
+        xf = xf * inv_smooth
+    s = xf.abs().amax(-1).clamp_min(EPS) / QMAX
+    return torch.round(xf / s[:, None]).clamp(-127, 127).to(torch.int8), s
+
+
+def _torch_mm(qx, sx, qw, sw, bias, out_dtype):
+    """The reference's fallback GEMM (int8_runtime.py:186-192) on torch's GPU int8 matmul."""
+    m = qx.shape[0]
+    a = qx if m > 16 else torch.cat((qx, qx.new_zeros(32 - m, qx.shape[1])), 0)
+    y = torch._int_mm(a, qw.t())[:m].float() * sx[:, None] * sw[None, :]
+    if bias is not None:
+        y = y + bias
+    return y.to(out_dtype)
+
+
+def _require_gpu(x):
+    if not x.is_cuda:
+        raise ValueError("mica_amd W8A8 modules run on the GPU only (got a CPU tensor)")
+
+
+class QLinear(nn.Module):
+    """W8A8 linear: per-token int8 activations x per-channel int8 weights, bf16 out.
+
+    forward(x) = 2 launches (act_quant + mm_i8), as the reference asserts in its self-test
+    (int8_runtime.py:385-402); forward_quantized(qx, sx) = 1 launch for callers that produced the
+    int8 activations themselves (the fused RMSNorm + quantizer).
+    """
+
+    def __init__(self, linear, smooth=None, backend="aot", keep_bf16=False):
+        super().__init__()
+        w = linear.weight.detach()
+        self.register_buffer("w16", w.contiguous() if keep_bf16 else None)
+        self.in_features, self.out_features = w.shape[1], w.shape[0]
+        self.out_dtype, self.backend, self.mode = w.dtype, backend, "int8"
+        wf = w.float()
+        if smooth is not None:
+            smooth = smooth.float().to(w.device)
+            wf = wf * smooth[None, :]
+            self.register_buffer("inv_smooth", (1.0 / smooth).contiguous())
+        else:
+            self.inv_smooth = None
+        q, s = quant_weight(wf)
+        self.register_buffer("qweight", q.contiguous())
+        self.register_buffer("wscale", s.contiguous())
+        self.register_buffer("bias", None if linear.bias is None else linear.bias.detach().float().contiguous())
+
+    @classmethod
+    def from_quantized(cls, qweight, wscale, bias=None, inv_smooth=None, out_dtype=torch.bfloat16):
+        """Wrap already-quantized buffers (the layout of int8_runtime.load_file, :748-776)."""
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.register_buffer("w16", None)
+        self.out_features, self.in_features = qweight.shape
+        self.out_dtype, self.backend, self.mode = out_dtype, "aot", "int8"
+        self.register_buffer("qweight", qweight.contiguous())
+        self.register_buffer("wscale", wscale.float().contiguous())
+        if inv_smooth is not None:
+            self.register_buffer("inv_smooth", inv_smooth.float().contiguous())
+        else:
+            self.inv_smooth = None
+        self.register_buffer("bias", None if bias is None else bias.float().contiguous())
+        return self
+
+    @classmethod
+    def empty(cls, in_features, out_features, out_dtype=torch.bfloat16, backend="aot", smooth=True, bias=False):
+        """Meta-device shell to be filled by a loader (int8_runtime.py:129-144)."""
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.register_buffer("w16", None)
+        self.in_features, self.out_features = in_features, out_features
+        self.out_dtype, self.backend, self.mode = out_dtype, backend, "int8"
+
+        def meta(*shape, dtype=torch.float32):
+            return torch.empty(*shape, dtype=dtype, device="meta")
+
+        if smooth:
+            self.register_buffer("inv_smooth", meta(in_features))
+        else:
+            self.inv_smooth = None
+        self.register_buffer("qweight", meta(out_features, in_features, dtype=torch.int8))
+        self.register_buffer("wscale", meta(out_features))
+        self.register_buffer("bias", meta(out_features) if bias else None)
+        return self
+
+    @property
+    def weight(self):
+        w = self.qweight.float() * self.wscale.reshape(-1, 1)
+        return (w * self.inv_smooth[None, :] if self.inv_smooth is not None else w).to(self.out_dtype)
+
+    def _quant(self, x2):
+        r = aot.act_quant(x2.contiguous(), self.inv_smooth)
+        return r if r is not None else _torch_quant_act(x2, self.inv_smooth)
+
+    def _mm(self, qx, sx, qw, sw, b, residual=None):
+        y = aot.mm_i8(qx, sx, qw, sw, b, self.out_dtype, residual=residual)
+        if y is None:
+            y = _torch_mm(qx, sx, qw, sw, b, self.out_dtype)
+            if residual is not None:
+                y = y + residual
+        return y
+
+    def rows_forward(self, x, ranges):
+        """Quantize once, one GEMM per output-row range (int8_runtime.py:153-170)."""
+        _require_gpu(x)
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        qx, sx = self._quant(x2)
+        outs = []
+        for lo, hi in ranges:
+            b = None if self.bias is None else self.bias[lo:hi]
+            y = self._mm(qx, sx, self.qweight[lo:hi], self.wscale[lo:hi], b)
+            outs.append(y.reshape(*shape[:-1], hi - lo))
+        return outs
+
+    def forward(self, x, residual=None):
+        """y = QLinear(x) (int8_runtime.py:172-192); ``residual`` (same shape as y) is added in the
+        GEMM epilogue after the bf16 rounding, i.e. ``residual + QLinear(x)``."""
+        if self.w16 is not None and PRECISION["mode"] == "bf16":
+            y = nn.functional.linear(x, self.w16, None if self.bias is None else self.bias.to(self.w16.dtype))
+            return y if residual is None else residual + y
+        _require_gpu(x)
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        if x2.shape[0] == 0:
+            return x.new_zeros(*shape[:-1], self.out_features, dtype=self.out_dtype)
+        qx, sx = self._quant(x2)
+        res = None if residual is None else residual.reshape(-1, self.out_features)
+        return self._mm(qx, sx, self.qweight, self.wscale, self.bias, res).reshape(*shape[:-1], self.out_features)
+
+    def forward_quantized(self, qx, sx, residual=None):
+        """GEMM + epilogue on activations already quantized per token (e.g. by rms_norm_quant)."""
+        _require_gpu(qx)
+        if qx.shape[0] == 0:
+            return torch.zeros(0, self.out_features, dtype=self.out_dtype, device=qx.device)
+        return self._mm(qx, sx, self.qweight, self.wscale, self.bias, residual)
+
+
+PRECISION = {"mode": "int8"}  # int8_runtime.py:21
+
+
+def pack_gate_up(qg, sg, qu, su, group: int = GATE_UP_GROUP):
+    """Interleave gate and up rows in groups of ``group``: [g_0..g_63, u_0..u_63, g_64.., u_64.., ...].
+
+    Within one 128-row group the fused GEMM's SILU_MUL epilogue finds gate column c and up column c in
+    the same lane, so silu(gate) * up never leaves registers."""
+    n, k = qg.shape
+    if qu.shape != (n, k) or n % group:
+        raise ValueError(f"gate/up weights must both be [N, K] with N % {group} == 0")
+    q = torch.stack((qg.reshape(n // group, group, k), qu.reshape(n // group, group, k)), 1).reshape(2 * n, k)
+    s = torch.stack((sg.reshape(n // group, group), su.reshape(n // group, group)), 1).reshape(2 * n)
+    return q.contiguous(), s.float().contiguous()
+
+
+class GateUpQLinear(nn.Module):
+    """gate_proj and up_proj of a gated MLP as one W8A8 GEMM (N = 2 x intermediate) whose epilogue
+    returns h = bf16(bf16(silu(gate)) * up) -- the reference's gate QLinear, up QLinear and swi_glu
+    (fast_runtime.py:126-132) in one launch, with the same roundings."""
+
+    def __init__(self, gate: QLinear, up: QLinear):
+        super().__init__()
+        if gate.inv_smooth is not None or up.inv_smooth is not None:
+            raise ValueError("the fused gate+up GEMM shares one activation quantization: no smoothing")
+        if gate.bias is not None or up.bias is not None:
+            raise ValueError("the fused gate+up GEMM has no bias")
+        q, s = pack_gate_up(gate.qweight, gate.wscale, up.qweight, up.wscale)
+        self.register_buffer("qweight", q)
+        self.register_buffer("wscale", s)
+        self.in_features = gate.in_features
+        self.out_features = gate.out_features
+
+    def forward_quantized(self, qx, sx):
+        _require_gpu(qx)
+        h = aot.mm_i8(qx, sx, self.qweight, self.wscale, None, torch.bfloat16, epilogue="silu_mul")
+        if h is None:
+            raise RuntimeError("fused gate+up GEMM is not supported for this input")
+        return h
+
+    def forward(self, x):
+        _require_gpu(x)
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        r = aot.act_quant(x2)
+        qx, sx = r if r is not None else _torch_quant_act(x2, None)
+        return self.forward_quantized(qx, sx).reshape(*shape[:-1], self.out_features)
+
+
+class W8A8MLP(nn.Module):
+    """post_attention_layernorm + gated MLP + residual of one decoder layer (fork.py:419-422), as
+    3 launches: fused RMSNorm+quant, fused gate+up GEMM with SiLU epilogue, act_quant of h, and the
+    down GEMM with the residual add in its epilogue (4 launches in total)."""
+
+    def __init__(self, norm_weight, eps, gate_up: GateUpQLinear, down: QLinear, offset=1.0):
+        super().__init__()
+        self.register_buffer("norm_weight", norm_weight.contiguous())
+        self.eps, self.offset = float(eps), float(offset)
+        self.gate_up, self.down = gate_up, down
+
+    def forward(self, h):
+        shape = h.shape
+        q, s = rms_norm_quant(h, self.norm_weight, self.eps, offset=self.offset)
+        g = self.gate_up.forward_quantized(q, s)
+        r = aot.act_quant(g)
+        qh, sh = r if r is not None else _torch_quant_act(g, None)
+        out = self.down.forward_quantized(qh, sh, residual=h.reshape(-1, shape[-1]))
+        return out.reshape(shape)
+
+
+# ---------------------------------------------------------------------------------- self-test
+def _row_rel(a, b):
+    return float(((a - b).norm(dim=-1) / b.norm(dim=-1).clamp_min(1e-30)).max())
+
+
+def selftest(shapes, device, rows=SELFTEST_ROWS, seed=SELFTEST_SEED):
+    """The reference's acceptance test (int8_runtime.py:362-443), on this build's kernels.
+
+    For every (N, K, has_bias) and every row count, with and without SmoothQuant factors: QLinear(x)
+    must take exactly 2 kernel launches, be finite, and its row-relative L2 error against the fp32
+    dequantized product must be <= 1.05 x that of an exact INT8 emulation.
+    """
+    t0 = time.perf_counter()
+    out = {"ok": False, "reason": "", "checked": 0, "worst_ratio": 0.0}
+    try:
+        dev = torch.device(device)
+        g = torch.Generator().manual_seed(seed)
+        launches0 = aot.STATS["launch"]
+        for n, k, has_bias in shapes:
+            n, k = int(n), int(k)
+            w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16)
+            amax = torch.rand(k, generator=g) * 4 + 0.05
+            amax[::61] *= 25.0
+            b = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).to(dev) if has_bias else None
+            lin = types.SimpleNamespace(weight=w.to(dev), bias=b)
+            for smooth in (smooth_factors(amax, w, ALPHA), None):
+                q = QLinear(lin, smooth)
+                wd = q.qweight.float() * q.wscale[:, None]
+                if q.inv_smooth is not None:
+                    wd = wd * q.inv_smooth[None, :]
+                for m in rows:
+                    x = (torch.randn(m, k, generator=g) * amax / 3).to(torch.bfloat16).to(dev)
+                    l0, f0 = aot.STATS["launch"], dict(aot.STATS["fallback"])
+                    y = q(x).float()
+                    launched = aot.STATS["launch"] - l0
+                    if launched != 2:
+                        miss = {r: c - f0.get(r, 0) for r, c in aot.STATS["fallback"].items() if c != f0.get(r, 0)}
+                        out["reason"] = f"N {n} K {k} M {m}: {launched} launches (expected 2), misses {miss}"
+                        return out
+                    ref = x.float() @ wd.t()
+                    qx, sx = _torch_quant_act(x, q.inv_smooth)
+                    emu = (qx.double() @ q.qweight.double().t()).float() * sx[:, None] * q.wscale[None, :]
+                    if q.bias is not None:
+                        ref, emu = ref + q.bias, emu + q.bias
+                    emu = emu.to(q.out_dtype).float()
+                    noise, err = _row_rel(emu, ref), _row_rel(y, ref)
+                    if not bool(torch.isfinite(y).all()):
+                        out["reason"] = f"non-finite output (N {n}, K {k}, M {m})"
+                        return out
+                    if not err <= SELFTEST_TOL * noise:
+                        out["reason"] = (f"N {n} K {k} M {m}: error {err:.4g} > {SELFTEST_TOL:.2f} x INT8 noise "
+                                         f"{noise:.4g}")
+                        return out
+                    out["worst_ratio"] = max(out["worst_ratio"], err / max(noise, 1e-30))
+                    out["checked"] += 1
+        if dev.type == "cuda":
+            torch.cuda.synchronize(dev)
+        out.update(ok=True, reason="ok", launches=aot.STATS["launch"] - launches0)
+        out["worst_ratio"] = round(out["worst_ratio"], 5)
+    except Exception as exc:  # noqa: BLE001 -- the reference reports any failure as a reason string
+        out["reason"] = f"{type(exc).__name__}: {exc}"[:300]
+    finally:
+        out["seconds"] = round(time.perf_counter() - t0, 2)
+    return out

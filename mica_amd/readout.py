@@ -1,0 +1,71 @@
+"""Last-position label readout on the gfx950 kernel: only the allowed answer rows of the output
+embedding are ever multiplied, and only at each request's last token.
+
+Reference: the readout closure built in HFJudge.__init__ (akivet/Mica
+v0.5/serving/lib/release_runtime.py:298-306) applied to ``body.norm`` of the last hidden row
+(prefill_engine.py:280-304), then the slice + softmax of judge_many (release_runtime.py:509-517).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .int8_kernels import DT, _gpu_ok, _launched, _on, _stream
+
+
+class LabelReadout:
+    """Readout over label rows of the output embedding.
+
+    ``gather=True`` copies the rows once as fp32, as the reference does (release_runtime.py:301);
+    ``gather=False`` keeps the bf16 table and indexes it by id inside the kernel.
+    """
+
+    def __init__(self, lm_head_weight: torch.Tensor, ids, gather: bool = True):
+        ids = torch.as_tensor(ids, dtype=torch.long, device=lm_head_weight.device)
+        self.n_labels = int(ids.numel())
+        if gather:
+            self.weight = lm_head_weight.detach().index_select(0, ids).float().contiguous()
+            self.ids = None
+        else:
+            if lm_head_weight.dtype != torch.bfloat16:
+                raise ValueError("an un-gathered table must be bf16")
+            self.weight = lm_head_weight.detach().contiguous()
+            self.ids = ids.to(torch.int32).contiguous()
+
+    def __call__(self, h, rows, norm_weight=None, eps=1e-6, offset=1.0, lo=None, cnt=None, probs_width=None):
+        """h: [T, K] bf16 hidden states (packed requests); rows: int [B] index of each request's last
+        token; norm_weight: the final RMSNorm weight or None (h already normed).
+        lo / cnt: int [B] start and length of each request's softmax slice (None: all labels).
+        Returns (logits fp32 [B, L], probs fp32 [B, width])."""
+        if not h.is_cuda:
+            raise ValueError("mica_amd readout runs on the GPU only (got a CPU tensor)")
+        if h.dtype != torch.bfloat16 or h.dim() != 2 or h.stride(1) != 1:
+            raise ValueError("h must be a 2-D bf16 tensor with unit feature stride")
+        dev = h.device
+        if not _gpu_ok(dev):
+            raise RuntimeError(f"mica_amd kernels need a gfx950 GPU (device {dev})")
+        K = h.shape[1]
+        rows = torch.as_tensor(rows, device=dev).to(torch.int32).contiguous()
+        B = rows.numel()
+        L = self.n_labels
+        logits = torch.empty((B, L), dtype=torch.float32, device=dev)
+        if lo is not None:
+            lo = torch.as_tensor(lo, device=dev).to(torch.int32).contiguous()
+            cnt = torch.as_tensor(cnt, device=dev).to(torch.int32).contiguous()
+            width = probs_width or int(cnt.max().item()) if B else 0
+        else:
+            width = L
+        probs = torch.zeros((B, max(width, 1)), dtype=torch.float32, device=dev)
+        nw = None if norm_weight is None else norm_weight.contiguous()
+        lib = _lib.load()
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        wdt = _lib.FP32 if self.weight.dtype == torch.float32 else _lib.BF16
+        rc = _lib.check(_on(dev, lambda: lib.mica_gather_logits(
+            h.data_ptr(), h.stride(0), h.shape[0], rows.data_ptr(), B, ptr(nw),
+            DT[nw.dtype] if nw is not None else 0, float(offset), float(eps), self.weight.data_ptr(), wdt,
+            self.weight.stride(0), self.weight.shape[0], ptr(self.ids), L, K, logits.data_ptr(), ptr(lo), ptr(cnt),
+            probs.data_ptr(), probs.shape[1], _stream(dev))), "mica_gather_logits")
+        if rc > 0:
+            raise ValueError(f"readout does not support this input ({_lib.status_name(rc)})")
+        _launched()
+        return logits, probs

@@ -1,0 +1,230 @@
+"""numpy restatement of the reference's W8A8 arithmetic (test infrastructure; see oracle/__init__.py).
+
+Conventions: bf16 tensors are numpy ``uint16`` arrays of bit patterns; every fp32 step is an explicit
+``np.float32`` operation, so IEEE single rounding happens exactly where the reference's torch code
+rounds.  Reference citations are into akivet/Mica ``v0.5/serving/``.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+QMAX = F32(127.0)   # int8_quant.py:11
+EPS = F32(1e-8)     # int8_quant.py:13 (a python float clamped against an fp32 tensor -> fp32)
+
+
+# ---------------------------------------------------------------- bf16 helpers
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns -> fp32 values (exact)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even (torch's ``.to(torch.bfloat16)``); NaN -> 0x7fc0."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(np.isnan(x), np.uint16(0x7FC0), rounded)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """Round fp32 values to bf16 and return them as fp32."""
+    return bf16_to_f32(f32_to_bf16(x))
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    return np.asarray(x, dtype=np.float32).astype(np.float16)
+
+
+def bf16_ulp(bits: np.ndarray) -> np.ndarray:
+    """Size of one bf16 unit in the last place at each value (fp32)."""
+    v = np.abs(bf16_to_f32(bits)).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(v, 2.0 ** -126)))
+    return (2.0 ** (e - 7)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- quantizers
+def quant_act(x: np.ndarray, inv_smooth: np.ndarray | None = None, rounding: str = "even"):
+    """Per-token symmetric INT8 quantizer.
+
+    rounding='even': int8_quant.quant_act (int8_quant.py:64-73): ``xf = x.float()``, optional
+    ``xf * inv_smooth``, ``s = amax.clamp_min(1e-8) / 127``, ``q = round_half_even(xf / s)`` clamped
+    to +-127.  rounding='away': the Triton act_quant (kernel_src/kernels.py:26-36):
+    ``v = x / scale; r = int(v + 0.5 if v >= 0 else v - 0.5)`` (fp32 add, truncation).
+
+    x: fp32 values (already widened from bf16/fp16), shape [M, K].  Returns (q int8 [M, K], s fp32 [M]).
+    """
+    xf = np.asarray(x, dtype=np.float32)
+    if inv_smooth is not None:
+        xf = xf * np.asarray(inv_smooth, dtype=np.float32)
+    amax = np.abs(xf).max(axis=-1) if xf.shape[-1] else np.zeros(xf.shape[:-1], np.float32)
+    s = np.maximum(amax, EPS) / QMAX
+    v = xf / s[..., None]
+    if rounding == "even":
+        r = np.rint(v)
+    elif rounding == "away":
+        r = np.trunc(np.where(v >= 0, v + F32(0.5), v - F32(0.5)))
+    else:
+        raise ValueError(rounding)
+    q = np.clip(r, -127, 127).astype(np.int8)
+    return q, s.astype(np.float32)
+
+
+def quant_weight(w: np.ndarray):
+    """Per-output-channel weight quantizer, int8_quant.quant_weight (int8_quant.py:54-61)."""
+    wf = np.asarray(w, dtype=np.float32)
+    s = np.maximum(np.abs(wf).max(axis=1), EPS) / QMAX
+    q = np.clip(np.rint(wf / s[:, None]), -127, 127).astype(np.int8)
+    return q, s.astype(np.float32)
+
+
+# ---------------------------------------------------------------- GEMM
+def int_gemm(qa: np.ndarray, qw: np.ndarray) -> np.ndarray:
+    """acc[m, n] = sum_k qa[m, k] * qw[n, k], exact int32 (int8_quant.int_gemm_exact, int8_quant.py:88-89).
+
+    Evaluated in float64 like the reference: every partial sum is an integer of magnitude
+    <= K * 127^2 < 2^53 for K < 5.5e8, so the float64 result is exact.
+    """
+    qa = np.asarray(qa, dtype=np.int8)
+    qw = np.asarray(qw, dtype=np.int8)
+    assert qa.shape[1] * 127 * 127 < 2 ** 53
+    return (qa.astype(np.float64) @ qw.astype(np.float64).T).astype(np.int32)
+
+
+def epilogue(acc: np.ndarray, sa: np.ndarray, sb: np.ndarray, bias: np.ndarray | None = None,
+             out: str = "bf16"):
+    """y = (f32(acc) * sa[m]) * sb[n] (+ bias[n]), then converted to the output dtype.
+
+    int8_runtime.py:186 ``torch_int_mm(qx, w).float() * sx[:, None] * wscale[None, :]``, :190-192
+    ``y + bias`` then ``.to(out_dtype)``; Triton kernels.py:65-68 in the same order.
+    Returns bf16 bits (out='bf16'), float16 (out='fp16') or float32 (out='fp32').
+    """
+    y = np.asarray(acc, dtype=np.int32).astype(np.float32) * np.asarray(sa, np.float32)[:, None]
+    y = y * np.asarray(sb, np.float32)[None, :]
+    if bias is not None:
+        y = y + np.asarray(bias, np.float32)[None, :]
+    if out == "bf16":
+        return f32_to_bf16(y)
+    if out == "fp16":
+        return f32_to_f16(y)
+    return y.astype(np.float32)
+
+
+def qlinear(x_bits: np.ndarray, qw: np.ndarray, sw: np.ndarray, bias=None, inv_smooth=None,
+            rounding: str = "even"):
+    """QLinear.forward on bf16 x (int8_runtime.py:172-192): quantize, exact GEMM, epilogue -> bf16 bits."""
+    q, s = quant_act(bf16_to_f32(x_bits), inv_smooth, rounding)
+    return epilogue(int_gemm(q, qw), s, sw, bias)
+
+
+# ---------------------------------------------------------------- RMSNorm
+def rms_norm(x_bits: np.ndarray, w: np.ndarray, eps: float, offset: float = 1.0,
+             residual_bits: np.ndarray | None = None):
+    """RMSNorm of fused_kernels.rms_norm, CPU branch (fused_kernels.py:51-56):
+
+    value = x (+ residual, rounded to bf16); xf = value.float()
+    y = bf16((xf * rsqrt(mean(xf^2) + eps)) * (offset + w))
+
+    offset=1 is the Qwen3.5 ``(1 + weight)``; offset=0 a plain gamma.  w: fp32 values of the weight.
+    mean(xf^2) is evaluated as RN32(exact sum) / K: torch's fp32 summation order is not a fixed
+    reference, so the exact sum rounded once is used (the kernel's fp32 tree may differ by ulps;
+    tests bound that at one bf16 ulp of y).  rsqrt = 1 / sqrt, two correctly rounded fp32 ops
+    (torch CPU's Vectorized<float>::rsqrt).
+    Returns (y_bits, value_bits).
+    """
+    x_bits = np.asarray(x_bits, dtype=np.uint16)
+    if residual_bits is not None:
+        value = f32_to_bf16(bf16_to_f32(x_bits) + bf16_to_f32(residual_bits))
+    else:
+        value = x_bits
+    xf = bf16_to_f32(value)
+    K = xf.shape[-1]
+    ss = F32((xf.astype(np.float64) ** 2).sum(axis=-1))  # squares of bf16 values are exact in fp64
+    ss = np.asarray(ss, dtype=np.float32)
+    mean = ss / F32(K)
+    rstd = F32(1.0) / np.sqrt(mean + F32(eps))
+    w1 = F32(offset) + np.asarray(w, dtype=np.float32)
+    y = (xf * rstd[..., None]) * w1
+    return f32_to_bf16(y), value
+
+
+def rms_norm_quant(x_bits, w, eps, offset=1.0, residual_bits=None, inv_smooth=None, rounding="even"):
+    """rms_norm followed by quant_act on its bf16 output (the QLinear input path, int8_runtime.py:181)."""
+    y, value = rms_norm(x_bits, w, eps, offset, residual_bits)
+    q, s = quant_act(bf16_to_f32(y), inv_smooth, rounding)
+    return q, s, y, value
+
+
+# ---------------------------------------------------------------- SwiGLU / MLP
+def silu_mul(g_bits: np.ndarray, u_bits: np.ndarray) -> np.ndarray:
+    """h = bf16(bf16(silu(g)) * u) on bf16 inputs.
+
+    CPU path ``F.silu(gate) * up`` (fused_kernels.py:86-87): F.silu on a bf16 tensor computes
+    g / (1 + exp(-g)) in fp32 and rounds to bf16, the product of two bf16 tensors is an fp32 product
+    rounded to bf16.  Same formula as the Triton swiglu (fused_kernels.py:36-42).  exp is evaluated
+    in float64 and the quotient rounded once to fp32 (the library exps differ by <= 1-2 fp32 ulp).
+    """
+    g = bf16_to_f32(g_bits).astype(np.float64)
+    with np.errstate(over="ignore"):
+        act = round_bf16((g / (1.0 + np.exp(-g))).astype(np.float32))
+    return f32_to_bf16(act * bf16_to_f32(u_bits))
+
+
+def pack_gate_up(qg, sg, qu, su, group: int = 64):
+    """Interleave gate and up weight rows in groups: [g0..g63, u0..u63, g64..g127, u64..u127, ...].
+
+    Layout contract of the fused gate+up GEMM's SILU_MUL epilogue (the reference keeps separate
+    gate/up QLinears, fast_runtime.py:126-132; the fusion is this build's).
+    """
+    n, k = qg.shape
+    assert n % group == 0 and qu.shape == qg.shape
+    q = np.stack([qg.reshape(n // group, group, k), qu.reshape(n // group, group, k)], axis=1)
+    s = np.stack([sg.reshape(n // group, group), su.reshape(n // group, group)], axis=1)
+    return q.reshape(2 * n, k), s.reshape(2 * n)
+
+
+def gated_mlp(x_bits, qg, sg, qu, su, qd, sd, residual_bits=None, rounding="even"):
+    """MLP of fast_runtime._fused_mlp (fast_runtime.py:126-132) on W8A8 linears, plus the block's
+    residual add (fork.py:419-422): gate = QLinear(x), up = QLinear(x), h = swi_glu(gate, up),
+    out = bf16(residual + QLinear_down(h)).  Returns (out_bits, h_bits)."""
+    q, s = quant_act(bf16_to_f32(x_bits), None, rounding)
+    g = epilogue(int_gemm(q, qg), s, sg)
+    u = epilogue(int_gemm(q, qu), s, su)
+    h = silu_mul(g, u)
+    qh, sh = quant_act(bf16_to_f32(h), None, rounding)
+    d = epilogue(int_gemm(qh, qd), sh, sd)
+    if residual_bits is not None:
+        d = f32_to_bf16(bf16_to_f32(d) + bf16_to_f32(residual_bits))
+    return d, h
+
+
+# ---------------------------------------------------------------- readout
+def readout(h_bits, rows, norm_w, eps, W, offset=1.0, ids=None):
+    """Label readout (release_runtime.py:298-306) on body.norm of the last hidden rows
+    (prefill_engine.py:280-281, pick :296-304): logits = f32(bf16 normed x) @ W_rows^T.
+
+    h_bits: bf16 bits [T, K]; rows: indices of each request's last token; W: fp32 [L, K] label rows
+    (or the full table indexed by ids).  The fp32 dot is evaluated in float64 and rounded once.
+    """
+    x = np.asarray(h_bits, dtype=np.uint16)[np.asarray(rows)]
+    if norm_w is not None:
+        x, _ = rms_norm(x, norm_w, eps, offset)
+    xf = bf16_to_f32(x).astype(np.float64)
+    Wr = np.asarray(W, dtype=np.float32)
+    if ids is not None:
+        Wr = Wr[np.asarray(ids)]
+    return (xf @ Wr.astype(np.float64).T).astype(np.float32)
+
+
+def softmax(z: np.ndarray) -> np.ndarray:
+    """softmax over the last axis (release_runtime.py:517), evaluated in float64."""
+    z = np.asarray(z, dtype=np.float64)
+    e = np.exp(z - z.max(axis=-1, keepdims=True))
+    return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+
+
+def option_probs(logits: np.ndarray, kind: str, n: int | None = None) -> np.ndarray:
+    """Slice + softmax of judge_many.put/finish (release_runtime.py:509-517): [:2] for a noul
+    question, [2:2+n] otherwise."""
+    z = logits[..., :2] if kind == "noul" else logits[..., 2:2 + n]
+    return softmax(z)

@@ -1,0 +1,139 @@
+"""The C-ABI library loads and exports every entry point include/mica_amd.h declares, and its
+argument validation (which runs before any HIP call) rejects bad inputs with the documented codes.
+No kernel is launched here: every call below returns before touching a device."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mica_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mica_amd.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mica_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared()
+    for n in ("mica_act_quant", "mica_rmsnorm_quant", "mica_mm_i8", "mica_gather_logits", "mica_swiglu",
+              "mica_version", "mica_status_name", "mica_device_info"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared():
+        assert hasattr(lib, name), f"{name} declared in mica_amd.h but not exported"
+    # and the ctypes signatures cover them all
+    assert set(declared()) == set(_lib.SIGNATURES)
+
+
+def test_version_and_status_names():
+    lib = _lib.load()
+    assert lib.mica_version() == (0 << 16) | 1
+    assert _lib.status_name(1) == "shape" and _lib.status_name(3) == "align"
+    assert lib.mica_status_name(0) == b"ok"
+    assert lib.mica_status_name(5) == b"i32_range"
+
+
+A16 = 1 << 20  # a 16-byte aligned fake address: never dereferenced, every call below is rejected first
+
+
+@pytest.mark.parametrize("args,code", [
+    # (A, lda, B, ldb, sa, sb, bias, res, ldr, C, ldc, out_dtype, M, N, K, epi)
+    ((None, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0), 6),      # NULL A
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 9, 8, 64, 64, 0), 2),       # bad out dtype
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 40, 0), 1),       # K % 16
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 96, 64, 1), 1),       # SILU: N % 128
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 2, 8, 128, 64, 1), 6),      # SILU: not bf16
+    ((A16, 48, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0), 4),       # lda < K
+    ((A16, 72, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0), 4),       # lda % 16
+    ((A16 + 8, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0), 3),   # misaligned A
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 1 << 30, 64, 64, 0), 5),  # M * lda >= 2^31
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 4, 8, 64, 64, 1), 6),       # int32 + SILU
+])
+def test_mm_i8_rejects(args, code):
+    lib = _lib.load()
+    assert lib.mica_mm_i8(*args, None) == code
+
+
+def test_mm_i8_empty_is_a_no_op():
+    lib = _lib.load()
+    assert lib.mica_mm_i8(A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 0, 64, 64, 0, None) == 0
+
+
+@pytest.mark.parametrize("args,code", [
+    # (x, x_dtype, ldx, inv, q, ldq, s, M, K, rounding)
+    ((None, 0, 64, None, A16, 64, A16, 4, 64, 0), 6),
+    ((A16, 3, 64, None, A16, 64, A16, 4, 64, 0), 2),      # int8 input
+    ((A16, 0, 64, None, A16, 64, A16, 4, 60, 0), 1),      # K % 8
+    ((A16, 0, 64, None, A16, 64, A16, 4, 32768, 0), 1),   # K > 16384
+    ((A16, 0, 60, None, A16, 64, A16, 4, 56, 0), 4),      # ldx % 8
+    ((A16, 0, 64, None, A16, 64, A16, 4, 64, 7), 6),      # rounding mode
+    ((A16, 0, 64, A16 + 4, A16, 64, A16, 4, 64, 0), 3),   # misaligned inv
+])
+def test_act_quant_rejects(args, code):
+    lib = _lib.load()
+    assert lib.mica_act_quant(*args, None) == code
+
+
+def test_rmsnorm_quant_rejects():
+    lib = _lib.load()
+    base = dict(x=A16, xd=0, ldx=64, r=None, ldr=0, w=A16, wd=0, off=1.0, eps=1e-6, inv=None, q=A16, ldq=64,
+                s=A16, y=None, ldy=0, sm=None, lds=0, M=4, K=64, rnd=0)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return lib.mica_rmsnorm_quant(*a.values(), None)
+
+    assert call(q=None, y=None) == 6          # nothing to write
+    assert call(s=None) == 6                  # q without s
+    assert call(sm=A16, lds=64) == 6          # sum without residual
+    assert call(xd=2) == 2                    # fp32 activations are not normed
+    assert call(wd=3) == 2
+    assert call(K=100) == 1
+    assert call(r=A16, ldr=32) == 4
+    assert call(M=0) == 0
+
+
+def test_gather_logits_rejects():
+    lib = _lib.load()
+    # (h, ldh, n_rows, rows, B, norm_w, norm_dtype, offset, eps, W, w_dtype, ldw, w_rows, ids, L, K, logits,
+    #  lo, cnt, probs, ldp)
+    ok = [A16, 64, 100, A16, 2, None, 0, 1.0, 1e-6, A16, 2, 64, 8, None, 8, 64, A16, None, None, None, 0]
+
+    def with_(**kw):
+        a = list(ok)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return lib.mica_gather_logits(*a, None)
+
+    assert with_(a10=1) == 2          # fp16 label rows
+    assert with_(a17=A16) == 6        # lo without cnt
+    assert with_(a14=9000) == 1       # L > 8192
+    assert with_(a12=4) == 1          # fewer label rows than L without ids
+    assert with_(a2=0) == 1           # no hidden rows
+    assert with_(a4=0) == 0           # no requests
+
+
+def test_swiglu_rejects():
+    lib = _lib.load()
+    assert lib.mica_swiglu(A16, A16, A16, 16, 2, None) == 2
+    assert lib.mica_swiglu(A16, A16 + 2, A16, 16, 0, None) == 3
+    assert lib.mica_swiglu(A16, A16, A16, 0, 0, None) == 0
+
+
+def test_ctypes_signature_arity_matches_header():
+    """Each ctypes prototype has as many arguments as the header declaration (stream included)."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), name
+    assert ctypes.sizeof(ctypes.c_void_p) == 8

@@ -1,0 +1,412 @@
+"""Parity of the gfx950 kernels with the CPU oracle, through the drop-in surface and the C ABI.
+
+Bar (from the hot path's contract): int8 activations, fp32 scales and int32 accumulators bit-exact;
+bf16 outputs bit-exact where the reference's arithmetic is fully determined (quantizer, GEMM epilogue)
+and within one bf16 ulp where it is not (the fp32 summation order inside RMSNorm, library exp in
+SiLU); option probabilities within 1e-3 absolute.  Shapes are the benchmark configurations; the
+largest ones are checked on a seeded sample of rows (rows of a GEMM are independent).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mica_amd import fused_kernels, int8_kernels, int8_runtime
+from mica_amd.readout import LabelReadout
+from oracle import w8a8 as O
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[case] {msg}", file=sys.stderr, flush=True)
+
+
+def to_gpu_bf16(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def bits_of(t):
+    return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def act_bits(rng, shape, outliers=8, scale=1.0):
+    x = rng.standard_normal(shape).astype(np.float32) * scale
+    if outliers:
+        x[..., rng.permutation(shape[-1])[:outliers]] *= 20.0
+    return O.f32_to_bf16(x)
+
+
+def assert_within_one_ulp(got_bits, ref_bits, min_exact=0.999):
+    g, r = O.bf16_to_f32(got_bits), O.bf16_to_f32(ref_bits)
+    assert np.all(np.abs(g - r) <= O.bf16_ulp(ref_bits) * 1.0001), "difference above one bf16 ulp"
+    assert np.mean(got_bits == ref_bits) >= min_exact
+
+
+@pytest.fixture(autouse=True)
+def _strict_and_clean(monkeypatch):
+    monkeypatch.setattr(int8_kernels, "STRICT", True)
+    yield
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------------------ quantizer
+def test_act_quant_known_answers(gpu, kat):
+    for i, case in enumerate(kat["quant"]):
+        note(f"act_quant KAT {i}")
+        x = to_gpu_bf16(np.array(case["x_bf16"], np.uint16)[None, :])
+        inv = torch.tensor(case["inv"], dtype=torch.float32, device=gpu) if "inv" in case else None
+        for mode, key in (("even", "q_even"), ("away", "q_away")):
+            q, s = int8_kernels.act_quant(x, inv, rounding=mode)
+            assert q.cpu()[0].tolist() == case[key], (i, mode)
+            assert s.cpu().numpy().view(np.uint32)[0] == case["s_bits"]
+
+
+@pytest.mark.parametrize("m,k,smooth,rounding,dtype", [
+    (512, 2560, False, "even", torch.bfloat16),      # config 0 activations
+    (4096, 9728, False, "even", torch.bfloat16),     # the down projection's input
+    (1500, 4096, False, "away", torch.bfloat16),
+    (608, 9216, True, "even", torch.bfloat16),       # reference shape with SmoothQuant factors
+    (200, 2560, False, "even", torch.float16),
+    (48, 2560, True, "away", torch.float32),
+    (3, 8, False, "even", torch.bfloat16),           # smallest K
+    (7, 1000, False, "even", torch.bfloat16),        # K not a multiple of 512 (masked chunks)
+])
+def test_act_quant_bit_exact(gpu, m, k, smooth, rounding, dtype):
+    note(f"act_quant m={m} k={k} smooth={smooth} {rounding} {dtype}")
+    rng = np.random.default_rng(m * 7 + k)
+    xb = act_bits(rng, (m, k))
+    xf = O.bf16_to_f32(xb)
+    if dtype == torch.float16:
+        xf = xf.astype(np.float16).astype(np.float32)
+    x = torch.from_numpy(xf).to(dtype).cuda()
+    inv = rng.uniform(0.2, 5.0, k).astype(np.float32) if smooth else None
+    q, s = int8_kernels.act_quant(x, None if inv is None else torch.from_numpy(inv).cuda(), rounding=rounding)
+    qo, so = O.quant_act(x.float().cpu().numpy(), inv, rounding)
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+# ------------------------------------------------------------------------------ RMSNorm + quant
+def test_rms_norm_known_answers(gpu, kat):
+    for i, case in enumerate(kat["rms_norm"]):
+        note(f"rms_norm KAT {i}")
+        x = to_gpu_bf16(np.array(case["x_bf16"], np.uint16)[None, :])
+        w = torch.tensor(case["w"], dtype=torch.float32, device=gpu)
+        y = fused_kernels.rms_norm(x, w, case["eps"], offset=case["offset"])
+        assert bits_of(y)[0].tolist() == case["y_bf16"], i
+
+
+@pytest.mark.parametrize("T", [256, 4096, 32768])
+@pytest.mark.parametrize("offset", [0.0, 1.0])
+def test_rmsnorm_quant_config1(gpu, T, offset):
+    """Config 1: X bf16 [T, 2560] ~N(0,1) + 8 outlier channels x20, gamma ~N(1, 0.1) (offset 0: a plain
+    gamma; offset 1: the same multiplier written as 1 + w), eps 1e-6."""
+    note(f"rmsnorm_quant T={T} offset={offset}")
+    rng = np.random.default_rng(T)
+    K = 2560
+    xb = act_bits(rng, (T, K))
+    gamma = O.round_bf16(rng.normal(1.0, 0.1, K).astype(np.float32))
+    w = gamma - np.float32(offset)
+    wt = to_gpu_bf16(O.f32_to_bf16(w))
+    x = to_gpu_bf16(xb)
+    q, s, y = fused_kernels.rms_norm_quant(x, wt, 1e-6, offset=offset, return_normed=True)
+    yk = bits_of(y)
+    yo, _ = O.rms_norm(xb, O.bf16_to_f32(O.f32_to_bf16(w)), 1e-6, offset)
+    # the normed row: within one bf16 ulp of the oracle (fp32 summation order), nearly always equal
+    assert_within_one_ulp(yk, yo)
+    # int8 and scales: bit-exact against the reference quantizer applied to the kernel's own row
+    qo, so = O.quant_act(O.bf16_to_f32(yk))
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    # and wherever the normed row matches, the whole output matches the oracle end to end
+    same = np.all(yk == yo, axis=1)
+    qe, se = O.quant_act(O.bf16_to_f32(yo))
+    assert np.array_equal(q.cpu().numpy()[same], qe[same])
+    assert same.mean() > 0.95
+
+
+def test_rmsnorm_quant_residual_and_smoothing(gpu):
+    note("rmsnorm_quant residual + inv_smooth")
+    rng = np.random.default_rng(77)
+    T, K = 333, 2560
+    xb, rb = act_bits(rng, (T, K)), act_bits(rng, (T, K), outliers=0)
+    w = O.round_bf16(rng.normal(0.0, 0.1, K).astype(np.float32))
+    inv = rng.uniform(0.3, 3.0, K).astype(np.float32)
+    q, s, y, v = fused_kernels.rms_norm_quant(to_gpu_bf16(xb), to_gpu_bf16(O.f32_to_bf16(w)), 1e-6,
+                                              inv_smooth=torch.from_numpy(inv).cuda(), residual=to_gpu_bf16(rb),
+                                              return_normed=True)
+    yo, vo = O.rms_norm(xb, w, 1e-6, 1.0, rb)
+    assert np.array_equal(bits_of(v), vo)  # the residual sum is exact bf16 arithmetic
+    yk = bits_of(y)
+    assert_within_one_ulp(yk, yo)
+    qo, so = O.quant_act(O.bf16_to_f32(yk), inv)
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+def test_rms_norm_op_matches_reference_surface(gpu):
+    """fused_kernels.rms_norm(x, w, eps, residual) -> y / (y, summed), the reference's signature."""
+    note("rms_norm op")
+    rng = np.random.default_rng(5)
+    xb, rb = act_bits(rng, (64, 4096)), act_bits(rng, (64, 4096))
+    w = O.round_bf16(rng.normal(0, 0.1, 4096).astype(np.float32))
+    wt = to_gpu_bf16(O.f32_to_bf16(w))
+    y = fused_kernels.rms_norm(to_gpu_bf16(xb), wt, 1e-6)
+    assert_within_one_ulp(bits_of(y), O.rms_norm(xb, w, 1e-6)[0])
+    y2, summed = fused_kernels.rms_norm(to_gpu_bf16(xb), wt, 1e-6, to_gpu_bf16(rb))
+    yo, vo = O.rms_norm(xb, w, 1e-6, 1.0, rb)
+    assert np.array_equal(bits_of(summed), vo)
+    assert_within_one_ulp(bits_of(y2), yo)
+
+
+# ------------------------------------------------------------------------------ GEMM
+def test_gemm_known_answers(gpu, kat):
+    for i, case in enumerate(kat["gemm"]):
+        note(f"gemm KAT {i}")
+        A = torch.tensor(case["A"], dtype=torch.int8, device=gpu)
+        B = torch.tensor(case["B"], dtype=torch.int8, device=gpu)
+        acc = int8_kernels.mm_i8_int32(A, B)
+        assert acc.cpu().tolist() == case["acc"]
+        sa = torch.tensor(case["sa"], dtype=torch.float32, device=gpu)
+        sb = torch.tensor(case["sb"], dtype=torch.float32, device=gpu)
+        bias = None if case["bias"] is None else torch.tensor(case["bias"], dtype=torch.float32, device=gpu)
+        y = int8_kernels.mm_i8(A, sa, B, sb, bias)
+        assert bits_of(y).tolist() == case["y_bf16"]
+
+
+def _rand_gemm(rng, m, n, k):
+    A = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    sa = rng.uniform(1e-3, 1e-2, m).astype(np.float32)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    return A, B, sa, sb
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (512, 9728, 2560),     # config 0
+    (300, 1000, 2560),     # ragged M and N
+    (256, 2560, 9728),     # down projection K
+    (96, 2560, 4096),      # o_proj K
+    (1, 32, 2560),         # single row, the reference's N=32 projection
+    (17, 300, 2576),       # K not a multiple of the 128-byte slab
+    (258, 514, 16),        # K of one chunk
+])
+def test_gemm_int32_and_epilogue_bit_exact(gpu, m, n, k):
+    note(f"gemm m={m} n={n} k={k}")
+    rng = np.random.default_rng(m + n + k)
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    tA, tB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+    acc = int8_kernels.mm_i8_int32(tA, tB).cpu().numpy()
+    ref = O.int_gemm(A, B)
+    assert np.array_equal(acc, ref)
+    bias = rng.uniform(-1, 1, n).astype(np.float32)
+    tsa, tsb, tbias = (torch.from_numpy(v).cuda() for v in (sa, sb, bias))
+    y = int8_kernels.mm_i8(tA, tsa, tB, tsb)
+    assert np.array_equal(bits_of(y), O.epilogue(ref, sa, sb))
+    yb = int8_kernels.mm_i8(tA, tsa, tB, tsb, tbias)
+    assert np.array_equal(bits_of(yb), O.epilogue(ref, sa, sb, bias))
+    y32 = int8_kernels.mm_i8(tA, tsa, tB, tsb, tbias, out_dtype=torch.float32)
+    assert np.array_equal(y32.cpu().numpy().view(np.uint32), O.epilogue(ref, sa, sb, bias, "fp32").view(np.uint32))
+    y16 = int8_kernels.mm_i8(tA, tsa, tB, tsb, out_dtype=torch.float16)
+    assert np.array_equal(y16.cpu().numpy(), O.epilogue(ref, sa, sb, None, "fp16"))
+
+
+def test_gemm_extreme_accumulators(gpu):
+    """|acc| up to K * 127^2 = 1.57e8 at K = 9728 (above 2^24: the int32 -> fp32 conversion rounds)."""
+    note("gemm extremes")
+    m, n, k = 64, 256, 9728
+    A = np.full((m, k), -127, np.int8)
+    A[1::2] = 127
+    B = np.full((n, k), -127, np.int8)
+    B[::3, ::2] = 127
+    acc = int8_kernels.mm_i8_int32(torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()).cpu().numpy()
+    assert np.array_equal(acc, O.int_gemm(A, B))
+    assert np.abs(acc).max() == k * 127 * 127
+
+
+def test_gemm_residual_epilogue(gpu):
+    note("gemm residual")
+    rng = np.random.default_rng(3)
+    m, n, k = 700, 2560, 9728
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    res = act_bits(rng, (m, n), outliers=0)
+    y = int8_kernels.mm_i8(*(torch.from_numpy(v).cuda() for v in (A, sa, B, sb)), residual=to_gpu_bf16(res))
+    d = O.epilogue(O.int_gemm(A, B), sa, sb)
+    ref = O.f32_to_bf16(O.bf16_to_f32(d) + O.bf16_to_f32(res))
+    assert np.array_equal(bits_of(y), ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(32768, 6144, 2560), (32768, 2560, 4096)])
+def test_gemm_config3_long_context_sampled_rows(gpu, m, n, k):
+    """Config 3 (T = 32768 packed prefill): QKV 2560 -> 6144 and O 4096 -> 2560, checked exactly on a
+    seeded sample of rows spread over all M tiles."""
+    note(f"gemm config3 m={m} n={n} k={k}")
+    rng = np.random.default_rng(m + n)
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    y = int8_kernels.mm_i8(*(torch.from_numpy(v).cuda() for v in (A, sa, B, sb)))
+    rows = np.unique(np.concatenate([rng.choice(m, 384, replace=False), [0, 255, 256, m - 1]]))
+    ref = O.epilogue(O.int_gemm(A[rows], B), sa[rows], sb)
+    assert np.array_equal(bits_of(y[torch.from_numpy(rows).cuda()]), ref)
+
+
+# ------------------------------------------------------------------------------ QLinear / MLP
+def test_qlinear_config0_end_to_end(gpu):
+    """Config 0: X bf16 [512, 2560] (8 outlier channels x20) -> per-token int8 (half-even) -> int32 GEMM
+    with W int8 [9728, 2560], sw ~U(1e-3, 1e-2) -> bf16; 2 launches, bit-exact."""
+    note("qlinear config0")
+    rng = np.random.default_rng(0)
+    xb = act_bits(rng, (512, 2560))
+    qw = rng.integers(-127, 128, (9728, 2560), dtype=np.int8)
+    sw = rng.uniform(1e-3, 1e-2, 9728).astype(np.float32)
+    lin = int8_runtime.QLinear.from_quantized(torch.from_numpy(qw).cuda(), torch.from_numpy(sw).cuda())
+    l0 = int8_kernels.STATS["launch"]
+    y = lin(to_gpu_bf16(xb))
+    torch.cuda.synchronize()
+    assert int8_kernels.STATS["launch"] - l0 == 2
+    assert np.array_equal(bits_of(y), O.qlinear(xb, qw, sw))
+    # rows_forward: one quantization, a GEMM per row range (the GDN qkv split)
+    outs = lin.rows_forward(to_gpu_bf16(xb[:64]), [(0, 2048), (2048, 4096), (4096, 9728)])
+    ref = O.qlinear(xb[:64], qw, sw)
+    assert np.array_equal(np.concatenate([bits_of(o) for o in outs], 1), ref)
+
+
+def test_qlinear_reference_selftest(gpu):
+    """The reference's own acceptance criterion (int8_runtime.selftest) on its shipped shapes."""
+    note("reference selftest")
+    shapes = [(32, 2560, False), (1024, 2560, True), (2048, 2560, False), (4096, 2560, False),
+              (8192, 2560, False), (9216, 2560, False), (2560, 4096, False), (2560, 9216, False)]
+    out = int8_runtime.selftest(shapes, "cuda")
+    assert out["ok"], out
+
+
+def test_fused_gate_up_silu_epilogue(gpu):
+    note("gate_up silu epilogue")
+    rng = np.random.default_rng(11)
+    m, inter, k = 1000, 1536, 2560
+    xb = act_bits(rng, (m, k))
+    qg, qu = (rng.integers(-127, 128, (inter, k), dtype=np.int8) for _ in range(2))
+    sg, su = (rng.uniform(1e-3, 1e-2, inter).astype(np.float32) for _ in range(2))
+    q, s = O.quant_act(O.bf16_to_f32(xb))
+    qp, sp = int8_runtime.pack_gate_up(*(torch.from_numpy(v) for v in (qg, sg, qu, su)))
+    h = int8_kernels.mm_i8(torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), qp.cuda(), sp.cuda(),
+                           epilogue="silu_mul")
+    g = O.epilogue(O.int_gemm(q, qg), s, sg)
+    u = O.epilogue(O.int_gemm(q, qu), s, su)
+    assert_within_one_ulp(bits_of(h), O.silu_mul(g, u))
+
+
+def test_gated_mlp_config2(gpu):
+    """Config 2 at T = 4096: fused gate+up (N = 2 x 9728) with the SiLU epilogue, requantization, down
+    GEMM (K = 9728) with the residual add.  Each stage is checked against the oracle applied to the
+    kernel's own input of that stage, on a seeded sample of rows."""
+    note("gated mlp config2")
+    rng = np.random.default_rng(2)
+    T, H, I = 4096, 2560, 9728
+    hb = act_bits(rng, (T, H))
+    gamma = O.round_bf16(rng.normal(1.0, 0.1, H).astype(np.float32))
+    mk = lambda n, k: (rng.integers(-127, 128, (n, k), dtype=np.int8), rng.uniform(1e-3, 1e-2, n).astype(np.float32))  # noqa: E731
+    (qg, sg), (qu, su), (qd, sd) = mk(I, H), mk(I, H), mk(H, I)
+    gate = int8_runtime.QLinear.from_quantized(torch.from_numpy(qg).cuda(), torch.from_numpy(sg).cuda())
+    up = int8_runtime.QLinear.from_quantized(torch.from_numpy(qu).cuda(), torch.from_numpy(su).cuda())
+    down = int8_runtime.QLinear.from_quantized(torch.from_numpy(qd).cuda(), torch.from_numpy(sd).cuda())
+    mlp = int8_runtime.W8A8MLP(to_gpu_bf16(O.f32_to_bf16(gamma)), 1e-6, int8_runtime.GateUpQLinear(gate, up), down,
+                               offset=0.0)
+    h = to_gpu_bf16(hb)
+    # stage by stage
+    q, s = fused_kernels.rms_norm_quant(h, mlp.norm_weight, 1e-6, offset=0.0)
+    hg = mlp.gate_up.forward_quantized(q, s)
+    qh, sh = int8_kernels.act_quant(hg)
+    out = mlp.down.forward_quantized(qh, sh, residual=h)
+    l0 = int8_kernels.STATS["launch"]
+    out2 = mlp(h)
+    torch.cuda.synchronize()
+    assert int8_kernels.STATS["launch"] - l0 == 4
+    assert torch.equal(out, out2)
+    rows = np.sort(rng.choice(T, 256, replace=False))
+    tr = torch.from_numpy(rows).cuda()
+    qn, sn = q[tr].cpu().numpy(), s[tr].cpu().numpy()
+    g = O.epilogue(O.int_gemm(qn, qg), sn, sg)
+    u = O.epilogue(O.int_gemm(qn, qu), sn, su)
+    hk = bits_of(hg[tr])
+    assert_within_one_ulp(hk, O.silu_mul(g, u))
+    qo, so = O.quant_act(O.bf16_to_f32(hk))
+    assert np.array_equal(qh[tr].cpu().numpy(), qo)
+    assert np.array_equal(sh[tr].cpu().numpy().view(np.uint32), so.view(np.uint32))
+    d = O.epilogue(O.int_gemm(qo, qd), so, sd)
+    ref = O.f32_to_bf16(O.bf16_to_f32(d) + O.bf16_to_f32(hb[rows]))
+    assert np.array_equal(bits_of(out[tr]), ref)
+
+
+def test_swi_glu_op(gpu, kat):
+    note("swi_glu op")
+    c = kat["silu_mul"]
+    h = fused_kernels.swi_glu(to_gpu_bf16(np.array(c["g_bf16"], np.uint16)), to_gpu_bf16(np.array(c["u_bf16"],
+                                                                                                   np.uint16)))
+    assert bits_of(h).tolist() == c["h_bf16"]
+    rng = np.random.default_rng(8)
+    g = O.f32_to_bf16(rng.standard_normal(1_000_003).astype(np.float32) * 4)
+    u = O.f32_to_bf16(rng.standard_normal(1_000_003).astype(np.float32))
+    assert_within_one_ulp(bits_of(fused_kernels.swi_glu(to_gpu_bf16(g), to_gpu_bf16(u))), O.silu_mul(g, u))
+
+
+# ------------------------------------------------------------------------------ readout
+def test_readout_config4_shape(gpu, kat):
+    """8 requests x 2048 packed tokens, hidden 2560: final RMSNorm at each last position, fp32 dot with
+    2 + 255 label rows gathered from a 151936-row table, softmax over [:2] (noul) or [2:2+n]."""
+    note("readout")
+    rng = np.random.default_rng(4)
+    B, S, K, V = 8, 2048, 2560, 151936
+    h = act_bits(rng, (B * S, K), scale=0.5)
+    rows = np.arange(B) * S + S - 1
+    norm_w = O.round_bf16(rng.normal(0, 0.1, K).astype(np.float32))
+    ids = rng.choice(V, 257, replace=False)
+    table_rows = O.f32_to_bf16(rng.normal(0, 0.02, (257, K)).astype(np.float32))
+    table = np.zeros((V, K), np.uint16)
+    table[ids] = table_rows
+    tt = to_gpu_bf16(table)
+    ro = LabelReadout(tt, torch.from_numpy(ids).cuda())
+    kinds = ["noul", "choice", "choice", "noul", "choice", "choice", "choice", "noul"]
+    ns = [2, 255, 7, 2, 100, 3, 255, 2]
+    lo = [0 if k == "noul" else 2 for k in kinds]
+    logits, probs = ro(to_gpu_bf16(h), torch.from_numpy(rows).cuda(), to_gpu_bf16(O.f32_to_bf16(norm_w)), 1e-6,
+                       lo=torch.tensor(lo).cuda(), cnt=torch.tensor(ns).cuda(), probs_width=255)
+    zo = O.readout(h, rows, norm_w, 1e-6, O.bf16_to_f32(table_rows))
+    np.testing.assert_allclose(logits.cpu().numpy(), zo, rtol=1e-4, atol=1e-4)
+    p = probs.cpu().numpy()
+    for b in range(B):
+        po = O.option_probs(zo[b], kinds[b], ns[b])
+        np.testing.assert_allclose(p[b, : ns[b]], po, atol=1e-3)
+        assert abs(p[b, : ns[b]].sum() - 1) < 1e-5
+    # the un-gathered table indexed by id inside the kernel gives the same logits
+    ro2 = LabelReadout(tt, torch.from_numpy(ids).cuda(), gather=False)
+    l2, _ = ro2(to_gpu_bf16(h), torch.from_numpy(rows).cuda(), to_gpu_bf16(O.f32_to_bf16(norm_w)), 1e-6)
+    np.testing.assert_allclose(l2.cpu().numpy(), logits.cpu().numpy(), rtol=1e-5, atol=1e-5)
+    # softmax known answers through the kernel: logits chosen so probs are closed forms
+    for case in kat["softmax"]:
+        z = np.array(case["z"], np.float32)
+        n = len(z)
+        x = np.zeros((1, 64), np.float32)
+        x[0, 0] = 1.0
+        W = np.zeros((n, 64), np.float32)
+        W[:, 0] = z
+        r3 = LabelReadout(torch.from_numpy(W).cuda(), list(range(n)))
+        r3.weight = torch.from_numpy(W).cuda()
+        _, pk = r3(to_gpu_bf16(O.f32_to_bf16(x)), torch.tensor([0]).cuda())
+        np.testing.assert_allclose(pk.cpu().numpy()[0, :n], case["p"], atol=1e-6)
+
+
+def test_readout_bad_indices_give_nan_not_a_fault(gpu):
+    note("readout bad indices")
+    h = torch.zeros(4, 64, dtype=torch.bfloat16, device=gpu)
+    table = torch.randn(10, 64, device=gpu).to(torch.bfloat16)
+    ro = LabelReadout(table, torch.tensor([1, 2, 3], device=gpu), gather=False)
+    ro.ids = torch.tensor([1, 2, 99], dtype=torch.int32, device=gpu)  # 99 is past the table
+    logits, _ = ro(h, torch.tensor([0, 7], device=gpu))  # row 7 is past h
+    z = logits.cpu()
+    assert torch.isnan(z[1]).all() and torch.isnan(z[0, 2]) and not torch.isnan(z[0, :2]).any()
+
+
+def test_no_fallbacks_were_taken(gpu):
+    assert not int8_kernels.STATS["fallback"], int8_kernels.STATS["fallback"]
