@@ -28,7 +28,13 @@ MICA_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
 MICA_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 MICA_DEVICE float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-MICA_DEVICE uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// fp32 -> fp16, round to nearest even, of the fp32 value as rounded.  The empty asm keeps the
+// compiler from folding a preceding multiply into the conversion (v_fma_mix*_f16 would round the
+// product once, straight to fp16, instead of to fp32 first).
+MICA_DEVICE uint16_t f32_to_f16(float f) {
+    __asm__ volatile("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 
 // Load element i of a row of dtype (bf16 / fp16 / fp32) as fp32.
 MICA_DEVICE float load_as_f32(const void *p, int dtype, long i) {

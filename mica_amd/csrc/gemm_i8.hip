@@ -1,16 +1,20 @@
 // W8A8 GEMM on the gfx950 matrix cores: C = epilogue(A[M, K] . B[N, K]^T), int8 x int8 -> int32.
 //
 // Tiling (one workgroup = 4 wavefronts = 256 threads, one workgroup per CU):
-//   * workgroup tile 256 (M) x 256 (N), K staged 128 bytes at a time;
-//   * the 4 waves form a 2 x 2 grid, each owns a 128 x 128 block = 4 x 4 tiles of
-//     v_mfma_i32_32x32x32_i8 (256 int32 accumulators per lane, held in AGPRs);
-//   * A and B K-slabs ([256][128] bytes each) are double-buffered in LDS (128 KiB total):
-//     while the waves run the MFMAs of slab k, the 16-byte global loads of slab k + 1 are in
-//     flight, and are written to the other buffer afterwards; one barrier per slab;
-//   * LDS rows are 128 bytes = 8 chunks of 16 bytes; chunk c of row r is stored at chunk
-//     c ^ ((r ^ (r >> 3)) & 7).  The 16-byte reads of an MFMA operand (32 consecutive rows,
-//     one chunk) and the 16-byte writes of a slab (8 lanes per row) then touch every bank once
-//     per 8 (32 banks) or 16 (64 banks) lanes: no bank conflicts in either direction.
+//   * workgroup tile 256 (M) x 256 (N); the 4 waves form a 2 x 2 grid, each owns 128 x 128 =
+//     4 x 4 tiles of v_mfma_i32_32x32x32_i8 (256 int32 accumulators per lane, in AGPRs).  The
+//     weight rows are the MFMA's A operand and the activation rows its B operand, so a lane ends
+//     up with 4 consecutive output columns of one row: the epilogue stores 8-byte vectors.
+//   * K is staged 64 bytes at a time through a ring of 4 LDS stages (4 x 32 KiB).  Stages are
+//     filled by buffer_load ... lds (global -> LDS without VGPRs), 3 slabs ahead of the MFMAs.
+//     The buffer resources carry the operand sizes, so rows past M / N and chunks past K read
+//     as zeros.
+//   * each wave double-buffers its MFMA operands in registers: the ds_reads of slab k + 1 are
+//     issued after the first half of slab k's MFMAs and land under its second half.  One
+//     barrier per slab, placed between the halves; explicit vmcnt / lgkmcnt waits order the DMA.
+//   * LDS rows are 64 bytes = 4 chunks of 16; chunk c of tile row r lives at chunk
+//     c ^ ((r >> 2) & 3), which makes the MFMA operand reads (32 consecutive rows, one chunk,
+//     16 bytes per lane) free of LDS bank conflicts; the DMA writes 1 KiB contiguous blocks.
 //
 // Workgroup order: the hardware hands workgroup i to XCD i % 8, and each XCD has its own L2.
 // Workgroups are renumbered so each XCD gets one contiguous range of tiles, and inside a range
@@ -28,21 +32,40 @@ namespace {
 
 constexpr int BM = 256;
 constexpr int BN = 256;
-constexpr int BK = 128;     // bytes of K per LDS slab
-constexpr int WM = 128;     // wave tile
-constexpr int WN = 128;
-constexpr int MB = WM / 32; // 32x32 MFMA tiles per wave along M
-constexpr int NB = WN / 32;
-constexpr int KS = BK / 32; // MFMA k-steps per slab
-constexpr int kThreads = 256;
-constexpr int kLoadIters = BM * BK / 16 / kThreads; // 16-byte chunks per thread per operand = 8
-constexpr int kSlab = (BM + BN) * BK;               // bytes of one LDS stage
+constexpr int BK = 64;      // bytes of K per LDS stage
+constexpr int NST = 4;      // LDS stages
+constexpr int KS = BK / 32; // MFMA k-steps per stage
+constexpr int kABytes = BM * BK;               // 16 KiB
+constexpr int kStage = (BM + BN) * BK;         // 32 KiB
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
+
+// Wave layout of the 256 x 256 workgroup tile: WGM x WGN waves, each owning WM x WN.
+template <int WGM, int WGN>
+struct Cfg {
+    static constexpr int kWaves = WGM * WGN;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int WM = BM / WGM;
+    static constexpr int WN = BN / WGN;
+    static constexpr int MB = WM / 32;                           // 32x32 MFMA tiles along M
+    static constexpr int NB = WN / 32;                           // ... along N
+    static constexpr int kBlocksPerWave = BM * BK / 1024 / kWaves; // 1 KiB DMA blocks per operand
+    static constexpr int kDmaPerSlab = 2 * kBlocksPerWave;       // buffer_load ... lds per wave per slab
+    // staged epilogue: each wave's WM x WN 16-bit block, rows padded by 16 bytes
+    static constexpr int kEpiPitch = WN * 2 + 16;
+    static constexpr int kEpiWave = WM * kEpiPitch;
+    static constexpr int kSmem = (NST * kStage > kWaves * kEpiWave) ? NST * kStage : kWaves * kEpiWave;
+    static_assert(WN == 128, "the SiLU epilogue needs one 128-row gate/up group per wave");
+};
+using CfgDefault = Cfg<4, 2>;
+static_assert(CfgDefault::kWaves == 8 && CfgDefault::WM == 64, "the ping-pong loop pairs two groups of 4 waves");
+
 // word 3 of a gfx9 buffer resource (raw buffer, 32-bit data format), as used by CK for gfx9xx
 constexpr int kBufferFlags = 0x00020000;
 // a buffer offset that fails the range check (every buffer here is < 2^31 bytes)
 constexpr int kOutOfRange = (int)0x80000000u;
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 struct GemmParams {
     const int8_t *A;
@@ -55,9 +78,31 @@ struct GemmParams {
     int lda, ldb, ldr, ldc;
     int M, N, K;
     int tiles_m, tiles_n;
+    int vec_ok; // ldc, ldr, N all multiples of 4: 4-column vector stores
 };
 
-MICA_DEVICE int swz(int row) { return (row ^ (row >> 3)) & 7; }
+// LDS placement of 16-byte chunk c of tile row r: chunk c ^ swz(r).  With 64-byte rows, the MFMA
+// operand reads (32 consecutive rows, one chunk, 16 bytes per lane) then run at the LDS's full
+// rate on gfx950; measured on the device against other XOR patterns (2-4x slower ones included).
+MICA_DEVICE int swz(int row) { return (row >> 2) & 3; }
+
+// s_waitcnt with only one counter constrained (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4],
+// lgkmcnt [11:8]; the other fields at their maxima)
+template <int N>
+MICA_DEVICE void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+MICA_DEVICE void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// wait until at most `slabs` (0..3) slabs of this wave's DMA are still in flight
+template <int kDmaPerSlab>
+MICA_DEVICE void wait_dma(int slabs) {
+    if (slabs >= 3) wait_vmcnt<3 * kDmaPerSlab>();
+    else if (slabs == 2) wait_vmcnt<2 * kDmaPerSlab>();
+    else if (slabs == 1) wait_vmcnt<kDmaPerSlab>();
+    else wait_vmcnt<0>();
+}
 
 // Map the hardware workgroup id to a tile (tm, tn).
 MICA_DEVICE void tile_of(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
@@ -76,176 +121,378 @@ MICA_DEVICE void tile_of(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
 }
 
 template <int OUT>
-MICA_DEVICE void store_out(void *C, long off, float v) {
-    if (OUT == MICA_BF16) ((uint16_t *)C)[off] = f32_to_bf16(v);
-    else if (OUT == MICA_INT32) return; // raw accumulators are stored by the caller
-    else if (OUT == MICA_FP16) ((uint16_t *)C)[off] = f32_to_f16(v);
-    else ((float *)C)[off] = v;
+MICA_DEVICE float to_out_precision(float v) {
+    if (OUT == MICA_BF16) return round_bf16(v);
+    if (OUT == MICA_FP16) return f16_to_f32(f32_to_f16(v));
+    return v;
+}
+
+// store 4 consecutive outputs of one row (vector store when allowed, else element by element)
+template <int OUT>
+MICA_DEVICE void store4(void *C, long off, const float (&v)[4], int valid, bool vec) {
+    if (OUT == MICA_BF16 || OUT == MICA_FP16) {
+        uint16_t h[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) h[t] = OUT == MICA_BF16 ? f32_to_bf16(v[t]) : f32_to_f16(v[t]);
+        uint16_t *p = (uint16_t *)C + off;
+        if (vec && valid == 4) {
+            u32x2 w;
+            w[0] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+            w[1] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+            *(u32x2 *)p = w;
+        } else {
+            for (int t = 0; t < valid; ++t) p[t] = h[t];
+        }
+    } else {
+        float *p = (float *)C + off;
+        if (vec && valid == 4) *(float4 *)p = make_float4(v[0], v[1], v[2], v[3]);
+        else for (int t = 0; t < valid; ++t) p[t] = v[t];
+    }
 }
 
 template <int OUT>
-MICA_DEVICE float load_res(const void *R, long off) {
-    if (OUT == MICA_BF16) return bf16_to_f32(((const uint16_t *)R)[off]);
-    if (OUT == MICA_FP16) return f16_to_f32(((const uint16_t *)R)[off]);
-    return ((const float *)R)[off];
+MICA_DEVICE void load4_res(const void *R, long off, float (&v)[4], int valid, bool vec) {
+    if (OUT == MICA_FP32) {
+        const float *p = (const float *)R + off;
+        if (vec && valid == 4) {
+            const float4 t = *(const float4 *)p;
+            v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        } else {
+            for (int t = 0; t < 4; ++t) v[t] = t < valid ? p[t] : 0.0f;
+        }
+        return;
+    }
+    const uint16_t *p = (const uint16_t *)R + off;
+    uint16_t h[4] = {0, 0, 0, 0};
+    if (vec && valid == 4) {
+        const u32x2 w = *(const u32x2 *)p;
+        h[0] = w[0] & 0xffff; h[1] = w[0] >> 16; h[2] = w[1] & 0xffff; h[3] = w[1] >> 16;
+    } else {
+        for (int t = 0; t < valid; ++t) h[t] = p[t];
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = OUT == MICA_BF16 ? bf16_to_f32(h[t]) : f16_to_f32(h[t]);
 }
 
-template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES>
-__global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(16))) int8_t smem[2 * kSlab];
+template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES, class C = CfgDefault>
+__global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
+    constexpr int WM = C::WM, WN = C::WN, MB = C::MB, NB = C::NB;
+    constexpr int kBlocksPerWave = C::kBlocksPerWave, kDmaPerSlab = C::kDmaPerSlab;
+    constexpr int kEpiPitch = C::kEpiPitch, kEpiWave = C::kEpiWave;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[C::kSmem];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / (BN / WN), wn = wave % (BN / WN);
 
     int tm, tn;
     tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.M, N = p.N, K = p.K;
 
-    // ---- global -> register -> LDS staging: thread owns chunk (tid & 7) of rows j*32 + tid/8 ----
-    // Raw buffer loads: offsets are 32-bit and a load whose offset lies past the buffer's
-    // range returns zeros, so rows past M / N and chunks past K read as 0 without branches.
-    const __amdgpu_buffer_rsrc_t rsrc_a =
-        __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, p.M * p.lda, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rsrc_b =
-        __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, p.N * p.ldb, kBufferFlags);
-    const int lrow = tid >> 3, lkc = tid & 7;
-    int a_off[kLoadIters], b_off[kLoadIters], l_off[kLoadIters];
+    // ---- DMA of one slab: this wave moves kBlocksPerWave 1 KiB blocks of the A and of the B tile ----
+    // lane i of a block writes LDS bytes [16 i, 16 i + 16): tile row blk * 16 + i / 4, physical chunk
+    // i % 4, so it fetches logical chunk (i % 4) ^ swz(row) of that row.
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, M * p.lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, N * p.ldb, kBufferFlags);
+    int a_row[kBlocksPerWave], b_row[kBlocksPerWave], kcol[kBlocksPerWave];
 #pragma unroll
-    for (int j = 0; j < kLoadIters; ++j) {
-        const int row = j * 32 + lrow;
-        a_off[j] = m0 + row < M ? (m0 + row) * p.lda + lkc * 16 : kOutOfRange;
-        b_off[j] = n0 + row < N ? (n0 + row) * p.ldb + lkc * 16 : kOutOfRange;
-        l_off[j] = row * BK + ((lkc ^ swz(row)) << 4);
+    for (int j = 0; j < kBlocksPerWave; ++j) {
+        const int r = (wave * kBlocksPerWave + j) * 16 + (lane >> 2);
+        kcol[j] = ((lane & 3) ^ swz(r)) << 4;
+        a_row[j] = m0 + r < M ? (m0 + r) * p.lda + kcol[j] : kOutOfRange;
+        b_row[j] = n0 + r < N ? (n0 + r) * p.ldb + kcol[j] : kOutOfRange;
     }
-    v4i ra[kLoadIters], rb[kLoadIters];
-    auto gload = [&](int k0) {
-        const bool kout = k0 + lkc * 16 >= K; // K % 16 == 0: a chunk is all in or all out
+    auto dma = [&](int slab) {
+        const int k0 = slab * BK;
+        int8_t *st = smem + (slab % NST) * kStage;
 #pragma unroll
-        for (int j = 0; j < kLoadIters; ++j) {
-            const int oa = kout ? kOutOfRange : a_off[j] + k0;
-            const int ob = kout ? kOutOfRange : b_off[j] + k0;
-            ra[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, oa, 0, 0));
-            rb[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, ob, 0, 0));
-        }
-    };
-    auto lstore = [&](int buf) {
-        int8_t *As = smem + buf * kSlab;
-        int8_t *Bs = As + BM * BK;
-#pragma unroll
-        for (int j = 0; j < kLoadIters; ++j) {
-            *(v4i *)(As + l_off[j]) = ra[j];
-            *(v4i *)(Bs + l_off[j]) = rb[j];
+        for (int j = 0; j < kBlocksPerWave; ++j) {
+            const bool kin = k0 + kcol[j] < K;
+            const int oa = (kin && a_row[j] != kOutOfRange) ? a_row[j] + k0 : kOutOfRange;
+            const int ob = (kin && b_row[j] != kOutOfRange) ? b_row[j] + k0 : kOutOfRange;
+            const int blk = wave * kBlocksPerWave + j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void *)(st + blk * 1024), 16, oa, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_void *)(st + kABytes + blk * 1024), 16, ob, 0,
+                                                     0, 0);
         }
     };
 
-    v16i acc[MB][NB];
+    // ---- MFMA operand offsets inside a stage: [tile][k-step] ----
+    const int r32 = lane & 31, khalf = lane >> 5;
+    int x_rd[MB][KS], w_rd[NB][KS];
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = v16i{};
-
-    const int khalf = lane >> 5;
-    const int r32 = lane & 31;
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
-    const int nk = (K + BK - 1) / BK;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
-        const int8_t *As = smem + buf * kSlab;
-        const int8_t *Bs = As + BM * BK;
+        for (int ks = 0; ks < KS; ++ks) {
+            const int rx = wm * WM + i * 32 + r32;
+            const int c = ks * 2 + khalf;
+            x_rd[i][ks] = rx * BK + ((c ^ swz(rx)) << 4);
+        }
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const int kc = ks * 2 + khalf;
-            v4i a[MB], b[NB];
+            const int rw = wn * WN + j * 32 + r32;
+            const int c = ks * 2 + khalf;
+            w_rd[j][ks] = kABytes + rw * BK + ((c ^ swz(rw)) << 4);
+        }
+
+    v16i acc[NB][MB]; // [n tile][m tile]
 #pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                const int row = wm * WM + i * 32 + r32;
-                a[i] = *(const v4i *)(As + row * BK + ((kc ^ swz(row)) << 4));
-            }
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int row = wn * WN + j * 32 + r32;
-                b[j] = *(const v4i *)(Bs + row * BK + ((kc ^ swz(row)) << 4));
-            }
+        for (int i = 0; i < MB; ++i) acc[j][i] = v16i{};
+
+    struct Ops {
+        v4i x[KS][MB];
+        v4i w[KS][NB];
+    };
+    auto lds_read = [&](Ops &o, int slab) {
+        const int8_t *st = smem + (slab % NST) * kStage;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) o.w[ks][j] = *(const v4i *)(st + w_rd[j][ks]);
+#pragma unroll
+            for (int i = 0; i < MB; ++i) o.x[ks][i] = *(const v4i *)(st + x_rd[i][ks]);
+        }
+    };
+    auto mfma_half = [&](const Ops &o, int ks) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int i = 0; i < MB; ++i)
-#pragma unroll
-                for (int j = 0; j < NB; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) lstore(buf ^ 1);
-        __syncthreads();
-    }
+                acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w[ks][j], o.x[ks][i], acc[j][i], 0, 0, 0);
+    };
 
-    // ---- epilogue.  acc[i][j][r]: row = 8 (r / 4) + 4 (lane / 32) + r % 4, col = lane % 32 ----
+    // ---- ping-pong main loop.  The 8 waves form two groups (waves 0-3: tile rows 0-127, waves 4-7:
+    // rows 128-255), one wave of each group per SIMD.  Time is cut into phases separated by
+    // workgroup barriers; group g handles slab k as load(k) in phase 2k + g (issue the DMA of
+    // slab k + 3, read slab k's operands from LDS) and compute(k) in phase 2k + g + 1 (16 MFMAs at
+    // raised wave priority).  So in every phase one wave per SIMD computes while the other loads.
+    // Slab k's stage is free once both groups have read it (end of phase 2k + 1); slab k + 3 is
+    // DMA'd into stage (k - 1) % 4 during load(k), phases 2k and 2k + 1.
+    const int nk = (K + BK - 1) / BK;
+    const int grp = wave >> 2;
+    const int pre = nk < NST ? nk : NST;
+    for (int sl = 0; sl < pre; ++sl) dma(sl);
+    wait_dma<kDmaPerSlab>(pre - 1); // slab 0 landed in this wave's blocks ...
+    __builtin_amdgcn_s_barrier();   // ... and in every wave's
+    Ops o;
+    const int nphase = 2 * nk + 1;
+    for (int ph = 0; ph < nphase; ++ph) {
+        const int t = ph - grp;
+        if (t >= 0 && t < 2 * nk) {
+            const int k = t >> 1;
+            if ((t & 1) == 0) {
+                if (k >= 1 && k + NST - 1 < nk) dma(k + NST - 1);
+                lds_read(o, k);
+                wait_lgkmcnt0(); // the stage may be recycled after the barrier below
+            } else {
+                __builtin_amdgcn_s_setprio(1);
+                mfma_half(o, 0);
+                mfma_half(o, 1);
+                __builtin_amdgcn_s_setprio(0);
+            }
+        }
+        // before group 0 loads slab s = (ph + 1) / 2 in the next phase, every wave's DMA of s landed;
+        // each wave's newest DMA is then slab min(k0 + 3, nk - 1), k0 = (ph - 1) / 2
+        if ((ph & 1) == 1) {
+            const int s_next = (ph + 1) >> 1;
+            if (s_next < nk) {
+                const int k0 = (ph - 1) >> 1;
+                const int newest = (k0 + NST - 1 < nk - 1) ? k0 + NST - 1 : nk - 1;
+                wait_dma<kDmaPerSlab>(newest - s_next);
+            }
+        }
+        __builtin_amdgcn_s_barrier();
+    }
+    wait_vmcnt<0>();
+
+    // ---- epilogue.  acc[j][i][r]: n = 8 (r / 4) + 4 (lane / 32) + r % 4 (4 consecutive per r / 4),
+    //      m = lane % 32 within the 32 x 32 tile (j, i) ----
     const int mw = m0 + wm * WM;
     const int nw = n0 + wn * WN;
+    const bool vec = p.vec_ok != 0;
+    float sav[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int m = mw + i * 32 + r32;
+        sav[i] = m < M ? p.sa[m] : 0.0f;
+    }
+    if constexpr (OUT == MICA_BF16 || OUT == MICA_FP16) {
+        // Staged through LDS: every wave writes its rounded 16-bit block (8 bytes per lane per
+        // store) into its own padded region, then streams it out row-contiguously, 16 bytes per
+        // lane, so each global store covers whole 256-byte row segments.
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier(); // every wave is done reading the operand stages
+        int8_t *ep = smem + wave * kEpiWave;
+        constexpr int kCols = EPI == MICA_EPI_SCALE ? WN : WN / 2; // output columns of this wave
+        const int col0 = EPI == MICA_EPI_SCALE ? nw : (nw >> 7) * 64;
+        const int ncols_out = EPI == MICA_EPI_SCALE ? N : (N >> 1);
+#pragma unroll
+        for (int j = 0; j < (EPI == MICA_EPI_SCALE ? NB : 2); ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int nl = j * 32 + 8 * q + 4 * khalf; // local output column of this lane's 4 values
+                float s1[4], s2[4], bv[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    if (EPI == MICA_EPI_SCALE) {
+                        const int n = nw + nl + t;
+                        s1[t] = n < N ? p.sb[n] : 0.0f;
+                        bv[t] = (HAS_BIAS && n < N) ? p.bias[n] : 0.0f;
+                    } else {
+                        s1[t] = p.sb[nw + nl + t];      // gate rows (N % 128 == 0: in range)
+                        s2[t] = p.sb[nw + 64 + nl + t]; // matching up rows
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < MB; ++i) {
+                    float y[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        if (EPI == MICA_EPI_SCALE) {
+                            y[t] = ((float)acc[j][i][4 * q + t] * sav[i]) * s1[t];
+                            if (HAS_BIAS) y[t] = y[t] + bv[t];
+                        } else {
+                            const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * s1[t]);
+                            const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * s2[t]);
+                            const float act = round_bf16(gv / (1.0f + expf(-gv)));
+                            y[t] = act * uv;
+                        }
+                    }
+                    u32x2 w;
+                    if (OUT == MICA_BF16) {
+                        w[0] = pack_bf16x2(y[0], y[1]);
+                        w[1] = pack_bf16x2(y[2], y[3]);
+                    } else {
+                        w[0] = (uint32_t)f32_to_f16(y[0]) | ((uint32_t)f32_to_f16(y[1]) << 16);
+                        w[1] = (uint32_t)f32_to_f16(y[2]) | ((uint32_t)f32_to_f16(y[3]) << 16);
+                    }
+                    *(u32x2 *)(ep + (i * 32 + r32) * kEpiPitch + nl * 2) = w;
+                }
+            }
+        }
+        wait_lgkmcnt0(); // a wave reads back only its own region: no barrier needed
+        constexpr int kLanesPerRow = kCols / 8;          // 16 (SCALE) or 8 (SILU_MUL) lanes x 8 columns
+        constexpr int kRowsPerPass = 64 / kLanesPerRow;  // 4 or 8 rows per pass
+        const int cl = (lane % kLanesPerRow) * 8;        // local column of this lane's 8 values
+        const int valid = ncols_out - (col0 + cl) < 8 ? (ncols_out - (col0 + cl) > 0 ? ncols_out - (col0 + cl) : 0) : 8;
+        const bool vec8 = vec && (p.ldc % 8 == 0) && (!HAS_RES || p.ldr % 8 == 0);
+#pragma unroll 4
+        for (int r0 = 0; r0 < WM; r0 += kRowsPerPass) {
+            const int rl = r0 + lane / kLanesPerRow;
+            const int m = mw + rl;
+            const u32x4 v = *(const u32x4 *)(ep + rl * kEpiPitch + cl * 2);
+            if (m >= M || valid == 0) continue;
+            u32x4 o = v;
+            if (HAS_RES) {
+                const uint16_t *rp = (const uint16_t *)p.res + (long)m * p.ldr + col0 + cl;
+                u32x4 rv = {0u, 0u, 0u, 0u};
+                if (vec8 && valid == 8) rv = *(const u32x4 *)rp;
+                else for (int t = 0; t < valid; ++t) rv[t >> 1] |= (uint32_t)rp[t] << (16 * (t & 1));
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float a0, a1, b0, b1;
+                    if (OUT == MICA_BF16) {
+                        a0 = bf16_lo(v[t]); a1 = bf16_hi(v[t]); b0 = bf16_lo(rv[t]); b1 = bf16_hi(rv[t]);
+                        o[t] = pack_bf16x2(a0 + b0, a1 + b1);
+                    } else {
+                        a0 = f16_to_f32(v[t] & 0xffff); a1 = f16_to_f32(v[t] >> 16);
+                        b0 = f16_to_f32(rv[t] & 0xffff); b1 = f16_to_f32(rv[t] >> 16);
+                        o[t] = (uint32_t)f32_to_f16(a0 + b0) | ((uint32_t)f32_to_f16(a1 + b1) << 16);
+                    }
+                }
+            }
+            uint16_t *cp = (uint16_t *)p.C + (long)m * p.ldc + col0 + cl;
+            if (vec8 && valid == 8) {
+                *(u32x4 *)cp = o;
+            } else {
+                for (int t = 0; t < valid; ++t) cp[t] = (uint16_t)(o[t >> 1] >> (16 * (t & 1)));
+            }
+        }
+        return;
+    }
+    // 32-bit outputs (fp32 / raw int32): direct 16-byte stores from the accumulator layout
     if (EPI == MICA_EPI_SCALE) {
-        float sbv[NB], bv[NB];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int n = nw + j * 32 + r32;
-            sbv[j] = n < N ? p.sb[n] : 0.0f;
-            bv[j] = (HAS_BIAS && n < N) ? p.bias[n] : 0.0f;
-        }
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
+            for (int q = 0; q < 4; ++q) {
+                const int nb = nw + j * 32 + 8 * q + 4 * khalf;
+                const int valid = N - nb < 4 ? (N - nb > 0 ? N - nb : 0) : 4;
+                if (valid == 0) continue;
+                float sbv[4], bv[4];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = mw + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
-                if (m >= M) continue;
-                const float sav = p.sa[m];
+                for (int t = 0; t < 4; ++t) {
+                    sbv[t] = t < valid ? p.sb[nb + t] : 0.0f;
+                    bv[t] = (HAS_BIAS && t < valid) ? p.bias[nb + t] : 0.0f;
+                }
 #pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const int n = nw + j * 32 + r32;
-                    if (n >= N) continue;
+                for (int i = 0; i < MB; ++i) {
+                    const int m = mw + i * 32 + r32;
+                    if (m >= M) continue;
+                    const long off = (long)m * p.ldc + nb;
                     if (OUT == MICA_INT32) {
-                        ((int *)p.C)[(long)m * p.ldc + n] = acc[i][j][r];
+                        int *c = (int *)p.C + off;
+                        if (vec && valid == 4) {
+                            *(v4i *)c = v4i{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
+                                            acc[j][i][4 * q + 3]};
+                        } else {
+                            for (int t = 0; t < valid; ++t) c[t] = acc[j][i][4 * q + t];
+                        }
                         continue;
                     }
-                    float y = ((float)acc[i][j][r] * sav) * sbv[j];
-                    if (HAS_BIAS) y = y + bv[j];
-                    if (HAS_RES) {
-                        y = round_to(y, OUT) + load_res<OUT>(p.res, (long)m * p.ldr + n);
+                    float y[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        y[t] = ((float)acc[j][i][4 * q + t] * sav[i]) * sbv[t];
+                        if (HAS_BIAS) y[t] = y[t] + bv[t];
                     }
-                    store_out<OUT>(p.C, (long)m * p.ldc + n, y);
+                    if (HAS_RES) {
+                        float rv[4];
+                        load4_res<OUT>(p.res, (long)m * p.ldr + nb, rv, valid, vec);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) y[t] = to_out_precision<OUT>(y[t]) + rv[t];
+                    }
+                    store4<OUT>(p.C, off, y, valid, vec);
                 }
             }
         }
     } else {
-        // SILU_MUL: this wave's 128 B-rows are one interleave group g = nw / 128:
-        // rows [0, 64) are gate columns 64 g + [0, 64), rows [64, 128) the matching up columns.
+        // SILU_MUL: this wave's 128 B-rows are one interleave group g = nw / 128: rows [0, 64) are
+        // gate columns 64 g + [0, 64), rows [64, 128) the matching up columns (tiles j and j + 2).
         const int g = nw >> 7;
-        float sgv[2], suv[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int ng = nw + j * 32 + r32;
-            sgv[j] = ng < N ? p.sb[ng] : 0.0f;
-            suv[j] = ng + 64 < N ? p.sb[ng + 64] : 0.0f;
-        }
         const int Nout = N >> 1;
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
+        for (int j = 0; j < 2; ++j) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = mw + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
-                if (m >= M) continue;
-                const float sav = p.sa[m];
+            for (int q = 0; q < 4; ++q) {
+                const int nr = j * 32 + 8 * q + 4 * khalf; // row within the group's gate half
+                const int col = g * 64 + nr;
+                if (col >= Nout) continue; // whole groups only (N % 128 == 0)
+                float sg[4], su[4];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int col = g * 64 + j * 32 + r32;
-                    if (col >= Nout) continue;
-                    const float gv = round_bf16(((float)acc[i][j][r] * sav) * sgv[j]);
-                    const float uv = round_bf16(((float)acc[i][j + 2][r] * sav) * suv[j]);
-                    const float act = round_bf16(gv / (1.0f + expf(-gv)));
-                    ((uint16_t *)p.C)[(long)m * p.ldc + col] = f32_to_bf16(act * uv);
+                for (int t = 0; t < 4; ++t) {
+                    sg[t] = p.sb[nw + nr + t];
+                    su[t] = p.sb[nw + 64 + nr + t];
+                }
+#pragma unroll
+                for (int i = 0; i < MB; ++i) {
+                    const int m = mw + i * 32 + r32;
+                    if (m >= M) continue;
+                    float hv[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * sg[t]);
+                        const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * su[t]);
+                        const float act = round_bf16(gv / (1.0f + expf(-gv)));
+                        hv[t] = act * uv;
+                    }
+                    store4<MICA_BF16>(p.C, (long)m * p.ldc + col, hv, 4, vec);
                 }
             }
         }
@@ -254,7 +501,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(GemmParams p) {
 
 template <int EPI, int OUT>
 int launch_out(const GemmParams &p, bool has_bias, bool has_res, hipStream_t st) {
-    dim3 grid(p.tiles_m * p.tiles_n), block(kThreads);
+    dim3 grid(p.tiles_m * p.tiles_n), block(CfgDefault::kThreads);
 #define MICA_G(B_, R_) hipLaunchKernelGGL((gemm_i8_kernel<EPI, OUT, B_, R_>), grid, block, 0, st, p)
     if (EPI == MICA_EPI_SILU_MUL) MICA_G(false, false);
     else if (has_bias && has_res) MICA_G(true, true);
@@ -295,6 +542,7 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     p.lda = lda; p.ldb = ldb; p.ldr = ldr; p.ldc = ldc; p.M = M; p.N = N; p.K = K;
     p.tiles_m = (M + BM - 1) / BM;
     p.tiles_n = (N + BN - 1) / BN;
+    p.vec_ok = (ldc % 4 == 0) && (Nout % 4 == 0) && (!residual || ldr % 4 == 0);
     if ((long long)p.tiles_m * p.tiles_n >= (1ll << 31)) return MICA_MISS_RANGE;
     hipStream_t st = (hipStream_t)stream;
     const bool hb = bias != nullptr, hr = residual != nullptr;

@@ -136,7 +136,7 @@ def act_quant(x, inv_smooth=None, rounding="even"):
     if x.dim() != 2 or x.device.type != "cuda" or x.dtype not in DT:
         return _miss("act_input")
     m, k = x.shape
-    if x.stride(1) != 1 or x.stride(0) != k:
+    if x.stride(1) != 1 or (m > 1 and x.stride(0) != k):  # a size-1 dim's stride is immaterial
         return _miss("act_contiguous")
     if not _gpu_ok(x.device):
         return _miss("no_container")
@@ -167,7 +167,8 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
         return _miss("mm_input")
     m, k = qx.shape
     n = qw.shape[0]
-    if qw.shape[1] != k or qx.stride(1) != 1 or qw.stride(1) != 1 or qx.stride(0) != k or qw.stride(0) != k:
+    if (qw.shape[1] != k or qx.stride(1) != 1 or qw.stride(1) != 1 or (m > 1 and qx.stride(0) != k)
+            or (n > 1 and qw.stride(0) != k)):
         return _miss("mm_contiguous")
     for t, size in ((sx, m), (sw, n)) + (((bias, n),) if bias is not None else ()):
         if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != size or t.device != qx.device:

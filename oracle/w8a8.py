@@ -161,12 +161,14 @@ def silu_mul(g_bits: np.ndarray, u_bits: np.ndarray) -> np.ndarray:
 
     CPU path ``F.silu(gate) * up`` (fused_kernels.py:86-87): F.silu on a bf16 tensor computes
     g / (1 + exp(-g)) in fp32 and rounds to bf16, the product of two bf16 tensors is an fp32 product
-    rounded to bf16.  Same formula as the Triton swiglu (fused_kernels.py:36-42).  exp is evaluated
-    in float64 and the quotient rounded once to fp32 (the library exps differ by <= 1-2 fp32 ulp).
+    rounded to bf16.  Same formula as the Triton swiglu (fused_kernels.py:36-42).  exp(-g) is
+    evaluated in float64 and rounded once to fp32 (so it overflows to inf for -g > 88.72, as the fp32
+    exp does); 1 + e and the quotient are fp32 operations.
     """
-    g = bf16_to_f32(g_bits).astype(np.float64)
+    g = bf16_to_f32(g_bits)
     with np.errstate(over="ignore"):
-        act = round_bf16((g / (1.0 + np.exp(-g))).astype(np.float32))
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    act = round_bf16(g / (F32(1.0) + e))
     return f32_to_bf16(act * bf16_to_f32(u_bits))
 
 
