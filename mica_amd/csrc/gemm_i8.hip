@@ -37,7 +37,7 @@ constexpr int NST = 4;      // LDS stages
 constexpr int KS = BK / 32; // MFMA k-steps per stage
 constexpr int kABytes = BM * BK;               // 16 KiB
 constexpr int kStage = (BM + BN) * BK;         // 32 KiB
-constexpr int kGroupM = 8;
+constexpr int kGroupM = 4;
 constexpr int kXcds = 8;
 
 // Wave layout of the 256 x 256 workgroup tile: WGM x WGN waves, each owning WM x WN.
@@ -58,7 +58,8 @@ struct Cfg {
     static_assert(WN == 128, "the SiLU epilogue needs one 128-row gate/up group per wave");
 };
 using CfgDefault = Cfg<4, 2>;
-static_assert(CfgDefault::kWaves == 8 && CfgDefault::WM == 64, "the ping-pong loop pairs two groups of 4 waves");
+static_assert(CfgDefault::kWaves == 8 && CfgDefault::MB == 2 && CfgDefault::NB == 4 &&
+                  CfgDefault::kBlocksPerWave == 2, "the main loop's instruction schedule is written for 8 waves of 64 x 128");
 
 // word 3 of a gfx9 buffer resource (raw buffer, 32-bit data format), as used by CK for gfx9xx
 constexpr int kBufferFlags = 0x00020000;
@@ -95,10 +96,11 @@ MICA_DEVICE void wait_vmcnt() {
 }
 MICA_DEVICE void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
 
-// wait until at most `slabs` (0..3) slabs of this wave's DMA are still in flight
+// wait until at most `slabs` (0..4) slabs of this wave's DMA are still in flight
 template <int kDmaPerSlab>
 MICA_DEVICE void wait_dma(int slabs) {
-    if (slabs >= 3) wait_vmcnt<3 * kDmaPerSlab>();
+    if (slabs >= 4) wait_vmcnt<4 * kDmaPerSlab>();
+    else if (slabs == 3) wait_vmcnt<3 * kDmaPerSlab>();
     else if (slabs == 2) wait_vmcnt<2 * kDmaPerSlab>();
     else if (slabs == 1) wait_vmcnt<kDmaPerSlab>();
     else wait_vmcnt<0>();
@@ -204,18 +206,22 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         a_row[j] = m0 + r < M ? (m0 + r) * p.lda + kcol[j] : kOutOfRange;
         b_row[j] = n0 + r < N ? (n0 + r) * p.ldb + kcol[j] : kOutOfRange;
     }
-    auto dma = [&](int slab) {
+    // one DMA instruction: block j (0 .. kBlocksPerWave-1) of operand op (0: A, 1: B) of a slab
+    auto dma1 = [&](int slab, int j, int op) {
         const int k0 = slab * BK;
         int8_t *st = smem + (slab % NST) * kStage;
+        const bool kin = k0 + kcol[j] < K;
+        const int row = op == 0 ? a_row[j] : b_row[j];
+        const int off = (kin && row != kOutOfRange) ? row + k0 : kOutOfRange;
+        const int blk = wave * kBlocksPerWave + j;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(op == 0 ? rsrc_a : rsrc_b,
+                                                 (lds_void *)(st + op * kABytes + blk * 1024), 16, off, 0, 0, 0);
+    };
+    auto dma = [&](int slab) {
 #pragma unroll
         for (int j = 0; j < kBlocksPerWave; ++j) {
-            const bool kin = k0 + kcol[j] < K;
-            const int oa = (kin && a_row[j] != kOutOfRange) ? a_row[j] + k0 : kOutOfRange;
-            const int ob = (kin && b_row[j] != kOutOfRange) ? b_row[j] + k0 : kOutOfRange;
-            const int blk = wave * kBlocksPerWave + j;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void *)(st + blk * 1024), 16, oa, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_void *)(st + kABytes + blk * 1024), 16, ob, 0,
-                                                     0, 0);
+            dma1(slab, j, 0);
+            dma1(slab, j, 1);
         }
     };
 
@@ -267,48 +273,67 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
                 acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w[ks][j], o.x[ks][i], acc[j][i], 0, 0, 0);
     };
 
-    // ---- ping-pong main loop.  The 8 waves form two groups (waves 0-3: tile rows 0-127, waves 4-7:
-    // rows 128-255), one wave of each group per SIMD.  Time is cut into phases separated by
-    // workgroup barriers; group g handles slab k as load(k) in phase 2k + g (issue the DMA of
-    // slab k + 3, read slab k's operands from LDS) and compute(k) in phase 2k + g + 1 (16 MFMAs at
-    // raised wave priority).  So in every phase one wave per SIMD computes while the other loads.
-    // Slab k's stage is free once both groups have read it (end of phase 2k + 1); slab k + 3 is
-    // DMA'd into stage (k - 1) % 4 during load(k), phases 2k and 2k + 1.
+    // ---- main loop.  Every wave runs the same software pipeline, one barrier per 64-byte slab k:
+    //   wait: this wave's DMA of slab k + 1 landed, its reads of slab k (registers X) completed
+    //   barrier: slab k + 1 is visible in LDS, and nobody reads slab k's stage any more
+    //   then, interleaved instruction by instruction: the 16 MFMAs of slab k (from X), the 12
+    //   operand reads of slab k + 1 (into Y) and the 4 DMA instructions of slab k + 4 (into the
+    //   stage slab k just left).
+    // All 8 waves keep the LDS busy together (operand reads and DMA writes share it) while the
+    // two waves of each SIMD keep its matrix core busy.  A DMA past the last slab is still issued
+    // (its offsets fail the range check and it writes zeros into a stage nobody reads), so every
+    // wave always has exactly 3 younger slabs in flight when it waits for slab k + 1.
     const int nk = (K + BK - 1) / BK;
-    const int grp = wave >> 2;
-    const int pre = nk < NST ? nk : NST;
-    for (int sl = 0; sl < pre; ++sl) dma(sl);
-    wait_dma<kDmaPerSlab>(pre - 1); // slab 0 landed in this wave's blocks ...
-    __builtin_amdgcn_s_barrier();   // ... and in every wave's
-    Ops o;
-    const int nphase = 2 * nk + 1;
-    for (int ph = 0; ph < nphase; ++ph) {
-        const int t = ph - grp;
-        if (t >= 0 && t < 2 * nk) {
-            const int k = t >> 1;
-            if ((t & 1) == 0) {
-                if (k >= 1 && k + NST - 1 < nk) dma(k + NST - 1);
-                lds_read(o, k);
-                wait_lgkmcnt0(); // the stage may be recycled after the barrier below
-            } else {
-                __builtin_amdgcn_s_setprio(1);
-                mfma_half(o, 0);
-                mfma_half(o, 1);
-                __builtin_amdgcn_s_setprio(0);
-            }
-        }
-        // before group 0 loads slab s = (ph + 1) / 2 in the next phase, every wave's DMA of s landed;
-        // each wave's newest DMA is then slab min(k0 + 3, nk - 1), k0 = (ph - 1) / 2
-        if ((ph & 1) == 1) {
-            const int s_next = (ph + 1) >> 1;
-            if (s_next < nk) {
-                const int k0 = (ph - 1) >> 1;
-                const int newest = (k0 + NST - 1 < nk - 1) ? k0 + NST - 1 : nk - 1;
-                wait_dma<kDmaPerSlab>(newest - s_next);
-            }
-        }
+#pragma unroll
+    for (int sl = 0; sl < NST; ++sl) dma(sl);
+    wait_vmcnt<(NST - 1) * kDmaPerSlab>(); // slab 0 landed in this wave's blocks ...
+    __builtin_amdgcn_s_barrier();          // ... and in every wave's
+    Ops X, Y;
+    lds_read(X, 0);
+
+    auto step = [&](Ops &cur, Ops &nxt, int k) {
+        wait_vmcnt<(NST - 2) * kDmaPerSlab>(); // slab k + 1 landed (slabs k + 2, k + 3 may be in flight)
+        wait_lgkmcnt0();                       // slab k's operands are in registers
         __builtin_amdgcn_s_barrier();
+        const int8_t *st = smem + ((k + 1) % NST) * kStage;
+        const int dslab = k + NST;
+        // 4 reads up front, then 4 x [MFMA, read, MFMA, read, MFMA, DMA, MFMA]
+        nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
+        nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
+        nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
+        nxt.x[0][1] = *(const v4i *)(st + x_rd[1][0]);
+        nxt.w[0][2] = *(const v4i *)(st + w_rd[2][0]);
+        nxt.w[0][3] = *(const v4i *)(st + w_rd[3][0]);
+        nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
+        nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
+        nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
+        nxt.x[1][1] = *(const v4i *)(st + x_rd[1][1]);
+        nxt.w[1][2] = *(const v4i *)(st + w_rd[2][1]);
+        nxt.w[1][3] = *(const v4i *)(st + w_rd[3][1]);
+        dma1(dslab, 0, 0);
+        dma1(dslab, 0, 1);
+        dma1(dslab, 1, 0);
+        dma1(dslab, 1, 1);
+        mfma_half(cur, 0);
+        mfma_half(cur, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+    };
+    int k = 0;
+    for (; k + 1 < nk; k += 2) {
+        step(X, Y, k);
+        step(Y, X, k + 1);
     }
+    if (k < nk) step(X, Y, k);
     wait_vmcnt<0>();
 
     // ---- epilogue.  acc[j][i][r]: n = 8 (r / 4) + 4 (lane / 32) + r % 4 (4 consecutive per r / 4),

@@ -123,7 +123,7 @@ def test_label_readout_gathers_rows_once():
         r(torch.zeros(8, 64, dtype=torch.bfloat16), [1, 2])
 
 
-def _tile_of(pid, tiles_m, tiles_n, group_m=8, xcds=8):
+def _tile_of(pid, tiles_m, tiles_n, group_m=4, xcds=8):
     """The GEMM kernel's workgroup -> tile map (tile_of in mica_amd/csrc/gemm_i8.hip)."""
     nt = tiles_m * tiles_n
     per, rem = divmod(nt, xcds)
