@@ -54,7 +54,10 @@ struct Cfg {
     // staged epilogue: each wave's WM x WN 16-bit block, rows padded by 16 bytes
     static constexpr int kEpiPitch = WN * 2 + 16;
     static constexpr int kEpiWave = WM * kEpiPitch;
-    static constexpr int kSmem = (NST * kStage > kWaves * kEpiWave) ? NST * kStage : kWaves * kEpiWave;
+    static constexpr int kSmemMain = (NST * kStage > kWaves * kEpiWave) ? NST * kStage : kWaves * kEpiWave;
+    // the tile's row scales, column scales and bias (fp32), staged at kernel start
+    static constexpr int kScaleOff = kSmemMain;
+    static constexpr int kSmem = kSmemMain + 3 * 256 * 4;
     static_assert(WN == 128, "the SiLU epilogue needs one 128-row gate/up group per wave");
 };
 using CfgDefault = Cfg<4, 2>;
@@ -284,8 +287,29 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
     // (its offsets fail the range check and it writes zeros into a stage nobody reads), so every
     // wave always has exactly 3 younger slabs in flight when it waits for slab k + 1.
     const int nk = (K + BK - 1) / BK;
+    // the epilogue's per-row / per-column factors: loaded before the prologue DMA and written to
+    // LDS after it, so their latency hides under the DMA's.  Threads 0-255: sa and bias of tile
+    // row / column tid, threads 256-511: sb of column tid - 256.
+    static_assert(C::kThreads == 512, "one scale load per thread");
+    float f1, f2 = 0.0f;
+    {
+        // branch-free: the index is clamped into range (values of rows / columns past the edge
+        // are never used), so no load waits for another
+        const int i = tid & 255;
+        const bool row = tid < 256;
+        const float *src = row ? p.sa : p.sb;
+        const int base = row ? m0 : n0;
+        const int lim = (row ? M : N) - base;
+        f1 = src[base + (i < lim ? i : lim - 1)];
+        if (HAS_BIAS) f2 = p.bias[n0 + (i < N - n0 ? i : N - n0 - 1)];
+    }
 #pragma unroll
     for (int sl = 0; sl < NST; ++sl) dma(sl);
+    {
+        float *sc = (float *)(smem + C::kScaleOff);
+        sc[tid] = f1;                       // [0, 256): sa, [256, 512): sb
+        if (tid < 256) sc[512 + tid] = f2;  // [512, 768): bias
+    }
     wait_vmcnt<(NST - 1) * kDmaPerSlab>(); // slab 0 landed in this wave's blocks ...
     __builtin_amdgcn_s_barrier();          // ... and in every wave's
     Ops X, Y;
@@ -341,12 +365,10 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
     const int mw = m0 + wm * WM;
     const int nw = n0 + wn * WN;
     const bool vec = p.vec_ok != 0;
+    const float *sc = (const float *)(smem + C::kScaleOff); // [0, 256): sa, [256, 512): sb, [512, 768): bias
     float sav[MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const int m = mw + i * 32 + r32;
-        sav[i] = m < M ? p.sa[m] : 0.0f;
-    }
+    for (int i = 0; i < MB; ++i) sav[i] = sc[wm * WM + i * 32 + r32];
     if constexpr (OUT == MICA_BF16 || OUT == MICA_FP16) {
         // Staged through LDS: every wave writes its rounded 16-bit block (8 bytes per lane per
         // store) into its own padded region, then streams it out row-contiguously, 16 bytes per
@@ -363,16 +385,12 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
             for (int q = 0; q < 4; ++q) {
                 const int nl = j * 32 + 8 * q + 4 * khalf; // local output column of this lane's 4 values
                 float s1[4], s2[4], bv[4];
+                const int cb = wn * WN + nl; // tile-local column of this lane's 4 values
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    if (EPI == MICA_EPI_SCALE) {
-                        const int n = nw + nl + t;
-                        s1[t] = n < N ? p.sb[n] : 0.0f;
-                        bv[t] = (HAS_BIAS && n < N) ? p.bias[n] : 0.0f;
-                    } else {
-                        s1[t] = p.sb[nw + nl + t];      // gate rows (N % 128 == 0: in range)
-                        s2[t] = p.sb[nw + 64 + nl + t]; // matching up rows
-                    }
+                    s1[t] = sc[256 + cb + t]; // SCALE: sb[n]; SILU_MUL: the gate rows' sb
+                    s2[t] = EPI == MICA_EPI_SCALE ? 0.0f : sc[256 + cb + 64 + t]; // the matching up rows
+                    bv[t] = HAS_BIAS ? sc[512 + cb + t] : 0.0f;
                 }
 #pragma unroll
                 for (int i = 0; i < MB; ++i) {
