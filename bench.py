@@ -40,6 +40,13 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 36-layer prefill measurement")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="only run the profiled kernels (headline GEMM, norm+quant T=32768, a 256 MiB copy) "
+                         "for rocprofv3 counter passes")
+    ap.add_argument("--summarize", nargs=2, metavar=("ROCPROF_DIR", "OUT_TXT"),
+                    help="write a text summary of rocprofv3 CSV output (kernel stats or counters)")
+    ap.add_argument("--command", default="", help="with --summarize: the command that produced ROCPROF_DIR")
     return ap.parse_args()
 
 
@@ -132,6 +139,12 @@ def traffic_from_profiles():
 
 def main():
     args = parse()
+    if args.summarize:
+        summarize(*args.summarize, command=args.command)
+        return
+    if args.pmc_workload:
+        pmc_workload()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the hot path is a single-GPU "
               f"kernel set; see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -245,9 +258,125 @@ def main():
         result["extra"] = extra
         result["prefill_tokens_per_s"] = layer["hot_path_tokens_per_s_36_layers"]
 
+    if not args.no_stack:
+        result["stack"] = stack_prefill(torch, dev)
+        result["prefill_tokens_per_s"] = result["stack"]["tokens_per_s"]
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, M, K, N)
     print(json.dumps(result), flush=True)
+
+
+def stack_prefill(torch, dev, reps=3):
+    """Config 4: the 36-layer 4B-shaped W8A8 stack on 8 requests x 2048 packed tokens, readout of 255
+    option ids at each request's last position.  Attention is torch SDPA (bf16)."""
+    from mica_amd.model import StackConfig, W8A8Stack
+
+    st = W8A8Stack(StackConfig(), device=dev, seed=0)
+    B, S = 8, 2048
+    ids = torch.randint(0, st.cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(0)).to(dev)
+    st.prefill(ids, B)  # warm-up
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        _, probs = st.prefill(ids, B)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    ops = st.linear_ops_per_token() * B * S
+    ok = bool(torch.isfinite(probs).all()) and bool(torch.allclose(probs.sum(1), torch.ones(B, device=dev)))
+    del st
+    torch.cuda.empty_cache()
+    return {"workload": "36 layers, hidden 2560, inter 9728, QKV 6144, vocab 151936; 8 requests x 2048 tokens "
+                        "packed; last-position readout over 255 option ids + softmax",
+            "ms_per_prefill": round(ms, 2), "tokens_per_s": round(B * S / (ms * 1e-3), 1),
+            "w8a8_linear_TOP": round(ops / 1e12, 2), "linear_TOPS_incl_attention_time": round(ops / (ms * 1e-3) / 1e12, 1),
+            "probs_valid": ok, "reps": reps}
+
+
+def pmc_workload():
+    """The kernels the committed counter summaries describe, each launched 10 times."""
+    import torch
+
+    from mica_amd import _lib, int8_kernels
+
+    dev = torch.device("cuda", torch.cuda.current_device())
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    M, K, N = 4096, HIDDEN, INTER
+    x, qw, sw = synthetic(torch, dev, M, K, N, seed=0)
+    qx, sx = int8_kernels.act_quant(x)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    gemm = gemm_launcher(torch, lib, qx, sx, qw, sw, out)
+    T = 32768
+    h = torch.randn(T, K, device=dev).to(torch.bfloat16)
+    w = torch.ones(K, device=dev).to(torch.bfloat16)
+    q = torch.empty(T, K, dtype=torch.int8, device=dev)
+    s = torch.empty(T, dtype=torch.float32, device=dev)
+    a = (h.data_ptr(), _lib.BF16, K, None, K, w.data_ptr(), _lib.BF16, 0.0, 1e-6, None, q.data_ptr(), K,
+         s.data_ptr(), None, K, None, K, T, K, 0, st)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        gemm()
+        if lib.mica_rmsnorm_quant(*a) != 0:
+            raise RuntimeError("mica_rmsnorm_quant failed")
+        dst.copy_(src)  # 256 MiB read + 256 MiB written: the calibration of FETCH_SIZE / WRITE_SIZE
+    torch.cuda.synchronize()
+    print("pmc workload done", flush=True)
+
+
+def summarize(indir, out_txt, command="", top=16):
+    """Text summary of rocprofv3 CSV output: kernel time statistics (--stats), per-dispatch durations
+    by launch shape (--kernel-trace) and/or per-dispatch counter means (--pmc), top entries only.
+    FETCH_SIZE / WRITE_SIZE are also converted to bytes with the factors that make the 256 MiB copy
+    of the --pmc-workload read and write exactly 256 MiB."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    lines = [f"# rocprofv3 summary of {indir}"]
+    if command:
+        lines.append(f"# command: {command}")
+    stats = sorted(glob.glob(os.path.join(indir, "**", "*kernel_stats.csv"), recursive=True))
+    for f in stats:
+        rows = list(csv.DictReader(open(f)))
+        lines.append(f"# kernel statistics ({os.path.basename(f)})")
+        lines.append(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>6}  kernel")
+        for r in rows[:top]:
+            name = r["Name"]
+            lines.append(f"{int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} {float(r['MinNs']) / 1e3:10.2f} "
+                         f"{float(r['MaxNs']) / 1e3:10.2f} {float(r['Percentage']):6.2f}  {name[:150]}")
+    traces = sorted(glob.glob(os.path.join(indir, "**", "*kernel_trace.csv"), recursive=True))
+    for f in traces:
+        groups = defaultdict(list)
+        for r in csv.DictReader(open(f)):
+            grid = (int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
+            groups[(r["Kernel_Name"][:150], grid)].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        lines.append(f"# per-dispatch durations by kernel and launch shape ({os.path.basename(f)})")
+        lines.append(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'grid':>9} {'wg':>5}  kernel")
+        for (k, (gx, wx)), v in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
+            lines.append(f"{len(v):6d} {sum(v) / len(v) / 1e3:10.2f} {min(v) / 1e3:10.2f} {max(v) / 1e3:10.2f} "
+                         f"{gx:9d} {wx:5d}  {k}")
+    pmc = sorted(glob.glob(os.path.join(indir, "**", "*counter_collection.csv"), recursive=True))
+    for f in pmc:
+        agg = defaultdict(list)
+        for r in csv.DictReader(open(f)):
+            agg[(r["Kernel_Name"][:150], r["Counter_Name"])].append(float(r["Counter_Value"]))
+        lines.append(f"# counters per dispatch, mean over dispatches ({os.path.basename(f)})")
+        for (k, c), v in sorted(agg.items()):
+            lines.append(f"{c:28s} {sum(v) / len(v):16.1f}  n={len(v):3d}  {k}")
+        copy = {c: sum(v) / len(v) for (k, c), v in agg.items() if "copyBuffer" in k or "copy_kernel" in k}
+        for c, kib in copy.items():
+            factor = (256 << 20) / (kib * 1024.0)
+            lines.append(f"# calibration: the 256 MiB copy (256 MiB read, 256 MiB written) counts {c} = {kib:.1f} KiB "
+                         f"-> bytes = KiB x 1024 x {factor:.4f}")
+            for (k, c2), v in sorted(agg.items()):
+                if c2 == c and "copyBuffer" not in k:
+                    lines.append(f"{c2 + '_bytes':28s} {sum(v) / len(v) * 1024.0 * factor:16.0f}  {k}")
+    with open(out_txt, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print(f"wrote {out_txt} ({len(lines)} lines)")
 
 
 if __name__ == "__main__":

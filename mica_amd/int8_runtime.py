@@ -42,23 +42,12 @@ def smooth_factors(act_amax, w, alpha=ALPHA, lo=0.0001, hi=10000.0):
     return s.clamp(lo, hi)
 
 
-def _torch_quant_act(x, inv_smooth):
-    """The reference's fallback quantizer (int8_quant.quant_act, int8_quant.py:64-73) on the GPU."""
-    xf = x.float()
-    if inv_smooth is not None:
-        xf = xf * inv_smooth
-    s = xf.abs().amax(-1).clamp_min(EPS) / QMAX
-    return torch.round(xf / s[:, None]).clamp(-127, 127).to(torch.int8), s
-
-
-def _torch_mm(qx, sx, qw, sw, bias, out_dtype):
-    """The reference's fallback GEMM (int8_runtime.py:186-192) on torch's GPU int8 matmul."""
-    m = qx.shape[0]
-    a = qx if m > 16 else torch.cat((qx, qx.new_zeros(32 - m, qx.shape[1])), 0)
-    y = torch._int_mm(a, qw.t())[:m].float() * sx[:, None] * sw[None, :]
-    if bias is not None:
-        y = y + bias
-    return y.to(out_dtype)
+def _hit(r, what):
+    """A kernel miss inside a module is an error: the modules have no torch or CPU fallback."""
+    if r is None:
+        reasons = ", ".join(f"{k}={v}" for k, v in aot.STATS["fallback"].items())
+        raise RuntimeError(f"mica_amd {what} kernel miss (misses so far: {reasons})")
+    return r
 
 
 def _require_gpu(x):
@@ -136,16 +125,10 @@ class QLinear(nn.Module):
         return (w * self.inv_smooth[None, :] if self.inv_smooth is not None else w).to(self.out_dtype)
 
     def _quant(self, x2):
-        r = aot.act_quant(x2.contiguous(), self.inv_smooth)
-        return r if r is not None else _torch_quant_act(x2, self.inv_smooth)
+        return _hit(aot.act_quant(x2.contiguous(), self.inv_smooth), "act_quant")
 
     def _mm(self, qx, sx, qw, sw, b, residual=None):
-        y = aot.mm_i8(qx, sx, qw, sw, b, self.out_dtype, residual=residual)
-        if y is None:
-            y = _torch_mm(qx, sx, qw, sw, b, self.out_dtype)
-            if residual is not None:
-                y = y + residual
-        return y
+        return _hit(aot.mm_i8(qx, sx, qw, sw, b, self.out_dtype, residual=residual), "mm_i8")
 
     def rows_forward(self, x, ranges):
         """Quantize once, one GEMM per output-row range (int8_runtime.py:153-170)."""
@@ -218,17 +201,14 @@ class GateUpQLinear(nn.Module):
 
     def forward_quantized(self, qx, sx):
         _require_gpu(qx)
-        h = aot.mm_i8(qx, sx, self.qweight, self.wscale, None, torch.bfloat16, epilogue="silu_mul")
-        if h is None:
-            raise RuntimeError("fused gate+up GEMM is not supported for this input")
-        return h
+        return _hit(aot.mm_i8(qx, sx, self.qweight, self.wscale, None, torch.bfloat16, epilogue="silu_mul"),
+                    "fused gate+up mm_i8")
 
     def forward(self, x):
         _require_gpu(x)
         shape = x.shape
         x2 = x.reshape(-1, shape[-1]).contiguous()
-        r = aot.act_quant(x2)
-        qx, sx = r if r is not None else _torch_quant_act(x2, None)
+        qx, sx = _hit(aot.act_quant(x2), "act_quant")
         return self.forward_quantized(qx, sx).reshape(*shape[:-1], self.out_features)
 
 
@@ -247,13 +227,22 @@ class W8A8MLP(nn.Module):
         shape = h.shape
         q, s = rms_norm_quant(h, self.norm_weight, self.eps, offset=self.offset)
         g = self.gate_up.forward_quantized(q, s)
-        r = aot.act_quant(g)
-        qh, sh = r if r is not None else _torch_quant_act(g, None)
+        qh, sh = _hit(aot.act_quant(g), "act_quant")
         out = self.down.forward_quantized(qh, sh, residual=h.reshape(-1, shape[-1]))
         return out.reshape(shape)
 
 
 # ---------------------------------------------------------------------------------- self-test
+def _emulated_quant(x, inv_smooth):
+    """The self-test's exact INT8 emulation of the quantizer (int8_quant.quant_act, int8_quant.py:64-73),
+    in torch on the test's device: the yardstick the kernels' error is measured against."""
+    xf = x.float()
+    if inv_smooth is not None:
+        xf = xf * inv_smooth
+    s = xf.abs().amax(-1).clamp_min(EPS) / QMAX
+    return torch.round(xf / s[:, None]).clamp(-127, 127).to(torch.int8), s
+
+
 def _row_rel(a, b):
     return float(((a - b).norm(dim=-1) / b.norm(dim=-1).clamp_min(1e-30)).max())
 
@@ -293,7 +282,7 @@ def selftest(shapes, device, rows=SELFTEST_ROWS, seed=SELFTEST_SEED):
                         out["reason"] = f"N {n} K {k} M {m}: {launched} launches (expected 2), misses {miss}"
                         return out
                     ref = x.float() @ wd.t()
-                    qx, sx = _torch_quant_act(x, q.inv_smooth)
+                    qx, sx = _emulated_quant(x, q.inv_smooth)
                     emu = (qx.double() @ q.qweight.double().t()).float() * sx[:, None] * q.wscale[None, :]
                     if q.bias is not None:
                         ref, emu = ref + q.bias, emu + q.bias

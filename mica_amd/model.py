@@ -1,0 +1,165 @@
+"""A 4B-shaped decoder stack whose linear layers run on the W8A8 hot path, for prefill-only scoring.
+
+Shape (the benchmark's synthetic 4B configuration): 36 layers, hidden 2560, MLP intermediate 9728,
+32 query heads and 8 K/V heads of dim 128 (QKV projection N = 4096 + 2 x 1024), vocabulary 151936.
+Weights are random int8 with per-output-channel fp32 scales; norms are gamma-style RMSNorm weights.
+
+Per layer (the call pattern of the reference's fork.layer_step, v0.5/serving/lib/fork.py:394-422):
+  q, s   = rms_norm_quant(h, input_norm)                     1 launch
+  qkv    = QKV W8A8 GEMM                                     1 launch
+  a      = causal GQA attention on each request (torch SDPA, bf16; outside the W8A8 path)
+  h      = h + O W8A8(a)          (residual in the epilogue)  2 launches (act_quant + GEMM)
+  q, s   = rms_norm_quant(h, post_attention_norm)            1 launch
+  g      = fused gate+up GEMM, SiLU(gate) * up epilogue      1 launch
+  h      = h + down W8A8(act_quant(g))                       2 launches
+Then, as PrefillEngine.final + the readout do (prefill_engine.py:280-304, release_runtime.py:298-306,
+:509-517), only each request's last position is normed and dotted with the allowed label rows, and
+the option slice is softmaxed.  Requests are packed back to back, all of the same length.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import int8_kernels as aot
+from .fused_kernels import rms_norm_quant
+from .int8_runtime import GateUpQLinear, QLinear
+from .readout import LabelReadout
+
+
+@dataclass
+class StackConfig:
+    layers: int = 36
+    hidden: int = 2560
+    intermediate: int = 9728
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    n_options: int = 255   # option labels after the No / Yes pair (mica/codebook.py:19)
+
+
+def _rand_qlinear(n, k, g, device):
+    qw = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8, device=device)
+    sw = torch.empty(n, device=device).uniform_(1e-3, 1e-2, generator=g)
+    return QLinear.from_quantized(qw, sw)
+
+
+def _rand_norm(n, g, device):
+    return (torch.randn(n, generator=g, device=device) * 0.1 + 1.0).to(torch.bfloat16)
+
+
+class Layer:
+    def __init__(self, cfg: StackConfig, g, device):
+        H = cfg.hidden
+        self.cfg = cfg
+        self.input_norm = _rand_norm(H, g, device)
+        self.post_norm = _rand_norm(H, g, device)
+        self.qkv = _rand_qlinear((cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim, H, g, device)
+        self.o = _rand_qlinear(H, cfg.heads * cfg.head_dim, g, device)
+        gate = _rand_qlinear(cfg.intermediate, H, g, device)
+        up = _rand_qlinear(cfg.intermediate, H, g, device)
+        self.gate_up = GateUpQLinear(gate, up)
+        self.down = _rand_qlinear(H, cfg.intermediate, g, device)
+
+
+def _rope(S, head_dim, theta, device):
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
+    ang = torch.arange(S, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+    return torch.cos(ang), torch.sin(ang)
+
+
+def _apply_rope(x, cos, sin):
+    # x [B, heads, S, d] bf16; rotate-half convention, computed in fp32
+    xf = x.float()
+    d = xf.shape[-1] // 2
+    x1, x2 = xf[..., :d], xf[..., d:]
+    c, s = cos[None, None], sin[None, None]
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), -1).to(x.dtype)
+
+
+class W8A8Stack:
+    """Random-init 4B-shaped stack; `prefill(ids, batch)` returns option probabilities."""
+
+    def __init__(self, cfg: StackConfig = StackConfig(), device="cuda", seed=0):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        H = cfg.hidden
+        self.embed = (torch.randn(cfg.vocab, H, generator=g, device=self.device) * 0.5).to(torch.bfloat16)
+        self.layers = [Layer(cfg, g, self.device) for _ in range(cfg.layers)]
+        self.final_norm = _rand_norm(H, g, self.device)
+        self.lm_head = (torch.randn(cfg.vocab, H, generator=g, device=self.device) * 0.02).to(torch.bfloat16)
+        ids = torch.randperm(cfg.vocab, generator=torch.Generator().manual_seed(seed))[: 2 + cfg.n_options]
+        self.label_ids = ids.to(self.device)
+        self.readout = LabelReadout(self.lm_head, self.label_ids)
+        self._rope = {}
+
+    def _attention(self, qkv, B, S):
+        cfg = self.cfg
+        hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
+        q = q.transpose(1, 2).contiguous()
+        k = k.transpose(1, 2).contiguous()
+        v = v.transpose(1, 2).contiguous()
+        if S not in self._rope:
+            self._rope[S] = _rope(S, d, cfg.rope_theta, qkv.device)
+        cos, sin = self._rope[S]
+        q, k = _apply_rope(q, cos, sin), _apply_rope(k, cos, sin)
+        k = k.repeat_interleave(hq // hk, dim=1)
+        v = v.repeat_interleave(hq // hk, dim=1)
+        a = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=1.0 / math.sqrt(d))
+        return a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
+
+    def layer_forward(self, L: Layer, h, B, S, trace=None):
+        cfg = self.cfg
+        q, s = rms_norm_quant(h, L.input_norm, cfg.eps, offset=0.0)
+        qkv = L.qkv.forward_quantized(q, s)
+        a = self._attention(qkv, B, S)
+        r = aot.act_quant(a)
+        h1 = L.o.forward_quantized(*r, residual=h)
+        q2, s2 = rms_norm_quant(h1, L.post_norm, cfg.eps, offset=0.0)
+        g = L.gate_up.forward_quantized(q2, s2)
+        qh, sh = aot.act_quant(g)
+        h2 = L.down.forward_quantized(qh, sh, residual=h1)
+        if trace is not None:
+            trace.append(dict(h=h, q=q, s=s, qkv=qkv, a=a, qa=r[0], sa=r[1], h1=h1, q2=q2, s2=s2, g=g, qh=qh,
+                              sh=sh, h2=h2))
+        return h2
+
+    @torch.no_grad()
+    def prefill(self, ids, batch, kinds=None, n_choices=None, trace=None):
+        """ids: int [batch * S] packed token ids of `batch` equal-length requests.  Returns
+        (logits [batch, 2 + n_options], probs [batch, width]) for the requests' last positions;
+        kinds[b] == 'noul' softmaxes logits[:2], otherwise logits[2 : 2 + n_choices[b]]."""
+        T = ids.numel()
+        S = T // batch
+        h = self.embed.index_select(0, ids)
+        for L in self.layers:
+            h = self.layer_forward(L, h, batch, S, trace)
+        rows = torch.arange(batch, device=h.device, dtype=torch.int32) * S + (S - 1)
+        if kinds is None:
+            kinds = ["choice"] * batch
+        if n_choices is None:
+            n_choices = [self.cfg.n_options] * batch
+        lo = torch.tensor([0 if k == "noul" else 2 for k in kinds], dtype=torch.int32, device=h.device)
+        cnt = torch.tensor([2 if k == "noul" else n for k, n in zip(kinds, n_choices)], dtype=torch.int32,
+                           device=h.device)
+        logits, probs = self.readout(h, rows, self.final_norm, self.cfg.eps, offset=0.0, lo=lo, cnt=cnt,
+                                     probs_width=self.cfg.n_options)
+        if trace is not None:
+            trace.append(dict(h_final=h, rows=rows, logits=logits, probs=probs))
+        return logits, probs
+
+    def linear_ops_per_token(self):
+        """int8 ops per token of the W8A8 linears (2 N K per projection), final readout excluded."""
+        c = self.cfg
+        qkv = (c.heads + 2 * c.kv_heads) * c.head_dim * c.hidden
+        o = c.hidden * c.heads * c.head_dim
+        mlp = 3 * c.intermediate * c.hidden
+        return 2 * (qkv + o + mlp) * c.layers

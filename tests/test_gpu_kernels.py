@@ -251,6 +251,28 @@ def test_gemm_residual_epilogue(gpu):
     assert np.array_equal(bits_of(y), ref)
 
 
+def test_gemm_headline_full_size(gpu):
+    """The benchmarked GEMM itself, M=4096 K=2560 N=9728 (every tile, including the partial last round
+    of tiles), bit-exact: int32 accumulators and the bf16 output.  Then a size-independent property
+    of the epilogue at the same size: scaling sa by 2^j scales every finite output by exactly 2^j."""
+    note("gemm headline 4096x9728x2560")
+    m, n, k = 4096, 9728, 2560
+    rng = np.random.default_rng(4096)
+    xb = act_bits(rng, (m, k))
+    A, sa = O.quant_act(O.bf16_to_f32(xb))
+    B = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    tA, tB, tsa, tsb = (torch.from_numpy(v).cuda() for v in (A, B, sa, sb))
+    ref = O.int_gemm(A, B)
+    assert_equal_diag(int8_kernels.mm_i8_int32(tA, tB).cpu().numpy(), ref, "int32 accumulators")
+    y = bits_of(int8_kernels.mm_i8(tA, tsa, tB, tsb))
+    assert_equal_diag(y, O.epilogue(ref, sa, sb), "bf16 output")
+    pow2 = np.float32(2.0) ** rng.integers(-3, 4, m).astype(np.float32)
+    y2 = bits_of(int8_kernels.mm_i8(tA, torch.from_numpy(sa * pow2).cuda(), tB, tsb))
+    want = O.f32_to_bf16(O.bf16_to_f32(y) * pow2[:, None])
+    assert_equal_diag(y2, want, "epilogue linearity in sa")
+
+
 @pytest.mark.parametrize("m,n,k", [(32768, 6144, 2560), (32768, 2560, 4096)])
 def test_gemm_config3_long_context_sampled_rows(gpu, m, n, k):
     """Config 3 (T = 32768 packed prefill): QKV 2560 -> 6144 and O 4096 -> 2560, checked exactly on a

@@ -1,0 +1,106 @@
+"""The synthetic W8A8 decoder stack (mica_amd.model) checked stage by stage against the oracle.
+
+Attention is a torch op outside the W8A8 path; every other stage of every layer is recomputed by the
+oracle from the kernel's own input to that stage: fused norm + quant (int8 / scales bit-exact given
+the kernel's normed row is within one bf16 ulp), QKV / O / down GEMMs with their residual epilogues
+(bit-exact), the fused gate+up SiLU epilogue (one bf16 ulp), the requantizations (bit-exact), and the
+last-position readout (logits 1e-4 relative, option probabilities 1e-3 absolute).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mica_amd import int8_kernels
+from mica_amd.model import StackConfig, W8A8Stack
+from oracle import w8a8 as O
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t):
+    return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def within_one_ulp(got, ref, min_exact=0.999):
+    g, r = O.bf16_to_f32(got), O.bf16_to_f32(ref)
+    assert np.all(np.abs(g - r) <= O.bf16_ulp(ref) * 1.0001)
+    assert np.mean(got == ref) >= min_exact
+
+
+@pytest.fixture(autouse=True)
+def _strict(monkeypatch):
+    monkeypatch.setattr(int8_kernels, "STRICT", True)
+
+
+def test_small_stack_stage_by_stage(gpu):
+    print("[case] small stack", file=sys.stderr, flush=True)
+    cfg = StackConfig(layers=2, hidden=512, intermediate=1024, heads=8, kv_heads=2, head_dim=64, vocab=4096,
+                      n_options=31)
+    st = W8A8Stack(cfg, device=gpu, seed=3)
+    B, S = 2, 96
+    ids = torch.randint(0, cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(5)).to(gpu)
+    trace = []
+    logits, probs = st.prefill(ids, B, kinds=["noul", "choice"], n_choices=[2, 17], trace=trace)
+    torch.cuda.synchronize()
+    for li, (L, t) in enumerate(zip(st.layers, trace[:-1])):
+        hb = bits(t["h"])
+        g1 = O.bf16_to_f32(bits(L.input_norm))
+        yo, _ = O.rms_norm(hb, g1, cfg.eps, 0.0)
+        qo, so = O.quant_act(O.bf16_to_f32(yo))
+        q, s = t["q"].cpu().numpy(), t["s"].cpu().numpy()
+        same = np.all(q == qo, axis=1) & (s == so)
+        assert same.mean() > 0.97, f"layer {li}: norm+quant rows differing: {(~same).sum()}"
+        # QKV GEMM from the kernel's q, s
+        qkv = O.epilogue(O.int_gemm(q, L.qkv.qweight.cpu().numpy()), s, L.qkv.wscale.cpu().numpy())
+        assert np.array_equal(bits(t["qkv"]), qkv), f"layer {li}: qkv"
+        # O projection + residual from the kernel's attention output
+        qa, sa = O.quant_act(O.bf16_to_f32(bits(t["a"])))
+        assert np.array_equal(t["qa"].cpu().numpy(), qa) and np.array_equal(t["sa"].cpu().numpy(), sa)
+        h1 = O.epilogue(O.int_gemm(qa, L.o.qweight.cpu().numpy()), sa, L.o.wscale.cpu().numpy())
+        h1 = O.f32_to_bf16(O.bf16_to_f32(h1) + O.bf16_to_f32(hb))
+        assert np.array_equal(bits(t["h1"]), h1), f"layer {li}: o_proj + residual"
+        # post-attention norm + quant
+        g2 = O.bf16_to_f32(bits(L.post_norm))
+        y2, _ = O.rms_norm(h1, g2, cfg.eps, 0.0)
+        q2o, s2o = O.quant_act(O.bf16_to_f32(y2))
+        q2, s2 = t["q2"].cpu().numpy(), t["s2"].cpu().numpy()
+        assert (np.all(q2 == q2o, axis=1) & (s2 == s2o)).mean() > 0.97
+        # fused gate+up SiLU from the kernel's q2, s2 (packed weight: 64-row gate / up groups)
+        qp, sp = L.gate_up.qweight.cpu().numpy(), L.gate_up.wscale.cpu().numpy()
+        n = qp.shape[0] // 2
+        grp = qp.reshape(n // 64, 2, 64, -1)
+        sgr = sp.reshape(n // 64, 2, 64)
+        qg, qu = grp[:, 0].reshape(n, -1), grp[:, 1].reshape(n, -1)
+        sg, su = sgr[:, 0].reshape(n), sgr[:, 1].reshape(n)
+        gv = O.epilogue(O.int_gemm(q2, qg), s2, sg)
+        uv = O.epilogue(O.int_gemm(q2, qu), s2, su)
+        within_one_ulp(bits(t["g"]), O.silu_mul(gv, uv))
+        # requant of h and the down projection + residual
+        qho, sho = O.quant_act(O.bf16_to_f32(bits(t["g"])))
+        assert np.array_equal(t["qh"].cpu().numpy(), qho) and np.array_equal(t["sh"].cpu().numpy(), sho)
+        h2 = O.epilogue(O.int_gemm(qho, L.down.qweight.cpu().numpy()), sho, L.down.wscale.cpu().numpy())
+        h2 = O.f32_to_bf16(O.bf16_to_f32(h2) + O.bf16_to_f32(bits(t["h1"])))
+        assert np.array_equal(bits(t["h2"]), h2), f"layer {li}: down + residual"
+    fin = trace[-1]
+    rows = fin["rows"].cpu().numpy()
+    W = st.readout.weight.cpu().numpy()
+    zo = O.readout(bits(fin["h_final"]), rows, O.bf16_to_f32(bits(st.final_norm)), cfg.eps, W, offset=0.0)
+    np.testing.assert_allclose(logits.cpu().numpy(), zo, rtol=1e-4, atol=1e-4)
+    p = probs.cpu().numpy()
+    np.testing.assert_allclose(p[0, :2], O.option_probs(zo[0], "noul"), atol=1e-3)
+    np.testing.assert_allclose(p[1, :17], O.option_probs(zo[1], "choice", 17), atol=1e-3)
+    assert not int8_kernels.STATS["fallback"]
+
+
+def test_full_shape_stack_runs_one_layer(gpu):
+    """The 4B shape itself (hidden 2560, intermediate 9728, QKV 6144, vocab 151936) with one layer
+    and 2 x 2048 packed tokens: finite option probabilities that sum to one."""
+    print("[case] 4B-shaped stack, 1 layer", file=sys.stderr, flush=True)
+    st = W8A8Stack(StackConfig(layers=1), device=gpu, seed=1)
+    ids = torch.randint(0, st.cfg.vocab, (2 * 2048,), device=gpu)
+    logits, probs = st.prefill(ids, 2)
+    p = probs.cpu().numpy()
+    assert np.isfinite(p).all() and np.allclose(p.sum(1), 1.0, atol=1e-5)
+    assert st.linear_ops_per_token() == 2 * (6144 * 2560 + 2560 * 4096 + 3 * 9728 * 2560)
