@@ -70,15 +70,18 @@ class Timer:
         return s.elapsed_time(e) / steps  # ms per launch
 
 
-def gemm_launcher(torch, lib, qx, sx, qw, sw, out, residual=None, epilogue=0):
+def gemm_launcher(torch, lib, qx, sx, qw, sw, out, residual=None, epilogue=0, split=False):
     """A zero-allocation closure over the C ABI (what the drop-in mm_i8 calls, minus torch.empty)."""
+    from mica_amd import int8_kernels
+
     M, K = qx.shape
     N = qw.shape[0]
     n_out = out.shape[1]
     stream = torch.cuda.current_stream().cuda_stream
+    ws, ws_bytes = int8_kernels.gemm_workspace(qx.device) if split else (None, 0)
     args = (qx.data_ptr(), K, qw.data_ptr(), K, sx.data_ptr(), sw.data_ptr(), None,
             None if residual is None else residual.data_ptr(), n_out, out.data_ptr(), n_out, 0, M, N, K, epilogue,
-            stream)
+            ws, ws_bytes, stream)
     fn = lib.mica_mm_i8
 
     def launch():

@@ -104,10 +104,21 @@ int mica_rmsnorm_quant(const void *x, int x_dtype, int ldx, const void *residual
  * out_dtype MICA_INT32 stores the raw accumulators acc[m, n] (SCALE only; scales, bias and
  * residual are ignored) -- the int32 matmul of int8_quant.torch_int_mm (int8_quant.py:92-96).
  * Requires K % 16 == 0, lda/ldb % 16 == 0, N % 128 == 0 for SILU_MUL.
+ *
+ * workspace: NULL, or workspace_bytes >= mica_mm_i8_workspace_bytes(device) bytes of device memory,
+ * 16-byte aligned, whose first 4 KiB are zero before its first use (every launch leaves them zero
+ * again).  With it, a tile count that would leave the last round of 256 x 256 tiles partly idle
+ * has its remainder tiles split along K over all CUs; partial int32 sums go through the workspace
+ * and are added exactly, so the result is bit-identical to the unsplit schedule.  Launches that
+ * share a workspace must be ordered (one stream); concurrent launches need one workspace each.
+ * The workspace has no counterpart in the reference (its Triton GEMM has no split schedule).
  */
 int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
                const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M, int N, int K,
-               int epilogue, mica_stream_t stream);
+               int epilogue, void *workspace, long long workspace_bytes, mica_stream_t stream);
+
+/* bytes of GEMM workspace for `device` (its CU count x 512 KiB + 4 KiB), or -(hipError_t) */
+long long mica_mm_i8_workspace_bytes(int device);
 
 /*
  * Elementwise SwiGLU y = bf16(bf16(silu(f32(g))) * f32(u)) over n elements of bf16.

@@ -1,30 +1,40 @@
 // W8A8 GEMM on the gfx950 matrix cores: C = epilogue(A[M, K] . B[N, K]^T), int8 x int8 -> int32.
 //
-// Tiling (one workgroup = 4 wavefronts = 256 threads, one workgroup per CU):
-//   * workgroup tile 256 (M) x 256 (N); the 4 waves form a 2 x 2 grid, each owns 128 x 128 =
-//     4 x 4 tiles of v_mfma_i32_32x32x32_i8 (256 int32 accumulators per lane, in AGPRs).  The
-//     weight rows are the MFMA's A operand and the activation rows its B operand, so a lane ends
-//     up with 4 consecutive output columns of one row: the epilogue stores 8-byte vectors.
-//   * K is staged 64 bytes at a time through a ring of 4 LDS stages (4 x 32 KiB).  Stages are
-//     filled by buffer_load ... lds (global -> LDS without VGPRs), 3 slabs ahead of the MFMAs.
-//     The buffer resources carry the operand sizes, so rows past M / N and chunks past K read
-//     as zeros.
-//   * each wave double-buffers its MFMA operands in registers: the ds_reads of slab k + 1 are
-//     issued after the first half of slab k's MFMAs and land under its second half.  One
-//     barrier per slab, placed between the halves; explicit vmcnt / lgkmcnt waits order the DMA.
+// Tiling (one workgroup = 8 wavefronts = 512 threads, one workgroup per CU):
+//   * workgroup tile 256 (M) x 256 (N); the 8 waves form a 4 (M) x 2 (N) grid, each owns 64 x 128 =
+//     2 x 4 tiles of v_mfma_i32_32x32x32_i8 (128 int32 accumulators per lane).  The weight rows
+//     are the MFMA's A operand and the activation rows its B operand, so a lane ends up with 4
+//     consecutive output columns of one row.
+//   * K is staged 64 bytes at a time through a ring of 4 LDS stages (4 x 32 KiB), filled by
+//     buffer_load ... lds (global -> LDS without VGPRs), 3 slabs ahead of the MFMAs.  The buffer
+//     resources carry the operand sizes, so rows past M / N and chunks past K read as zeros.
+//   * software pipeline, one barrier per slab: every wave issues the operand reads of slab k + 1
+//     and the DMA of slab k + 4 between the MFMAs of slab k; explicit vmcnt / lgkmcnt waits order
+//     the DMA, because the compiler does not track LDS DMA across loop iterations.
 //   * LDS rows are 64 bytes = 4 chunks of 16; chunk c of tile row r lives at chunk
 //     c ^ ((r >> 2) & 3), which makes the MFMA operand reads (32 consecutive rows, one chunk,
 //     16 bytes per lane) free of LDS bank conflicts; the DMA writes 1 KiB contiguous blocks.
 //
+// Schedule.  Tiles are numbered in an XCD-aware grouped order (tile_of).  The first dp_tiles run
+// whole, one per workgroup per round.  When the tile count leaves a partial last round, the
+// remaining sk_tiles are split along K over every workgroup of a persistent grid (stream-K):
+// workgroup g takes the contiguous range [g W / G, (g + 1) W / G) of the W = sk_tiles * nk
+// (tile, slab) iterations.  A workgroup that ends with part of a tile stores its int32 partial
+// accumulators to the workspace, publishes them (device-scope release) and counts itself in the
+// tile's arrival counter; the last of the tile's contributors to arrive adds the others' partials
+// to its own (integer addition: exact in any order) and runs the epilogue, then re-zeroes the
+// counter for the next launch.  Nobody waits for anybody, so the schedule cannot deadlock.
+//
 // Workgroup order: the hardware hands workgroup i to XCD i % 8, and each XCD has its own L2.
-// Workgroups are renumbered so each XCD gets one contiguous range of tiles, and inside a range
-// tiles go in groups of kGroupM M-tiles, column by column, so the workgroups that run together
-// on an XCD share A and B panels in that XCD's L2.
+// Tiles are renumbered so each XCD gets one contiguous range of tiles, and inside a range tiles go
+// in groups of kGroupM M-tiles, column by column, so the workgroups that run together on an XCD
+// share A and B panels in that XCD's L2.
 //
 // Epilogue (per accumulator): y = (f32(acc) * sa[m]) * sb[n] (+ bias[n]) in this order
 // (kernel_src/kernels.py:65-67, int8_runtime.py:186-190), converted with round-to-nearest-even
 // (fp32 -> bf16 via v_cvt_pk_bf16_f32).  SILU_MUL pairs gate and up columns held by the same
-// lane (see mica_amd.h).  The residual is added after that rounding.
+// lane (see mica_amd.h).  The residual is added after that rounding.  16-bit outputs are staged
+// through LDS so every lane stores 16 contiguous bytes of a row.
 
 #include "common.h"
 
@@ -57,7 +67,11 @@ struct Cfg {
     static constexpr int kSmemMain = (NST * kStage > kWaves * kEpiWave) ? NST * kStage : kWaves * kEpiWave;
     // the tile's row scales, column scales and bias (fp32), staged at kernel start
     static constexpr int kScaleOff = kSmemMain;
-    static constexpr int kSmem = kSmemMain + 3 * 256 * 4;
+    // the arrival count read back by a split tile's contributors
+    static constexpr int kFlagOff = kScaleOff + 3 * 256 * 4;
+    static constexpr int kSmem = kFlagOff + 16;
+    // int32x4 vectors of one lane's accumulators (a split tile's partial sums)
+    static constexpr int kPartialVecs = NB * MB * 4;
     static_assert(WN == 128, "the SiLU epilogue needs one 128-row gate/up group per wave");
 };
 using CfgDefault = Cfg<4, 2>;
@@ -83,6 +97,11 @@ struct GemmParams {
     int M, N, K;
     int tiles_m, tiles_n;
     int vec_ok; // ldc, ldr, N all multiples of 4: 4-column vector stores
+    // schedule: tiles [0, dp_tiles) of the grouped order run whole, one per workgroup per round;
+    // tiles [dp_tiles, dp_tiles + sk_tiles) are split along K over all gridDim.x workgroups
+    int dp_tiles, sk_tiles;
+    v4i *partials; // [gridDim.x][2][kPartialVecs][kThreads]: a workgroup's partial accumulators
+    int *arrivals; // [sk_tiles]: contributors arrived so far; zero between launches
 };
 
 // LDS placement of 16-byte chunk c of tile row r: chunk c ^ swz(r).  With 64-byte rows, the MFMA
@@ -179,6 +198,12 @@ MICA_DEVICE void load4_res(const void *R, long off, float (&v)[4], int valid, bo
     for (int t = 0; t < 4; ++t) v[t] = OUT == MICA_BF16 ? bf16_to_f32(h[t]) : f16_to_f32(h[t]);
 }
 
+// Stream-K partition of W (tile, slab) iterations over G workgroups: workgroup g owns
+// [sk_begin(g), sk_begin(g + 1)).  With W >= G every range is non-empty.
+MICA_DEVICE long long sk_begin(int g, long long W, int G) { return (long long)g * W / G; }
+// the workgroup whose range holds iteration i (the largest g with sk_begin(g) <= i)
+MICA_DEVICE int sk_owner(long long i, long long W, int G) { return (int)(((i + 1) * G + W - 1) / W) - 1; }
+
 template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES, class C = CfgDefault>
 __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
     constexpr int WM = C::WM, WN = C::WN, MB = C::MB, NB = C::NB;
@@ -190,30 +215,26 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave / (BN / WN), wn = wave % (BN / WN);
-
-    int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.M, N = p.N, K = p.K;
+    const int nk = (K + BK - 1) / BK;
 
     // ---- DMA of one slab: this wave moves kBlocksPerWave 1 KiB blocks of the A and of the B tile ----
     // lane i of a block writes LDS bytes [16 i, 16 i + 16): tile row blk * 16 + i / 4, physical chunk
     // i % 4, so it fetches logical chunk (i % 4) ^ swz(row) of that row.
     const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, M * p.lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, N * p.ldb, kBufferFlags);
-    int a_row[kBlocksPerWave], b_row[kBlocksPerWave], kcol[kBlocksPerWave];
+    int a_row[kBlocksPerWave], b_row[kBlocksPerWave], kcol[kBlocksPerWave], trow[kBlocksPerWave];
 #pragma unroll
     for (int j = 0; j < kBlocksPerWave; ++j) {
-        const int r = (wave * kBlocksPerWave + j) * 16 + (lane >> 2);
-        kcol[j] = ((lane & 3) ^ swz(r)) << 4;
-        a_row[j] = m0 + r < M ? (m0 + r) * p.lda + kcol[j] : kOutOfRange;
-        b_row[j] = n0 + r < N ? (n0 + r) * p.ldb + kcol[j] : kOutOfRange;
+        trow[j] = (wave * kBlocksPerWave + j) * 16 + (lane >> 2);
+        kcol[j] = ((lane & 3) ^ swz(trow[j])) << 4;
     }
+    int kend = 0; // slabs at or past kend are not fetched (the DMA writes zeros instead)
     // one DMA instruction: block j (0 .. kBlocksPerWave-1) of operand op (0: A, 1: B) of a slab
     auto dma1 = [&](int slab, int j, int op) {
         const int k0 = slab * BK;
         int8_t *st = smem + (slab % NST) * kStage;
-        const bool kin = k0 + kcol[j] < K;
+        const bool kin = slab < kend && k0 + kcol[j] < K;
         const int row = op == 0 ? a_row[j] : b_row[j];
         const int off = (kin && row != kOutOfRange) ? row + k0 : kOutOfRange;
         const int blk = wave * kBlocksPerWave + j;
@@ -249,10 +270,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         }
 
     v16i acc[NB][MB]; // [n tile][m tile]
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int i = 0; i < MB; ++i) acc[j][i] = v16i{};
 
     struct Ops {
         v4i x[KS][MB];
@@ -276,275 +293,376 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
                 acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w[ks][j], o.x[ks][i], acc[j][i], 0, 0, 0);
     };
 
-    // ---- main loop.  Every wave runs the same software pipeline, one barrier per 64-byte slab k:
+    // ---- slabs [k0, k1) of tile (m0, n0) into acc.  Every wave runs the same software pipeline,
+    // one barrier per 64-byte slab k:
     //   wait: this wave's DMA of slab k + 1 landed, its reads of slab k (registers X) completed
     //   barrier: slab k + 1 is visible in LDS, and nobody reads slab k's stage any more
     //   then, interleaved instruction by instruction: the 16 MFMAs of slab k (from X), the 12
     //   operand reads of slab k + 1 (into Y) and the 4 DMA instructions of slab k + 4 (into the
     //   stage slab k just left).
     // All 8 waves keep the LDS busy together (operand reads and DMA writes share it) while the
-    // two waves of each SIMD keep its matrix core busy.  A DMA past the last slab is still issued
-    // (its offsets fail the range check and it writes zeros into a stage nobody reads), so every
-    // wave always has exactly 3 younger slabs in flight when it waits for slab k + 1.
-    const int nk = (K + BK - 1) / BK;
-    // the epilogue's per-row / per-column factors: loaded before the prologue DMA and written to
-    // LDS after it, so their latency hides under the DMA's.  Threads 0-255: sa and bias of tile
-    // row / column tid, threads 256-511: sb of column tid - 256.
+    // two waves of each SIMD keep its matrix core busy.  A DMA past slab k1 is still issued (it
+    // fails the range check and writes zeros into a stage nobody reads), so every wave always has
+    // exactly 3 younger slabs in flight when it waits for slab k + 1.
+    // The tile's per-row / per-column epilogue factors are loaded before the prologue DMA and
+    // written to LDS after it, so their latency hides under the DMA's.  Threads 0-255: sa and bias
+    // of tile row / column tid, threads 256-511: sb of column tid - 256.
     static_assert(C::kThreads == 512, "one scale load per thread");
-    float f1, f2 = 0.0f;
-    {
-        // branch-free: the index is clamped into range (values of rows / columns past the edge
-        // are never used), so no load waits for another
-        const int i = tid & 255;
-        const bool row = tid < 256;
-        const float *src = row ? p.sa : p.sb;
-        const int base = row ? m0 : n0;
-        const int lim = (row ? M : N) - base;
-        f1 = src[base + (i < lim ? i : lim - 1)];
-        if (HAS_BIAS) f2 = p.bias[n0 + (i < N - n0 ? i : N - n0 - 1)];
-    }
+    auto run = [&](int m0, int n0, int k0, int k1) {
 #pragma unroll
-    for (int sl = 0; sl < NST; ++sl) dma(sl);
-    {
-        float *sc = (float *)(smem + C::kScaleOff);
-        sc[tid] = f1;                       // [0, 256): sa, [256, 512): sb
-        if (tid < 256) sc[512 + tid] = f2;  // [512, 768): bias
-    }
-    wait_vmcnt<(NST - 1) * kDmaPerSlab>(); // slab 0 landed in this wave's blocks ...
-    __builtin_amdgcn_s_barrier();          // ... and in every wave's
-    Ops X, Y;
-    lds_read(X, 0);
-
-    auto step = [&](Ops &cur, Ops &nxt, int k) {
-        wait_vmcnt<(NST - 2) * kDmaPerSlab>(); // slab k + 1 landed (slabs k + 2, k + 3 may be in flight)
-        wait_lgkmcnt0();                       // slab k's operands are in registers
+        for (int j = 0; j < kBlocksPerWave; ++j) {
+            a_row[j] = m0 + trow[j] < M ? (m0 + trow[j]) * p.lda + kcol[j] : kOutOfRange;
+            b_row[j] = n0 + trow[j] < N ? (n0 + trow[j]) * p.ldb + kcol[j] : kOutOfRange;
+        }
+        kend = k1;
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < MB; ++i) acc[j][i] = v16i{};
+        float f1, f2 = 0.0f;
+        {
+            // branch-free: the index is clamped into range (values of rows / columns past the edge
+            // are never used), so no load waits for another
+            const int i = tid & 255;
+            const bool row = tid < 256;
+            const float *src = row ? p.sa : p.sb;
+            const int base = row ? m0 : n0;
+            const int lim = (row ? M : N) - base;
+            f1 = src[base + (i < lim ? i : lim - 1)];
+            if (HAS_BIAS) f2 = p.bias[n0 + (i < N - n0 ? i : N - n0 - 1)];
+        }
+        // the previous tile's epilogue (LDS staging, scale reads) is finished in every wave
+        wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
-        const int8_t *st = smem + ((k + 1) % NST) * kStage;
-        const int dslab = k + NST;
-        // 4 reads up front, then 4 x [MFMA, read, MFMA, read, MFMA, DMA, MFMA]
-        nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
-        nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
-        nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
-        nxt.x[0][1] = *(const v4i *)(st + x_rd[1][0]);
-        nxt.w[0][2] = *(const v4i *)(st + w_rd[2][0]);
-        nxt.w[0][3] = *(const v4i *)(st + w_rd[3][0]);
-        nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
-        nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
-        nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
-        nxt.x[1][1] = *(const v4i *)(st + x_rd[1][1]);
-        nxt.w[1][2] = *(const v4i *)(st + w_rd[2][1]);
-        nxt.w[1][3] = *(const v4i *)(st + w_rd[3][1]);
-        dma1(dslab, 0, 0);
-        dma1(dslab, 0, 1);
-        dma1(dslab, 1, 0);
-        dma1(dslab, 1, 1);
-        mfma_half(cur, 0);
-        mfma_half(cur, 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        for (int sl = 0; sl < NST; ++sl) dma(k0 + sl);
+        {
+            float *sc = (float *)(smem + C::kScaleOff);
+            sc[tid] = f1;                       // [0, 256): sa, [256, 512): sb
+            if (tid < 256) sc[512 + tid] = f2;  // [512, 768): bias
+        }
+        wait_vmcnt<(NST - 1) * kDmaPerSlab>(); // slab k0 landed in this wave's blocks ...
+        __builtin_amdgcn_s_barrier();          // ... and in every wave's
+        Ops X, Y;
+        lds_read(X, k0);
+
+        auto step = [&](Ops &cur, Ops &nxt, int k) {
+            wait_vmcnt<(NST - 2) * kDmaPerSlab>(); // slab k + 1 landed (slabs k + 2, k + 3 may be in flight)
+            wait_lgkmcnt0();                       // slab k's operands are in registers
+            __builtin_amdgcn_s_barrier();
+            const int8_t *st = smem + ((k + 1) % NST) * kStage;
+            const int dslab = k + NST;
+            // 4 reads up front, then 4 x [MFMA, read, MFMA, read, MFMA, DMA, MFMA]
+            nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
+            nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
+            nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
+            nxt.x[0][1] = *(const v4i *)(st + x_rd[1][0]);
+            nxt.w[0][2] = *(const v4i *)(st + w_rd[2][0]);
+            nxt.w[0][3] = *(const v4i *)(st + w_rd[3][0]);
+            nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
+            nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
+            nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
+            nxt.x[1][1] = *(const v4i *)(st + x_rd[1][1]);
+            nxt.w[1][2] = *(const v4i *)(st + w_rd[2][1]);
+            nxt.w[1][3] = *(const v4i *)(st + w_rd[3][1]);
+            dma1(dslab, 0, 0);
+            dma1(dslab, 0, 1);
+            dma1(dslab, 1, 0);
+            dma1(dslab, 1, 1);
+            mfma_half(cur, 0);
+            mfma_half(cur, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+        };
+        int k = k0;
+        for (; k + 1 < k1; k += 2) {
+            step(X, Y, k);
+            step(Y, X, k + 1);
+        }
+        if (k < k1) step(X, Y, k);
+        wait_vmcnt<0>();
+    };
+
+    // ---- epilogue of tile (m0, n0) from acc.  acc[j][i][r]: n = 8 (r / 4) + 4 (lane / 32) + r % 4
+    //      (4 consecutive per r / 4), m = lane % 32 within the 32 x 32 tile (j, i) ----
+    auto epilogue = [&](int m0, int n0) {
+        const int mw = m0 + wm * WM;
+        const int nw = n0 + wn * WN;
+        const bool vec = p.vec_ok != 0;
+        const float *sc = (const float *)(smem + C::kScaleOff); // [0, 256): sa, [256, 512): sb, [512, 768): bias
+        float sav[MB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) sav[i] = sc[wm * WM + i * 32 + r32];
+        if constexpr (OUT == MICA_BF16 || OUT == MICA_FP16) {
+            // Staged through LDS: every wave writes its rounded 16-bit block (8 bytes per lane per
+            // store) into its own padded region, then streams it out row-contiguously, 16 bytes per
+            // lane, so each global store covers whole 256-byte row segments.
+            wait_lgkmcnt0();
+            __builtin_amdgcn_s_barrier(); // every wave is done reading the operand stages
+            int8_t *ep = smem + wave * kEpiWave;
+            constexpr int kCols = EPI == MICA_EPI_SCALE ? WN : WN / 2; // output columns of this wave
+            const int col0 = EPI == MICA_EPI_SCALE ? nw : (nw >> 7) * 64;
+            const int ncols_out = EPI == MICA_EPI_SCALE ? N : (N >> 1);
+#pragma unroll
+            for (int j = 0; j < (EPI == MICA_EPI_SCALE ? NB : 2); ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int nl = j * 32 + 8 * q + 4 * khalf; // local output column of this lane's 4 values
+                    float s1[4], s2[4], bv[4];
+                    const int cb = wn * WN + nl; // tile-local column of this lane's 4 values
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        s1[t] = sc[256 + cb + t]; // SCALE: sb[n]; SILU_MUL: the gate rows' sb
+                        s2[t] = EPI == MICA_EPI_SCALE ? 0.0f : sc[256 + cb + 64 + t]; // the matching up rows
+                        bv[t] = HAS_BIAS ? sc[512 + cb + t] : 0.0f;
+                    }
+#pragma unroll
+                    for (int i = 0; i < MB; ++i) {
+                        float y[4];
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            if (EPI == MICA_EPI_SCALE) {
+                                y[t] = ((float)acc[j][i][4 * q + t] * sav[i]) * s1[t];
+                                if (HAS_BIAS) y[t] = y[t] + bv[t];
+                            } else {
+                                const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * s1[t]);
+                                const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * s2[t]);
+                                const float act = round_bf16(gv / (1.0f + expf(-gv)));
+                                y[t] = act * uv;
+                            }
+                        }
+                        u32x2 w;
+                        if (OUT == MICA_BF16) {
+                            w[0] = pack_bf16x2(y[0], y[1]);
+                            w[1] = pack_bf16x2(y[2], y[3]);
+                        } else {
+                            w[0] = (uint32_t)f32_to_f16(y[0]) | ((uint32_t)f32_to_f16(y[1]) << 16);
+                            w[1] = (uint32_t)f32_to_f16(y[2]) | ((uint32_t)f32_to_f16(y[3]) << 16);
+                        }
+                        *(u32x2 *)(ep + (i * 32 + r32) * kEpiPitch + nl * 2) = w;
+                    }
+                }
+            }
+            wait_lgkmcnt0(); // a wave reads back only its own region: no barrier needed
+            constexpr int kLanesPerRow = kCols / 8;          // 16 (SCALE) or 8 (SILU_MUL) lanes x 8 columns
+            constexpr int kRowsPerPass = 64 / kLanesPerRow;  // 4 or 8 rows per pass
+            const int cl = (lane % kLanesPerRow) * 8;        // local column of this lane's 8 values
+            const int valid = ncols_out - (col0 + cl) < 8 ? (ncols_out - (col0 + cl) > 0 ? ncols_out - (col0 + cl) : 0) : 8;
+            const bool vec8 = vec && (p.ldc % 8 == 0) && (!HAS_RES || p.ldr % 8 == 0);
+#pragma unroll 4
+            for (int r0 = 0; r0 < WM; r0 += kRowsPerPass) {
+                const int rl = r0 + lane / kLanesPerRow;
+                const int m = mw + rl;
+                const u32x4 v = *(const u32x4 *)(ep + rl * kEpiPitch + cl * 2);
+                if (m >= M || valid == 0) continue;
+                u32x4 o = v;
+                if (HAS_RES) {
+                    const uint16_t *rp = (const uint16_t *)p.res + (long)m * p.ldr + col0 + cl;
+                    u32x4 rv = {0u, 0u, 0u, 0u};
+                    if (vec8 && valid == 8) rv = *(const u32x4 *)rp;
+                    else for (int t = 0; t < valid; ++t) rv[t >> 1] |= (uint32_t)rp[t] << (16 * (t & 1));
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        float a0, a1, b0, b1;
+                        if (OUT == MICA_BF16) {
+                            a0 = bf16_lo(v[t]); a1 = bf16_hi(v[t]); b0 = bf16_lo(rv[t]); b1 = bf16_hi(rv[t]);
+                            o[t] = pack_bf16x2(a0 + b0, a1 + b1);
+                        } else {
+                            a0 = f16_to_f32(v[t] & 0xffff); a1 = f16_to_f32(v[t] >> 16);
+                            b0 = f16_to_f32(rv[t] & 0xffff); b1 = f16_to_f32(rv[t] >> 16);
+                            o[t] = (uint32_t)f32_to_f16(a0 + b0) | ((uint32_t)f32_to_f16(a1 + b1) << 16);
+                        }
+                    }
+                }
+                uint16_t *cp = (uint16_t *)p.C + (long)m * p.ldc + col0 + cl;
+                if (vec8 && valid == 8) {
+                    *(u32x4 *)cp = o;
+                } else {
+                    for (int t = 0; t < valid; ++t) cp[t] = (uint16_t)(o[t >> 1] >> (16 * (t & 1)));
+                }
+            }
+            return;
+        }
+        // 32-bit outputs (fp32 / raw int32): direct 16-byte stores from the accumulator layout
+        if (EPI == MICA_EPI_SCALE) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int nb = nw + j * 32 + 8 * q + 4 * khalf;
+                    const int valid = N - nb < 4 ? (N - nb > 0 ? N - nb : 0) : 4;
+                    if (valid == 0) continue;
+                    float sbv[4], bv[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        sbv[t] = t < valid ? p.sb[nb + t] : 0.0f;
+                        bv[t] = (HAS_BIAS && t < valid) ? p.bias[nb + t] : 0.0f;
+                    }
+#pragma unroll
+                    for (int i = 0; i < MB; ++i) {
+                        const int m = mw + i * 32 + r32;
+                        if (m >= M) continue;
+                        const long off = (long)m * p.ldc + nb;
+                        if (OUT == MICA_INT32) {
+                            int *c = (int *)p.C + off;
+                            if (vec && valid == 4) {
+                                *(v4i *)c = v4i{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
+                                                acc[j][i][4 * q + 3]};
+                            } else {
+                                for (int t = 0; t < valid; ++t) c[t] = acc[j][i][4 * q + t];
+                            }
+                            continue;
+                        }
+                        float y[4];
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            y[t] = ((float)acc[j][i][4 * q + t] * sav[i]) * sbv[t];
+                            if (HAS_BIAS) y[t] = y[t] + bv[t];
+                        }
+                        if (HAS_RES) {
+                            float rv[4];
+                            load4_res<OUT>(p.res, (long)m * p.ldr + nb, rv, valid, vec);
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) y[t] = to_out_precision<OUT>(y[t]) + rv[t];
+                        }
+                        store4<OUT>(p.C, off, y, valid, vec);
+                    }
+                }
+            }
+        } else {
+            // SILU_MUL: this wave's 128 B-rows are one interleave group g = nw / 128: rows [0, 64) are
+            // gate columns 64 g + [0, 64), rows [64, 128) the matching up columns (tiles j and j + 2).
+            const int g = nw >> 7;
+            const int Nout = N >> 1;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int nr = j * 32 + 8 * q + 4 * khalf; // row within the group's gate half
+                    const int col = g * 64 + nr;
+                    if (col >= Nout) continue; // whole groups only (N % 128 == 0)
+                    float sg[4], su[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        sg[t] = p.sb[nw + nr + t];
+                        su[t] = p.sb[nw + 64 + nr + t];
+                    }
+#pragma unroll
+                    for (int i = 0; i < MB; ++i) {
+                        const int m = mw + i * 32 + r32;
+                        if (m >= M) continue;
+                        float hv[4];
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * sg[t]);
+                            const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * su[t]);
+                            const float act = round_bf16(gv / (1.0f + expf(-gv)));
+                            hv[t] = act * uv;
+                        }
+                        store4<MICA_BF16>(p.C, (long)m * p.ldc + col, hv, 4, vec);
+                    }
+                }
+            }
         }
     };
-    int k = 0;
-    for (; k + 1 < nk; k += 2) {
-        step(X, Y, k);
-        step(Y, X, k + 1);
-    }
-    if (k < nk) step(X, Y, k);
-    wait_vmcnt<0>();
 
-    // ---- epilogue.  acc[j][i][r]: n = 8 (r / 4) + 4 (lane / 32) + r % 4 (4 consecutive per r / 4),
-    //      m = lane % 32 within the 32 x 32 tile (j, i) ----
-    const int mw = m0 + wm * WM;
-    const int nw = n0 + wn * WN;
-    const bool vec = p.vec_ok != 0;
-    const float *sc = (const float *)(smem + C::kScaleOff); // [0, 256): sa, [256, 512): sb, [512, 768): bias
-    float sav[MB];
+    // ---- split tiles: publish this workgroup's partial sums of tile `rel` (a stream-K tile) and
+    // report whether it arrived last, in which case acc now holds the tile's full sums ----
+    int *flag = (int *)(smem + C::kFlagOff);
+    const long long W = (long long)p.sk_tiles * nk;
+    const int G = gridDim.x;
+    const long long my_begin = p.sk_tiles > 0 ? sk_begin(blockIdx.x, W, G) : 0;
+    const long long my_end = p.sk_tiles > 0 ? sk_begin(blockIdx.x + 1, W, G) : 0;
+    // Partial sums move with device-scope (sc1) buffer stores and loads: written through to the
+    // device's coherence point and read from it, so no cache-wide write-back or invalidation (a
+    // device-scope fence) is needed, only the ordering below.
+    constexpr int kDeviceScope = 16; // cache policy bits: sc1
+    constexpr int kSlotBytes = C::kPartialVecs * C::kThreads * 16;
+    const __amdgpu_buffer_rsrc_t rsrc_p =
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.partials, 0, p.sk_tiles > 0 ? G * 2 * kSlotBytes : 0, kBufferFlags);
+    auto slot_off = [&](int g, int seg) { return (g * 2 + seg) * kSlotBytes + tid * 16; };
+    auto fixup = [&](int rel) -> bool {
+        const long long tb = (long long)rel * nk;      // the tile's first iteration
+        const int seg = tb > my_begin ? 1 : 0;          // first (0) or last (1) range segment of this workgroup
+        const int g0 = sk_owner(tb, W, G), g1 = sk_owner(tb + nk - 1, W, G);
+        const int mine = slot_off(blockIdx.x, seg);
 #pragma unroll
-    for (int i = 0; i < MB; ++i) sav[i] = sc[wm * WM + i * 32 + r32];
-    if constexpr (OUT == MICA_BF16 || OUT == MICA_FP16) {
-        // Staged through LDS: every wave writes its rounded 16-bit block (8 bytes per lane per
-        // store) into its own padded region, then streams it out row-contiguously, 16 bytes per
-        // lane, so each global store covers whole 256-byte row segments.
-        wait_lgkmcnt0();
-        __builtin_amdgcn_s_barrier(); // every wave is done reading the operand stages
-        int8_t *ep = smem + wave * kEpiWave;
-        constexpr int kCols = EPI == MICA_EPI_SCALE ? WN : WN / 2; // output columns of this wave
-        const int col0 = EPI == MICA_EPI_SCALE ? nw : (nw >> 7) * 64;
-        const int ncols_out = EPI == MICA_EPI_SCALE ? N : (N >> 1);
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int j = 0; j < (EPI == MICA_EPI_SCALE ? NB : 2); ++j) {
+            for (int i = 0; i < MB; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int nl = j * 32 + 8 * q + 4 * khalf; // local output column of this lane's 4 values
-                float s1[4], s2[4], bv[4];
-                const int cb = wn * WN + nl; // tile-local column of this lane's 4 values
+                for (int q = 0; q < 4; ++q)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        v4i{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]},
+                        rsrc_p, mine + ((j * MB + i) * 4 + q) * C::kThreads * 16, 0, kDeviceScope);
+        wait_vmcnt<0>();  // this wave's partial sums reached the coherence point ...
+        __syncthreads();  // ... and every wave's, before the arrival is counted
+        if (tid == 0) *flag = __hip_atomic_fetch_add(p.arrivals + rel, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*flag != g1 - g0) return false; // a later contributor finishes the tile
+        for (int g = g0; g <= g1; ++g) {
+            if (g == (int)blockIdx.x) continue;
+            const int src = slot_off(g, tb > sk_begin(g, W, G) ? 1 : 0);
+            // two halves of 64 registers each: the operand registers of the main loop are free
+            // here, but not all 128 accumulators' worth on top of the accumulators themselves
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    s1[t] = sc[256 + cb + t]; // SCALE: sb[n]; SILU_MUL: the gate rows' sb
-                    s2[t] = EPI == MICA_EPI_SCALE ? 0.0f : sc[256 + cb + 64 + t]; // the matching up rows
-                    bv[t] = HAS_BIAS ? sc[512 + cb + t] : 0.0f;
-                }
+            for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int i = 0; i < MB; ++i) {
-                    float y[4];
+                for (int j = h * NB / 2; j < (h + 1) * NB / 2; ++j)
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        if (EPI == MICA_EPI_SCALE) {
-                            y[t] = ((float)acc[j][i][4 * q + t] * sav[i]) * s1[t];
-                            if (HAS_BIAS) y[t] = y[t] + bv[t];
-                        } else {
-                            const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * s1[t]);
-                            const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * s2[t]);
-                            const float act = round_bf16(gv / (1.0f + expf(-gv)));
-                            y[t] = act * uv;
+                    for (int i = 0; i < MB; ++i)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const v4i v = __builtin_amdgcn_raw_buffer_load_b128(
+                                rsrc_p, src + ((j * MB + i) * 4 + q) * C::kThreads * 16, 0, kDeviceScope);
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) acc[j][i][4 * q + t] += v[t];
                         }
-                    }
-                    u32x2 w;
-                    if (OUT == MICA_BF16) {
-                        w[0] = pack_bf16x2(y[0], y[1]);
-                        w[1] = pack_bf16x2(y[2], y[3]);
-                    } else {
-                        w[0] = (uint32_t)f32_to_f16(y[0]) | ((uint32_t)f32_to_f16(y[1]) << 16);
-                        w[1] = (uint32_t)f32_to_f16(y[2]) | ((uint32_t)f32_to_f16(y[3]) << 16);
-                    }
-                    *(u32x2 *)(ep + (i * 32 + r32) * kEpiPitch + nl * 2) = w;
-                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        wait_lgkmcnt0(); // a wave reads back only its own region: no barrier needed
-        constexpr int kLanesPerRow = kCols / 8;          // 16 (SCALE) or 8 (SILU_MUL) lanes x 8 columns
-        constexpr int kRowsPerPass = 64 / kLanesPerRow;  // 4 or 8 rows per pass
-        const int cl = (lane % kLanesPerRow) * 8;        // local column of this lane's 8 values
-        const int valid = ncols_out - (col0 + cl) < 8 ? (ncols_out - (col0 + cl) > 0 ? ncols_out - (col0 + cl) : 0) : 8;
-        const bool vec8 = vec && (p.ldc % 8 == 0) && (!HAS_RES || p.ldr % 8 == 0);
-#pragma unroll 4
-        for (int r0 = 0; r0 < WM; r0 += kRowsPerPass) {
-            const int rl = r0 + lane / kLanesPerRow;
-            const int m = mw + rl;
-            const u32x4 v = *(const u32x4 *)(ep + rl * kEpiPitch + cl * 2);
-            if (m >= M || valid == 0) continue;
-            u32x4 o = v;
-            if (HAS_RES) {
-                const uint16_t *rp = (const uint16_t *)p.res + (long)m * p.ldr + col0 + cl;
-                u32x4 rv = {0u, 0u, 0u, 0u};
-                if (vec8 && valid == 8) rv = *(const u32x4 *)rp;
-                else for (int t = 0; t < valid; ++t) rv[t >> 1] |= (uint32_t)rp[t] << (16 * (t & 1));
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float a0, a1, b0, b1;
-                    if (OUT == MICA_BF16) {
-                        a0 = bf16_lo(v[t]); a1 = bf16_hi(v[t]); b0 = bf16_lo(rv[t]); b1 = bf16_hi(rv[t]);
-                        o[t] = pack_bf16x2(a0 + b0, a1 + b1);
-                    } else {
-                        a0 = f16_to_f32(v[t] & 0xffff); a1 = f16_to_f32(v[t] >> 16);
-                        b0 = f16_to_f32(rv[t] & 0xffff); b1 = f16_to_f32(rv[t] >> 16);
-                        o[t] = (uint32_t)f32_to_f16(a0 + b0) | ((uint32_t)f32_to_f16(a1 + b1) << 16);
-                    }
-                }
-            }
-            uint16_t *cp = (uint16_t *)p.C + (long)m * p.ldc + col0 + cl;
-            if (vec8 && valid == 8) {
-                *(u32x4 *)cp = o;
-            } else {
-                for (int t = 0; t < valid; ++t) cp[t] = (uint16_t)(o[t >> 1] >> (16 * (t & 1)));
-            }
+        if (tid == 0) __hip_atomic_store(p.arrivals + rel, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    };
+
+    // ---- the workgroup's work list: whole tiles blockIdx.x, blockIdx.x + G, ... below dp_tiles,
+    // then its stream-K range of (tile, slab) iterations ----
+    int pid = blockIdx.x;
+    long long it = my_begin;
+    for (;;) {
+        int tm, tn, k0, k1, rel = -1;
+        if (pid < p.dp_tiles) {
+            tile_of(pid, p.tiles_m, p.tiles_n, tm, tn);
+            k0 = 0;
+            k1 = nk;
+            pid += G;
+        } else if (it < my_end) {
+            rel = (int)(it / nk);
+            k0 = (int)(it - (long long)rel * nk);
+            k1 = (long long)(nk - k0) < my_end - it ? nk : k0 + (int)(my_end - it);
+            tile_of(p.dp_tiles + rel, p.tiles_m, p.tiles_n, tm, tn);
+            it += k1 - k0;
+        } else {
+            break;
         }
-        return;
-    }
-    // 32-bit outputs (fp32 / raw int32): direct 16-byte stores from the accumulator layout
-    if (EPI == MICA_EPI_SCALE) {
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int nb = nw + j * 32 + 8 * q + 4 * khalf;
-                const int valid = N - nb < 4 ? (N - nb > 0 ? N - nb : 0) : 4;
-                if (valid == 0) continue;
-                float sbv[4], bv[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    sbv[t] = t < valid ? p.sb[nb + t] : 0.0f;
-                    bv[t] = (HAS_BIAS && t < valid) ? p.bias[nb + t] : 0.0f;
-                }
-#pragma unroll
-                for (int i = 0; i < MB; ++i) {
-                    const int m = mw + i * 32 + r32;
-                    if (m >= M) continue;
-                    const long off = (long)m * p.ldc + nb;
-                    if (OUT == MICA_INT32) {
-                        int *c = (int *)p.C + off;
-                        if (vec && valid == 4) {
-                            *(v4i *)c = v4i{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
-                                            acc[j][i][4 * q + 3]};
-                        } else {
-                            for (int t = 0; t < valid; ++t) c[t] = acc[j][i][4 * q + t];
-                        }
-                        continue;
-                    }
-                    float y[4];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        y[t] = ((float)acc[j][i][4 * q + t] * sav[i]) * sbv[t];
-                        if (HAS_BIAS) y[t] = y[t] + bv[t];
-                    }
-                    if (HAS_RES) {
-                        float rv[4];
-                        load4_res<OUT>(p.res, (long)m * p.ldr + nb, rv, valid, vec);
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) y[t] = to_out_precision<OUT>(y[t]) + rv[t];
-                    }
-                    store4<OUT>(p.C, off, y, valid, vec);
-                }
-            }
-        }
-    } else {
-        // SILU_MUL: this wave's 128 B-rows are one interleave group g = nw / 128: rows [0, 64) are
-        // gate columns 64 g + [0, 64), rows [64, 128) the matching up columns (tiles j and j + 2).
-        const int g = nw >> 7;
-        const int Nout = N >> 1;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int nr = j * 32 + 8 * q + 4 * khalf; // row within the group's gate half
-                const int col = g * 64 + nr;
-                if (col >= Nout) continue; // whole groups only (N % 128 == 0)
-                float sg[4], su[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    sg[t] = p.sb[nw + nr + t];
-                    su[t] = p.sb[nw + 64 + nr + t];
-                }
-#pragma unroll
-                for (int i = 0; i < MB; ++i) {
-                    const int m = mw + i * 32 + r32;
-                    if (m >= M) continue;
-                    float hv[4];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * sg[t]);
-                        const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * su[t]);
-                        const float act = round_bf16(gv / (1.0f + expf(-gv)));
-                        hv[t] = act * uv;
-                    }
-                    store4<MICA_BF16>(p.C, (long)m * p.ldc + col, hv, 4, vec);
-                }
-            }
-        }
+        run(tm * BM, tn * BN, k0, k1);
+        if ((k0 != 0 || k1 != nk) && !fixup(rel)) continue;
+        epilogue(tm * BM, tn * BN);
     }
 }
 
 template <int EPI, int OUT>
-int launch_out(const GemmParams &p, bool has_bias, bool has_res, hipStream_t st) {
-    dim3 grid(p.tiles_m * p.tiles_n), block(CfgDefault::kThreads);
+int launch_out(const GemmParams &p, int grid_size, bool has_bias, bool has_res, hipStream_t st) {
+    dim3 grid(grid_size), block(CfgDefault::kThreads);
 #define MICA_G(B_, R_) hipLaunchKernelGGL((gemm_i8_kernel<EPI, OUT, B_, R_>), grid, block, 0, st, p)
     if (EPI == MICA_EPI_SILU_MUL) MICA_G(false, false);
     else if (has_bias && has_res) MICA_G(true, true);
@@ -555,11 +673,34 @@ int launch_out(const GemmParams &p, bool has_bias, bool has_res, hipStream_t st)
     return mica_err(hipGetLastError());
 }
 
+// Workspace of the split-tile schedule on a device with `cus` compute units: the arrival counters
+// (one per split tile, at most cus of them), padded to 4 KiB, then two partial-sum slots of
+// kPartialVecs x kThreads int32x4 per workgroup.
+constexpr long long kCounterBytes = 4096;
+constexpr long long kSlotBytes = (long long)CfgDefault::kPartialVecs * CfgDefault::kThreads * 16;
+long long workspace_bytes_for(int cus) { return kCounterBytes + (long long)cus * 2 * kSlotBytes; }
+
+int cu_count(int device) {
+    static int cached[64];
+    if (device >= 0 && device < 64 && cached[device] > 0) return cached[device];
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || v <= 0) return 0;
+    if (device >= 0 && device < 64) cached[device] = v;
+    return v;
+}
+
 }  // namespace
+
+extern "C" long long mica_mm_i8_workspace_bytes(int device) {
+    const int cus = cu_count(device);
+    if (cus <= 0 || cus > 1024) return -(long long)hipErrorInvalidDevice;
+    return workspace_bytes_for(cus);
+}
 
 extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
                           const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M,
-                          int N, int K, int epilogue, mica_stream_t stream) {
+                          int N, int K, int epilogue, void *workspace, long long workspace_bytes,
+                          mica_stream_t stream) {
     if (A == nullptr || B == nullptr || sa == nullptr || sb == nullptr || C == nullptr) return MICA_MISS_ARG;
     if (epilogue != MICA_EPI_SCALE && epilogue != MICA_EPI_SILU_MUL) return MICA_MISS_ARG;
     if (out_dtype != MICA_BF16 && out_dtype != MICA_FP16 && out_dtype != MICA_FP32 && out_dtype != MICA_INT32)
@@ -577,8 +718,10 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
         (long long)M * ldc >= (1ll << 31) || (residual && (long long)M * ldr >= (1ll << 31)))
         return MICA_MISS_RANGE;
     if (!mica_aligned16(A) || !mica_aligned16(B) || !mica_aligned16(sa) || !mica_aligned16(sb) ||
-        !mica_aligned16(C) || (bias && !mica_aligned16(bias)) || (residual && !mica_aligned16(residual)))
+        !mica_aligned16(C) || (bias && !mica_aligned16(bias)) || (residual && !mica_aligned16(residual)) ||
+        (workspace && !mica_aligned16(workspace)))
         return MICA_MISS_ALIGN;
+    if (workspace_bytes < 0) return MICA_MISS_ARG;
     if (M == 0) return 0;
     GemmParams p{};
     p.A = A; p.B = B; p.sa = sa; p.sb = sb; p.bias = bias; p.res = residual; p.C = C;
@@ -586,12 +729,33 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     p.tiles_m = (M + BM - 1) / BM;
     p.tiles_n = (N + BN - 1) / BN;
     p.vec_ok = (ldc % 4 == 0) && (Nout % 4 == 0) && (!residual || ldr % 4 == 0);
-    if ((long long)p.tiles_m * p.tiles_n >= (1ll << 31)) return MICA_MISS_RANGE;
+    const long long tiles = (long long)p.tiles_m * p.tiles_n;
+    if (tiles >= (1ll << 31)) return MICA_MISS_RANGE;
+    // Schedule.  Whole tiles, one workgroup each, unless the last round of tiles would leave CUs
+    // idle: then the remainder tiles are split along K over a persistent grid of one workgroup per
+    // CU, provided every workgroup gets at least kMinSlabs slabs and the workspace is there.
+    constexpr int kMinSlabs = 4;
+    p.dp_tiles = (int)tiles;
+    p.sk_tiles = 0;
+    int grid = (int)tiles;
+    int dev = 0;
+    if (workspace != nullptr && hipGetDevice(&dev) == hipSuccess) {
+        const int cus = cu_count(dev);
+        const long long nk = (K + BK - 1) / BK;
+        const long long rem = cus > 0 ? tiles % cus : 0;
+        if (rem != 0 && cus <= 1024 && workspace_bytes >= workspace_bytes_for(cus) && rem * nk >= (long long)kMinSlabs * cus) {
+            p.dp_tiles = (int)(tiles - rem);
+            p.sk_tiles = (int)rem;
+            p.arrivals = (int *)workspace;
+            p.partials = (v4i *)((char *)workspace + kCounterBytes);
+            grid = cus;
+        }
+    }
     hipStream_t st = (hipStream_t)stream;
     const bool hb = bias != nullptr, hr = residual != nullptr;
-    if (epilogue == MICA_EPI_SILU_MUL) return launch_out<MICA_EPI_SILU_MUL, MICA_BF16>(p, false, false, st);
-    if (out_dtype == MICA_BF16) return launch_out<MICA_EPI_SCALE, MICA_BF16>(p, hb, hr, st);
-    if (out_dtype == MICA_FP16) return launch_out<MICA_EPI_SCALE, MICA_FP16>(p, hb, hr, st);
-    if (out_dtype == MICA_INT32) return launch_out<MICA_EPI_SCALE, MICA_INT32>(p, false, false, st);
-    return launch_out<MICA_EPI_SCALE, MICA_FP32>(p, hb, hr, st);
+    if (epilogue == MICA_EPI_SILU_MUL) return launch_out<MICA_EPI_SILU_MUL, MICA_BF16>(p, grid, false, false, st);
+    if (out_dtype == MICA_BF16) return launch_out<MICA_EPI_SCALE, MICA_BF16>(p, grid, hb, hr, st);
+    if (out_dtype == MICA_FP16) return launch_out<MICA_EPI_SCALE, MICA_FP16>(p, grid, hb, hr, st);
+    if (out_dtype == MICA_INT32) return launch_out<MICA_EPI_SCALE, MICA_INT32>(p, grid, false, false, st);
+    return launch_out<MICA_EPI_SCALE, MICA_FP32>(p, grid, hb, hr, st);
 }

@@ -8,7 +8,11 @@
 // 8-element chunks [c * 512 + 8 l, c * 512 + 8 l + 8) for c < NCH = ceil(K / 512): every
 // load is a 16-byte vector and a wave's 64 lanes cover 1 KiB of contiguous bf16 per chunk.
 // The sum of squares and the absmax are wavefront reductions (no LDS, no barrier).
-// Waves walk rows with a grid stride; blocks are 256 threads (4 rows in flight per block).
+// Waves walk rows with a grid stride over a grid sized to the CU count; rows of up to 2560
+// elements keep the next row's load in flight while the current one is processed.
+// The int8 rows are written with non-temporal stores (streamed out once, read by the next
+// kernel), measured faster than cached stores on MI355X; cached loads measured faster than
+// non-temporal ones.
 
 #include "common.h"
 
@@ -16,6 +20,7 @@ namespace {
 
 constexpr int kChunk = 8;          // elements per lane per chunk
 constexpr int kRowStep = 64 * kChunk; // elements per chunk across the wave
+
 
 struct RowParams {
     const void *x;
@@ -82,26 +87,72 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// Round-to-int8 of one value with a compile-time rounding mode (RND 0: half even, 1: half away,
+// 2: the mode given at run time).
+template <bool kFast, int RND>
+MICA_DEVICE int quantize_r(float x, float s, float inv, int rounding) {
+    return quantize_one<kFast>(x, s, inv, RND == 2 ? rounding : RND);
+}
+
 // Quantize one chunk of 8 fp32 values with the row's scale and store 8 bytes.
-template <bool kFast>
-MICA_DEVICE void quant_store8(const float (&v)[kChunk], float s, float r, int rounding, int8_t *dst) {
-    int qv[kChunk];
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) qv[j] = quantize_one<kFast>(v[j], s, r, rounding);
+// The bf16 / half-even case rounds with the 1.5 * 2^23 trick: for |t| <= 127, t + 12582912 is an
+// integer-valued float (its rounding is the IEEE round-half-even of t), whose low mantissa byte is
+// that integer in two's complement; v_perm_b32 then gathers the four low bytes into one dword.
+template <bool kFast, int RND>
+MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int rounding, int8_t *dst) {
     u32x2 packed;
-    packed[0] = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
-    packed[1] = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
-    *(u32x2 *)dst = packed;
+    if (kFast && RND == MICA_ROUND_EVEN) {
+        uint32_t b[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const float y = v[j] * r;
+            const float rem = __builtin_fmaf(-y, s, v[j]);
+            float t = __builtin_fmaf(rem, r, y);
+            t = __builtin_fminf(__builtin_fmaxf(t, -127.0f), 127.0f);
+            b[j] = __float_as_uint(t + 12582912.0f);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t lo = __builtin_amdgcn_perm(b[4 * h + 1], b[4 * h], 0x0c0c0400u);
+            const uint32_t hi = __builtin_amdgcn_perm(b[4 * h + 3], b[4 * h + 2], 0x0c0c0400u);
+            packed[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+    } else {
+        int qv[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) qv[j] = quantize_r<kFast, RND>(v[j], s, r, rounding);
+        packed[0] = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
+        packed[1] = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
+    }
+    __builtin_nontemporal_store(packed, (u32x2 *)dst); // written once, read by the next kernel
 }
 
 // XT: dtype of x / residual / y / sum (bf16 or fp16).  NORM: apply the RMSNorm first.
 // HAS_INV: multiply by inv_smooth before the absmax (forces the IEEE-division quotient).
-template <int NCH, int XT, bool NORM, bool HAS_INV>
+// FULL: K == NCH * 512, so no chunk needs a bounds mask.  RND: rounding mode (2: at run time).
+// Each wave prefetches its next row while it works on the current one; the row is unpacked to
+// fp32 once, and after the norm it stays in fp32 registers (already rounded to XT), so the
+// absmax and the quantizer work on registers.
+template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
 __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
     constexpr bool kFast = (XT == MICA_BF16) && !HAS_INV;
     const int lane = threadIdx.x & 63;
     const int nwaves = gridDim.x * (blockDim.x >> 6);
     const int K = p.K;
+    auto live = [&](int c) { return FULL || c * kRowStep + lane * kChunk < K; };
+
+    auto load_row = [&](u32x4 (&raw)[NCH], int row) {
+        const uint16_t *xr = (const uint16_t *)p.x + (long)row * p.ldx;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            raw[c] = live(c) ? *(const u32x4 *)(xr + idx) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    // the wave's first row is requested before the weights, so the two latencies overlap
+    int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    u32x4 bufA[NCH], bufB[NCH <= 5 ? NCH : 1];
+    if (row < p.M) load_row(bufA, row);
 
     // per-lane weight multipliers (offset + w), fp32, cached across the rows this wave visits
     float w1[NORM ? NCH : 1][kChunk];
@@ -109,7 +160,7 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int idx = c * kRowStep + lane * kChunk;
-            if (idx < K) {
+            if (live(c)) {
                 load_w8(p.w, p.w_dtype, idx, w1[c]);
 #pragma unroll
                 for (int j = 0; j < kChunk; ++j) w1[c][j] = p.offset + w1[c][j];
@@ -120,38 +171,53 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
         }
     }
 
-    for (int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < p.M; row += nwaves) {
-        u32x4 raw[NCH];
-        const uint16_t *xr = (const uint16_t *)p.x + (long)row * p.ldx;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
+    // one row, held in cur (raw bits).  Short rows (kF32) are unpacked to fp32 once and stay in
+    // fp32 registers through the norm, the absmax and the quantizer; long rows stay packed and are
+    // unpacked again in each pass, which keeps enough waves resident.
+    constexpr bool kF32 = NCH <= 8;
+    constexpr bool kPrefetch = NCH <= 5; // long rows already keep enough bytes in flight per wave
+    auto unpack_inv = [&](const u32x4 &raw, int c, float (&a)[kChunk]) {
+        unpack8<XT>(raw, a);
+        if (HAS_INV) {
             const int idx = c * kRowStep + lane * kChunk;
-            raw[c] = idx < K ? *(const u32x4 *)(xr + idx) : u32x4{0u, 0u, 0u, 0u};
+            float iv[kChunk];
+            if (live(c)) load_inv8(p.inv, idx, iv);
+            else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) a[j] = a[j] * iv[j];
         }
+    };
+    auto process = [&](u32x4 (&cur)[NCH], int row) {
         if (NORM && p.res != nullptr) {
             // v = (x + r) rounded to the activation dtype (fused_kernels.py:27-30, :52)
             const uint16_t *rr = (const uint16_t *)p.res + (long)row * p.ldr;
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 const int idx = c * kRowStep + lane * kChunk;
-                if (idx < K) {
+                if (live(c)) {
                     u32x4 rc = *(const u32x4 *)(rr + idx);
                     float a[kChunk], b[kChunk];
-                    unpack8<XT>(raw[c], a);
+                    unpack8<XT>(cur[c], a);
                     unpack8<XT>(rc, b);
 #pragma unroll
                     for (int j = 0; j < kChunk; ++j) a[j] = a[j] + b[j];
-                    raw[c] = pack8<XT>(a);
-                    if (p.sum != nullptr) *(u32x4 *)((uint16_t *)p.sum + (long)row * p.lds + idx) = raw[c];
+                    cur[c] = pack8<XT>(a);
+                    if (p.sum != nullptr) *(u32x4 *)((uint16_t *)p.sum + (long)row * p.lds + idx) = cur[c];
                 }
             }
+        }
+        float v[kF32 ? NCH : 1][kChunk];
+        if (kF32) {
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) unpack8<XT>(cur[c], v[kF32 ? c : 0]);
         }
         if (NORM) {
             float ss = 0.0f;
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                float a[kChunk];
-                unpack8<XT>(raw[c], a);
+                float t[kChunk];
+                if (!kF32) unpack8<XT>(cur[c], t);
+                const float(&a)[kChunk] = kF32 ? v[kF32 ? c : 0] : t;
 #pragma unroll
                 for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(a[j], a[j], ss);
             }
@@ -161,34 +227,46 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 const int idx = c * kRowStep + lane * kChunk;
-                float a[kChunk];
-                unpack8<XT>(raw[c], a);
+                float t[kChunk];
+                if (!kF32) unpack8<XT>(cur[c], t);
+                float(&a)[kChunk] = kF32 ? v[kF32 ? c : 0] : t;
 #pragma unroll
                 for (int j = 0; j < kChunk; ++j) a[j] = (a[j] * rstd) * w1[c][j];
-                raw[c] = pack8<XT>(a);
-                if (p.y != nullptr && idx < K) *(u32x4 *)((uint16_t *)p.y + (long)row * p.ldy + idx) = raw[c];
+                const u32x4 packed = pack8<XT>(a);
+                if (kF32) unpack8<XT>(packed, a);
+                else cur[c] = packed;
+                if (p.y != nullptr && live(c)) *(u32x4 *)((uint16_t *)p.y + (long)row * p.ldy + idx) = packed;
             }
         }
-        if (p.q == nullptr) continue;
-
-        // absmax of the (smoothed) row
+        if (p.q == nullptr) return;
+        if (kF32 && HAS_INV) {
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int idx = c * kRowStep + lane * kChunk;
+                float iv[kChunk];
+                if (live(c)) load_inv8(p.inv, idx, iv);
+                else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) v[kF32 ? c : 0][j] = v[kF32 ? c : 0][j] * iv[j];
+            }
+        }
+        // absmax of the (smoothed) row; masked chunks hold zeros
         float amax = 0.0f;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            const int idx = c * kRowStep + lane * kChunk;
-            float a[kChunk];
-            unpack8<XT>(raw[c], a);
-            if (HAS_INV) {
-                float iv[kChunk];
-                if (idx < K) load_inv8(p.inv, idx, iv);
-                else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
-#pragma unroll
-                for (int j = 0; j < kChunk; ++j) a[j] = a[j] * iv[j];
-            }
+            float t[kChunk];
+            if (!kF32) unpack_inv(cur[c], c, t);
+            const float(&a)[kChunk] = kF32 ? v[kF32 ? c : 0] : t;
 #pragma unroll
             for (int j = 0; j < kChunk; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(a[j]));
         }
         amax = wave_max(amax);
+        if (!kF32) {
+            // the quantizer unpacks the row again: keep the compiler from holding the first
+            // pass's fp32 values live instead (that would cost the registers kF32 = false saves)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) __asm__ volatile("" : "+v"(cur[c]));
+        }
         const float s = row_scale(amax);
         const float r = 1.0f / s;
         if (lane == 0) p.s[row] = s;
@@ -196,16 +274,30 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int idx = c * kRowStep + lane * kChunk;
-            if (idx >= K) continue;
-            float a[kChunk];
-            unpack8<XT>(raw[c], a);
-            if (HAS_INV) {
-                float iv[kChunk];
-                load_inv8(p.inv, idx, iv);
-#pragma unroll
-                for (int j = 0; j < kChunk; ++j) a[j] = a[j] * iv[j];
-            }
-            quant_store8<kFast>(a, s, r, p.rounding, qr + idx);
+            float t[kChunk];
+            if (!kF32) unpack_inv(cur[c], c, t);
+            const float(&a)[kChunk] = kF32 ? v[kF32 ? c : 0] : t;
+            if (live(c)) quant_store8r<kFast, RND>(a, s, r, p.rounding, qr + idx);
+        }
+    };
+
+    if constexpr (kPrefetch) {
+        // two row buffers used in turn (no registers are copied between rows); each wave's next
+        // row is requested before the current one is worked on
+        for (;;) {
+            if (row >= p.M) break;
+            if (row + nwaves < p.M) load_row(bufB, row + nwaves);
+            process(bufA, row);
+            row += nwaves;
+            if (row >= p.M) break;
+            if (row + nwaves < p.M) load_row(bufA, row + nwaves);
+            process(bufB, row);
+            row += nwaves;
+        }
+    } else {
+        for (; row < p.M; row += nwaves) {
+            if (row != blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) load_row(bufA, row);
+            process(bufA, row);
         }
     }
 }
@@ -248,7 +340,7 @@ __global__ __launch_bounds__(256) void row32_kernel(RowParams p) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int idx = c * kRowStep + lane * kChunk;
-            if (idx < K) quant_store8<false>(v[c], s, r, p.rounding, qr + idx);
+            if (idx < K) quant_store8r<false, 2>(v[c], s, r, p.rounding, qr + idx);
         }
     }
 }
@@ -277,17 +369,36 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *g, const ui
     }
 }
 
+// Workgroups (4 waves each) per CU that a row launch asks for: 3 per CU keep every wave of the
+// hot kernels (3 to 4 waves per SIMD) resident from the start, each walking its rows with a grid
+// stride (its weights are loaded once, its next row is always in flight); measured against 4, 6
+// and 12 per CU on MI355X.
+#ifndef MICA_ROW_BLOCKS_PER_CU
+#define MICA_ROW_BLOCKS_PER_CU 3
+#endif
+
+int cu_count_of_current_device() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] > 0) return cached[dev];
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 256;
+    cached[dev] = v;
+    return v;
+}
+
 int row_grid(int M) {
-    // enough waves to fill 256 CUs several times over; the row loop covers the rest
     const int blocks = (M + 3) / 4;
-    return blocks < 4096 ? blocks : 4096;
+    const int cap = cu_count_of_current_device() * MICA_ROW_BLOCKS_PER_CU;
+    return blocks < cap ? blocks : cap;
 }
 
 template <int NCH>
 int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st) {
     dim3 grid(row_grid(p.M)), block(256);
 #define MICA_ROW16(XT_, NORM_, INV_) \
-    hipLaunchKernelGGL((row16_kernel<NCH, XT_, NORM_, INV_>), grid, block, 0, st, p)
+    hipLaunchKernelGGL((row16_kernel<NCH, XT_, NORM_, INV_, false, 2>), grid, block, 0, st, p)
     if (xt == MICA_BF16) {
         if (norm) { if (has_inv) MICA_ROW16(MICA_BF16, true, true); else MICA_ROW16(MICA_BF16, true, false); }
         else { if (has_inv) MICA_ROW16(MICA_BF16, false, true); else MICA_ROW16(MICA_BF16, false, false); }
@@ -299,6 +410,21 @@ int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st
     return mica_err(hipGetLastError());
 }
 
+// bf16 rows of exactly NCH * 512 elements (the hot widths): no masks, rounding fixed at compile time
+template <int NCH>
+int launch16_full(const RowParams &p, bool norm, bool has_inv, hipStream_t st) {
+    dim3 grid(row_grid(p.M)), block(256);
+#define MICA_ROWF(NORM_, INV_, RND_) \
+    hipLaunchKernelGGL((row16_kernel<NCH, MICA_BF16, NORM_, INV_, true, RND_>), grid, block, 0, st, p)
+#define MICA_ROWF2(NORM_, INV_) \
+    if (p.rounding == MICA_ROUND_EVEN) MICA_ROWF(NORM_, INV_, MICA_ROUND_EVEN); else MICA_ROWF(NORM_, INV_, MICA_ROUND_AWAY);
+    if (norm) { if (has_inv) { MICA_ROWF2(true, true) } else { MICA_ROWF2(true, false) } }
+    else { if (has_inv) { MICA_ROWF2(false, true) } else { MICA_ROWF2(false, false) } }
+#undef MICA_ROWF2
+#undef MICA_ROWF
+    return mica_err(hipGetLastError());
+}
+
 template <int NCH>
 int launch32(const RowParams &p, bool has_inv, hipStream_t st) {
     dim3 grid(row_grid(p.M)), block(256);
@@ -307,11 +433,17 @@ int launch32(const RowParams &p, bool has_inv, hipStream_t st) {
     return mica_err(hipGetLastError());
 }
 
-// NCH = ceil(K / 512) in 1..32 (K <= 16384).  Widths of the hot shapes (K = 2560: 5,
-// 4096: 8, 9216: 18, 9728: 19) have their own instantiation; any other width runs on the next
-// larger one, whose surplus chunks are masked off.
+// NCH = ceil(K / 512) in 1..32 (K <= 16384).  bf16 rows of the hot widths (K = 2560: 5,
+// 4096: 8, 9216: 18, 9728: 19) run unmasked with the rounding mode compiled in; any other width
+// runs on the next larger instantiation, whose surplus chunks are masked off.
 int dispatch_rows(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st) {
     const int nch = (p.K + kRowStep - 1) / kRowStep;
+    if (xt == MICA_BF16 && p.K == nch * kRowStep) {
+        if (nch == 5) return launch16_full<5>(p, norm, has_inv, st);
+        if (nch == 8) return launch16_full<8>(p, norm, has_inv, st);
+        if (nch == 18) return launch16_full<18>(p, norm, has_inv, st);
+        if (nch == 19) return launch16_full<19>(p, norm, has_inv, st);
+    }
 #define MICA_CASE(N_) \
     if (nch <= N_) return xt == MICA_FP32 ? launch32<N_>(p, has_inv, st) : launch16<N_>(p, xt, norm, has_inv, st);
     MICA_CASE(1) MICA_CASE(2) MICA_CASE(4) MICA_CASE(5) MICA_CASE(8) MICA_CASE(12) MICA_CASE(16) MICA_CASE(18)

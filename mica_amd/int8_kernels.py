@@ -131,6 +131,29 @@ def _gpu_ok(dev):
     return dev.type == "cuda" and _gfx(dev) == 950
 
 
+_WORKSPACE = {}
+_WS_LOCK = threading.Lock()
+
+
+def gemm_workspace(dev):
+    """The GEMM's split-tile workspace for torch's current stream on ``dev``: allocated (zeroed) once
+    per (device, stream) and kept for the life of the process, so a HIP graph that captured it
+    stays valid; every launch leaves its counters zero again.  Returns (pointer, bytes)."""
+    stream = torch.cuda.current_stream(dev)
+    key = (dev.index, stream.cuda_stream)
+    ws = _WORKSPACE.get(key)
+    if ws is None:
+        with _WS_LOCK:
+            ws = _WORKSPACE.get(key)
+            if ws is None:
+                nbytes = int(_lib.load().mica_mm_i8_workspace_bytes(dev.index))
+                if nbytes <= 0:
+                    raise RuntimeError(f"mica_mm_i8_workspace_bytes({dev.index}) failed: {nbytes}")
+                ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+                _WORKSPACE[key] = ws
+    return ws.data_ptr(), ws.numel()
+
+
 def act_quant(x, inv_smooth=None, rounding="even"):
     """Per-token INT8 quantization of a 2-D activation (int8_kernels.py:325-353)."""
     if x.dim() != 2 or x.device.type != "cuda" or x.dtype not in DT:
@@ -156,12 +179,14 @@ def act_quant(x, inv_smooth=None, rounding="even"):
     return (q, s) if ok else None
 
 
-def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, epilogue="none"):
+def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, epilogue="none", split=False):
     """C = (qx . qw^T)_i32 * sx[m] * sw[n] (+ bias[n]) -> out_dtype (int8_kernels.py:359-406).
 
     Extensions: ``residual`` ([M, N] of out_dtype) is added after the output rounding;
     ``epilogue='silu_mul'`` treats qw as gate/up rows interleaved in groups of 64
-    (int8_runtime.pack_gate_up) and returns bf16(bf16(silu(gate)) * up) of shape [M, N / 2].
+    (int8_runtime.pack_gate_up) and returns bf16(bf16(silu(gate)) * up) of shape [M, N / 2];
+    ``split=True`` lets the kernel split a partial last round of tiles along K over all CUs
+    (exact int32 partial sums through a per-stream workspace; same bits as the default schedule).
     """
     if qx.dim() != 2 or qw.dim() != 2 or qx.dtype != torch.int8 or qw.dtype != torch.int8 or out_dtype not in DT:
         return _miss("mm_input")
@@ -195,14 +220,15 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
     if not _aligned(qx, qw, sx, sw, out, *extra):
         return _miss("align")
     L = _lib.load()
+    ws, ws_bytes = gemm_workspace(_dev(qx.device)) if split else (None, 0)
     ok = _run(qx.device, "mica_mm_i8", L.mica_mm_i8, qx.data_ptr(), k, qw.data_ptr(), k, sx.data_ptr(),
               sw.data_ptr(), None if bias is None else bias.data_ptr(),
               None if residual is None else residual.data_ptr(), n_out, out.data_ptr(), n_out, DT[out_dtype],
-              m, n, k, EPILOGUE[epilogue])
+              m, n, k, EPILOGUE[epilogue], ws, ws_bytes)
     return out if ok else None
 
 
-def mm_i8_int32(qx, qw):
+def mm_i8_int32(qx, qw, split=False):
     """Raw int32 accumulators qx . qw^T on the matrix cores (the int32 result of
     int8_quant.torch_int_mm, int8_quant.py:92-96), or None on a miss."""
     if qx.dim() != 2 or qw.dim() != 2 or qx.dtype != torch.int8 or qw.dtype != torch.int8:
@@ -222,8 +248,9 @@ def mm_i8_int32(qx, qw):
     if not _aligned(qx, qw, out):
         return _miss("align")
     L = _lib.load()
+    ws, ws_bytes = gemm_workspace(_dev(qx.device)) if split else (None, 0)
     ok = _run(qx.device, "mica_mm_i8", L.mica_mm_i8, qx.data_ptr(), k, qw.data_ptr(), k, dummy.data_ptr(),
-              dummy.data_ptr(), None, None, n, out.data_ptr(), n, _lib.INT32, m, n, k, _lib.EPI_SCALE)
+              dummy.data_ptr(), None, None, n, out.data_ptr(), n, _lib.INT32, m, n, k, _lib.EPI_SCALE, ws, ws_bytes)
     return out if ok else None
 
 

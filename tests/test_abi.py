@@ -60,12 +60,19 @@ A16 = 1 << 20  # a 16-byte aligned fake address: never dereferenced, every call 
 ])
 def test_mm_i8_rejects(args, code):
     lib = _lib.load()
-    assert lib.mica_mm_i8(*args, None) == code
+    assert lib.mica_mm_i8(*args, None, 0, None) == code
+
+
+def test_mm_i8_rejects_bad_workspace():
+    lib = _lib.load()
+    ok = (A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0)
+    assert lib.mica_mm_i8(*ok, A16 + 4, 1 << 20, None) == 3    # misaligned workspace
+    assert lib.mica_mm_i8(*ok, A16, -1, None) == 6             # negative size
 
 
 def test_mm_i8_empty_is_a_no_op():
     lib = _lib.load()
-    assert lib.mica_mm_i8(A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 0, 64, 64, 0, None) == 0
+    assert lib.mica_mm_i8(A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 0, 64, 64, 0, None, 0, None) == 0
 
 
 @pytest.mark.parametrize("args,code", [

@@ -273,6 +273,41 @@ def test_gemm_headline_full_size(gpu):
     assert_equal_diag(y2, want, "epilogue linearity in sa")
 
 
+@pytest.mark.parametrize("m,n,k,epi", [
+    (4096, 9728, 2560, "none"),      # 608 tiles: 96 split over 256 CUs
+    (4096, 2560, 4096, "none"),      # 160 tiles: every tile split
+    (700, 2560, 9728, "residual"),   # 30 tiles, K = 9728: ~26 contributors per tile
+    (1000, 3072, 2560, "silu_mul"),  # the fused gate+up epilogue after a split
+])
+def test_gemm_split_schedule_bit_exact(gpu, m, n, k, epi):
+    """split=True (remainder tiles split along K, int32 partial sums through the workspace) gives the
+    same bits as the oracle, twice in a row (the arrival counters must come back to zero)."""
+    note(f"gemm split m={m} n={n} k={k} epi={epi}")
+    rng = np.random.default_rng(m + n + k + 1)
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    tA, tB, tsa, tsb = (torch.from_numpy(v).cuda() for v in (A, B, sa, sb))
+    acc = O.int_gemm(A, B)
+    for rep in range(2):
+        assert_equal_diag(int8_kernels.mm_i8_int32(tA, tB, split=True).cpu().numpy(), acc, f"int32 (call {rep})")
+    if epi == "silu_mul":
+        n2 = n // 2
+        grp = B.reshape(n // 128, 2, 64, k)
+        sgr = sb.reshape(n // 128, 2, 64)
+        gv = O.epilogue(O.int_gemm(A, grp[:, 0].reshape(n2, k)), sa, sgr[:, 0].reshape(n2))
+        uv = O.epilogue(O.int_gemm(A, grp[:, 1].reshape(n2, k)), sa, sgr[:, 1].reshape(n2))
+        ref = O.silu_mul(gv, uv)
+        for rep in range(2):
+            assert_within_one_ulp(bits_of(int8_kernels.mm_i8(tA, tsa, tB, tsb, epilogue="silu_mul", split=True)), ref)
+        return
+    res = act_bits(rng, (m, n), outliers=0) if epi == "residual" else None
+    ref = O.epilogue(acc, sa, sb)
+    if res is not None:
+        ref = O.f32_to_bf16(O.bf16_to_f32(ref) + O.bf16_to_f32(res))
+    for rep in range(2):
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, residual=None if res is None else to_gpu_bf16(res), split=True)
+        assert_equal_diag(bits_of(y), ref, f"bf16 (call {rep})")
+
+
 @pytest.mark.parametrize("m,n,k", [(32768, 6144, 2560), (32768, 2560, 4096)])
 def test_gemm_config3_long_context_sampled_rows(gpu, m, n, k):
     """Config 3 (T = 32768 packed prefill): QKV 2560 -> 6144 and O 4096 -> 2560, checked exactly on a

@@ -145,3 +145,70 @@ def test_gemm_tile_map_is_a_bijection(m, n):
     seen = {_tile_of(p, tm_, tn_) for p in range(tm_ * tn_)}
     assert len(seen) == tm_ * tn_
     assert all(0 <= a < tm_ and 0 <= b < tn_ for a, b in seen)
+
+
+# ------------------------------------------------------------------ GEMM split-tile (stream-K) schedule
+def _gemm_schedule(M, N, K, cus, min_slabs=4):
+    """mica_mm_i8's schedule choice (gemm_i8.hip): (dp_tiles, sk_tiles, grid)."""
+    tiles = -(-M // 256) * -(-N // 256)
+    nk = -(-K // 64)
+    rem = tiles % cus
+    if rem and rem * nk >= min_slabs * cus:
+        return tiles - rem, rem, cus
+    return tiles, 0, tiles
+
+
+def _sk_begin(g, W, G):
+    return g * W // G
+
+
+def _sk_owner(i, W, G):
+    return ((i + 1) * G + W - 1) // W - 1
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 9728, 2560), (4096, 6144, 2560), (4096, 2560, 4096), (4096, 2560, 9728),
+                                   (512, 9728, 2560), (4096, 19456, 2560), (32768, 6144, 2560), (300, 1000, 2576),
+                                   (16384, 2560, 9728), (1, 9728, 2560), (2048, 4096, 2560)])
+@pytest.mark.parametrize("cus", [256, 304, 80])
+def test_gemm_split_schedule_covers_every_slab_once(m, n, k, cus):
+    """Replays the kernel's work loop on the CPU: every (tile, slab) is computed exactly once; every
+    split tile is finished by exactly one contributor, the one that counts itself last; the partial
+    slots it reads are exactly those the other contributors wrote, and no slot is written twice."""
+    dp, sk, G = _gemm_schedule(m, n, k, cus)
+    nk = -(-k // 64)
+    tiles_m, tiles_n = -(-m // 256), -(-n // 256)
+    W = sk * nk
+    done = {}
+    written = {}              # (g, seg) -> tile
+    contrib = {}              # tile -> set of g
+    for g in range(G):
+        pid = g
+        while pid < dp:
+            t = _tile_of(pid, tiles_m, tiles_n)
+            for s in range(nk):
+                done[(t, s)] = done.get((t, s), 0) + 1
+            pid += G
+        if not sk:
+            continue
+        b, e = _sk_begin(g, W, G), _sk_begin(g + 1, W, G)
+        assert e > b, "a workgroup without stream-K work would break the arrival count"
+        it = b
+        while it < e:
+            rel, k0 = divmod(it, nk)
+            k1 = nk if nk - k0 < e - it else k0 + (e - it)
+            t = _tile_of(dp + rel, tiles_m, tiles_n)
+            for s in range(k0, k1):
+                done[(t, s)] = done.get((t, s), 0) + 1
+            if k0 != 0 or k1 != nk:
+                seg = 1 if rel * nk > b else 0
+                assert (g, seg) not in written
+                written[(g, seg)] = rel
+                contrib.setdefault(rel, set()).add(g)
+            it += k1 - k0
+    assert len(done) == tiles_m * tiles_n * nk and set(done.values()) == {1}
+    for rel, gs in contrib.items():
+        tb = rel * nk
+        g0, g1 = _sk_owner(tb, W, G), _sk_owner(tb + nk - 1, W, G)
+        assert gs == set(range(g0, g1 + 1)), "the arrival target g1 - g0 + 1 must count the real contributors"
+        for g in gs:  # the slot the finisher reads for g is the one g wrote for this tile
+            assert written[(g, 1 if tb > _sk_begin(g, W, G) else 0)] == rel
