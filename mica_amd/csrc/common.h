@@ -20,9 +20,11 @@ MICA_DEVICE float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h <
 
 // fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
 MICA_DEVICE uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
-// Two values packed low | high << 16.
+// Two values packed low | high << 16, each rounded to nearest even: one v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 MICA_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 // Round an fp32 value to the nearest bf16 and return it as fp32.
 MICA_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }

@@ -63,7 +63,10 @@ template <int XT>
 MICA_DEVICE u32x4 pack8(const float (&v)[kChunk]) {
     u32x4 c;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) c[j] = (uint32_t)to16<XT>(v[2 * j]) | ((uint32_t)to16<XT>(v[2 * j + 1]) << 16);
+    for (int j = 0; j < 4; ++j) {
+        if (XT == MICA_BF16) c[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+        else c[j] = (uint32_t)to16<XT>(v[2 * j]) | ((uint32_t)to16<XT>(v[2 * j + 1]) << 16);
+    }
     return c;
 }
 
@@ -95,9 +98,12 @@ MICA_DEVICE int quantize_r(float x, float s, float inv, int rounding) {
 }
 
 // Quantize one chunk of 8 fp32 values with the row's scale and store 8 bytes.
-// The bf16 / half-even case rounds with the 1.5 * 2^23 trick: for |t| <= 127, t + 12582912 is an
+// The bf16 / half-even case rounds with the 1.5 * 2^23 trick: for |t| < 2^22, t + 12582912 is an
 // integer-valued float (its rounding is the IEEE round-half-even of t), whose low mantissa byte is
 // that integer in two's complement; v_perm_b32 then gathers the four low bytes into one dword.
+// No clamp is needed there: |x| <= amax and s = RN(max(amax, 1e-8) / 127) give
+// |x / s| <= 127 / (1 - 2^-24) < 127.5, so round(x / s) is already within +-127 (the reference's
+// clamp is the identity on finite rows; a row holding Inf or NaN yields 0 for those elements).
 template <bool kFast, int RND>
 MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int rounding, int8_t *dst) {
     u32x2 packed;
@@ -107,8 +113,7 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
         for (int j = 0; j < kChunk; ++j) {
             const float y = v[j] * r;
             const float rem = __builtin_fmaf(-y, s, v[j]);
-            float t = __builtin_fmaf(rem, r, y);
-            t = __builtin_fminf(__builtin_fmaxf(t, -127.0f), 127.0f);
+            const float t = __builtin_fmaf(rem, r, y);
             b[j] = __float_as_uint(t + 12582912.0f);
         }
 #pragma unroll
