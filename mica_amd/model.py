@@ -7,7 +7,7 @@ Weights are random int8 with per-output-channel fp32 scales; norms are gamma-sty
 Per layer (the call pattern of the reference's fork.layer_step, v0.5/serving/lib/fork.py:394-422):
   q, s   = rms_norm_quant(h, input_norm)                     1 launch
   qkv    = QKV W8A8 GEMM                                     1 launch
-  a      = causal GQA attention on each request (torch SDPA, bf16; outside the W8A8 path)
+  a      = causal GQA attention on each request (RoPE + torch SDPA, bf16; outside the W8A8 path)
   h      = h + O W8A8(a)          (residual in the epilogue)  2 launches (act_quant + GEMM)
   q, s   = rms_norm_quant(h, post_attention_norm)            1 launch
   g      = fused gate+up GEMM, SiLU(gate) * up epilogue      1 launch
@@ -69,18 +69,20 @@ class Layer:
 
 
 def _rope(S, head_dim, theta, device):
+    """Rotate-half RoPE tables as bf16 [1, S, 1, head_dim]: (cos, cos) and (-sin, sin)."""
     inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
     ang = torch.arange(S, device=device, dtype=torch.float32)[:, None] * inv[None, :]
-    return torch.cos(ang), torch.sin(ang)
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    cs = torch.cat((cos, cos), -1).to(torch.bfloat16)[None, :, None, :]
+    sn = torch.cat((-sin, sin), -1).to(torch.bfloat16)[None, :, None, :]
+    return cs, sn
 
 
-def _apply_rope(x, cos, sin):
-    # x [B, heads, S, d] bf16; rotate-half convention, computed in fp32
-    xf = x.float()
-    d = xf.shape[-1] // 2
-    x1, x2 = xf[..., :d], xf[..., d:]
-    c, s = cos[None, None], sin[None, None]
-    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), -1).to(x.dtype)
+def _apply_rope(x, cs, sn):
+    """x: [B, S, heads, d] (a view into the QKV output), in bf16 like the model's own attention:
+    x * (cos, cos) + rotate_half(x) * (-sin, sin)."""
+    h = x.shape[-1] // 2
+    return x * cs + torch.cat((x[..., h:], x[..., :h]), -1) * sn
 
 
 class W8A8Stack:
@@ -101,19 +103,19 @@ class W8A8Stack:
         self._rope = {}
 
     def _attention(self, qkv, B, S):
+        """Causal GQA attention per request on torch SDPA.  RoPE works on [B, S, heads, d] views of
+        the QKV output and SDPA reads them through transposed strides (enable_gqa shares each K/V
+        head with its group of query heads, no repeated copies); the output comes back
+        [B, S, heads, d]-contiguous, i.e. already the O projection's [T, heads * d] rows."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
         q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
-        q = q.transpose(1, 2).contiguous()
-        k = k.transpose(1, 2).contiguous()
-        v = v.transpose(1, 2).contiguous()
         if S not in self._rope:
             self._rope[S] = _rope(S, d, cfg.rope_theta, qkv.device)
-        cos, sin = self._rope[S]
-        q, k = _apply_rope(q, cos, sin), _apply_rope(k, cos, sin)
-        k = k.repeat_interleave(hq // hk, dim=1)
-        v = v.repeat_interleave(hq // hk, dim=1)
-        a = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=1.0 / math.sqrt(d))
+        cs, sn = self._rope[S]
+        q, k = _apply_rope(q, cs, sn), _apply_rope(k, cs, sn)
+        a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
+                                           scale=1.0 / math.sqrt(d), enable_gqa=True)
         return a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
 
     def layer_forward(self, L: Layer, h, B, S, trace=None):
