@@ -298,7 +298,7 @@ def stack_prefill(torch, dev, reps=3):
 
 
 def pmc_workload():
-    """The kernels the committed counter summaries describe, each launched 10 times."""
+    """The kernels the committed counter summaries describe, each launched 20 times."""
     import torch
 
     from mica_amd import _lib, int8_kernels
@@ -320,7 +320,7 @@ def pmc_workload():
          s.data_ptr(), None, K, None, K, T, K, 0, st)
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(10):
+    for _ in range(20):
         gemm()
         if lib.mica_rmsnorm_quant(*a) != 0:
             raise RuntimeError("mica_rmsnorm_quant failed")
@@ -353,9 +353,28 @@ def summarize(indir, out_txt, command="", top=16):
     traces = sorted(glob.glob(os.path.join(indir, "**", "*kernel_trace.csv"), recursive=True))
     for f in traces:
         groups = defaultdict(list)
-        for r in csv.DictReader(open(f)):
+        rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
+        for r in rows:
             grid = (int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
             groups[(r["Kernel_Name"][:150], grid)].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        # runs of >= 20 back-to-back dispatches of one kernel and launch shape, in launch order (a
+        # timed loop of the bench is one such run: its warm-up launches, then its timed launches)
+        runs, cur = [], None
+        for r in rows:
+            key = (r["Kernel_Name"][:150], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
+            d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            if cur is not None and cur[0] == key:
+                cur[1].append(d)
+            else:
+                cur = (key, [d])
+                runs.append(cur)
+        lines.append(f"# runs of >= 20 back-to-back dispatches, in launch order ({os.path.basename(f)})")
+        lines.append(f"{'run':>4} {'calls':>6} {'avg_us':>10} {'avg_last':>10} {'min_us':>10} {'max_us':>10} {'grid':>9}  kernel"
+                     f"  (avg_last: the last calls - 20, i.e. without the warm-up)")
+        for i, (key, v) in enumerate(r_ for r_ in runs if len(r_[1]) >= 20):
+            tail = v[20:] if len(v) > 20 else v
+            lines.append(f"{i:4d} {len(v):6d} {sum(v) / len(v) / 1e3:10.2f} {sum(tail) / len(tail) / 1e3:10.2f} "
+                         f"{min(v) / 1e3:10.2f} {max(v) / 1e3:10.2f} {key[1]:9d}  {key[0]}")
         lines.append(f"# per-dispatch durations by kernel and launch shape ({os.path.basename(f)})")
         lines.append(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'grid':>9} {'wg':>5}  kernel")
         for (k, (gx, wx)), v in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
@@ -369,7 +388,8 @@ def summarize(indir, out_txt, command="", top=16):
         lines.append(f"# counters per dispatch, mean over dispatches ({os.path.basename(f)})")
         for (k, c), v in sorted(agg.items()):
             lines.append(f"{c:28s} {sum(v) / len(v):16.1f}  n={len(v):3d}  {k}")
-        copy = {c: sum(v) / len(v) for (k, c), v in agg.items() if "copyBuffer" in k or "copy_kernel" in k}
+        copy = {c: sum(v) / len(v) for (k, c), v in agg.items()
+                if ("copyBuffer" in k or "copy_kernel" in k) and c in ("FETCH_SIZE", "WRITE_SIZE") and sum(v) > 0}
         for c, kib in copy.items():
             factor = (256 << 20) / (kib * 1024.0)
             lines.append(f"# calibration: the 256 MiB copy (256 MiB read, 256 MiB written) counts {c} = {kib:.1f} KiB "
@@ -377,6 +397,28 @@ def summarize(indir, out_txt, command="", top=16):
             for (k, c2), v in sorted(agg.items()):
                 if c2 == c and "copyBuffer" not in k:
                     lines.append(f"{c2 + '_bytes':28s} {sum(v) / len(v) * 1024.0 * factor:16.0f}  {k}")
+        # derived figures per kernel.  GRBM_GUI_ACTIVE comes summed over the XCCs; rocprofv3's own
+        # MfmaUtil divides the SIMD-summed MFMA busy cycles by the per-XCC active cycles x SIMD count
+        simds, xccs = 1024, 8  # MI355X, unless the run's agent info says otherwise
+        for ai in glob.glob(os.path.join(os.path.dirname(f), "*agent_info.csv")):
+            for a in csv.DictReader(open(ai)):
+                if a.get("Name", "").startswith("gfx"):
+                    simds, xccs = int(a["Simd_Count"]), int(a["Num_Xcc"])
+        per = defaultdict(dict)
+        for (k, c), v in agg.items():
+            per[k][c] = sum(v) / len(v)
+        for k, d in sorted(per.items()):
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in d and d.get("GRBM_GUI_ACTIVE"):
+                util = 100.0 * d["SQ_VALU_MFMA_BUSY_CYCLES"] / (d["GRBM_GUI_ACTIVE"] / xccs * simds)
+                lines.append(f"{'MFMA_util_pct':28s} {util:16.2f}  (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / "
+                             f"{xccs} XCCs x {simds} SIMDs), rocprofv3's MfmaUtil)  {k}")
+            if "SQ_INSTS_VALU_MFMA_MOPS_I8" in d:
+                lines.append(f"{'int8_ops_per_dispatch':28s} {d['SQ_INSTS_VALU_MFMA_MOPS_I8'] * 512:16.4g}"
+                             f"  (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512)  {k}")
+            if "SQ_LDS_BANK_CONFLICT" in d and d.get("SQ_LDS_IDX_ACTIVE"):
+                active = d["SQ_LDS_IDX_ACTIVE"] - d["SQ_LDS_BANK_CONFLICT"]
+                lines.append(f"{'LDS_conflict_per_access':28s} {d['SQ_LDS_BANK_CONFLICT'] / max(active, 1.0):16.4f}"
+                             f"  (SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT))  {k}")
     with open(out_txt, "w") as fh:
         fh.write("\n".join(lines) + "\n")
     print(f"wrote {out_txt} ({len(lines)} lines)")

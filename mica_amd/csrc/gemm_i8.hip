@@ -40,43 +40,45 @@
 
 namespace {
 
-constexpr int BM = 256;
-constexpr int BN = 256;
 constexpr int BK = 64;      // bytes of K per LDS stage
 constexpr int NST = 4;      // LDS stages
 constexpr int KS = BK / 32; // MFMA k-steps per stage
-constexpr int kABytes = BM * BK;               // 16 KiB
-constexpr int kStage = (BM + BN) * BK;         // 32 KiB
+constexpr int kTile = 256;  // edge of the schedule's (whole) tiles
 constexpr int kGroupM = 4;
 constexpr int kXcds = 8;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
 
-// Wave layout of the 256 x 256 workgroup tile: WGM x WGN waves, each owning WM x WN.
-template <int WGM, int WGN>
+// A BM x BN workgroup tile computed by 8 waves in a 4 (M) x 2 (N) grid, each owning WM x WN.
+template <int BM_, int BN_>
 struct Cfg {
-    static constexpr int kWaves = WGM * WGN;
-    static constexpr int kThreads = 64 * kWaves;
-    static constexpr int WM = BM / WGM;
-    static constexpr int WN = BN / WGN;
-    static constexpr int MB = WM / 32;                           // 32x32 MFMA tiles along M
-    static constexpr int NB = WN / 32;                           // ... along N
-    static constexpr int kBlocksPerWave = BM * BK / 1024 / kWaves; // 1 KiB DMA blocks per operand
-    static constexpr int kDmaPerSlab = 2 * kBlocksPerWave;       // buffer_load ... lds per wave per slab
+    static constexpr int BM = BM_, BN = BN_;
+    static constexpr int WM = BM / 4;
+    static constexpr int WN = BN / 2;
+    static constexpr int MB = WM / 32;                      // 32x32 MFMA tiles along M
+    static constexpr int NB = WN / 32;                      // ... along N
+    static constexpr int kABytes = BM * BK;                 // A part of an LDS stage
+    static constexpr int kStage = (BM + BN) * BK;
+    static constexpr int kABlk = BM * BK / 1024 / kWaves;   // 1 KiB DMA blocks of A per wave per slab
+    static constexpr int kBBlk = BN * BK / 1024 / kWaves;   // ... of B
+    static constexpr int kDmaPerSlab = kABlk + kBBlk;       // buffer_load ... lds per wave per slab
     // staged epilogue: each wave's WM x WN 16-bit block, rows padded by 16 bytes
     static constexpr int kEpiPitch = WN * 2 + 16;
     static constexpr int kEpiWave = WM * kEpiPitch;
     static constexpr int kSmemMain = (NST * kStage > kWaves * kEpiWave) ? NST * kStage : kWaves * kEpiWave;
-    // the tile's row scales, column scales and bias (fp32), staged at kernel start
-    static constexpr int kScaleOff = kSmemMain;
-    // the arrival count read back by a split tile's contributors
-    static constexpr int kFlagOff = kScaleOff + 3 * 256 * 4;
-    static constexpr int kSmem = kFlagOff + 16;
     // int32x4 vectors of one lane's accumulators (a split tile's partial sums)
     static constexpr int kPartialVecs = NB * MB * 4;
-    static_assert(WN == 128, "the SiLU epilogue needs one 128-row gate/up group per wave");
 };
-using CfgDefault = Cfg<4, 2>;
-static_assert(CfgDefault::kWaves == 8 && CfgDefault::MB == 2 && CfgDefault::NB == 4 &&
-                  CfgDefault::kBlocksPerWave == 2, "the main loop's instruction schedule is written for 8 waves of 64 x 128");
+using CfgFull = Cfg<256, 256>; // waves of 64 x 128: 2 x 4 MFMA tiles, 4 DMA per slab
+using CfgHalf = Cfg<256, 128>; // waves of 64 x 64: 2 x 2 MFMA tiles, 3 DMA per slab
+static_assert(CfgFull::MB == 2 && CfgFull::NB == 4 && CfgFull::kABlk == 2 && CfgFull::kBBlk == 2, "schedule");
+static_assert(CfgHalf::MB == 2 && CfgHalf::NB == 2 && CfgHalf::kABlk == 2 && CfgHalf::kBBlk == 1, "schedule");
+// LDS: the larger configuration's stages / staging, then the tile's row scales, column scales and
+// bias (fp32, 3 x 256), then the arrival count a split tile's contributors read back
+constexpr int kSmemMain = CfgFull::kSmemMain > CfgHalf::kSmemMain ? CfgFull::kSmemMain : CfgHalf::kSmemMain;
+constexpr int kScaleOff = kSmemMain;
+constexpr int kFlagOff = kScaleOff + 3 * 256 * 4;
+constexpr int kSmem = kFlagOff + 16;
 
 // word 3 of a gfx9 buffer resource (raw buffer, 32-bit data format), as used by CK for gfx9xx
 constexpr int kBufferFlags = 0x00020000;
@@ -95,11 +97,12 @@ struct GemmParams {
     void *C;
     int lda, ldb, ldr, ldc;
     int M, N, K;
-    int tiles_m, tiles_n;
-    int vec_ok; // ldc, ldr, N all multiples of 4: 4-column vector stores
-    // schedule: tiles [0, dp_tiles) of the grouped order run whole, one per workgroup per round;
-    // tiles [dp_tiles, dp_tiles + sk_tiles) are split along K over all gridDim.x workgroups
-    int dp_tiles, sk_tiles;
+    int tiles_m, tiles_n; // 256 x 256 tiles
+    int vec_ok;           // ldc, ldr, N all multiples of 4: 4-column vector stores
+    // schedule over the tiles in grouped order (tile_of): [0, dp_tiles) run whole, one per workgroup
+    // per round; the next half_tiles run as two 256 x 128 halves each; the next sk_tiles are split
+    // along K over all gridDim.x workgroups (at most one of half_tiles, sk_tiles is nonzero)
+    int dp_tiles, half_tiles, sk_tiles;
     v4i *partials; // [gridDim.x][2][kPartialVecs][kThreads]: a workgroup's partial accumulators
     int *arrivals; // [sk_tiles]: contributors arrived so far; zero between launches
 };
@@ -117,16 +120,6 @@ MICA_DEVICE void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 MICA_DEVICE void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
-
-// wait until at most `slabs` (0..4) slabs of this wave's DMA are still in flight
-template <int kDmaPerSlab>
-MICA_DEVICE void wait_dma(int slabs) {
-    if (slabs >= 4) wait_vmcnt<4 * kDmaPerSlab>();
-    else if (slabs == 3) wait_vmcnt<3 * kDmaPerSlab>();
-    else if (slabs == 2) wait_vmcnt<2 * kDmaPerSlab>();
-    else if (slabs == 1) wait_vmcnt<kDmaPerSlab>();
-    else wait_vmcnt<0>();
-}
 
 // Map the hardware workgroup id to a tile (tm, tn).
 MICA_DEVICE void tile_of(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
@@ -204,70 +197,13 @@ MICA_DEVICE long long sk_begin(int g, long long W, int G) { return (long long)g 
 // the workgroup whose range holds iteration i (the largest g with sk_begin(g) <= i)
 MICA_DEVICE int sk_owner(long long i, long long W, int G) { return (int)(((i + 1) * G + W - 1) / W) - 1; }
 
-template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES, class C = CfgDefault>
-__global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
-    constexpr int WM = C::WM, WN = C::WN, MB = C::MB, NB = C::NB;
-    constexpr int kBlocksPerWave = C::kBlocksPerWave, kDmaPerSlab = C::kDmaPerSlab;
-    constexpr int kEpiPitch = C::kEpiPitch, kEpiWave = C::kEpiWave;
-    __shared__ __attribute__((aligned(1024))) int8_t smem[C::kSmem];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / (BN / WN), wn = wave % (BN / WN);
-    const int M = p.M, N = p.N, K = p.K;
-    const int nk = (K + BK - 1) / BK;
-
-    // ---- DMA of one slab: this wave moves kBlocksPerWave 1 KiB blocks of the A and of the B tile ----
-    // lane i of a block writes LDS bytes [16 i, 16 i + 16): tile row blk * 16 + i / 4, physical chunk
-    // i % 4, so it fetches logical chunk (i % 4) ^ swz(row) of that row.
-    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, M * p.lda, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, N * p.ldb, kBufferFlags);
-    int a_row[kBlocksPerWave], b_row[kBlocksPerWave], kcol[kBlocksPerWave], trow[kBlocksPerWave];
-#pragma unroll
-    for (int j = 0; j < kBlocksPerWave; ++j) {
-        trow[j] = (wave * kBlocksPerWave + j) * 16 + (lane >> 2);
-        kcol[j] = ((lane & 3) ^ swz(trow[j])) << 4;
-    }
-    int kend = 0; // slabs at or past kend are not fetched (the DMA writes zeros instead)
-    // one DMA instruction: block j (0 .. kBlocksPerWave-1) of operand op (0: A, 1: B) of a slab
-    auto dma1 = [&](int slab, int j, int op) {
-        const int k0 = slab * BK;
-        int8_t *st = smem + (slab % NST) * kStage;
-        const bool kin = slab < kend && k0 + kcol[j] < K;
-        const int row = op == 0 ? a_row[j] : b_row[j];
-        const int off = (kin && row != kOutOfRange) ? row + k0 : kOutOfRange;
-        const int blk = wave * kBlocksPerWave + j;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(op == 0 ? rsrc_a : rsrc_b,
-                                                 (lds_void *)(st + op * kABytes + blk * 1024), 16, off, 0, 0, 0);
-    };
-    auto dma = [&](int slab) {
-#pragma unroll
-        for (int j = 0; j < kBlocksPerWave; ++j) {
-            dma1(slab, j, 0);
-            dma1(slab, j, 1);
-        }
-    };
-
-    // ---- MFMA operand offsets inside a stage: [tile][k-step] ----
-    const int r32 = lane & 31, khalf = lane >> 5;
-    int x_rd[MB][KS], w_rd[NB][KS];
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int rx = wm * WM + i * 32 + r32;
-            const int c = ks * 2 + khalf;
-            x_rd[i][ks] = rx * BK + ((c ^ swz(rx)) << 4);
-        }
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int rw = wn * WN + j * 32 + r32;
-            const int c = ks * 2 + khalf;
-            w_rd[j][ks] = kABytes + rw * BK + ((c ^ swz(rw)) << 4);
-        }
+// One workgroup tile of configuration C: its accumulators, the main loop that fills them from
+// slabs [k0, k1) and the epilogue that writes them out.
+template <class C, int EPI, int OUT, bool HAS_BIAS, bool HAS_RES>
+struct TileEngine {
+    static constexpr int WM = C::WM, WN = C::WN, MB = C::MB, NB = C::NB;
+    static constexpr int kDmaPerSlab = C::kDmaPerSlab;
+    static constexpr int kEpiPitch = C::kEpiPitch, kEpiWave = C::kEpiWave;
 
     v16i acc[NB][MB]; // [n tile][m tile]
 
@@ -275,31 +211,13 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         v4i x[KS][MB];
         v4i w[KS][NB];
     };
-    auto lds_read = [&](Ops &o, int slab) {
-        const int8_t *st = smem + (slab % NST) * kStage;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int j = 0; j < NB; ++j) o.w[ks][j] = *(const v4i *)(st + w_rd[j][ks]);
-#pragma unroll
-            for (int i = 0; i < MB; ++i) o.x[ks][i] = *(const v4i *)(st + x_rd[i][ks]);
-        }
-    };
-    auto mfma_half = [&](const Ops &o, int ks) {
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
-                acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w[ks][j], o.x[ks][i], acc[j][i], 0, 0, 0);
-    };
 
     // ---- slabs [k0, k1) of tile (m0, n0) into acc.  Every wave runs the same software pipeline,
     // one barrier per 64-byte slab k:
     //   wait: this wave's DMA of slab k + 1 landed, its reads of slab k (registers X) completed
     //   barrier: slab k + 1 is visible in LDS, and nobody reads slab k's stage any more
-    //   then, interleaved instruction by instruction: the 16 MFMAs of slab k (from X), the 12
-    //   operand reads of slab k + 1 (into Y) and the 4 DMA instructions of slab k + 4 (into the
-    //   stage slab k just left).
+    //   then, interleaved instruction by instruction: the MFMAs of slab k (from X), the operand
+    //   reads of slab k + 1 (into Y) and the DMA of slab k + 4 (into the stage slab k just left).
     // All 8 waves keep the LDS busy together (operand reads and DMA writes share it) while the
     // two waves of each SIMD keep its matrix core busy.  A DMA past slab k1 is still issued (it
     // fails the range check and writes zeros into a stage nobody reads), so every wave always has
@@ -307,14 +225,78 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
     // The tile's per-row / per-column epilogue factors are loaded before the prologue DMA and
     // written to LDS after it, so their latency hides under the DMA's.  Threads 0-255: sa and bias
     // of tile row / column tid, threads 256-511: sb of column tid - 256.
-    static_assert(C::kThreads == 512, "one scale load per thread");
-    auto run = [&](int m0, int n0, int k0, int k1) {
+    MICA_DEVICE void run(const GemmParams &p, int8_t *smem, __amdgpu_buffer_rsrc_t rsrc_a,
+                         __amdgpu_buffer_rsrc_t rsrc_b, int m0, int n0, int k0, int k1) {
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int wm = wave / 2, wn = wave % 2;
+        const int M = p.M, N = p.N, K = p.K;
+        // DMA: lane i of 1 KiB block b of an operand writes LDS bytes [16 i, 16 i + 16): tile row
+        // 16 b + i / 4, physical chunk i % 4, so it fetches logical chunk (i % 4) ^ swz(row)
+        int a_off[C::kABlk], b_off[C::kBBlk];
 #pragma unroll
-        for (int j = 0; j < kBlocksPerWave; ++j) {
-            a_row[j] = m0 + trow[j] < M ? (m0 + trow[j]) * p.lda + kcol[j] : kOutOfRange;
-            b_row[j] = n0 + trow[j] < N ? (n0 + trow[j]) * p.ldb + kcol[j] : kOutOfRange;
+        for (int j = 0; j < C::kABlk; ++j) {
+            const int r = (wave * C::kABlk + j) * 16 + (lane >> 2);
+            const int kc = ((lane & 3) ^ swz(r)) << 4;
+            a_off[j] = m0 + r < M ? (m0 + r) * p.lda + kc : kOutOfRange;
         }
-        kend = k1;
+#pragma unroll
+        for (int j = 0; j < C::kBBlk; ++j) {
+            const int r = (wave * C::kBBlk + j) * 16 + (lane >> 2);
+            const int kc = ((lane & 3) ^ swz(r)) << 4;
+            b_off[j] = n0 + r < N ? (n0 + r) * p.ldb + kc : kOutOfRange;
+        }
+        const int kc_lane = ((lane & 3) ^ swz(lane >> 2)) << 4; // chunk column; swz(r) == swz(lane >> 2)
+        auto dma1 = [&](int slab, int j, int op) {
+            const int kb = slab * BK;
+            int8_t *st = smem + (slab % NST) * C::kStage;
+            const bool kin = slab < k1 && kb + kc_lane < K;
+            const int row = op == 0 ? a_off[j] : b_off[j];
+            const int off = (kin && row != kOutOfRange) ? row + kb : kOutOfRange;
+            const int blk = wave * (op == 0 ? C::kABlk : C::kBBlk) + j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(op == 0 ? rsrc_a : rsrc_b,
+                                                     (lds_void *)(st + op * C::kABytes + blk * 1024), 16, off, 0, 0, 0);
+        };
+        auto dma = [&](int slab) {
+#pragma unroll
+            for (int j = 0; j < C::kABlk; ++j) dma1(slab, j, 0);
+#pragma unroll
+            for (int j = 0; j < C::kBBlk; ++j) dma1(slab, j, 1);
+        };
+        // MFMA operand offsets inside a stage: [tile][k-step]
+        const int r32 = lane & 31, khalf = lane >> 5;
+        int x_rd[MB][KS], w_rd[NB][KS];
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int rx = wm * WM + i * 32 + r32;
+                x_rd[i][ks] = rx * BK + (((ks * 2 + khalf) ^ swz(rx)) << 4);
+            }
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int rw = wn * WN + j * 32 + r32;
+                w_rd[j][ks] = C::kABytes + rw * BK + (((ks * 2 + khalf) ^ swz(rw)) << 4);
+            }
+        auto lds_read = [&](Ops &o, int slab) {
+            const int8_t *st = smem + (slab % NST) * C::kStage;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) o.w[ks][j] = *(const v4i *)(st + w_rd[j][ks]);
+#pragma unroll
+                for (int i = 0; i < MB; ++i) o.x[ks][i] = *(const v4i *)(st + x_rd[i][ks]);
+            }
+        };
+        auto mfma_half = [&](const Ops &o, int ks) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w[ks][j], o.x[ks][i], acc[j][i], 0, 0, 0);
+        };
+
 #pragma unroll
         for (int j = 0; j < NB; ++j)
 #pragma unroll
@@ -337,7 +319,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
 #pragma unroll
         for (int sl = 0; sl < NST; ++sl) dma(k0 + sl);
         {
-            float *sc = (float *)(smem + C::kScaleOff);
+            float *sc = (float *)(smem + kScaleOff);
             sc[tid] = f1;                       // [0, 256): sa, [256, 512): sb
             if (tid < 256) sc[512 + tid] = f2;  // [512, 768): bias
         }
@@ -350,36 +332,64 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
             wait_vmcnt<(NST - 2) * kDmaPerSlab>(); // slab k + 1 landed (slabs k + 2, k + 3 may be in flight)
             wait_lgkmcnt0();                       // slab k's operands are in registers
             __builtin_amdgcn_s_barrier();
-            const int8_t *st = smem + ((k + 1) % NST) * kStage;
+            const int8_t *st = smem + ((k + 1) % NST) * C::kStage;
             const int dslab = k + NST;
-            // 4 reads up front, then 4 x [MFMA, read, MFMA, read, MFMA, DMA, MFMA]
-            nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
-            nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
-            nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
-            nxt.x[0][1] = *(const v4i *)(st + x_rd[1][0]);
-            nxt.w[0][2] = *(const v4i *)(st + w_rd[2][0]);
-            nxt.w[0][3] = *(const v4i *)(st + w_rd[3][0]);
-            nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
-            nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
-            nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
-            nxt.x[1][1] = *(const v4i *)(st + x_rd[1][1]);
-            nxt.w[1][2] = *(const v4i *)(st + w_rd[2][1]);
-            nxt.w[1][3] = *(const v4i *)(st + w_rd[3][1]);
-            dma1(dslab, 0, 0);
-            dma1(dslab, 0, 1);
-            dma1(dslab, 1, 0);
-            dma1(dslab, 1, 1);
-            mfma_half(cur, 0);
-            mfma_half(cur, 1);
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
+            if constexpr (NB == 4) {
+                // 12 reads, 4 DMA, 16 MFMA: 4 reads up front, then 4 x [M, R, M, R, M, D, M]
+                nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
+                nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
+                nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
+                nxt.x[0][1] = *(const v4i *)(st + x_rd[1][0]);
+                nxt.w[0][2] = *(const v4i *)(st + w_rd[2][0]);
+                nxt.w[0][3] = *(const v4i *)(st + w_rd[3][0]);
+                nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
+                nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
+                nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
+                nxt.x[1][1] = *(const v4i *)(st + x_rd[1][1]);
+                nxt.w[1][2] = *(const v4i *)(st + w_rd[2][1]);
+                nxt.w[1][3] = *(const v4i *)(st + w_rd[3][1]);
+                dma1(dslab, 0, 0);
+                dma1(dslab, 0, 1);
+                dma1(dslab, 1, 0);
+                dma1(dslab, 1, 1);
+                mfma_half(cur, 0);
+                mfma_half(cur, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+                for (int r = 0; r < 4; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
+            } else {
+                // 8 reads, 3 DMA, 8 MFMA: 4 reads up front, then 3 x [M, R, M, D] + [M, R, M]
+                nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
+                nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
+                nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
+                nxt.x[0][1] = *(const v4i *)(st + x_rd[1][0]);
+                nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
+                nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
+                nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
+                nxt.x[1][1] = *(const v4i *)(st + x_rd[1][1]);
+                dma1(dslab, 0, 0);
+                dma1(dslab, 0, 1);
+                dma1(dslab, 1, 0);
+                mfma_half(cur, 0);
+                mfma_half(cur, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
+#pragma unroll
+                for (int r = 0; r < 3; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
+                }
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         };
@@ -390,22 +400,26 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         }
         if (k < k1) step(X, Y, k);
         wait_vmcnt<0>();
-    };
+    }
 
     // ---- epilogue of tile (m0, n0) from acc.  acc[j][i][r]: n = 8 (r / 4) + 4 (lane / 32) + r % 4
     //      (4 consecutive per r / 4), m = lane % 32 within the 32 x 32 tile (j, i) ----
-    auto epilogue = [&](int m0, int n0) {
+    MICA_DEVICE void epilogue(const GemmParams &p, int8_t *smem, int m0, int n0) {
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int wm = wave / 2, wn = wave % 2;
+        const int r32 = lane & 31, khalf = lane >> 5;
+        const int M = p.M, N = p.N;
         const int mw = m0 + wm * WM;
         const int nw = n0 + wn * WN;
         const bool vec = p.vec_ok != 0;
-        const float *sc = (const float *)(smem + C::kScaleOff); // [0, 256): sa, [256, 512): sb, [512, 768): bias
+        const float *sc = (const float *)(smem + kScaleOff); // [0, 256): sa, [256, 512): sb, [512, 768): bias
         float sav[MB];
 #pragma unroll
         for (int i = 0; i < MB; ++i) sav[i] = sc[wm * WM + i * 32 + r32];
         if constexpr (OUT == MICA_BF16 || OUT == MICA_FP16) {
             // Staged through LDS: every wave writes its rounded 16-bit block (8 bytes per lane per
             // store) into its own padded region, then streams it out row-contiguously, 16 bytes per
-            // lane, so each global store covers whole 256-byte row segments.
+            // lane, so each global store covers whole 128- or 256-byte row segments.
             wait_lgkmcnt0();
             __builtin_amdgcn_s_barrier(); // every wave is done reading the operand stages
             int8_t *ep = smem + wave * kEpiWave;
@@ -453,8 +467,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
                 }
             }
             wait_lgkmcnt0(); // a wave reads back only its own region: no barrier needed
-            constexpr int kLanesPerRow = kCols / 8;          // 16 (SCALE) or 8 (SILU_MUL) lanes x 8 columns
-            constexpr int kRowsPerPass = 64 / kLanesPerRow;  // 4 or 8 rows per pass
+            constexpr int kLanesPerRow = kCols / 8;          // lanes x 8 columns per row
+            constexpr int kRowsPerPass = 64 / kLanesPerRow;
             const int cl = (lane % kLanesPerRow) * 8;        // local column of this lane's 8 values
             const int valid = ncols_out - (col0 + cl) < 8 ? (ncols_out - (col0 + cl) > 0 ? ncols_out - (col0 + cl) : 0) : 8;
             const bool vec8 = vec && (p.ldc % 8 == 0) && (!HAS_RES || p.ldr % 8 == 0);
@@ -538,57 +552,61 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
                     }
                 }
             }
-        } else {
-            // SILU_MUL: this wave's 128 B-rows are one interleave group g = nw / 128: rows [0, 64) are
-            // gate columns 64 g + [0, 64), rows [64, 128) the matching up columns (tiles j and j + 2).
-            const int g = nw >> 7;
-            const int Nout = N >> 1;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int nr = j * 32 + 8 * q + 4 * khalf; // row within the group's gate half
-                    const int col = g * 64 + nr;
-                    if (col >= Nout) continue; // whole groups only (N % 128 == 0)
-                    float sg[4], su[4];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        sg[t] = p.sb[nw + nr + t];
-                        su[t] = p.sb[nw + 64 + nr + t];
-                    }
-#pragma unroll
-                    for (int i = 0; i < MB; ++i) {
-                        const int m = mw + i * 32 + r32;
-                        if (m >= M) continue;
-                        float hv[4];
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * sg[t]);
-                            const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * su[t]);
-                            const float act = round_bf16(gv / (1.0f + expf(-gv)));
-                            hv[t] = act * uv;
-                        }
-                        store4<MICA_BF16>(p.C, (long)m * p.ldc + col, hv, 4, vec);
-                    }
-                }
+        }
+    }
+};
+
+template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES>
+__global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kSmem];
+    static_assert(EPI == MICA_EPI_SCALE || CfgFull::WN == 128,
+                  "the SiLU epilogue needs one 128-row gate/up group per wave");
+    const int tid = threadIdx.x;
+    const int K = p.K;
+    const int nk = (K + BK - 1) / BK;
+    const int G = gridDim.x;
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, p.M * p.lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, p.N * p.ldb, kBufferFlags);
+
+    TileEngine<CfgFull, EPI, OUT, HAS_BIAS, HAS_RES> full;
+
+    // ---- whole tiles: blockIdx.x, blockIdx.x + G, ... below dp_tiles ----
+    for (int pid = blockIdx.x; pid < p.dp_tiles; pid += G) {
+        int tm, tn;
+        tile_of(pid, p.tiles_m, p.tiles_n, tm, tn);
+        full.run(p, smem, rsrc_a, rsrc_b, tm * kTile, tn * kTile, 0, nk);
+        full.epilogue(p, smem, tm * kTile, tn * kTile);
+    }
+
+    // ---- half tiles: the next half_tiles tiles, each as two 256 x 128 halves ----
+    if constexpr (EPI == MICA_EPI_SCALE) {
+        if (p.half_tiles > 0) {
+            TileEngine<CfgHalf, EPI, OUT, HAS_BIAS, HAS_RES> half;
+            for (int h = blockIdx.x; h < 2 * p.half_tiles; h += G) {
+                int tm, tn;
+                tile_of(p.dp_tiles + (h >> 1), p.tiles_m, p.tiles_n, tm, tn);
+                const int n0 = tn * kTile + (h & 1) * CfgHalf::BN;
+                half.run(p, smem, rsrc_a, rsrc_b, tm * kTile, n0, 0, nk);
+                half.epilogue(p, smem, tm * kTile, n0);
             }
         }
-    };
+    }
 
-    // ---- split tiles: publish this workgroup's partial sums of tile `rel` (a stream-K tile) and
-    // report whether it arrived last, in which case acc now holds the tile's full sums ----
-    int *flag = (int *)(smem + C::kFlagOff);
+    if (p.sk_tiles == 0) return;
+    // ---- split tiles: this workgroup's stream-K range of (tile, slab) iterations.  A workgroup
+    // ending with part of a tile publishes its partial sums; the tile's last contributor to
+    // arrive adds the others' to its own and runs the epilogue ----
+    int *flag = (int *)(smem + kFlagOff);
     const long long W = (long long)p.sk_tiles * nk;
-    const int G = gridDim.x;
-    const long long my_begin = p.sk_tiles > 0 ? sk_begin(blockIdx.x, W, G) : 0;
-    const long long my_end = p.sk_tiles > 0 ? sk_begin(blockIdx.x + 1, W, G) : 0;
+    const long long my_begin = sk_begin(blockIdx.x, W, G);
+    const long long my_end = sk_begin(blockIdx.x + 1, W, G);
     // Partial sums move with device-scope (sc1) buffer stores and loads: written through to the
     // device's coherence point and read from it, so no cache-wide write-back or invalidation (a
     // device-scope fence) is needed, only the ordering below.
     constexpr int kDeviceScope = 16; // cache policy bits: sc1
-    constexpr int kSlotBytes = C::kPartialVecs * C::kThreads * 16;
+    constexpr int kSlotBytes = CfgFull::kPartialVecs * kThreads * 16;
     const __amdgpu_buffer_rsrc_t rsrc_p =
-        __builtin_amdgcn_make_buffer_rsrc((void *)p.partials, 0, p.sk_tiles > 0 ? G * 2 * kSlotBytes : 0, kBufferFlags);
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.partials, 0, G * 2 * kSlotBytes, kBufferFlags);
     auto slot_off = [&](int g, int seg) { return (g * 2 + seg) * kSlotBytes + tid * 16; };
     auto fixup = [&](int rel) -> bool {
         const long long tb = (long long)rel * nk;      // the tile's first iteration
@@ -596,14 +614,15 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         const int g0 = sk_owner(tb, W, G), g1 = sk_owner(tb + nk - 1, W, G);
         const int mine = slot_off(blockIdx.x, seg);
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
+        for (int j = 0; j < CfgFull::NB; ++j)
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
+            for (int i = 0; i < CfgFull::MB; ++i)
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     __builtin_amdgcn_raw_buffer_store_b128(
-                        v4i{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]},
-                        rsrc_p, mine + ((j * MB + i) * 4 + q) * C::kThreads * 16, 0, kDeviceScope);
+                        v4i{full.acc[j][i][4 * q], full.acc[j][i][4 * q + 1], full.acc[j][i][4 * q + 2],
+                            full.acc[j][i][4 * q + 3]},
+                        rsrc_p, mine + ((j * CfgFull::MB + i) * 4 + q) * kThreads * 16, 0, kDeviceScope);
         wait_vmcnt<0>();  // this wave's partial sums reached the coherence point ...
         __syncthreads();  // ... and every wave's, before the arrival is counted
         if (tid == 0) *flag = __hip_atomic_fetch_add(p.arrivals + rel, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -617,15 +636,15 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int j = h * NB / 2; j < (h + 1) * NB / 2; ++j)
+                for (int j = h * CfgFull::NB / 2; j < (h + 1) * CfgFull::NB / 2; ++j)
 #pragma unroll
-                    for (int i = 0; i < MB; ++i)
+                    for (int i = 0; i < CfgFull::MB; ++i)
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             const v4i v = __builtin_amdgcn_raw_buffer_load_b128(
-                                rsrc_p, src + ((j * MB + i) * 4 + q) * C::kThreads * 16, 0, kDeviceScope);
+                                rsrc_p, src + ((j * CfgFull::MB + i) * 4 + q) * kThreads * 16, 0, kDeviceScope);
 #pragma unroll
-                            for (int t = 0; t < 4; ++t) acc[j][i][4 * q + t] += v[t];
+                            for (int t = 0; t < 4; ++t) full.acc[j][i][4 * q + t] += v[t];
                         }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -633,36 +652,22 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         if (tid == 0) __hip_atomic_store(p.arrivals + rel, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return true;
     };
-
-    // ---- the workgroup's work list: whole tiles blockIdx.x, blockIdx.x + G, ... below dp_tiles,
-    // then its stream-K range of (tile, slab) iterations ----
-    int pid = blockIdx.x;
-    long long it = my_begin;
-    for (;;) {
-        int tm, tn, k0, k1, rel = -1;
-        if (pid < p.dp_tiles) {
-            tile_of(pid, p.tiles_m, p.tiles_n, tm, tn);
-            k0 = 0;
-            k1 = nk;
-            pid += G;
-        } else if (it < my_end) {
-            rel = (int)(it / nk);
-            k0 = (int)(it - (long long)rel * nk);
-            k1 = (long long)(nk - k0) < my_end - it ? nk : k0 + (int)(my_end - it);
-            tile_of(p.dp_tiles + rel, p.tiles_m, p.tiles_n, tm, tn);
-            it += k1 - k0;
-        } else {
-            break;
-        }
-        run(tm * BM, tn * BN, k0, k1);
+    for (long long it = my_begin; it < my_end;) {
+        const int rel = (int)(it / nk);
+        const int k0 = (int)(it - (long long)rel * nk);
+        const int k1 = (long long)(nk - k0) < my_end - it ? nk : k0 + (int)(my_end - it);
+        int tm, tn;
+        tile_of(p.dp_tiles + rel, p.tiles_m, p.tiles_n, tm, tn);
+        it += k1 - k0;
+        full.run(p, smem, rsrc_a, rsrc_b, tm * kTile, tn * kTile, k0, k1);
         if ((k0 != 0 || k1 != nk) && !fixup(rel)) continue;
-        epilogue(tm * BM, tn * BN);
+        full.epilogue(p, smem, tm * kTile, tn * kTile);
     }
 }
 
 template <int EPI, int OUT>
 int launch_out(const GemmParams &p, int grid_size, bool has_bias, bool has_res, hipStream_t st) {
-    dim3 grid(grid_size), block(CfgDefault::kThreads);
+    dim3 grid(grid_size), block(kThreads);
 #define MICA_G(B_, R_) hipLaunchKernelGGL((gemm_i8_kernel<EPI, OUT, B_, R_>), grid, block, 0, st, p)
     if (EPI == MICA_EPI_SILU_MUL) MICA_G(false, false);
     else if (has_bias && has_res) MICA_G(true, true);
@@ -677,7 +682,7 @@ int launch_out(const GemmParams &p, int grid_size, bool has_bias, bool has_res, 
 // (one per split tile, at most cus of them), padded to 4 KiB, then two partial-sum slots of
 // kPartialVecs x kThreads int32x4 per workgroup.
 constexpr long long kCounterBytes = 4096;
-constexpr long long kSlotBytes = (long long)CfgDefault::kPartialVecs * CfgDefault::kThreads * 16;
+constexpr long long kSlotBytes = (long long)CfgFull::kPartialVecs * kThreads * 16;
 long long workspace_bytes_for(int cus) { return kCounterBytes + (long long)cus * 2 * kSlotBytes; }
 
 int cu_count(int device) {
@@ -726,29 +731,37 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     GemmParams p{};
     p.A = A; p.B = B; p.sa = sa; p.sb = sb; p.bias = bias; p.res = residual; p.C = C;
     p.lda = lda; p.ldb = ldb; p.ldr = ldr; p.ldc = ldc; p.M = M; p.N = N; p.K = K;
-    p.tiles_m = (M + BM - 1) / BM;
-    p.tiles_n = (N + BN - 1) / BN;
+    p.tiles_m = (M + kTile - 1) / kTile;
+    p.tiles_n = (N + kTile - 1) / kTile;
     p.vec_ok = (ldc % 4 == 0) && (Nout % 4 == 0) && (!residual || ldr % 4 == 0);
     const long long tiles = (long long)p.tiles_m * p.tiles_n;
     if (tiles >= (1ll << 31)) return MICA_MISS_RANGE;
-    // Schedule.  Whole tiles, one workgroup each, unless the last round of tiles would leave CUs
-    // idle: then the remainder tiles are split along K over a persistent grid of one workgroup per
-    // CU, provided every workgroup gets at least kMinSlabs slabs and the workspace is there.
+    // Schedule over a grid of at most one workgroup per CU.  Whole tiles, one per workgroup per
+    // round; when the last round would be at most half full, its tiles run as two 256 x 128 halves
+    // each instead (the halves fill up to one round; SCALE epilogue only).  With a workspace, a
+    // partial last round is instead split along K over all CUs, provided every workgroup gets at
+    // least kMinSlabs slabs.
     constexpr int kMinSlabs = 4;
     p.dp_tiles = (int)tiles;
+    p.half_tiles = 0;
     p.sk_tiles = 0;
     int grid = (int)tiles;
     int dev = 0;
-    if (workspace != nullptr && hipGetDevice(&dev) == hipSuccess) {
-        const int cus = cu_count(dev);
-        const long long nk = (K + BK - 1) / BK;
-        const long long rem = cus > 0 ? tiles % cus : 0;
-        if (rem != 0 && cus <= 1024 && workspace_bytes >= workspace_bytes_for(cus) && rem * nk >= (long long)kMinSlabs * cus) {
+    const int cus = hipGetDevice(&dev) == hipSuccess ? cu_count(dev) : 0;
+    const long long nk = (K + BK - 1) / BK;
+    const long long rem = cus > 0 ? tiles % cus : 0;
+    if (rem != 0 && cus <= 1024) {
+        if (workspace != nullptr && workspace_bytes >= workspace_bytes_for(cus) && rem * nk >= (long long)kMinSlabs * cus) {
             p.dp_tiles = (int)(tiles - rem);
             p.sk_tiles = (int)rem;
             p.arrivals = (int *)workspace;
             p.partials = (v4i *)((char *)workspace + kCounterBytes);
             grid = cus;
+        } else if (epilogue == MICA_EPI_SCALE && 2 * rem <= cus) {
+            p.dp_tiles = (int)(tiles - rem);
+            p.half_tiles = (int)rem;
+            grid = cus < tiles ? cus : (int)tiles;
+            if (grid < 2 * rem) grid = (int)(2 * rem);
         }
     }
     hipStream_t st = (hipStream_t)stream;
