@@ -201,6 +201,25 @@ def main():
 
     if not args.no_extra:
         extra = {}
+        # the headline GEMM with cold caches: before each launch a 512 MiB fill evicts the operands from
+        # L2 and the 256 MB Infinity Cache; each launch is timed on its own (events around the GEMM only)
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        gemm = gemm_launcher(torch, lib, qx, sx, qw, sw, out)
+        times = []
+        for i in range(args.warmup + 20):
+            flush.fill_(i & 0xff)
+            s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s_ev.record()
+            gemm()
+            e_ev.record()
+            e_ev.synchronize()
+            if i >= args.warmup:
+                times.append(s_ev.elapsed_time(e_ev))
+        del flush
+        ms_c = statistics.median(times)
+        extra["gemm_headline_cold_caches"] = {"us": round(ms_c * 1e3, 2), "TOPS": round(ops / (ms_c * 1e-3) / 1e12, 1),
+                                              "pct_peak": round(100 * ops / (ms_c * 1e-3) / 1e12 / PEAK_INT8_TOPS, 1),
+                                              "launches": len(times), "note": "median; 512 MiB fill before each"}
         # fused RMSNorm + quant (config 1): T * (2K + K + 4) + 2K algorithmic bytes
         for T in (4096, 32768):
             g = torch.Generator().manual_seed(T)

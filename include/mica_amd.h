@@ -94,6 +94,21 @@ int mica_rmsnorm_quant(const void *x, int x_dtype, int ldx, const void *residual
                        void *sum, int lds, int M, int K, int rounding, mica_stream_t stream);
 
 /*
+ * The same fused RMSNorm, with the normed row quantized for n_out (1 to 4) consumers at once: the
+ * input projections that share one norm in the reference model (q/k/v, or the linear-attention
+ * in_proj_qkv / in_proj_z / in_proj_a / in_proj_b, or gate/up), each with its own SmoothQuant
+ * factors (int8_quant.py:64-73 with inv_smooth = that QLinear's buffer, int8_runtime.py:124-127),
+ * so the row is read once instead of once per consumer.  inv_smooth, q, ldq and s are host arrays of
+ * n_out entries (device pointers; an inv_smooth entry may be NULL: no smoothing for that consumer).
+ * Output o is bit-identical to mica_rmsnorm_quant with inv_smooth[o], q[o], ldq[o], s[o].
+ * No counterpart in the reference, whose QLinears each quantize the shared normed row themselves.
+ */
+int mica_rmsnorm_quant_multi(const void *x, int x_dtype, int ldx, const void *residual, int ldr, const void *w,
+                             int w_dtype, float offset, float eps, int n_out, const float *const *inv_smooth,
+                             int8_t *const *q, const int *ldq, float *const *s, void *y, int ldy, void *sum, int lds,
+                             int M, int K, int rounding, mica_stream_t stream);
+
+/*
  * W8A8 GEMM on the gfx950 i8 matrix cores: acc[m, n] = sum_k A[m, k] * B[n, k] (exact int32),
  * then the epilogue.  Replaces int8_kernels.mm_i8 (v0.5/serving/lib/int8_kernels.py:359-406),
  * Triton mm_i8 (kernel_src/kernels.py:40-68); CPU fallback int8_runtime.py:186-192.

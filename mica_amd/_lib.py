@@ -34,6 +34,8 @@ SIGNATURES = {
     "mica_act_quant": (_I, [_P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _P]),
     "mica_rmsnorm_quant": (_I, [_P, _I, _I, _P, _I, _P, _I, _F, _F, _P, _P, _I, _P, _P, _I, _P, _I, _I, _I, _I,
                                 _P]),
+    "mica_rmsnorm_quant_multi": (_I, [_P, _I, _I, _P, _I, _P, _I, _F, _F, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I,
+                                      _I, _P]),
     "mica_mm_i8": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _LL, _P]),
     "mica_mm_i8_workspace_bytes": (_LL, [_I]),
     "mica_swiglu": (_I, [_P, _P, _P, _LL, _I, _P]),

@@ -22,16 +22,22 @@ constexpr int kChunk = 8;          // elements per lane per chunk
 constexpr int kRowStep = 64 * kChunk; // elements per chunk across the wave
 
 
+constexpr int kMaxOut = 4; // quantized copies one row launch can write (mica_rmsnorm_quant_multi)
+
 struct RowParams {
     const void *x;
     const void *res;
     const void *w;
-    const float *inv;
-    int8_t *q;
-    float *s;
+    // the quantized outputs: n_out of them, each with its own smoothing factors (or NULL), int8
+    // rows (row stride ldq) and per-row scales
+    const float *inv[kMaxOut];
+    int8_t *q[kMaxOut];
+    float *s[kMaxOut];
+    int ldq[kMaxOut];
+    int n_out;
     void *y;
     void *sum;
-    int ldx, ldr, ldq, ldy, lds;
+    int ldx, ldr, ldy, lds;
     int M, K;
     int w_dtype;
     int rounding;
@@ -133,14 +139,15 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
 }
 
 // XT: dtype of x / residual / y / sum (bf16 or fp16).  NORM: apply the RMSNorm first.
-// HAS_INV: multiply by inv_smooth before the absmax (forces the IEEE-division quotient).
+// HAS_INV: some output multiplies by its inv_smooth before the absmax (that output then uses the
+// IEEE-division quotient).
 // FULL: K == NCH * 512, so no chunk needs a bounds mask.  RND: rounding mode (2: at run time).
 // Each wave prefetches its next row while it works on the current one; the row is unpacked to
 // fp32 once, and after the norm it stays in fp32 registers (already rounded to XT), so the
 // absmax and the quantizer work on registers.
 template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
 __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
-    constexpr bool kFast = (XT == MICA_BF16) && !HAS_INV;
+    constexpr bool kFast = XT == MICA_BF16; // the fast quotient is exact for unsmoothed bf16 rows
     const int lane = threadIdx.x & 63;
     const int nwaves = gridDim.x * (blockDim.x >> 6);
     const int K = p.K;
@@ -181,17 +188,6 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
     // unpacked again in each pass, which keeps enough waves resident.
     constexpr bool kF32 = NCH <= 8;
     constexpr bool kPrefetch = NCH <= 5; // long rows already keep enough bytes in flight per wave
-    auto unpack_inv = [&](const u32x4 &raw, int c, float (&a)[kChunk]) {
-        unpack8<XT>(raw, a);
-        if (HAS_INV) {
-            const int idx = c * kRowStep + lane * kChunk;
-            float iv[kChunk];
-            if (live(c)) load_inv8(p.inv, idx, iv);
-            else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kChunk; ++j) a[j] = a[j] * iv[j];
-        }
-    };
     auto process = [&](u32x4 (&cur)[NCH], int row) {
         if (NORM && p.res != nullptr) {
             // v = (x + r) rounded to the activation dtype (fused_kernels.py:27-30, :52)
@@ -243,46 +239,56 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
                 if (p.y != nullptr && live(c)) *(u32x4 *)((uint16_t *)p.y + (long)row * p.ldy + idx) = packed;
             }
         }
-        if (p.q == nullptr) return;
-        if (kF32 && HAS_INV) {
+        // the quantized outputs: per output, the absmax of the (smoothed) row, its scale, then the
+        // int8 row.  The smoothing product x * inv is formed on the fly in both passes, so the row
+        // itself stays unsmoothed for the next output.  Masked chunks hold zeros.
+#pragma unroll 1
+        for (int o = 0; o < p.n_out; ++o) {
+            const float *inv = HAS_INV ? p.inv[o] : nullptr;
+            auto chunk = [&](int c, float (&t)[kChunk]) {
+                if (kF32) {
+#pragma unroll
+                    for (int j = 0; j < kChunk; ++j) t[j] = v[kF32 ? c : 0][j];
+                } else {
+                    unpack8<XT>(cur[c], t);
+                }
+                if (HAS_INV && inv != nullptr) {
+                    float iv[kChunk];
+                    if (live(c)) load_inv8(inv, c * kRowStep + lane * kChunk, iv);
+                    else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < kChunk; ++j) t[j] = t[j] * iv[j];
+                }
+            };
+            float amax = 0.0f;
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                const int idx = c * kRowStep + lane * kChunk;
-                float iv[kChunk];
-                if (live(c)) load_inv8(p.inv, idx, iv);
-                else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
+                float t[kChunk];
+                chunk(c, t);
 #pragma unroll
-                for (int j = 0; j < kChunk; ++j) v[kF32 ? c : 0][j] = v[kF32 ? c : 0][j] * iv[j];
+                for (int j = 0; j < kChunk; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(t[j]));
             }
-        }
-        // absmax of the (smoothed) row; masked chunks hold zeros
-        float amax = 0.0f;
+            amax = wave_max(amax);
+            if (!kF32) {
+                // the quantizer unpacks the row again: keep the compiler from holding the first
+                // pass's fp32 values live instead (that would cost the registers kF32 = false saves)
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            float t[kChunk];
-            if (!kF32) unpack_inv(cur[c], c, t);
-            const float(&a)[kChunk] = kF32 ? v[kF32 ? c : 0] : t;
+                for (int c = 0; c < NCH; ++c) __asm__ volatile("" : "+v"(cur[c]));
+            }
+            const float sc = row_scale(amax);
+            const float r = 1.0f / sc;
+            if (lane == 0) p.s[o][row] = sc;
+            int8_t *qr = p.q[o] + (long)row * p.ldq[o];
+            const bool smoothed = HAS_INV && inv != nullptr;
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(a[j]));
-        }
-        amax = wave_max(amax);
-        if (!kF32) {
-            // the quantizer unpacks the row again: keep the compiler from holding the first
-            // pass's fp32 values live instead (that would cost the registers kF32 = false saves)
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) __asm__ volatile("" : "+v"(cur[c]));
-        }
-        const float s = row_scale(amax);
-        const float r = 1.0f / s;
-        if (lane == 0) p.s[row] = s;
-        int8_t *qr = p.q + (long)row * p.ldq;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int idx = c * kRowStep + lane * kChunk;
-            float t[kChunk];
-            if (!kF32) unpack_inv(cur[c], c, t);
-            const float(&a)[kChunk] = kF32 ? v[kF32 ? c : 0] : t;
-            if (live(c)) quant_store8r<kFast, RND>(a, s, r, p.rounding, qr + idx);
+            for (int c = 0; c < NCH; ++c) {
+                float t[kChunk];
+                chunk(c, t);
+                if (!live(c)) continue;
+                // smoothed values are fp32 products (not bf16): IEEE quotient
+                if (smoothed) quant_store8r<false, RND>(t, sc, r, p.rounding, qr + c * kRowStep + lane * kChunk);
+                else quant_store8r<kFast, RND>(t, sc, r, p.rounding, qr + c * kRowStep + lane * kChunk);
+            }
         }
     };
 
@@ -326,7 +332,7 @@ __global__ __launch_bounds__(256) void row32_kernel(RowParams p) {
                 v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
                 if (HAS_INV) {
                     float iv[kChunk];
-                    load_inv8(p.inv, idx, iv);
+                    load_inv8(p.inv[0], idx, iv);
 #pragma unroll
                     for (int j = 0; j < kChunk; ++j) v[c][j] = v[c][j] * iv[j];
                 }
@@ -340,8 +346,8 @@ __global__ __launch_bounds__(256) void row32_kernel(RowParams p) {
         amax = wave_max(amax);
         const float s = row_scale(amax);
         const float r = 1.0f / s;
-        if (lane == 0) p.s[row] = s;
-        int8_t *qr = p.q + (long)row * p.ldq;
+        if (lane == 0) p.s[0][row] = s;
+        int8_t *qr = p.q[0] + (long)row * p.ldq[0];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int idx = c * kRowStep + lane * kChunk;
@@ -474,41 +480,78 @@ extern "C" int mica_act_quant(const void *x, int x_dtype, int ldx, const float *
         return MICA_MISS_ALIGN;
     if (M == 0) return 0;
     RowParams p{};
-    p.x = x; p.inv = inv_smooth; p.q = q; p.s = s;
-    p.ldx = ldx; p.ldq = ldq; p.M = M; p.K = K; p.rounding = rounding;
+    p.x = x;
+    p.inv[0] = inv_smooth; p.q[0] = q; p.s[0] = s; p.ldq[0] = ldq; p.n_out = 1;
+    p.ldx = ldx; p.M = M; p.K = K; p.rounding = rounding;
     return dispatch_rows(p, x_dtype, false, inv_smooth != nullptr, (hipStream_t)stream);
 }
 
-extern "C" int mica_rmsnorm_quant(const void *x, int x_dtype, int ldx, const void *residual, int ldr, const void *w,
-                                  int w_dtype, float offset, float eps, const float *inv_smooth, int8_t *q, int ldq,
-                                  float *s, void *y, int ldy, void *sum, int lds, int M, int K, int rounding,
-                                  mica_stream_t stream) {
-    if (x == nullptr || w == nullptr || (q == nullptr && y == nullptr)) return MICA_MISS_ARG;
-    if (q != nullptr && s == nullptr) return MICA_MISS_ARG;
+namespace {
+
+// Checks and launch shared by the one- and several-output RMSNorm + quantizer entry points.
+int rmsnorm_quant_n(const void *x, int x_dtype, int ldx, const void *residual, int ldr, const void *w, int w_dtype,
+                    float offset, float eps, int n_out, const float *const *inv_smooth, int8_t *const *q,
+                    const int *ldq, float *const *s, void *y, int ldy, void *sum, int lds, int M, int K, int rounding,
+                    mica_stream_t stream) {
+    if (x == nullptr || w == nullptr || (n_out == 0 && y == nullptr)) return MICA_MISS_ARG;
+    if (n_out < 0 || n_out > kMaxOut) return MICA_MISS_ARG;
     if (sum != nullptr && residual == nullptr) return MICA_MISS_ARG;
     if (x_dtype != MICA_BF16 && x_dtype != MICA_FP16) return MICA_MISS_DTYPE;
     if (w_dtype != MICA_BF16 && w_dtype != MICA_FP16 && w_dtype != MICA_FP32) return MICA_MISS_DTYPE;
     if (rounding != MICA_ROUND_EVEN && rounding != MICA_ROUND_AWAY) return MICA_MISS_ARG;
     if (M < 0 || K < 8 || K > 16384 || K % 8 != 0) return MICA_MISS_SHAPE;
-    if (!ld_ok(ldx, K) || (residual && !ld_ok(ldr, K)) || (q && !ld_ok(ldq, K)) || (y && !ld_ok(ldy, K)) ||
-        (sum && !ld_ok(lds, K)))
+    if (!ld_ok(ldx, K) || (residual && !ld_ok(ldr, K)) || (y && !ld_ok(ldy, K)) || (sum && !ld_ok(lds, K)))
         return MICA_MISS_STRIDE;
     long long maxld = ldx;
     if (residual && ldr > maxld) maxld = ldr;
-    if (q && ldq > maxld) maxld = ldq;
     if (y && ldy > maxld) maxld = ldy;
     if (sum && lds > maxld) maxld = lds;
+    bool has_inv = false;
+    for (int o = 0; o < n_out; ++o) {
+        if (q[o] == nullptr || s[o] == nullptr) return MICA_MISS_ARG;
+        if (!ld_ok(ldq[o], K)) return MICA_MISS_STRIDE;
+        if (ldq[o] > maxld) maxld = ldq[o];
+        if (!mica_aligned16(q[o]) || !mica_aligned16(s[o]) || (inv_smooth[o] && !mica_aligned16(inv_smooth[o])))
+            return MICA_MISS_ALIGN;
+        has_inv = has_inv || inv_smooth[o] != nullptr;
+    }
     if ((long long)M * maxld >= (1ll << 31)) return MICA_MISS_RANGE;
     if (!mica_aligned16(x) || !mica_aligned16(w) || (residual && !mica_aligned16(residual)) ||
-        (q && !mica_aligned16(q)) || (s && !mica_aligned16(s)) || (y && !mica_aligned16(y)) ||
-        (sum && !mica_aligned16(sum)) || (inv_smooth && !mica_aligned16(inv_smooth)))
+        (y && !mica_aligned16(y)) || (sum && !mica_aligned16(sum)))
         return MICA_MISS_ALIGN;
     if (M == 0) return 0;
     RowParams p{};
-    p.x = x; p.res = residual; p.w = w; p.inv = inv_smooth; p.q = q; p.s = s; p.y = y; p.sum = sum;
-    p.ldx = ldx; p.ldr = ldr; p.ldq = ldq; p.ldy = ldy; p.lds = lds;
+    p.x = x; p.res = residual; p.w = w; p.y = y; p.sum = sum;
+    for (int o = 0; o < n_out; ++o) {
+        p.inv[o] = inv_smooth[o]; p.q[o] = q[o]; p.s[o] = s[o]; p.ldq[o] = ldq[o];
+    }
+    p.n_out = n_out;
+    p.ldx = ldx; p.ldr = ldr; p.ldy = ldy; p.lds = lds;
     p.M = M; p.K = K; p.w_dtype = w_dtype; p.rounding = rounding; p.offset = offset; p.eps = eps;
-    return dispatch_rows(p, x_dtype, true, inv_smooth != nullptr && q != nullptr, (hipStream_t)stream);
+    return dispatch_rows(p, x_dtype, true, has_inv, (hipStream_t)stream);
+}
+
+}  // namespace
+
+extern "C" int mica_rmsnorm_quant(const void *x, int x_dtype, int ldx, const void *residual, int ldr, const void *w,
+                                  int w_dtype, float offset, float eps, const float *inv_smooth, int8_t *q, int ldq,
+                                  float *s, void *y, int ldy, void *sum, int lds, int M, int K, int rounding,
+                                  mica_stream_t stream) {
+    if (q != nullptr && s == nullptr) return MICA_MISS_ARG;
+    const int n_out = q != nullptr ? 1 : 0;
+    return rmsnorm_quant_n(x, x_dtype, ldx, residual, ldr, w, w_dtype, offset, eps, n_out, &inv_smooth, &q, &ldq, &s, y,
+                           ldy, sum, lds, M, K, rounding, stream);
+}
+
+extern "C" int mica_rmsnorm_quant_multi(const void *x, int x_dtype, int ldx, const void *residual, int ldr,
+                                        const void *w, int w_dtype, float offset, float eps, int n_out,
+                                        const float *const *inv_smooth, int8_t *const *q, const int *ldq,
+                                        float *const *s, void *y, int ldy, void *sum, int lds, int M, int K,
+                                        int rounding, mica_stream_t stream) {
+    if (n_out < 1 || n_out > kMaxOut || inv_smooth == nullptr || q == nullptr || ldq == nullptr || s == nullptr)
+        return MICA_MISS_ARG;
+    return rmsnorm_quant_n(x, x_dtype, ldx, residual, ldr, w, w_dtype, offset, eps, n_out, inv_smooth, q, ldq, s, y,
+                           ldy, sum, lds, M, K, rounding, stream);
 }
 
 extern "C" int mica_swiglu(const void *g, const void *u, void *y, long long n, int dtype, mica_stream_t stream) {

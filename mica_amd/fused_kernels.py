@@ -4,11 +4,14 @@ plus the fused RMSNorm + INT8 quantizer of the W8A8 hot path, on the gfx950 HIP 
   rms_norm(x, weight, eps, residual=None)            fused_kernels.py:50-82
   swi_glu(gate, up)                                  fused_kernels.py:85-96
   rms_norm_quant(x, weight, eps, ...)                new: the norm and QLinear's act_quant in one pass
+  rms_norm_quant_multi(x, weight, eps, inv_smooths)  new: one norm, quantized for up to 4 consumers
 
 The reference runs Triton here on a GPU and torch formulas on the CPU; this build has no CPU compute
 path: a CPU tensor raises ValueError (the reference raises ValueError for unsupported layouts, :57-58).
 """
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -65,6 +68,60 @@ def _launch_norm(x, weight, eps, residual, offset, inv_smooth, want_q, want_y, r
     _launched()
     shape = x.shape
     return (q, s, None if y is None else y.view(shape), None if summed is None else summed.view(shape))
+
+
+def rms_norm_quant_multi(x, weight, eps, inv_smooths, residual=None, offset=1.0, rounding="even"):
+    """One RMSNorm of x, quantized per token for each of ``len(inv_smooths)`` (1 to 4) consumers,
+    consumer i with its own SmoothQuant factors ``inv_smooths[i]`` (fp32 [K], or None): one read of x.
+
+    Returns a list of (q_i, s_i), each equal to ``rms_norm_quant(x, weight, eps, inv_smooths[i], ...)``,
+    plus the summed input v when ``residual`` is given: ([(q, s), ...], v).
+    """
+    _check_row_input(x, weight, residual)
+    K = x.shape[-1]
+    n = len(inv_smooths)
+    if not 1 <= n <= 4:
+        raise ValueError("rms_norm_quant_multi takes 1 to 4 consumers")
+    for inv in inv_smooths:
+        if inv is not None and (inv.dtype != torch.float32 or inv.numel() != K or not inv.is_contiguous()
+                                or inv.device != x.device):
+            raise ValueError("each inv_smooth must be None or a contiguous fp32 [K] tensor on x's device")
+    flat = x.reshape(-1, K)
+    if flat.stride(0) != K:
+        flat = flat.contiguous()
+    M = flat.shape[0]
+    res = None
+    if residual is not None:
+        res = residual.reshape(-1, K)
+        if not res.is_contiguous():
+            res = res.contiguous()
+    dev = x.device
+    qs = [torch.empty((M, K), dtype=torch.int8, device=dev) for _ in range(n)]
+    ss = [torch.empty((M,), dtype=torch.float32, device=dev) for _ in range(n)]
+    summed = torch.empty((M, K), dtype=x.dtype, device=dev) if res is not None else None
+    tensors = [t for t in [flat, weight, res, summed, *qs, *ss, *inv_smooths] if t is not None]
+    if not _aligned(*tensors):
+        raise ValueError("fused RMSNorm requires 16-byte aligned rows")
+    if not _gpu_ok(dev):
+        raise RuntimeError(f"mica_amd kernels need a gfx950 GPU (device {dev})")
+    L = _lib.load()
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    P = ctypes.c_void_p
+    invs = (P * n)(*[ptr(t) for t in inv_smooths])
+    qp = (P * n)(*[t.data_ptr() for t in qs])
+    sp = (P * n)(*[t.data_ptr() for t in ss])
+    ldq = (ctypes.c_int * n)(*([K] * n))
+    rc = _lib.check(_on(dev, lambda: L.mica_rmsnorm_quant_multi(
+        ptr(flat), NORM_DT[x.dtype], K, ptr(res), K, ptr(weight), DT[weight.dtype], float(offset), float(eps), n,
+        invs, qp, ldq, sp, None, K, ptr(summed), K, M, K, ROUNDING[rounding], _stream(dev))),
+        "mica_rmsnorm_quant_multi")
+    if rc > 0:
+        reason = _lib.status_name(rc)
+        _miss("norm_" + reason)
+        raise ValueError(f"fused RMSNorm does not support this input ({reason})")
+    _launched()
+    out = list(zip(qs, ss))
+    return out if residual is None else (out, summed.view(x.shape))
 
 
 def rms_norm(x, weight, eps, residual=None, offset=1.0):

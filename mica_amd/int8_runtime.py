@@ -14,7 +14,7 @@ import torch
 from torch import nn
 
 from . import int8_kernels as aot
-from .fused_kernels import rms_norm_quant
+from .fused_kernels import rms_norm_quant, rms_norm_quant_multi
 
 EPS = 1e-08              # int8_quant.py:13
 QMAX = 127.0             # int8_quant.py:11
@@ -230,6 +230,35 @@ class W8A8MLP(nn.Module):
         qh, sh = _hit(aot.act_quant(g), "act_quant")
         out = self.down.forward_quantized(qh, sh, residual=h.reshape(-1, shape[-1]))
         return out.reshape(shape)
+
+
+class SharedNormQLinears(nn.Module):
+    """An RMSNorm and the W8A8 linears that consume its output: the reference model's q/k/v
+    projections, or its linear-attention in_proj_qkv / in_proj_z / in_proj_a / in_proj_b (each a
+    QLinear with its own SmoothQuant factors, int8_runtime.py:124-127, fed by one input_layernorm,
+    fork.py:394-422).  forward(h) normalizes h once, quantizes it for every linear in one kernel
+    (each with that linear's inv_smooth) and runs one GEMM per linear: 1 + len(linears) launches."""
+
+    def __init__(self, norm_weight, eps, linears, offset=1.0):
+        super().__init__()
+        if not 1 <= len(linears) <= 4:
+            raise ValueError("SharedNormQLinears takes 1 to 4 linears")
+        if len({q.in_features for q in linears}) != 1:
+            raise ValueError("the linears must share their input width")
+        self.register_buffer("norm_weight", norm_weight.contiguous())
+        self.eps, self.offset = float(eps), float(offset)
+        self.linears = nn.ModuleList(linears)
+
+    def forward(self, h, residual=None):
+        """Returns [y_i] for each linear (and the summed input with a residual: ([y_i], h + residual))."""
+        _require_gpu(h)
+        shape = h.shape
+        r = rms_norm_quant_multi(h, self.norm_weight, self.eps, [q.inv_smooth for q in self.linears],
+                                 residual=residual, offset=self.offset)
+        qs, summed = (r, None) if residual is None else r
+        outs = [lin.forward_quantized(qx, sx).reshape(*shape[:-1], lin.out_features)
+                for lin, (qx, sx) in zip(self.linears, qs)]
+        return outs if residual is None else (outs, summed)
 
 
 # ---------------------------------------------------------------------------------- self-test

@@ -109,6 +109,28 @@ def test_rmsnorm_quant_rejects():
     assert call(M=0) == 0
 
 
+def test_rmsnorm_quant_multi_rejects():
+    import ctypes
+    lib = _lib.load()
+    P = ctypes.c_void_p
+
+    def call(n, q=A16, ldq=64, inv=None, arrays=True, M=4):
+        invs, qs, ss = (P * 5)(*([inv] * 5)), (P * 5)(*([q] * 5)), (P * 5)(*([A16] * 5))
+        lds = (ctypes.c_int * 5)(*([ldq] * 5))
+        if not arrays:
+            invs = None
+        return lib.mica_rmsnorm_quant_multi(A16, 0, 64, None, 0, A16, 0, 1.0, 1e-6, n, invs, qs, lds, ss, None, 0,
+                                            None, 0, M, 64, 0, None)
+
+    assert call(0) == 6                    # no consumer
+    assert call(5) == 6                    # more than 4
+    assert call(2, arrays=False) == 6      # missing pointer array
+    assert call(2, q=None) == 6            # a consumer without int8 output
+    assert call(2, ldq=32) == 4            # a consumer's row stride < K
+    assert call(2, inv=A16 + 4) == 3       # misaligned smoothing factors
+    assert call(4, M=0) == 0
+
+
 def test_gather_logits_rejects():
     lib = _lib.load()
     # (h, ldh, n_rows, rows, B, norm_w, norm_dtype, offset, eps, W, w_dtype, ldw, w_rows, ids, L, K, logits,

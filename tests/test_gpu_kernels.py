@@ -159,6 +159,56 @@ def test_rmsnorm_quant_residual_and_smoothing(gpu):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
 
 
+@pytest.mark.parametrize("T,K", [(333, 2560), (64, 1000), (257, 9728)])
+def test_rmsnorm_quant_multi_consumers(gpu, T, K):
+    """One norm quantized for 3 consumers (unsmoothed, two different SmoothQuant factors): each output is
+    bit-identical to the single-consumer launch, and to the reference quantizer applied to the kernel's
+    normed row times that consumer's factors."""
+    note(f"rmsnorm_quant_multi T={T} K={K}")
+    rng = np.random.default_rng(T + K)
+    xb, rb = act_bits(rng, (T, K)), act_bits(rng, (T, K), outliers=0)
+    x, r = to_gpu_bf16(xb), to_gpu_bf16(rb)
+    w = O.round_bf16(rng.normal(0.0, 0.1, K).astype(np.float32))
+    wt = to_gpu_bf16(O.f32_to_bf16(w))
+    invs = [None] + [rng.uniform(0.3, 3.0, K).astype(np.float32) for _ in range(2)]
+    tinvs = [None if v is None else torch.from_numpy(v).cuda() for v in invs]
+    outs, v = fused_kernels.rms_norm_quant_multi(x, wt, 1e-6, tinvs, residual=r)
+    _, _, y, v1 = fused_kernels.rms_norm_quant(x, wt, 1e-6, residual=r, return_normed=True)
+    assert np.array_equal(bits_of(v), bits_of(v1))
+    yk = bits_of(y)
+    for i, ((q, s), inv, tinv) in enumerate(zip(outs, invs, tinvs)):
+        q1, s1, _ = fused_kernels.rms_norm_quant(x, wt, 1e-6, inv_smooth=tinv, residual=r)
+        assert np.array_equal(q.cpu().numpy(), q1.cpu().numpy()), f"consumer {i}"
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), s1.cpu().numpy().view(np.uint32)), f"consumer {i}"
+        qo, so = O.quant_act(O.bf16_to_f32(yk), inv)
+        assert np.array_equal(q.cpu().numpy(), qo), f"consumer {i} vs oracle"
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32)), f"consumer {i} vs oracle"
+
+
+def test_shared_norm_qlinears_match_separate_path(gpu):
+    """SharedNormQLinears (one norm + quant launch for q/k/v-style consumers, then a GEMM each) gives the
+    bits of the reference's call pattern: rms_norm, then each QLinear quantizing with its own factors."""
+    note("shared-norm qlinears")
+    rng = np.random.default_rng(5)
+    T, K = 300, 2560
+    h = to_gpu_bf16(act_bits(rng, (T, K)))
+    nw = to_gpu_bf16(O.f32_to_bf16(O.round_bf16(rng.normal(0.0, 0.1, K).astype(np.float32))))
+    lins = []
+    for n, smooth in ((1024, True), (512, False), (512, True)):
+        qw = torch.from_numpy(rng.integers(-127, 128, (n, K), dtype=np.int8)).cuda()
+        sw = torch.from_numpy(rng.uniform(1e-3, 1e-2, n).astype(np.float32)).cuda()
+        inv = torch.from_numpy(rng.uniform(0.5, 2.0, K).astype(np.float32)).cuda() if smooth else None
+        lins.append(int8_runtime.QLinear.from_quantized(qw, sw, inv_smooth=inv))
+    mod = int8_runtime.SharedNormQLinears(nw, 1e-6, lins)
+    l0 = int8_kernels.STATS["launch"]
+    outs = mod(h)
+    torch.cuda.synchronize()
+    assert int8_kernels.STATS["launch"] - l0 == 1 + len(lins)
+    y = fused_kernels.rms_norm(h, nw, 1e-6)
+    for lin, o in zip(lins, outs):
+        assert np.array_equal(bits_of(o), bits_of(lin(y)))
+
+
 def test_rms_norm_op_matches_reference_surface(gpu):
     """fused_kernels.rms_norm(x, w, eps, residual) -> y / (y, summed), the reference's signature."""
     note("rms_norm op")
