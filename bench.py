@@ -241,6 +241,29 @@ def main():
             gbs = nbytes / (ms_n * 1e-3) / 1e9
             extra[f"rmsnorm_quant_T{T}"] = {"us": round(ms_n * 1e3, 2), "GB/s": round(gbs, 1),
                                            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
+            if T == 4096:
+                # one norm for 3 consumers (the q / k / v pattern), unsmoothed and with SmoothQuant factors,
+                # through the C ABI on preallocated outputs: T * (2K + 3 (K + 4)) + 2K (+ 3 * 4K) bytes
+                import ctypes
+                P = ctypes.c_void_p
+                invs = [(torch.rand(K, generator=g) + 0.5).to(dev) for _ in range(3)]
+                q3 = [torch.empty(T, K, dtype=torch.int8, device=dev) for _ in range(3)]
+                s3 = [torch.empty(T, dtype=torch.float32, device=dev) for _ in range(3)]
+                qp, sp = (P * 3)(*[t.data_ptr() for t in q3]), (P * 3)(*[t.data_ptr() for t in s3])
+                ld3 = (ctypes.c_int * 3)(K, K, K)
+                for tag, iv in (("", [None] * 3), ("_smoothed", [t.data_ptr() for t in invs])):
+                    ivp = (P * 3)(*iv)
+                    a3 = (h.data_ptr(), _lib.BF16, K, None, K, w.data_ptr(), _lib.BF16, 0.0, 1e-6, 3, ivp, qp, ld3, sp,
+                          None, K, None, K, T, K, 0, stream)
+
+                    def norm3(a3=a3):
+                        if lib.mica_rmsnorm_quant_multi(*a3) != 0:
+                            raise RuntimeError("mica_rmsnorm_quant_multi failed")
+                    ms_3 = timer.run(norm3, 50, args.warmup)
+                    b3 = T * (2 * K + 3 * (K + 4)) + 2 * K + (12 * K if tag else 0)
+                    extra[f"rmsnorm_quant_3consumers{tag}_T4096"] = {
+                        "us": round(ms_3 * 1e3, 2), "GB/s": round(b3 / (ms_3 * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(b3 / (ms_3 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": b3}
         # the 4B layer's GEMMs at T = 4096 and the per-layer W8A8 hot path
         T = 4096
         layer = {}

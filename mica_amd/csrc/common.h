@@ -64,35 +64,6 @@ MICA_DEVICE float wave_max(float v) {
     return v;
 }
 
-// ---- the activation quantizer's per-element step --------------------------------------------
-// q = clamp(round(x / s), -127, 127) with x / s the IEEE fp32 quotient (int8_quant.py:70;
-// kernels.py:34-36 for the half-away variant).  `inv` is the correctly rounded 1 / s of the row.
-//
-// exact == true: the quotient is formed as y = x * inv, y += fma(-y, s, x) * inv.  For every
-// bf16 x and every s = max(a, 1e-8) / 127 with a a bf16 absmax >= |x|, round_even(y) and
-// round_away(y) equal those of the IEEE quotient; this was checked exhaustively over all
-// 1.07e9 such (x, a) pairs (tests/native/quotient_check.c).  exact == false (fp16 / fp32 /
-// smoothed inputs, outside that proof) uses the IEEE division itself.
-template <bool kFastQuotient>
-MICA_DEVICE int quantize_one(float x, float s, float inv, int rounding) {
-    float v;
-    if (kFastQuotient) {
-        float y = x * inv;
-        float rem = __builtin_fmaf(-y, s, x);
-        v = __builtin_fmaf(rem, inv, y);
-    } else {
-        v = x / s;
-    }
-    float r;
-    if (rounding == MICA_ROUND_EVEN) {
-        r = __builtin_rintf(v);
-    } else {
-        r = __builtin_truncf(v >= 0.0f ? v + 0.5f : v - 0.5f);
-    }
-    r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
-    return (int)r;
-}
-
 // Pack four int8 values (given as int) into one dword, element 0 in the low byte.
 MICA_DEVICE uint32_t pack_i8x4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |

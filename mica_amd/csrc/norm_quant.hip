@@ -96,32 +96,49 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-// Round-to-int8 of one value with a compile-time rounding mode (RND 0: half even, 1: half away,
-// 2: the mode given at run time).
-template <bool kFast, int RND>
-MICA_DEVICE int quantize_r(float x, float s, float inv, int rounding) {
-    return quantize_one<kFast>(x, s, inv, RND == 2 ? rounding : RND);
-}
-
-// Quantize one chunk of 8 fp32 values with the row's scale and store 8 bytes.
-// The bf16 / half-even case rounds with the 1.5 * 2^23 trick: for |t| < 2^22, t + 12582912 is an
-// integer-valued float (its rounding is the IEEE round-half-even of t), whose low mantissa byte is
-// that integer in two's complement; v_perm_b32 then gathers the four low bytes into one dword.
-// No clamp is needed there: |x| <= amax and s = RN(max(amax, 1e-8) / 127) give
-// |x / s| <= 127 / (1 - 2^-24) < 127.5, so round(x / s) is already within +-127 (the reference's
-// clamp is the identity on finite rows; a row holding Inf or NaN yields 0 for those elements).
+// Quantize one chunk of 8 fp32 values with the row's scale s (r = 1 / s) and store 8 bytes; the
+// reference's q = clamp(round(x / s), -127, 127) with x / s the IEEE fp32 quotient
+// (int8_quant.py:70; kernel_src/kernels.py:34-36 for half away).  RND: the rounding mode
+// (MICA_ROUND_EVEN / MICA_ROUND_AWAY, or 2: the one given at run time).
+//
+// The quotient is y = x * r corrected once: y + fma(-y, s, x) * r.  For bf16 x with a bf16 absmax
+// (kFast: unsmoothed bf16 rows) its rounded integer equals the IEEE quotient's for every input
+// (tests/native/quotient_check.c, exhaustive).  For other values (SmoothQuant-scaled rows, fp16 and
+// fp32 activations) the corrected quotient stays within one ulp of the IEEE one, so the integers can
+// only differ near a rounding boundary: lanes whose quotient lies within 2^-13 of k + 0.5 recompute
+// it with the IEEE division (tests/native/guarded_quotient_check.c: 2^28 samples, no mismatch, the
+// slow path on ~5e-5 of the values).
+//
+// Half even rounds with the 1.5 * 2^23 trick: for |t| < 2^22, t + 12582912 is an integer-valued
+// float (its rounding is the IEEE round-half-even of t), whose low mantissa byte is that integer in
+// two's complement; v_perm_b32 gathers the four low bytes into one dword.  No clamp is needed:
+// |x| <= amax and s = RN(max(amax, 1e-8) / 127) give |x / s| <= 127 / (1 - 2^-24) < 127.5, so
+// round(x / s) is already within +-127 (the reference's clamp is the identity on finite rows; a row
+// holding Inf or NaN yields 0 for those elements).
 template <bool kFast, int RND>
 MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int rounding, int8_t *dst) {
+    float t[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+        const float y = v[j] * r;
+        t[j] = __builtin_fmaf(__builtin_fmaf(-y, s, v[j]), r, y);
+    }
+    if (!kFast) {
+        bool near = false;
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j)
+            near = near || __builtin_fabsf(__builtin_fabsf(t[j] - __builtin_rintf(t[j])) - 0.5f) <= 0x1p-13f;
+        if (near) {
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) t[j] = v[j] / s;
+        }
+    }
     u32x2 packed;
-    if (kFast && RND == MICA_ROUND_EVEN) {
+    const int mode = RND == 2 ? rounding : RND;
+    if (mode == MICA_ROUND_EVEN) {
         uint32_t b[kChunk];
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            const float y = v[j] * r;
-            const float rem = __builtin_fmaf(-y, s, v[j]);
-            const float t = __builtin_fmaf(rem, r, y);
-            b[j] = __float_as_uint(t + 12582912.0f);
-        }
+        for (int j = 0; j < kChunk; ++j) b[j] = __float_as_uint(t[j] + 12582912.0f);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t lo = __builtin_amdgcn_perm(b[4 * h + 1], b[4 * h], 0x0c0c0400u);
@@ -131,7 +148,10 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
     } else {
         int qv[kChunk];
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) qv[j] = quantize_r<kFast, RND>(v[j], s, r, rounding);
+        for (int j = 0; j < kChunk; ++j) {
+            const float a = __builtin_truncf(t[j] >= 0.0f ? t[j] + 0.5f : t[j] - 0.5f);
+            qv[j] = (int)__builtin_fminf(__builtin_fmaxf(a, -127.0f), 127.0f);
+        }
         packed[0] = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
         packed[1] = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
     }

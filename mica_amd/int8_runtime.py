@@ -7,8 +7,11 @@ Buffers follow the reference (int8_runtime.py:124-127): ``qweight`` int8 [N, K] 
 """
 from __future__ import annotations
 
+import json
+import re
 import time
 import types
+from pathlib import Path
 
 import torch
 from torch import nn
@@ -259,6 +262,114 @@ class SharedNormQLinears(nn.Module):
         outs = [lin.forward_quantized(qx, sx).reshape(*shape[:-1], lin.out_features)
                 for lin, (qx, sx) in zip(self.linears, qs)]
         return outs if residual is None else (outs, summed)
+
+
+# ---------------------------------------------------------------------------------- checkpoints
+FILE = "model-int8.safetensors"   # int8_runtime.py:639
+FILE_FORMAT = "int8-w8a8/1"       # int8_runtime.py:640
+LINEAR_NAMES = ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b", "out_proj",   # int8_quant.py:6-9
+                "q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def _safetensors_header(path):
+    """The JSON header of a .safetensors file (8-byte little-endian length, then JSON); no tensor data
+    is read."""
+    with open(path, "rb") as f:
+        n = int.from_bytes(f.read(8), "little")
+        if not 0 < n < (1 << 30):
+            raise ValueError(f"{path}: not a safetensors file")
+        return json.loads(f.read(n).decode("utf-8"))
+
+
+def linear_shapes(folder):
+    """(N, K, has_bias) of every decoder-layer W8A8 linear in a checkpoint folder, from file headers only
+    (int8_runtime.linear_shapes, int8_runtime.py:312-355): the ``qweight`` buffers of a
+    ``model-int8.safetensors``, else the ``weight`` of the bf16 ``model*.safetensors`` shards.  The
+    linear-attention in_proj_qkv also contributes its q / k and v row ranges, which rows_forward runs
+    as separate GEMMs, when config.json gives the head sizes.  Multi-token-prediction layers (``mtp``)
+    are skipped.  These are the shapes the self-test checks before a model is served."""
+    folder = Path(folder)
+    if (folder / FILE).is_file():
+        files, leaf = [folder / FILE], "qweight"
+    else:
+        index = folder / "model.safetensors.index.json"
+        names = (sorted(set(json.loads(index.read_text(encoding="utf-8"))["weight_map"].values()))
+                 if index.is_file() else ["model.safetensors"])
+        files, leaf = [folder / n for n in names if (folder / n).is_file()], "weight"
+    layer = re.compile(r"(?:^|\.)layers\.\d+\.")
+    out = set()
+    for path in files:
+        head = _safetensors_header(path)
+        for key, info in head.items():
+            if key == "__metadata__" or key.startswith("mtp") or not layer.search(key):
+                continue
+            parts = key.split(".")
+            if len(parts) < 2 or parts[-1] != leaf or parts[-2] not in LINEAR_NAMES or len(info["shape"]) != 2:
+                continue
+            n, k = info["shape"]
+            out.add((n, k, key[: -len(leaf)] + "bias" in head))
+    try:
+        cfg = json.loads((folder / "config.json").read_text(encoding="utf-8"))
+        cfg = cfg.get("text_config", cfg)
+        hidden = cfg["hidden_size"]
+        kd = cfg["linear_num_key_heads"] * cfg["linear_key_head_dim"]
+        vd = cfg["linear_num_value_heads"] * cfg["linear_value_head_dim"]
+        if (2 * kd + vd, hidden, False) in out:
+            out |= {(kd, hidden, False), (vd, hidden, False)}
+    except (OSError, KeyError, ValueError):
+        pass
+    return sorted(out)
+
+
+def load_linears(path, device="cuda"):
+    """Read a ``model-int8.safetensors`` (format ``int8-w8a8/1``, int8_runtime.py:666-716) into this
+    package's modules.
+
+    Returns (linears, tensors): ``linears`` maps every prefix that has a ``<prefix>.qweight`` to a
+    QLinear built from its ``qweight`` (int8 [N, K]), ``wscale`` (fp32 [N]), optional ``inv_smooth``
+    (fp32 [K]) and optional ``bias`` (fp32 [N]); ``tensors`` holds every other tensor, with the file's
+    ``ties`` metadata (alias -> source key) resolved to the source tensor.  A file that is not in this
+    format, or whose buffers disagree in dtype or shape, raises ValueError('invalid_model') as the
+    reference's loader does."""
+    from safetensors import safe_open
+
+    path = Path(path)
+    if path.is_dir():
+        path = path / FILE
+    dev = torch.device(device)
+    with safe_open(str(path), framework="pt", device=str(dev) if dev.type == "cuda" else "cpu") as f:
+        meta = f.metadata() or {}
+        if meta.get("format") != FILE_FORMAT:
+            raise ValueError("invalid_model")
+        keys = set(f.keys())
+        ties = json.loads(meta.get("ties") or "{}")
+        if any(t not in keys for t in ties.values()) or any(a in keys for a in ties):
+            raise ValueError("invalid_model")
+        prefixes = {k[: -len(".qweight")] for k in keys if k.endswith(".qweight")}
+        owned = set()
+        linears = {}
+        for pre in sorted(prefixes):
+            qw = f.get_tensor(pre + ".qweight")
+            sw = f.get_tensor(pre + ".wscale") if pre + ".wscale" in keys else None
+            inv = f.get_tensor(pre + ".inv_smooth") if pre + ".inv_smooth" in keys else None
+            bias = f.get_tensor(pre + ".bias") if pre + ".bias" in keys else None
+            if qw.dtype != torch.int8 or qw.dim() != 2 or sw is None:
+                raise ValueError("invalid_model")
+            n, k = qw.shape
+            if sw.dtype != torch.float32 or tuple(sw.shape) != (n,):
+                raise ValueError("invalid_model")
+            if inv is not None and (inv.dtype != torch.float32 or tuple(inv.shape) != (k,)):
+                raise ValueError("invalid_model")
+            if bias is not None and (bias.dtype != torch.float32 or tuple(bias.shape) != (n,)):
+                raise ValueError("invalid_model")
+            linears[pre] = QLinear.from_quantized(qw, sw, bias=bias, inv_smooth=inv)
+            owned |= {pre + "." + leaf for leaf in ("qweight", "wscale", "inv_smooth", "bias")}
+        tensors = {k: f.get_tensor(k) for k in sorted(keys - owned)}
+    for alias, source in ties.items():
+        tensors[alias] = tensors[source] if source in tensors else None
+        if tensors[alias] is None:
+            raise ValueError("invalid_model")
+    return linears, tensors
 
 
 # ---------------------------------------------------------------------------------- self-test

@@ -1,6 +1,6 @@
 /*
  * Exhaustive proof, on the CPU, of the quotient the gfx950 quantizer kernels use for bf16 inputs
- * (quantize_one<true> in mica_amd/csrc/common.h):
+ * (quant_store8r<true, ...> in mica_amd/csrc/norm_quant.hip):
  *
  *     s   = max(a, 1e-8f) / 127.0f           a: the row's absmax, a bf16 value >= |x|
  *     inv = 1.0f / s                         (once per row, IEEE division)

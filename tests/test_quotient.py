@@ -26,3 +26,23 @@ def test_fast_quotient_matches_ieee_division_exhaustively(tmp_path):
     assert fields["mismatch_even"] == "0" and fields["mismatch_away"] == "0" and fields["mismatch_magic"] == "0"
     assert float(fields["max_abs_v"]) < 127.5
     assert r.returncode == 0
+
+
+@pytest.mark.slow
+def test_guarded_quotient_matches_ieee_division_sampled(tmp_path):
+    """The guarded quotient of smoothed / fp16 / fp32 rows: 2^28 sampled (x, absmax) pairs, no integer
+    differs from the IEEE quotient's, and the corrected quotient stays within 4 ulps of it (the guard
+    window is 2^-13, at least 16 ulps for every |x / s| <= 128)."""
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    exe = tmp_path / "guarded_quotient_check"
+    subprocess.run([gcc, "-O2", "-fopenmp", "-ffp-contract=off", str(HERE / "native" / "guarded_quotient_check.c"),
+                    "-o", str(exe), "-lm"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
+    print(r.stdout)
+    fields = dict(kv.split("=") for kv in r.stdout.split())
+    assert int(fields["samples"]) == 1 << 28
+    assert fields["mismatch_even"] == "0" and fields["mismatch_away"] == "0"
+    assert float(fields["max_gap_ulp"]) <= 4.0
+    assert r.returncode == 0
