@@ -160,6 +160,58 @@ int mica_gather_logits(const void *h, int ldh, int n_rows, const int *rows, int 
                        int K, float *logits, const int *lo, const int *cnt, float *probs, int ldp,
                        mica_stream_t stream);
 
+/* ---- gated delta net (GDN) token mixer ------------------------------------------------------- */
+
+/*
+ * Depthwise causal convolution over time + SiLU, optionally followed by an l2 normalisation of
+ * each of the first n_norm 128-channel heads (the q / k heads of a GDN layer).
+ * Replaces causal_conv1d_fn as the reference calls it on channel-last activations
+ * (v0.5/serving/lib/fork.py:94-113, conv_channel_last :163-175) and, with n_norm > 0, the q / k
+ * l2norm of use_qk_l2norm_in_kernel (fork.py:145).
+ *   y[b, t, c] = bf16(act(bias[c] + sum_j w[c, j] x[b, t - width + 1 + j, c]))      (fp32 sums)
+ *   y[b, t, head] = bf16(y / sqrt(sum_head y^2 + eps))                for the first n_norm heads
+ * x, y: bf16 [B][T][C] with batch stride sbx / sby and token stride ldx / ldy (elements);
+ * w: [C][width] of w_dtype (bf16 / fp32), bias: [C] of w_dtype or NULL; width <= 4.
+ * init_state / final_state: bf16 [B][C][width - 1] (the inputs before t = 0 / the last width - 1
+ * inputs, with history when T < width - 1), each optional.  C % 8 == 0, strides % 8 == 0.
+ */
+int mica_causal_conv1d(const void *x, long long sbx, int ldx, const void *w, const void *bias, int w_dtype, int width,
+                       const void *init_state, void *final_state, void *y, long long sby, int ldy, int B, int T, int C,
+                       int silu, int n_norm, float eps, mica_stream_t stream);
+
+/*
+ * Chunked gated delta rule (chunk length 64), head dims 128 x 128.
+ * Replaces attn.chunk_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state, output_final_state,
+ * use_qk_l2norm_in_kernel) as called at fork.py:137-147 (flash-linear-attention 0.5.2's
+ * chunk_gated_delta_rule), with q / k already l2-normalised (mica_causal_conv1d with n_norm) and
+ * grouped value heads read in place (value head h uses key head h / (HV / HK), the
+ * repeat_interleave of fork.py:134-136, without the copy).  Per sequence b and value head h:
+ *   S <- exp(g_t) S;  S <- S + k_t (beta_t (v_t - S^T k_t))^T;  o_t = scale S^T q_t
+ * q, k: bf16 [B][T][HK][128] (batch stride sbq / sbk, token stride ldq / ldk); v: bf16 [B][T][HV][128];
+ * g: fp32 [B][T][HV] (log decays, <= 0); beta: [B][T][HV] of beta_dtype (bf16 / fp32);
+ * initial_state / final_state: fp32 [B][HV][128][128] or NULL; o: bf16 [B][T][HV][128].
+ * workspace: mica_gdn_workspace_bytes(B, T, HV) bytes, 16-byte aligned, no initialisation needed.
+ */
+int mica_gdn_chunk(const void *q, long long sbq, int ldq, const void *k, long long sbk, int ldk, const void *v,
+                   long long sbv, int ldv, const float *g, const void *beta, int beta_dtype,
+                   const float *initial_state, float *final_state, void *o, float scale, int B, int T, int HK, int HV,
+                   void *workspace, long long workspace_bytes, mica_stream_t stream);
+
+/* bytes of mica_gdn_chunk workspace: B x HV x ceil(T / 64) x 33 KiB (W, U and the in-chunk decays) */
+long long mica_gdn_workspace_bytes(int B, int T, int HV);
+
+/*
+ * Gated RMSNorm over each 128-wide value head (attn.norm(out, z), fork.py:148; transformers
+ * Qwen3_5RMSNormGated) fused with the per-token INT8 quantisation of out_proj's input
+ * (int8_quant.quant_act, int8_quant.py:64-73):
+ *   h = bf16(x rsqrt(mean_head x^2 + eps));  h = bf16(w h);  y = bf16(h silu(f32(z)))
+ *   s[m] = max(amax_row |y|, 1e-8) / 127;  q = round_half_even(y / s[m])
+ * x, z: bf16 [M][N] (ldx / ldz), w: bf16 [128], y: bf16 [M][N] or NULL; q int8 [M][N] (ldq), s fp32 [M].
+ * N % 512 == 0, N <= 8192.
+ */
+int mica_gated_rmsnorm_quant(const void *x, int ldx, const void *z, int ldz, const void *w, float eps, void *y,
+                             int ldy, int8_t *q, int ldq, float *s, int M, int N, mica_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,761 @@
+// Gated delta net (GDN) token mixer on gfx950: the causal depthwise convolution in front of it and
+// the chunked gated-delta-rule scan (the reference's causal_conv1d_fn + chunk_gated_delta_rule,
+// v0.5/serving/lib/fork.py:71-147; the scan's arithmetic is that of flash-linear-attention 0.5.2's
+// chunk_gated_delta_rule, which the reference calls).
+//
+// Recurrence, per sequence b and value head h, state S [128 (dk), 128 (dv)]:
+//     S <- exp(g_t) S;   S <- S + k_t (beta_t (v_t - S^T k_t))^T;   o_t = scale S^T q_t
+// computed 64 tokens (one chunk) at a time in the WY form:
+//     G = in-chunk cumulative sum of g;  L[i][j] = beta_i (k_i . k_j) exp(G_i - G_j), j < i
+//     T = (I + L)^-1;  W = T (beta exp(G) K);  U = T (beta V)                       (prep kernel)
+//     v_new = U - W S;  o = scale (exp(G) (Q S) + [(Q K^T) exp(G_i - G_j)]_{j<=i} v_new)
+//     S <- exp(G_63) S + K^T (exp(G_63 - G) v_new)                                   (scan kernel)
+// Matrix products run on v_mfma_f32_32x32x16_bf16 with bf16 operands and fp32 accumulation;
+// T, W, U, S, v_new and the masked Q K^T are rounded to bf16 where they enter a product, as in the
+// reference's kernels.  The state stays in fp32 accumulators between chunks.
+//
+// Work split.  prep: one workgroup per (sequence, value head, chunk) -- fully parallel -- writes
+// W and U in the register layouts the scan consumes, plus G.  scan: one workgroup per (sequence,
+// value head, 64-column half of dv); chunks in order; every product of a chunk is one MFMA pass
+// over LDS-resident tiles, two barriers per chunk.  No per-chunk state is stored to memory.
+
+#include "common.h"
+
+namespace {
+
+constexpr int kDk = 128, kDv = 128; // head dims (Qwen3.5 GDN: linear_key_head_dim = linear_value_head_dim = 128)
+constexpr int kC = 64;              // chunk length
+constexpr int kDvb = 64;            // dv columns per scan workgroup
+constexpr int kGdnThreads = 256;    // 4 waves
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+MICA_DEVICE f32x16 mfma(const bf16x8 &a, const bf16x8 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+MICA_DEVICE bf16x8 as_bf16x8(const u32x4 &v) { return __builtin_bit_cast(bf16x8, v); }
+MICA_DEVICE bf16x8 ld_frag(const void *p) { return __builtin_bit_cast(bf16x8, *(const u32x4 *)p); }
+
+// Accumulator element r of a 32 x 32 tile in lane l: row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+MICA_DEVICE int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// Sum of a value over the 4 lanes of each quad (DPP quad permutations [1,0,3,2] and [2,3,0,1]).
+MICA_DEVICE float quad_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    return v;
+}
+
+// ================================================================================================
+// Causal depthwise convolution (width W <= 4) + optional SiLU, then optional l2 normalisation of
+// each of the first n_norm 128-channel heads (the q / k heads).  One thread: 8 channels x kConvT
+// tokens (a sliding window over W - 1 + kConvT input rows).  out[t][c] = act(bias[c] +
+// sum_j w[c][j] x[t - W + 1 + j][c]) in fp32 (the order of causal_conv1d_fn), rounded to bf16;
+// the l2 norm rescales the rounded values by 1 / sqrt(sum x^2 + eps) and rounds again.
+constexpr int kConvT = 16;
+constexpr int kConvThreads = 128; // 1024 channels per workgroup
+
+struct ConvParams {
+    const uint16_t *x; long long sbx; int ldx;   // bf16 [B][T][C], strides in elements
+    const void *w; const void *bias; int w_dtype; int width; // [C][width]
+    const uint16_t *init;                        // bf16 [B][C][width - 1] or null
+    uint16_t *final_state;                       // bf16 [B][C][width - 1] or null
+    uint16_t *y; long long sby; int ldy;         // bf16 out
+    int B, T, C, silu, n_norm; float eps;
+};
+
+__global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
+    const int b = blockIdx.z;
+    const int c0 = (blockIdx.y * kConvThreads + threadIdx.x) * 8;
+    const int t0 = blockIdx.x * kConvT;
+    const bool active = c0 < p.C;
+    const int W = p.width;
+    float w[8][4], bs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int c = active ? c0 + e : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[e][j] = j < W ? load_as_f32(p.w, p.w_dtype, (long)c * W + j) : 0.0f;
+        bs[e] = p.bias ? load_as_f32(p.bias, p.w_dtype, c) : 0.0f;
+    }
+    // input row s (may be negative: history) as 8 fp32 values
+    auto load_row = [&](int s, float *v) {
+        if (!active) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+            return;
+        }
+        if (s >= 0) {
+            const u32x4 r = *(const u32x4 *)(p.x + b * p.sbx + (long)s * p.ldx + c0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { v[2 * e] = bf16_lo(r[e]); v[2 * e + 1] = bf16_hi(r[e]); }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                v[e] = p.init ? bf16_to_f32(p.init[((long)b * p.C + c0 + e) * (W - 1) + (W - 1 + s)]) : 0.0f;
+        }
+    };
+    float win[4][8]; // rows t - 3 .. t of the window (slot 3 = current row)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int s = t0 - 3 + j;
+        if (s >= -(W - 1)) load_row(s, win[j]);
+        else for (int e = 0; e < 8; ++e) win[j][e] = 0.0f;
+    }
+    const int head = c0 >> 7;
+    const bool norm = active && head < p.n_norm;
+    for (int tt = 0; tt < kConvT; ++tt) {
+        const int t = t0 + tt;
+        if (t >= p.T) break; // uniform across the workgroup (same t0)
+        load_row(t, win[3]);
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float a = bs[e];
+            // tap j of width W multiplies x[t - W + 1 + j] = window slot 4 - W + j
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j < W) a += w[e][j] * win[4 - W + j][e];
+            if (p.silu) a = a / (1.0f + expf(-a));
+            o[e] = round_bf16(a);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += o[e] * o[e];
+        // the 16 threads of a 128-channel head are 16 consecutive lanes
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+        if (norm) {
+            const float r = 1.0f / sqrtf(ss + p.eps);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] *= r;
+        }
+        if (active) {
+            u32x4 out;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
+            *(u32x4 *)(p.y + b * p.sby + (long)t * p.ldy + c0) = out;
+        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
+    }
+    // the last W - 1 input rows (with history when T < W - 1) become the next call's initial state
+    if (p.final_state && active && t0 + kConvT >= p.T && t0 < p.T) {
+        for (int j = 0; j < W - 1; ++j) {
+            float v[8];
+            const int s = p.T - (W - 1) + j;
+            if (s >= -(W - 1)) load_row(s, v);
+            else for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) p.final_state[((long)b * p.C + c0 + e) * (W - 1) + j] = f32_to_bf16(v[e]);
+        }
+    }
+}
+
+// ================================================================================================
+// Shared by prep and scan.
+struct GdnParams {
+    const uint16_t *q; long long sbq; int ldq;  // bf16 [B][T][HK][128] (token stride ldq, batch stride sbq)
+    const uint16_t *k; long long sbk; int ldk;
+    const uint16_t *v; long long sbv; int ldv;  // bf16 [B][T][HV][128]
+    const float *g;                             // fp32 [B][T][HV]
+    const void *beta; int beta_dtype;           // [B][T][HV], bf16 or fp32
+    const float *h0;                            // fp32 [B][HV][128][128] or null
+    float *hT;                                  // fp32 [B][HV][128][128] or null
+    uint16_t *o;                                // bf16 [B][T][HV][128]
+    uint16_t *wf, *uf;                          // workspace: per (b, h, chunk) 8192 + 8192 bf16
+    float *gc;                                  // workspace: per (b, h) NT * 64 fp32 (G)
+    float scale;
+    int B, T, HK, HV, NT;
+};
+
+// per (b, h, chunk) workspace blocks
+MICA_DEVICE long chunk_id(const GdnParams &p, int b, int h, int c) { return ((long)b * p.HV + h) * p.NT + c; }
+
+// ---- prep: one workgroup per (chunk, value head, sequence) ------------------------------------
+// LDS (bytes): K rows, V rows (64 x 128 bf16, rows padded to 272 B), L (64 x 64 fp32, permuted for
+// the solve), T (64 x 64 bf16, rows padded to 144 B), W staging (64 x 128 bf16), G, exp(G), beta.
+constexpr int kRowP = 136;          // bf16 elements per padded 128-wide row
+constexpr int kRowC = 72;           // bf16 elements per padded 64-wide row
+constexpr int kPrepK = 0;
+constexpr int kPrepV = kPrepK + kC * kRowP * 2;
+constexpr int kPrepL = kPrepV + kC * kRowP * 2;
+constexpr int kPrepT = kPrepL + kC * kC * 4;
+constexpr int kPrepW = kPrepT + kC * kRowC * 2;
+constexpr int kPrepG = kPrepW + kC * kRowP * 2;
+constexpr int kPrepSmem = kPrepG + 3 * kC * 4;
+
+__global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
+    __shared__ __attribute__((aligned(16))) int8_t smem[kPrepSmem];
+    uint16_t *Ks = (uint16_t *)(smem + kPrepK);
+    uint16_t *Vs = (uint16_t *)(smem + kPrepV);
+    float *Lp = (float *)(smem + kPrepL);
+    uint16_t *Ts = (uint16_t *)(smem + kPrepT);
+    uint16_t *Ws = (uint16_t *)(smem + kPrepW);
+    float *Gs = (float *)(smem + kPrepG);
+    float *Es = Gs + kC;  // exp(G)
+    float *Bs = Es + kC;  // beta
+
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hk = h / (p.HV / p.HK);
+    const int tbase = c * kC;
+
+    // ---- K and V rows of the chunk (zeros past T), g and beta ----
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int piece = tid + i * kGdnThreads; // 64 rows x 16 pieces of 16 bytes
+        const int r = piece >> 4, col = (piece & 15) * 8;
+        const int t = tbase + r;
+        u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+        if (t < p.T) {
+            kv = *(const u32x4 *)(p.k + b * p.sbk + (long)t * p.ldk + hk * kDk + col);
+            vv = *(const u32x4 *)(p.v + b * p.sbv + (long)t * p.ldv + h * kDv + col);
+        }
+        *(u32x4 *)(Ks + r * kRowP + col) = kv;
+        *(u32x4 *)(Vs + r * kRowP + col) = vv;
+    }
+    float gval = 0.0f;
+    if (tid < kC) {
+        const int t = tbase + tid;
+        float bv = 0.0f;
+        if (t < p.T) {
+            const long gi = ((long)b * p.T + t) * p.HV + h;
+            gval = p.g[gi];
+            bv = load_as_f32(p.beta, p.beta_dtype, gi);
+        }
+        Gs[tid] = gval;
+        Bs[tid] = bv;
+    }
+    __syncthreads();
+    // ---- G = in-chunk cumulative sum of g, in token order ----
+    if (tid < kC) {
+        float acc = 0.0f;
+        for (int j = 0; j <= tid; ++j) acc += Gs[j];
+        // every lane has read Gs before any lane of this wave overwrites it (lockstep within the
+        // wave; only wave 0 touches Gs here)
+        __builtin_amdgcn_wave_barrier();
+        Gs[tid] = acc;
+        Es[tid] = expf(acc);
+        p.gc[((long)b * p.HV + h) * p.NT * kC + tbase + tid] = acc;
+    }
+    __syncthreads();
+
+    // ---- L = beta_i (k_i . k_j) exp(G_i - G_j) for j < i: one 32 x 32 tile per wave ----
+    {
+        const int ti = wave >> 1, tj = wave & 1;
+        f32x16 acc = {};
+        const int kh = (lane >> 5) * 8;
+#pragma unroll
+        for (int s = 0; s < kDk / 16; ++s) {
+            const bf16x8 a = ld_frag(Ks + (ti * 32 + (lane & 31)) * kRowP + s * 16 + kh);
+            const bf16x8 bb = ld_frag(Ks + (tj * 32 + (lane & 31)) * kRowP + s * 16 + kh);
+            acc = mfma(a, bb, acc);
+        }
+        const int j = tj * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = ti * 32 + acc_row(r, lane);
+            const float l = j < i ? (Bs[i] * acc[r]) * expf(Gs[i] - Gs[j]) : 0.0f;
+            // permuted: Lp[i][j % 4][j / 4], so a solving lane reads its 16 values contiguously
+            Lp[i * kC + (j & 3) * 16 + (j >> 2)] = l;
+        }
+    }
+    __syncthreads();
+
+    // ---- T = (I + L)^-1 by forward substitution: wave w solves columns 16 w .. 16 w + 15, four
+    // lanes per column; lane (j, q) holds T[4 s + q][j] for s = 0..15 and sums the terms m = 4 s + q
+    // of T[i][j] = delta_ij - sum_{m<i} L[i][m] T[m][j], the quad adds the four partial sums ----
+    {
+        const int j = wave * 16 + (lane >> 2), q = lane & 3;
+        float t[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) t[s] = (4 * s + q == j) ? 1.0f : 0.0f;
+#pragma unroll
+        for (int i = 1; i < kC; ++i) {
+            const float *row = Lp + i * kC + q * 16;
+            const int ns = (i - 1) / 4 + 1; // s with 4 s <= i - 1 (terms with m >= i are zero in L)
+            float part = 0.0f;
+#pragma unroll
+            for (int s4 = 0; s4 < (ns + 3) / 4; ++s4) {
+                const float4 lv = *(const float4 *)(row + s4 * 4);
+                if (s4 * 4 + 0 < ns) part += lv.x * t[s4 * 4 + 0];
+                if (s4 * 4 + 1 < ns) part += lv.y * t[s4 * 4 + 1];
+                if (s4 * 4 + 2 < ns) part += lv.z * t[s4 * 4 + 2];
+                if (s4 * 4 + 3 < ns) part += lv.w * t[s4 * 4 + 3];
+            }
+            const float val = (i == j ? 1.0f : 0.0f) - quad_sum(part);
+            if (q == (i & 3)) t[i >> 2] = val;
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) Ts[(4 * s + q) * kRowC + j] = f32_to_bf16(t[s]);
+    }
+    __syncthreads();
+
+    // ---- W = T (beta exp(G) K), U = T (beta V): wave w computes the 32 columns 32 w .. 32 w + 31 of
+    // both, for all 64 rows (two 32-row tiles); the B operands are columns of K / V, scaled per
+    // token and rounded to bf16 ----
+    {
+        const int col = wave * 32 + (lane & 31);
+        const int kh = (lane >> 5) * 8;
+        f32x16 aw[2] = {}, au[2] = {};
+#pragma unroll
+        for (int s = 0; s < kC / 16; ++s) {
+            const int m0 = s * 16 + kh;
+            u32x4 kb, vb;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + 2 * e;
+                const float k0 = bf16_to_f32(Ks[m * kRowP + col]) * Bs[m] * Es[m];
+                const float k1 = bf16_to_f32(Ks[(m + 1) * kRowP + col]) * Bs[m + 1] * Es[m + 1];
+                const float v0 = bf16_to_f32(Vs[m * kRowP + col]) * Bs[m];
+                const float v1 = bf16_to_f32(Vs[(m + 1) * kRowP + col]) * Bs[m + 1];
+                kb[e] = pack_bf16x2(k0, k1);
+                vb[e] = pack_bf16x2(v0, v1);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const bf16x8 a = ld_frag(Ts + (mt * 32 + (lane & 31)) * kRowC + m0);
+                aw[mt] = mfma(a, as_bf16x8(kb), aw[mt]);
+                au[mt] = mfma(a, as_bf16x8(vb), au[mt]);
+            }
+        }
+        const long cid = chunk_id(p, b, h, c);
+        // U: stored in the accumulator layout, tile (mt, dv tile = wave), 16 values per lane
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            u32x4 lo, hi;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                lo[e] = pack_bf16x2(au[mt][2 * e], au[mt][2 * e + 1]);
+                hi[e] = pack_bf16x2(au[mt][8 + 2 * e], au[mt][8 + 2 * e + 1]);
+            }
+            uint16_t *dst = p.uf + cid * (kC * kDv) + ((mt * 4 + wave) * 64 + lane) * 16;
+            *(u32x4 *)dst = lo;
+            *(u32x4 *)(dst + 8) = hi;
+            // W: staged row-major, re-read below in the operand layout
+#pragma unroll
+            for (int r = 0; r < 16; ++r) Ws[(mt * 32 + acc_row(r, lane)) * kRowP + col] = f32_to_bf16(aw[mt][r]);
+        }
+    }
+    __syncthreads();
+    // W in the MFMA A-operand layout: fragment f = (row tile mt, k-step s) of 64 lanes x 8 values,
+    // lane l holding row 32 mt + l % 32, columns 16 s + 8 (l / 32) .. + 7
+    {
+        const long cid = chunk_id(p, b, h, c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int piece = tid + i * kGdnThreads; // 16 fragments x 64 lanes
+            const int f = piece >> 6, l = piece & 63;
+            const int mt = f >> 3, s = f & 7;
+            const u32x4 v = *(const u32x4 *)(Ws + (mt * 32 + (l & 31)) * kRowP + s * 16 + (l >> 5) * 8);
+            *(u32x4 *)(p.wf + cid * (kC * kDk) + (long)piece * 8) = v;
+        }
+    }
+}
+
+// ---- scan: one workgroup per (dv half, value head, sequence) ----------------------------------
+// LDS (bytes): S^T (64 dv rows x 128 dk, bf16, rows padded to 272 B); K rows of the chunk, two
+// buffers (alternate chunks); v_new^T and its decayed copy (64 dv x 64 tokens, bf16); P = masked
+// Q K^T (64 x 64 bf16, rows 144 B; also the per-wave output staging of waves 2-3); G, two buffers.
+constexpr int kScanS = 0;
+constexpr int kScanK = kScanS + kDvb * kRowP * 2;
+constexpr int kScanVn = kScanK + 2 * kC * kRowP * 2;
+constexpr int kScanVd = kScanVn + kDvb * kRowC * 2;
+constexpr int kScanP = kScanVd + kDvb * kRowC * 2;
+constexpr int kScanG = kScanP + kC * kRowC * 2;
+constexpr int kScanSmem = kScanG + 2 * kC * 4;
+static_assert(2 * kScanSmem <= 160 * 1024, "two scan workgroups per CU");
+
+__global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
+    __shared__ __attribute__((aligned(16))) int8_t smem[kScanSmem];
+    uint16_t *Sst = (uint16_t *)(smem + kScanS);
+    uint16_t *Vn = (uint16_t *)(smem + kScanVn);
+    uint16_t *Vd = (uint16_t *)(smem + kScanVd);
+    uint16_t *Ps = (uint16_t *)(smem + kScanP);
+
+    const int blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hk = h / (p.HV / p.HK);
+    const int l32 = lane & 31, kh = (lane >> 5) * 8;
+    const long bh = (long)b * p.HV + h;
+
+    // state: wave w holds S[dk = 32 w .. 32 w + 31][dv = 64 blk + 32 dvt .. + 31], dvt = 0, 1
+    f32x16 S[2];
+#pragma unroll
+    for (int dvt = 0; dvt < 2; ++dvt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int dk = wave * 32 + acc_row(r, lane), dv = blk * kDvb + dvt * 32 + l32;
+            S[dvt][r] = p.h0 ? p.h0[(bh * kDk + dk) * kDv + dv] : 0.0f;
+        }
+    auto store_state_bf16 = [&]() {
+#pragma unroll
+        for (int dvt = 0; dvt < 2; ++dvt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int dk = wave * 32 + 8 * r4 + 4 * (lane >> 5);
+                u32x2 w2;
+                w2[0] = pack_bf16x2(S[dvt][4 * r4], S[dvt][4 * r4 + 1]);
+                w2[1] = pack_bf16x2(S[dvt][4 * r4 + 2], S[dvt][4 * r4 + 3]);
+                *(u32x2 *)(Sst + (dvt * 32 + l32) * kRowP + dk) = w2;
+            }
+    };
+    store_state_bf16();
+
+    const int mq = wave & 1;  // Q row tile of this wave (P^T column tile; o rows for waves 2, 3)
+    const int mk = wave >> 1; // K row tile of this wave's P^T tile
+    for (int c = 0; c < p.NT; ++c) {
+        const int tbase = c * kC;
+        const long cid = chunk_id(p, b, h, c);
+        uint16_t *Ks = (uint16_t *)(smem + kScanK) + (c & 1) * kC * kRowP;
+        float *Gs = (float *)(smem + kScanG) + (c & 1) * kC;
+        // ---- loads: K rows -> LDS, G -> LDS, Q rows / W and U fragments -> registers ----
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int piece = tid + i * kGdnThreads;
+            const int r = piece >> 4, col = (piece & 15) * 8;
+            const int t = tbase + r;
+            u32x4 kv = {0u, 0u, 0u, 0u};
+            if (t < p.T) kv = *(const u32x4 *)(p.k + b * p.sbk + (long)t * p.ldk + hk * kDk + col);
+            *(u32x4 *)(Ks + r * kRowP + col) = kv;
+        }
+        if (tid < kC) Gs[tid] = p.gc[bh * p.NT * kC + tbase + tid];
+        bf16x8 qf[8];
+        {
+            const int t = tbase + mq * 32 + l32;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (t < p.T) v = *(const u32x4 *)(p.q + b * p.sbq + (long)t * p.ldq + hk * kDk + s * 16 + kh);
+                qf[s] = as_bf16x8(v);
+            }
+        }
+        bf16x8 wfr[8];
+        u32x4 uf[2][2];
+        if (wave < 2) {
+            const uint16_t *wsrc = p.wf + cid * (kC * kDk) + ((long)(wave * 8) * 64 + lane) * 8;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) wfr[s] = ld_frag(wsrc + s * 64 * 8);
+#pragma unroll
+            for (int dvt = 0; dvt < 2; ++dvt) {
+                const uint16_t *usrc = p.uf + cid * (kC * kDv) + ((wave * 4 + blk * 2 + dvt) * 64 + lane) * 16;
+                uf[dvt][0] = *(const u32x4 *)usrc;
+                uf[dvt][1] = *(const u32x4 *)(usrc + 8);
+            }
+        }
+        __syncthreads(); // (A) K rows, G and the state S^T visible to every wave
+
+        // ---- X = [W; Q] S: waves 0-1 rows of W (tile = wave), waves 2-3 rows of Q (tile = wave - 2) ----
+        f32x16 X[2] = {};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const bf16x8 a = wave < 2 ? wfr[s] : qf[s];
+#pragma unroll
+            for (int dvt = 0; dvt < 2; ++dvt)
+                X[dvt] = mfma(a, ld_frag(Sst + (dvt * 32 + l32) * kRowP + s * 16 + kh), X[dvt]);
+        }
+        // ---- P^T tile (K rows mk) x (Q rows mq): P[i][j] = (q_i . k_j) exp(G_i - G_j), j <= i ----
+        {
+            f32x16 pt = {};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) pt = mfma(ld_frag(Ks + (mk * 32 + l32) * kRowP + s * 16 + kh), qf[s], pt);
+            const int i = mq * 32 + l32; // query token (column of P^T)
+            const float gi = Gs[i];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int j0 = mk * 32 + 8 * r4 + 4 * (lane >> 5); // key tokens j0 .. j0 + 3
+                float e[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) e[u] = (j0 + u <= i) ? pt[4 * r4 + u] * expf(gi - Gs[j0 + u]) : 0.0f;
+                u32x2 w2;
+                w2[0] = pack_bf16x2(e[0], e[1]);
+                w2[1] = pack_bf16x2(e[2], e[3]);
+                *(u32x2 *)(Ps + i * kRowC + j0) = w2;
+            }
+        }
+        // ---- v_new = U - W S (waves 0-1), stored transposed, plain and decayed by exp(G_63 - G_m) ----
+        if (wave < 2) {
+            const float glast = Gs[kC - 1];
+#pragma unroll
+            for (int dvt = 0; dvt < 2; ++dvt) {
+                const int dv = dvt * 32 + l32;
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int m0 = wave * 32 + 8 * r4 + 4 * (lane >> 5);
+                    const uint32_t u01 = uf[dvt][r4 >> 1][(r4 & 1) * 2], u23 = uf[dvt][r4 >> 1][(r4 & 1) * 2 + 1];
+                    float vn[4] = {bf16_lo(u01) - X[dvt][4 * r4], bf16_hi(u01) - X[dvt][4 * r4 + 1],
+                                   bf16_lo(u23) - X[dvt][4 * r4 + 2], bf16_hi(u23) - X[dvt][4 * r4 + 3]};
+                    u32x2 a2, d2;
+                    a2[0] = pack_bf16x2(vn[0], vn[1]);
+                    a2[1] = pack_bf16x2(vn[2], vn[3]);
+                    float dec[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) dec[u] = vn[u] * expf(glast - Gs[m0 + u]);
+                    d2[0] = pack_bf16x2(dec[0], dec[1]);
+                    d2[1] = pack_bf16x2(dec[2], dec[3]);
+                    *(u32x2 *)(Vn + dv * kRowC + m0) = a2;
+                    *(u32x2 *)(Vd + dv * kRowC + m0) = d2;
+                }
+            }
+        }
+        __syncthreads(); // (B) v_new, P visible; every wave is done reading S^T
+
+        // ---- o = scale (exp(G_i) (Q S)_i + P v_new) for the rows of waves 2-3 ----
+        if (wave >= 2) {
+            f32x16 O[2] = {};
+#pragma unroll
+            for (int s = 0; s < kC / 16; ++s) {
+                const bf16x8 a = ld_frag(Ps + (mq * 32 + l32) * kRowC + s * 16 + kh);
+#pragma unroll
+                for (int dvt = 0; dvt < 2; ++dvt)
+                    O[dvt] = mfma(a, ld_frag(Vn + (dvt * 32 + l32) * kRowC + s * 16 + kh), O[dvt]);
+            }
+            // stage this wave's 32 x 64 block over its own rows of P (no other wave reads them now)
+            uint16_t *ost = Ps + mq * 32 * kRowC;
+#pragma unroll
+            for (int dvt = 0; dvt < 2; ++dvt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int ml = acc_row(r, lane);
+                    const float y = X[dvt][r] * expf(Gs[mq * 32 + ml]) * p.scale + O[dvt][r] * p.scale;
+                    ost[ml * kRowC + dvt * 32 + l32] = f32_to_bf16(y);
+                }
+            // write out: 32 rows x 128 bytes, 8 lanes per row
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int ml = it * 8 + (lane >> 3), cc = (lane & 7) * 8;
+                const int t = tbase + mq * 32 + ml;
+                const u32x4 v = *(const u32x4 *)(ost + ml * kRowC + cc);
+                if (t < p.T) *(u32x4 *)(p.o + (((long)b * p.T + t) * p.HV + h) * kDv + blk * kDvb + cc) = v;
+            }
+        }
+        // ---- S <- exp(G_63) S + K^T (decayed v_new): wave w updates dk rows 32 w .. 32 w + 31 ----
+        {
+            const float dl = expf(Gs[kC - 1]);
+#pragma unroll
+            for (int dvt = 0; dvt < 2; ++dvt) S[dvt] *= dl;
+            const int dk = wave * 32 + l32;
+#pragma unroll
+            for (int s = 0; s < kC / 16; ++s) {
+                const int m0 = s * 16 + kh;
+                u32x4 kt;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    kt[e] = (uint32_t)Ks[(m0 + 2 * e) * kRowP + dk] | ((uint32_t)Ks[(m0 + 2 * e + 1) * kRowP + dk] << 16);
+#pragma unroll
+                for (int dvt = 0; dvt < 2; ++dvt)
+                    S[dvt] = mfma(as_bf16x8(kt), ld_frag(Vd + (dvt * 32 + l32) * kRowC + s * 16 + kh), S[dvt]);
+            }
+        }
+        store_state_bf16(); // read after barrier (A) of the next chunk
+    }
+    if (p.hT) {
+#pragma unroll
+        for (int dvt = 0; dvt < 2; ++dvt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dk = wave * 32 + acc_row(r, lane), dv = blk * kDvb + dvt * 32 + l32;
+                p.hT[(bh * kDk + dk) * kDv + dv] = S[dvt][r];
+            }
+    }
+}
+
+// ================================================================================================
+// Gated RMSNorm over each 128-wide value head (attn.norm(out, z), fork.py:148) fused with the
+// per-token INT8 quantisation of the normalised row for out_proj.  One wave per token row of
+// HV x 128 values: h = bf16(x rsqrt(mean x^2 + eps)); h = bf16(w h); y = bf16(h silu(z));
+// then s = max(amax(y), 1e-8) / 127 and q = round_half_even(y / s) (int8_quant.py:64-73).
+constexpr int kGnWaves = 4;
+
+struct GatedNormParams {
+    const uint16_t *x; int ldx; const uint16_t *z; int ldz; const uint16_t *w; // w: bf16 [128]
+    uint16_t *y; int ldy;       // optional bf16 output
+    int8_t *q; int ldq; float *s;
+    int M, N; float eps;        // N = HV * 128 <= 8192
+};
+
+__global__ __launch_bounds__(64 * kGnWaves) void gated_norm_quant_kernel(GatedNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kGnWaves + (threadIdx.x >> 6);
+    if (row >= p.M) return;
+    const int per_lane = p.N / 64; // multiple of 8 (N multiple of 512)
+    float wv[8];
+    float y[128];                   // at most 8192 / 64 values per lane
+    float amax = 0.0f;
+    // lane owns 8-column pieces at columns 8 lane + 512 i: the 16 lanes of one 128-wide head are
+    // 16 consecutive lanes
+    {
+        const u32x4 wr = *(const u32x4 *)(p.w + (lane & 15) * 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { wv[2 * e] = bf16_lo(wr[e]); wv[2 * e + 1] = bf16_hi(wr[e]); }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if (i * 8 >= per_lane) break;
+        const int col = i * 512 + lane * 8;
+        const u32x4 xr = *(const u32x4 *)(p.x + (long)row * p.ldx + col);
+        const u32x4 zr = *(const u32x4 *)(p.z + (long)row * p.ldz + col);
+        float xv[8], zv[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            xv[2 * e] = bf16_lo(xr[e]); xv[2 * e + 1] = bf16_hi(xr[e]);
+            zv[2 * e] = bf16_lo(zr[e]); zv[2 * e + 1] = bf16_hi(zr[e]);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+        const float rstd = 1.0f / sqrtf(ss / 128.0f + p.eps);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float hn = round_bf16(xv[e] * rstd);
+            const float hw = round_bf16(wv[e] * hn);
+            const float sz = zv[e] / (1.0f + expf(-zv[e]));
+            const float v = round_bf16(hw * sz);
+            y[i * 8 + e] = v;
+            amax = fmaxf(amax, fabsf(v));
+        }
+    }
+    amax = wave_max(amax);
+    const float s = row_scale(amax);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if (i * 8 >= per_lane) break;
+        const int col = i * 512 + lane * 8;
+        if (p.y) {
+            u32x4 out;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(y[i * 8 + 2 * e], y[i * 8 + 2 * e + 1]);
+            *(u32x4 *)(p.y + (long)row * p.ldy + col) = out;
+        }
+        u32x2 qq;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            int v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = (int)__builtin_rintf(y[i * 8 + 4 * e + u] / s);
+            qq[e] = pack_i8x4(v[0], v[1], v[2], v[3]);
+        }
+        *(u32x2 *)(p.q + (long)row * p.ldq + col) = qq;
+    }
+    if (lane == 0) p.s[row] = s;
+}
+
+// dst = src (or zeros when src is null): the final state of an empty scan
+__global__ void state_fill_kernel(const float *src, float *dst, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src ? src[i] : 0.0f;
+}
+
+long long gdn_ws_bytes(long long B, long long T, long long HV) {
+    const long long NT = (T + kC - 1) / kC;
+    return B * HV * NT * (2LL * kC * kDk * 2 + kC * 4);
+}
+
+}  // namespace
+
+// ================================================================================================
+extern "C" int mica_causal_conv1d(const void *x, long long sbx, int ldx, const void *w, const void *bias,
+                                  int w_dtype, int width, const void *init_state, void *final_state, void *y,
+                                  long long sby, int ldy, int B, int T, int C, int silu, int n_norm, float eps,
+                                  mica_stream_t stream) {
+    if (x == nullptr || w == nullptr || y == nullptr) return MICA_MISS_ARG;
+    if (w_dtype != MICA_BF16 && w_dtype != MICA_FP32) return MICA_MISS_DTYPE;
+    if (width < 1 || width > 4 || B < 0 || T < 0 || C <= 0 || C % 8 != 0 || n_norm < 0 || n_norm * 128 > C)
+        return MICA_MISS_SHAPE;
+    if (ldx < C || ldy < C || ldx % 8 != 0 || ldy % 8 != 0 || sbx < (long long)T * ldx || sby < (long long)T * ldy ||
+        sbx % 8 != 0 || sby % 8 != 0)
+        return MICA_MISS_STRIDE;
+    if (!mica_aligned16(x) || !mica_aligned16(y)) return MICA_MISS_ALIGN;
+    if (B == 0 || T == 0) return 0;
+    ConvParams p{};
+    p.x = (const uint16_t *)x; p.sbx = sbx; p.ldx = ldx;
+    p.w = w; p.bias = bias; p.w_dtype = w_dtype; p.width = width;
+    p.init = (const uint16_t *)init_state; p.final_state = (uint16_t *)final_state;
+    p.y = (uint16_t *)y; p.sby = sby; p.ldy = ldy;
+    p.B = B; p.T = T; p.C = C; p.silu = silu != 0; p.n_norm = n_norm; p.eps = eps;
+    dim3 grid((T + kConvT - 1) / kConvT, (C / 8 + kConvThreads - 1) / kConvThreads, B);
+    hipLaunchKernelGGL(conv_kernel, grid, dim3(kConvThreads), 0, (hipStream_t)stream, p);
+    return mica_err(hipGetLastError());
+}
+
+extern "C" long long mica_gdn_workspace_bytes(int B, int T, int HV) {
+    if (B < 0 || T < 0 || HV <= 0) return -1;
+    return gdn_ws_bytes(B, T, HV);
+}
+
+extern "C" int mica_gdn_chunk(const void *q, long long sbq, int ldq, const void *k, long long sbk, int ldk,
+                              const void *v, long long sbv, int ldv, const float *g, const void *beta,
+                              int beta_dtype, const float *initial_state, float *final_state, void *o, float scale,
+                              int B, int T, int HK, int HV, void *workspace, long long workspace_bytes,
+                              mica_stream_t stream) {
+    if (beta_dtype != MICA_BF16 && beta_dtype != MICA_FP32) return MICA_MISS_DTYPE;
+    if (B < 0 || T < 0 || HK <= 0 || HV <= 0 || HV % HK != 0) return MICA_MISS_SHAPE;
+    // empty inputs have no token data (their pointers may be NULL)
+    if (B > 0 && T > 0 && (q == nullptr || k == nullptr || v == nullptr || g == nullptr || beta == nullptr || o == nullptr))
+        return MICA_MISS_ARG;
+    if (ldq < HK * kDk || ldk < HK * kDk || ldv < HV * kDv || ldq % 8 || ldk % 8 || ldv % 8 || sbq % 8 || sbk % 8 ||
+        sbv % 8 || sbq < (long long)T * ldq || sbk < (long long)T * ldk || sbv < (long long)T * ldv)
+        return MICA_MISS_STRIDE;
+    if (!mica_aligned16(q) || !mica_aligned16(k) || !mica_aligned16(v) || !mica_aligned16(o) ||
+        (initial_state && !mica_aligned16(initial_state)) || (final_state && !mica_aligned16(final_state)) ||
+        (workspace && !mica_aligned16(workspace)))
+        return MICA_MISS_ALIGN;
+    if ((long long)B * T * HV * kDv >= (1LL << 31) || (long long)B * HV * kDk * kDv >= (1LL << 31))
+        return MICA_MISS_RANGE;
+    if (B == 0) return 0;
+    if (T == 0) {
+        // nothing to scan: the final state is the initial one (or zeros)
+        if (final_state) {
+            const long n = (long)B * HV * kDk * kDv;
+            hipLaunchKernelGGL(state_fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                               initial_state, final_state, n);
+            return mica_err(hipGetLastError());
+        }
+        return 0;
+    }
+    if (workspace == nullptr || workspace_bytes < gdn_ws_bytes(B, T, HV)) return MICA_MISS_ARG;
+    GdnParams p{};
+    p.q = (const uint16_t *)q; p.sbq = sbq; p.ldq = ldq;
+    p.k = (const uint16_t *)k; p.sbk = sbk; p.ldk = ldk;
+    p.v = (const uint16_t *)v; p.sbv = sbv; p.ldv = ldv;
+    p.g = g; p.beta = beta; p.beta_dtype = beta_dtype;
+    p.h0 = initial_state; p.hT = final_state; p.o = (uint16_t *)o; p.scale = scale;
+    p.B = B; p.T = T; p.HK = HK; p.HV = HV; p.NT = (T + kC - 1) / kC;
+    const long long blocks = (long long)B * HV * p.NT;
+    p.wf = (uint16_t *)workspace;
+    p.uf = p.wf + blocks * kC * kDk;
+    p.gc = (float *)(p.uf + blocks * kC * kDv);
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(gdn_prep_kernel, dim3(p.NT, HV, B), dim3(kGdnThreads), 0, st, p);
+    int rc = mica_err(hipGetLastError());
+    if (rc) return rc;
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(kDv / kDvb, HV, B), dim3(kGdnThreads), 0, st, p);
+    return mica_err(hipGetLastError());
+}
+
+extern "C" int mica_gated_rmsnorm_quant(const void *x, int ldx, const void *z, int ldz, const void *w, float eps,
+                                        void *y, int ldy, int8_t *q, int ldq, float *s, int M, int N,
+                                        mica_stream_t stream) {
+    if (x == nullptr || z == nullptr || w == nullptr || q == nullptr || s == nullptr) return MICA_MISS_ARG;
+    if (M < 0 || N <= 0 || N % 512 != 0 || N > 8192) return MICA_MISS_SHAPE;
+    if (ldx < N || ldz < N || ldq < N || (y && ldy < N) || ldx % 8 || ldz % 8 || ldq % 8 || (y && ldy % 8))
+        return MICA_MISS_STRIDE;
+    if (!mica_aligned16(x) || !mica_aligned16(z) || !mica_aligned16(w) || !mica_aligned16(q) || (y && !mica_aligned16(y)))
+        return MICA_MISS_ALIGN;
+    if ((long long)M * ldx >= (1LL << 31) || (long long)M * ldz >= (1LL << 31) || (long long)M * ldq >= (1LL << 31))
+        return MICA_MISS_RANGE;
+    if (M == 0) return 0;
+    GatedNormParams p{};
+    p.x = (const uint16_t *)x; p.ldx = ldx; p.z = (const uint16_t *)z; p.ldz = ldz; p.w = (const uint16_t *)w;
+    p.y = (uint16_t *)y; p.ldy = ldy; p.q = q; p.ldq = ldq; p.s = s; p.M = M; p.N = N; p.eps = eps;
+    hipLaunchKernelGGL(gated_norm_quant_kernel, dim3((M + kGnWaves - 1) / kGnWaves), dim3(64 * kGnWaves), 0,
+                       (hipStream_t)stream, p);
+    return mica_err(hipGetLastError());
+}
