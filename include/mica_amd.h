@@ -207,7 +207,7 @@ long long mica_gdn_workspace_bytes(int B, int T, int HV);
  *   h = bf16(x rsqrt(mean_head x^2 + eps));  h = bf16(w h);  y = bf16(h silu(f32(z)))
  *   s[m] = max(amax_row |y|, 1e-8) / 127;  q = round_half_even(y / s[m])
  * x, z: bf16 [M][N] (ldx / ldz), w: bf16 [128], y: bf16 [M][N] or NULL; q int8 [M][N] (ldq), s fp32 [M].
- * N % 512 == 0, N <= 8192.
+ * N / 512 a power of two, N <= 8192.
  */
 int mica_gated_rmsnorm_quant(const void *x, int ldx, const void *z, int ldz, const void *w, float eps, void *y,
                              int ldy, int8_t *q, int ldq, float *s, int M, int N, mica_stream_t stream);

@@ -41,6 +41,12 @@ MICA_DEVICE bf16x8 ld_frag(const void *p) { return __builtin_bit_cast(bf16x8, *(
 // Accumulator element r of a 32 x 32 tile in lane l: row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 MICA_DEVICE int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+// exp(x) as v_exp_f32 (2^x) of x log2(e): a few ulps, enough for the decay factors (all <= 1 here)
+MICA_DEVICE float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+// silu(x) = x / (1 + exp(-x)) with the hardware exp2 and reciprocal (a few ulps in fp32; the
+// outputs are rounded to bf16 after it)
+MICA_DEVICE float fsilu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + fexp(-x)); }
+
 // Sum of a value over the 4 lanes of each quad (DPP quad permutations [1,0,3,2] and [2,3,0,1]).
 MICA_DEVICE float quad_sum(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
@@ -50,75 +56,85 @@ MICA_DEVICE float quad_sum(float v) {
 
 // ================================================================================================
 // Causal depthwise convolution (width W <= 4) + optional SiLU, then optional l2 normalisation of
-// each of the first n_norm 128-channel heads (the q / k heads).  One thread: 8 channels x kConvT
-// tokens (a sliding window over W - 1 + kConvT input rows).  out[t][c] = act(bias[c] +
-// sum_j w[c][j] x[t - W + 1 + j][c]) in fp32 (the order of causal_conv1d_fn), rounded to bf16;
-// the l2 norm rescales the rounded values by 1 / sqrt(sum x^2 + eps) and rounds again.
-constexpr int kConvT = 16;
-constexpr int kConvThreads = 128; // 1024 channels per workgroup
+// each of the first n_norm 128-channel heads (the q / k heads).  One thread: kConvT consecutive
+// tokens x 8 channels; its kConvT + 3 input rows are loaded together before any math, and the
+// weights once.  out[t][c] = act(bias[c] + sum_j w[c][j] x[t - W + 1 + j][c]) in fp32 (the order
+// of causal_conv1d_fn), rounded to bf16; the l2 norm rescales the rounded values by
+// 1 / sqrt(sum x^2 + eps) and rounds again.
+constexpr int kConvThreads = 256; // 2048 channels per workgroup
+constexpr int kConvT = 8;         // tokens per thread
 
 struct ConvParams {
     const uint16_t *x; long long sbx; int ldx;   // bf16 [B][T][C], strides in elements
     const void *w; const void *bias; int w_dtype; int width; // [C][width]
+    int w_vec;                                   // width 4, bf16, 16-byte aligned: vector weight loads
     const uint16_t *init;                        // bf16 [B][C][width - 1] or null
     uint16_t *final_state;                       // bf16 [B][C][width - 1] or null
     uint16_t *y; long long sby; int ldy;         // bf16 out
     int B, T, C, silu, n_norm; float eps;
 };
 
+template <int W>
 __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
-    const int b = blockIdx.z;
-    const int c0 = (blockIdx.y * kConvThreads + threadIdx.x) * 8;
-    const int t0 = blockIdx.x * kConvT;
+    const int b = blockIdx.z, t0 = blockIdx.y * kConvT;
+    const int c0 = (blockIdx.x * kConvThreads + threadIdx.x) * 8;
     const bool active = c0 < p.C;
-    const int W = p.width;
-    float w[8][4], bs[8];
+    // slot j holds input row t0 - 3 + j (j = 0 .. kConvT + 2); output t0 + i uses slots i + 4 - W .. i + 3
+    u32x4 rows[kConvT + 3];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const int c = active ? c0 + e : 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[e][j] = j < W ? load_as_f32(p.w, p.w_dtype, (long)c * W + j) : 0.0f;
-        bs[e] = p.bias ? load_as_f32(p.bias, p.w_dtype, c) : 0.0f;
-    }
-    // input row s (may be negative: history) as 8 fp32 values
-    auto load_row = [&](int s, float *v) {
-        if (!active) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
-            return;
-        }
-        if (s >= 0) {
-            const u32x4 r = *(const u32x4 *)(p.x + b * p.sbx + (long)s * p.ldx + c0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) { v[2 * e] = bf16_lo(r[e]); v[2 * e + 1] = bf16_hi(r[e]); }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                v[e] = p.init ? bf16_to_f32(p.init[((long)b * p.C + c0 + e) * (W - 1) + (W - 1 + s)]) : 0.0f;
-        }
-    };
-    float win[4][8]; // rows t - 3 .. t of the window (slot 3 = current row)
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < kConvT + 3; ++j) {
         const int s = t0 - 3 + j;
-        if (s >= -(W - 1)) load_row(s, win[j]);
-        else for (int e = 0; e < 8; ++e) win[j][e] = 0.0f;
+        rows[j] = u32x4{0u, 0u, 0u, 0u};
+        if (!active || s >= p.T || s < -(W - 1)) continue;
+        if (s >= 0) {
+            rows[j] = *(const u32x4 *)(p.x + b * p.sbx + (long)s * p.ldx + c0);
+        } else if (p.init) {
+            const uint16_t *h = p.init + ((long)b * p.C + c0) * (W - 1) + (W - 1 + s);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                rows[j][e] = (uint32_t)h[(2 * e) * (W - 1)] | ((uint32_t)h[(2 * e + 1) * (W - 1)] << 16);
+        }
     }
-    const int head = c0 >> 7;
-    const bool norm = active && head < p.n_norm;
-    for (int tt = 0; tt < kConvT; ++tt) {
-        const int t = t0 + tt;
-        if (t >= p.T) break; // uniform across the workgroup (same t0)
-        load_row(t, win[3]);
+    float w[8][4], bs[8];
+    if (active && p.w_vec) {
+        const u32x4 *wp = (const u32x4 *)((const uint16_t *)p.w + (long)c0 * 4); // 8 channels x 4 taps
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            const u32x4 v = wp[e2]; // channels 2 e2, 2 e2 + 1
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                w[2 * e2 + u][0] = bf16_lo(v[2 * u]);
+                w[2 * e2 + u][1] = bf16_hi(v[2 * u]);
+                w[2 * e2 + u][2] = bf16_lo(v[2 * u + 1]);
+                w[2 * e2 + u][3] = bf16_hi(v[2 * u + 1]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                w[e][j] = (active && j < W) ? load_as_f32(p.w, p.w_dtype, (long)(c0 + e) * W + j) : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bs[e] = (active && p.bias) ? load_as_f32(p.bias, p.w_dtype, c0 + e) : 0.0f;
+    const bool norm = active && (c0 >> 7) < p.n_norm;
+
+#pragma unroll
+    for (int i = 0; i < kConvT; ++i) {
+        const int t = t0 + i;
+        if (t >= p.T) break; // uniform: every thread of the workgroup has the same t0
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             float a = bs[e];
-            // tap j of width W multiplies x[t - W + 1 + j] = window slot 4 - W + j
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (j < W) a += w[e][j] * win[4 - W + j][e];
-            if (p.silu) a = a / (1.0f + expf(-a));
+            for (int j = 0; j < 4; ++j) {
+                if (j >= W) continue;
+                const uint32_t r = rows[i + 4 - W + j][e >> 1];
+                a += w[e][j] * ((e & 1) ? bf16_hi(r) : bf16_lo(r));
+            }
+            if (p.silu) a = fsilu(a);
             o[e] = round_bf16(a);
         }
         float ss = 0.0f;
@@ -128,7 +144,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
 #pragma unroll
         for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
         if (norm) {
-            const float r = 1.0f / sqrtf(ss + p.eps);
+            const float r = __builtin_amdgcn_rsqf(ss + p.eps);
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] *= r;
         }
@@ -138,20 +154,19 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
             for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
             *(u32x4 *)(p.y + b * p.sby + (long)t * p.ldy + c0) = out;
         }
-#pragma unroll
-        for (int j = 0; j < 3; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
     }
-    // the last W - 1 input rows (with history when T < W - 1) become the next call's initial state
-    if (p.final_state && active && t0 + kConvT >= p.T && t0 < p.T) {
+    // the last W - 1 input rows (history included when T < W - 1) become the next call's initial
+    // state: inputs T - W + 1 .. T - 1 are slots T - W + 4 - t0 .. T + 2 - t0
+    if (p.final_state && active && t0 + kConvT >= p.T) {
         for (int j = 0; j < W - 1; ++j) {
-            float v[8];
-            const int s = p.T - (W - 1) + j;
-            if (s >= -(W - 1)) load_row(s, v);
-            else for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+            const int slot = p.T - W + 4 + j - t0;
+            u32x4 r = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) p.final_state[((long)b * p.C + c0 + e) * (W - 1) + j] = f32_to_bf16(v[e]);
+            for (int k = 0; k < kConvT + 3; ++k)
+                if (k == slot) r = rows[k];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                p.final_state[((long)b * p.C + c0 + e) * (W - 1) + j] = (uint16_t)(r[e >> 1] >> (16 * (e & 1)));
         }
     }
 }
@@ -232,15 +247,16 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
         Bs[tid] = bv;
     }
     __syncthreads();
-    // ---- G = in-chunk cumulative sum of g, in token order ----
-    if (tid < kC) {
-        float acc = 0.0f;
-        for (int j = 0; j <= tid; ++j) acc += Gs[j];
-        // every lane has read Gs before any lane of this wave overwrites it (lockstep within the
-        // wave; only wave 0 touches Gs here)
-        __builtin_amdgcn_wave_barrier();
+    // ---- G = in-chunk cumulative sum of g (wave 0: one token per lane, log-step scan) ----
+    if (wave == 0) {
+        float acc = gval;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float n = __shfl_up(acc, off, 64);
+            if (lane >= off) acc += n;
+        }
         Gs[tid] = acc;
-        Es[tid] = expf(acc);
+        Es[tid] = fexp(acc);
         p.gc[((long)b * p.HV + h) * p.NT * kC + tbase + tid] = acc;
     }
     __syncthreads();
@@ -260,7 +276,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int i = ti * 32 + acc_row(r, lane);
-            const float l = j < i ? (Bs[i] * acc[r]) * expf(Gs[i] - Gs[j]) : 0.0f;
+            const float l = j < i ? (Bs[i] * acc[r]) * fexp(Gs[i] - Gs[j]) : 0.0f;
             // permuted: Lp[i][j % 4][j / 4], so a solving lane reads its 16 values contiguously
             Lp[i * kC + (j & 3) * 16 + (j >> 2)] = l;
         }
@@ -279,16 +295,16 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
         for (int i = 1; i < kC; ++i) {
             const float *row = Lp + i * kC + q * 16;
             const int ns = (i - 1) / 4 + 1; // s with 4 s <= i - 1 (terms with m >= i are zero in L)
-            float part = 0.0f;
+            float p0 = 0.0f, p1 = 0.0f; // two independent FMA chains
 #pragma unroll
             for (int s4 = 0; s4 < (ns + 3) / 4; ++s4) {
                 const float4 lv = *(const float4 *)(row + s4 * 4);
-                if (s4 * 4 + 0 < ns) part += lv.x * t[s4 * 4 + 0];
-                if (s4 * 4 + 1 < ns) part += lv.y * t[s4 * 4 + 1];
-                if (s4 * 4 + 2 < ns) part += lv.z * t[s4 * 4 + 2];
-                if (s4 * 4 + 3 < ns) part += lv.w * t[s4 * 4 + 3];
+                if (s4 * 4 + 0 < ns) p0 = __builtin_fmaf(lv.x, t[s4 * 4 + 0], p0);
+                if (s4 * 4 + 1 < ns) p1 = __builtin_fmaf(lv.y, t[s4 * 4 + 1], p1);
+                if (s4 * 4 + 2 < ns) p0 = __builtin_fmaf(lv.z, t[s4 * 4 + 2], p0);
+                if (s4 * 4 + 3 < ns) p1 = __builtin_fmaf(lv.w, t[s4 * 4 + 3], p1);
             }
-            const float val = (i == j ? 1.0f : 0.0f) - quad_sum(part);
+            const float val = (i == j ? 1.0f : 0.0f) - quad_sum(p0 + p1);
             if (q == (i & 3)) t[i >> 2] = val;
         }
 #pragma unroll
@@ -371,7 +387,7 @@ constexpr int kScanG = kScanP + kC * kRowC * 2;
 constexpr int kScanSmem = kScanG + 2 * kC * 4;
 static_assert(2 * kScanSmem <= 160 * 1024, "two scan workgroups per CU");
 
-__global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
+__global__ __launch_bounds__(kGdnThreads, 2) void gdn_scan_kernel(GdnParams p) {
     __shared__ __attribute__((aligned(16))) int8_t smem[kScanSmem];
     uint16_t *Sst = (uint16_t *)(smem + kScanS);
     uint16_t *Vn = (uint16_t *)(smem + kScanVn);
@@ -409,6 +425,26 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
 
     const int mq = wave & 1;  // Q row tile of this wave (P^T column tile; o rows for waves 2, 3)
     const int mk = wave >> 1; // K row tile of this wave's P^T tile
+    // L2 prefetch: one dword of each 128-byte line the next chunk reads (K and Q rows, W, this
+    // workgroup's U tiles: 448 lines, two per thread), consumed one chunk later so no wait stalls
+    auto prefetch_line = [&](int c, int i) -> uint32_t {
+        if (c >= p.NT) return 0u;
+        const int t0 = c * kC;
+        const long cid = chunk_id(p, b, h, c);
+        if (i < 128) { // K rows: 2 lines per row
+            const int t = t0 + (i >> 1);
+            return t < p.T ? *(const uint32_t *)(p.k + b * p.sbk + (long)t * p.ldk + hk * kDk + (i & 1) * 64) : 0u;
+        }
+        if (i < 256) {
+            const int t = t0 + ((i - 128) >> 1);
+            return t < p.T ? *(const uint32_t *)(p.q + b * p.sbq + (long)t * p.ldq + hk * kDk + (i & 1) * 64) : 0u;
+        }
+        if (i < 384) return *(const uint32_t *)(p.wf + cid * (kC * kDk) + (i - 256) * 64);
+        const int u = i - 384; // 64 lines: tiles (mt, blk * 2 + dvt), 16 lines each
+        const int tile = (u >> 5) * 4 + blk * 2 + ((u >> 4) & 1);
+        return *(const uint32_t *)(p.uf + cid * (kC * kDv) + tile * 1024 + (u & 15) * 64);
+    };
+    uint32_t pf0 = prefetch_line(0, tid), pf1 = tid < 192 ? prefetch_line(0, tid + 256) : 0u, sink = 0u;
     for (int c = 0; c < p.NT; ++c) {
         const int tbase = c * kC;
         const long cid = chunk_id(p, b, h, c);
@@ -448,6 +484,9 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
                 uf[dvt][1] = *(const u32x4 *)(usrc + 8);
             }
         }
+        sink ^= pf0 ^ pf1; // the lines of this chunk, fetched a chunk ago
+        pf0 = prefetch_line(c + 1, tid);
+        pf1 = tid < 192 ? prefetch_line(c + 1, tid + 256) : 0u;
         __syncthreads(); // (A) K rows, G and the state S^T visible to every wave
 
         // ---- X = [W; Q] S: waves 0-1 rows of W (tile = wave), waves 2-3 rows of Q (tile = wave - 2) ----
@@ -471,7 +510,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
                 const int j0 = mk * 32 + 8 * r4 + 4 * (lane >> 5); // key tokens j0 .. j0 + 3
                 float e[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) e[u] = (j0 + u <= i) ? pt[4 * r4 + u] * expf(gi - Gs[j0 + u]) : 0.0f;
+                for (int u = 0; u < 4; ++u) e[u] = (j0 + u <= i) ? pt[4 * r4 + u] * fexp(gi - Gs[j0 + u]) : 0.0f;
                 u32x2 w2;
                 w2[0] = pack_bf16x2(e[0], e[1]);
                 w2[1] = pack_bf16x2(e[2], e[3]);
@@ -495,7 +534,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
                     a2[1] = pack_bf16x2(vn[2], vn[3]);
                     float dec[4];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) dec[u] = vn[u] * expf(glast - Gs[m0 + u]);
+                    for (int u = 0; u < 4; ++u) dec[u] = vn[u] * fexp(glast - Gs[m0 + u]);
                     d2[0] = pack_bf16x2(dec[0], dec[1]);
                     d2[1] = pack_bf16x2(dec[2], dec[3]);
                     *(u32x2 *)(Vn + dv * kRowC + m0) = a2;
@@ -522,7 +561,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int ml = acc_row(r, lane);
-                    const float y = X[dvt][r] * expf(Gs[mq * 32 + ml]) * p.scale + O[dvt][r] * p.scale;
+                    const float y = X[dvt][r] * fexp(Gs[mq * 32 + ml]) * p.scale + O[dvt][r] * p.scale;
                     ost[ml * kRowC + dvt * 32 + l32] = f32_to_bf16(y);
                 }
             // write out: 32 rows x 128 bytes, 8 lanes per row
@@ -536,7 +575,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
         }
         // ---- S <- exp(G_63) S + K^T (decayed v_new): wave w updates dk rows 32 w .. 32 w + 31 ----
         {
-            const float dl = expf(Gs[kC - 1]);
+            const float dl = fexp(Gs[kC - 1]);
 #pragma unroll
             for (int dvt = 0; dvt < 2; ++dvt) S[dvt] *= dl;
             const int dk = wave * 32 + l32;
@@ -563,6 +602,8 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_scan_kernel(GdnParams p) {
                 p.hT[(bh * kDk + dk) * kDv + dv] = S[dvt][r];
             }
     }
+    // keeps the prefetch loads alive; never true (B >= 1 whenever this kernel runs)
+    if (p.B < 0) p.o[tid] = (uint16_t)(sink ^ pf0 ^ pf1);
 }
 
 // ================================================================================================
@@ -579,68 +620,75 @@ struct GatedNormParams {
     int M, N; float eps;        // N = HV * 128 <= 8192
 };
 
+// NI = N / 512 pieces of 8 columns per lane: lane l owns columns 8 l + 512 i, so the 16 lanes of
+// one 128-wide head are 16 consecutive lanes.  All of a row's loads are issued before any math.
+template <int NI>
 __global__ __launch_bounds__(64 * kGnWaves) void gated_norm_quant_kernel(GatedNormParams p) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * kGnWaves + (threadIdx.x >> 6);
     if (row >= p.M) return;
-    const int per_lane = p.N / 64; // multiple of 8 (N multiple of 512)
+    u32x4 xr[NI], zr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        xr[i] = *(const u32x4 *)(p.x + (long)row * p.ldx + i * 512 + lane * 8);
+        zr[i] = *(const u32x4 *)(p.z + (long)row * p.ldz + i * 512 + lane * 8);
+    }
     float wv[8];
-    float y[128];                   // at most 8192 / 64 values per lane
-    float amax = 0.0f;
-    // lane owns 8-column pieces at columns 8 lane + 512 i: the 16 lanes of one 128-wide head are
-    // 16 consecutive lanes
     {
         const u32x4 wr = *(const u32x4 *)(p.w + (lane & 15) * 8);
 #pragma unroll
         for (int e = 0; e < 4; ++e) { wv[2 * e] = bf16_lo(wr[e]); wv[2 * e + 1] = bf16_hi(wr[e]); }
     }
+    u32x4 yr[NI];
+    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        if (i * 8 >= per_lane) break;
-        const int col = i * 512 + lane * 8;
-        const u32x4 xr = *(const u32x4 *)(p.x + (long)row * p.ldx + col);
-        const u32x4 zr = *(const u32x4 *)(p.z + (long)row * p.ldz + col);
-        float xv[8], zv[8];
+    for (int i = 0; i < NI; ++i) {
+        float xv[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            xv[2 * e] = bf16_lo(xr[e]); xv[2 * e + 1] = bf16_hi(xr[e]);
-            zv[2 * e] = bf16_lo(zr[e]); zv[2 * e + 1] = bf16_hi(zr[e]);
-        }
+        for (int e = 0; e < 4; ++e) { xv[2 * e] = bf16_lo(xr[i][e]); xv[2 * e + 1] = bf16_hi(xr[i][e]); }
         float ss = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
 #pragma unroll
         for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
         const float rstd = 1.0f / sqrtf(ss / 128.0f + p.eps);
+        float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
+            const float zv = (e & 1) ? bf16_hi(zr[i][e >> 1]) : bf16_lo(zr[i][e >> 1]);
             const float hn = round_bf16(xv[e] * rstd);
             const float hw = round_bf16(wv[e] * hn);
-            const float sz = zv[e] / (1.0f + expf(-zv[e]));
-            const float v = round_bf16(hw * sz);
-            y[i * 8 + e] = v;
-            amax = fmaxf(amax, fabsf(v));
+            v[e] = hw * fsilu(zv);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            yr[i][e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+            amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(yr[i][e])), fabsf(bf16_hi(yr[i][e]))));
         }
     }
     amax = wave_max(amax);
     const float s = row_scale(amax);
+    const float r = 1.0f / s;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        if (i * 8 >= per_lane) break;
+    for (int i = 0; i < NI; ++i) {
         const int col = i * 512 + lane * 8;
-        if (p.y) {
-            u32x4 out;
+        if (p.y) *(u32x4 *)(p.y + (long)row * p.ldy + col) = yr[i];
+        // y / s as y r plus one correction step, then half-even rounding from the low byte of
+        // v + 1.5 * 2^23: for bf16 y and a bf16 row maximum this gives the integer of the IEEE
+        // quotient and |v| < 127.5 (checked exhaustively on the CPU, tests/native/quotient_check.c)
+        uint32_t bq[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(y[i * 8 + 2 * e], y[i * 8 + 2 * e + 1]);
-            *(u32x4 *)(p.y + (long)row * p.ldy + col) = out;
+        for (int e = 0; e < 8; ++e) {
+            const float x = (e & 1) ? bf16_hi(yr[i][e >> 1]) : bf16_lo(yr[i][e >> 1]);
+            const float y0 = x * r;
+            bq[e] = __float_as_uint(__builtin_fmaf(__builtin_fmaf(-y0, s, x), r, y0) + 12582912.0f);
         }
         u32x2 qq;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            int v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = (int)__builtin_rintf(y[i * 8 + 4 * e + u] / s);
-            qq[e] = pack_i8x4(v[0], v[1], v[2], v[3]);
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const uint32_t lo = __builtin_amdgcn_perm(bq[4 * h2 + 1], bq[4 * h2], 0x0c0c0400u);
+            const uint32_t hi = __builtin_amdgcn_perm(bq[4 * h2 + 3], bq[4 * h2 + 2], 0x0c0c0400u);
+            qq[h2] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
         *(u32x2 *)(p.q + (long)row * p.ldq + col) = qq;
     }
@@ -677,11 +725,19 @@ extern "C" int mica_causal_conv1d(const void *x, long long sbx, int ldx, const v
     ConvParams p{};
     p.x = (const uint16_t *)x; p.sbx = sbx; p.ldx = ldx;
     p.w = w; p.bias = bias; p.w_dtype = w_dtype; p.width = width;
+    p.w_vec = width == 4 && w_dtype == MICA_BF16 && mica_aligned16(w);
     p.init = (const uint16_t *)init_state; p.final_state = (uint16_t *)final_state;
     p.y = (uint16_t *)y; p.sby = sby; p.ldy = ldy;
     p.B = B; p.T = T; p.C = C; p.silu = silu != 0; p.n_norm = n_norm; p.eps = eps;
-    dim3 grid((T + kConvT - 1) / kConvT, (C / 8 + kConvThreads - 1) / kConvThreads, B);
-    hipLaunchKernelGGL(conv_kernel, grid, dim3(kConvThreads), 0, (hipStream_t)stream, p);
+    if ((T + kConvT - 1) / kConvT > 65535 || B > 65535) return MICA_MISS_SHAPE;
+    dim3 grid((C / 8 + kConvThreads - 1) / kConvThreads, (T + kConvT - 1) / kConvT, B);
+    hipStream_t st = (hipStream_t)stream;
+    switch (width) {
+    case 1: hipLaunchKernelGGL(conv_kernel<1>, grid, dim3(kConvThreads), 0, st, p); break;
+    case 2: hipLaunchKernelGGL(conv_kernel<2>, grid, dim3(kConvThreads), 0, st, p); break;
+    case 3: hipLaunchKernelGGL(conv_kernel<3>, grid, dim3(kConvThreads), 0, st, p); break;
+    default: hipLaunchKernelGGL(conv_kernel<4>, grid, dim3(kConvThreads), 0, st, p); break;
+    }
     return mica_err(hipGetLastError());
 }
 
@@ -744,7 +800,7 @@ extern "C" int mica_gated_rmsnorm_quant(const void *x, int ldx, const void *z, i
                                         void *y, int ldy, int8_t *q, int ldq, float *s, int M, int N,
                                         mica_stream_t stream) {
     if (x == nullptr || z == nullptr || w == nullptr || q == nullptr || s == nullptr) return MICA_MISS_ARG;
-    if (M < 0 || N <= 0 || N % 512 != 0 || N > 8192) return MICA_MISS_SHAPE;
+    if (M < 0 || N <= 0 || N % 512 != 0 || N > 8192 || ((N / 512) & (N / 512 - 1)) != 0) return MICA_MISS_SHAPE;
     if (ldx < N || ldz < N || ldq < N || (y && ldy < N) || ldx % 8 || ldz % 8 || ldq % 8 || (y && ldy % 8))
         return MICA_MISS_STRIDE;
     if (!mica_aligned16(x) || !mica_aligned16(z) || !mica_aligned16(w) || !mica_aligned16(q) || (y && !mica_aligned16(y)))
@@ -755,7 +811,15 @@ extern "C" int mica_gated_rmsnorm_quant(const void *x, int ldx, const void *z, i
     GatedNormParams p{};
     p.x = (const uint16_t *)x; p.ldx = ldx; p.z = (const uint16_t *)z; p.ldz = ldz; p.w = (const uint16_t *)w;
     p.y = (uint16_t *)y; p.ldy = ldy; p.q = q; p.ldq = ldq; p.s = s; p.M = M; p.N = N; p.eps = eps;
-    hipLaunchKernelGGL(gated_norm_quant_kernel, dim3((M + kGnWaves - 1) / kGnWaves), dim3(64 * kGnWaves), 0,
-                       (hipStream_t)stream, p);
+    const dim3 grid((M + kGnWaves - 1) / kGnWaves), block(64 * kGnWaves);
+    hipStream_t st = (hipStream_t)stream;
+    switch (N / 512) {
+    case 1: hipLaunchKernelGGL(gated_norm_quant_kernel<1>, grid, block, 0, st, p); break;
+    case 2: hipLaunchKernelGGL(gated_norm_quant_kernel<2>, grid, block, 0, st, p); break;
+    case 4: hipLaunchKernelGGL(gated_norm_quant_kernel<4>, grid, block, 0, st, p); break;
+    case 8: hipLaunchKernelGGL(gated_norm_quant_kernel<8>, grid, block, 0, st, p); break;
+    case 16: hipLaunchKernelGGL(gated_norm_quant_kernel<16>, grid, block, 0, st, p); break;
+    default: return MICA_MISS_SHAPE;
+    }
     return mica_err(hipGetLastError());
 }
