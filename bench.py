@@ -30,6 +30,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "W8A8 GEMM TOPS (% INT8 peak) + prefill tokens/s, 4B shapes, T=4096"
 PEAK_INT8_TOPS = 5000.0    # MI355X dense INT8 matrix peak, 5.0 POP/s (spec sheet; no sparsity)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak, 2.5 PFLOP/s
 HIDDEN, INTER, QKV_N, O_K, LAYERS = 2560, 9728, 6144, 4096, 36
 
 
@@ -300,6 +301,7 @@ def main():
         layer["note"] = ("per 4B layer at T=4096: 2 fused RMSNorm+quant, QKV, O(+residual), fused gate+up with SiLU "
                          "epilogue, requant of h, down(+residual); attention (a torch op) not included")
         extra["layer_T4096"] = layer
+        extra["gdn_8x2048"] = gdn_token_mixer(torch, dev, timer, args)
         result["extra"] = extra
         result["prefill_tokens_per_s"] = layer["hot_path_tokens_per_s_36_layers"]
 
@@ -309,6 +311,52 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, M, K, N)
     print(json.dumps(result), flush=True)
+
+
+def gdn_token_mixer(torch, dev, timer, args):
+    """The GDN layer's token mixer of the 4B model (16 key / 32 value heads of 128, conv width 4) on
+    8 sequences x 2048 tokens: conv + SiLU + q/k l2norm over the 8192 projected channels, the chunked
+    gated delta rule (prep + scan), and the gated RMSNorm fused with out_proj's int8 quantisation.
+    Algorithmic bytes count each input read once and each output written once; the scan's flops are
+    the chunked form's matrix products (11.5 MFLOP per 64-token chunk and value head)."""
+    from mica_amd import gdn
+
+    B, T, HK, HV, D = 8, 2048, 16, 32, 128
+    C = 2 * HK * D + HV * D
+    g = torch.Generator(device=dev).manual_seed(7)
+    mixed = torch.randn(B, T, C, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(C, 4, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    conv = gdn.causal_conv1d_fn(mixed.transpose(1, 2), w, activation="silu", l2norm_heads=2 * HK).transpose(1, 2)
+    q = conv[..., :HK * D].unflatten(-1, (HK, D))
+    k = conv[..., HK * D:2 * HK * D].unflatten(-1, (HK, D))
+    v = conv[..., 2 * HK * D:].unflatten(-1, (HV, D))
+    gg = -torch.rand(B, T, HV, device=dev, generator=g) * 0.5
+    beta = torch.rand(B, T, HV, device=dev, generator=g).to(torch.bfloat16)
+    z = torch.randn(B * T, HV * D, device=dev, generator=g).to(torch.bfloat16)
+    nw = torch.ones(D, device=dev, dtype=torch.bfloat16)
+    out = {}
+    steps = max(args.steps // 10, 10)
+    ms = timer.run(lambda: gdn.causal_conv1d_fn(mixed.transpose(1, 2), w, activation="silu", l2norm_heads=2 * HK),
+                   steps, args.warmup)
+    nb = 2 * B * T * C * 2 + C * 4 * 2
+    out["conv_silu_l2norm"] = {"us": round(ms * 1e3, 1), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                               "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": nb}
+    ms = timer.run(lambda: gdn.chunk_gated_delta_rule(q, k, v, gg, beta, output_final_state=True), steps,
+                   args.warmup)
+    flops = 11.5e6 * B * HV * (T // 64)
+    nb = B * T * (2 * HK * D * 2 + 2 * HV * D * 2 + HV * 6) + B * HV * D * D * 4
+    out["chunk_gated_delta_rule"] = {"us": round(ms * 1e3, 1), "Mtokens/s": round(B * T / (ms * 1e-3) / 1e6, 2),
+                                     "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+                                     "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                     "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "flops": flops, "bytes": nb}
+    ms = timer.run(lambda: gdn.gated_rmsnorm_quant(v.reshape(B * T, HV * D), z, nw), steps, args.warmup)
+    nb = B * T * HV * D * 5 + B * T * 4 + D * 2
+    out["gated_rmsnorm_quant"] = {"us": round(ms * 1e3, 1), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                                  "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": nb}
+    out["token_mixer_us"] = round(sum(x["us"] for x in out.values()), 1)
+    out["note"] = ("8 x 2048 tokens, 16 key / 32 value heads of 128; excludes the in/out projections (W8A8 "
+                   "GEMMs); chunk_gated_delta_rule = prep (chunk-parallel WY) + scan (sequential) kernels")
+    return out
 
 
 def stack_prefill(torch, dev, reps=3):

@@ -16,8 +16,8 @@
 //
 // Work split.  prep: one workgroup per (sequence, value head, chunk) -- fully parallel -- writes
 // W and U in the register layouts the scan consumes, plus G.  scan: one workgroup per (sequence,
-// value head, 64-column half of dv); chunks in order; every product of a chunk is one MFMA pass
-// over LDS-resident tiles, two barriers per chunk.  No per-chunk state is stored to memory.
+// value head), 8 waves; chunks in order; every product of a chunk is one MFMA pass over
+// LDS-resident tiles, two barriers per chunk.  No per-chunk state is stored to memory.
 
 #include "common.h"
 
@@ -25,7 +25,6 @@ namespace {
 
 constexpr int kDk = 128, kDv = 128; // head dims (Qwen3.5 GDN: linear_key_head_dim = linear_value_head_dim = 128)
 constexpr int kC = 64;              // chunk length
-constexpr int kDvb = 64;            // dv columns per scan workgroup
 constexpr int kGdnThreads = 256;    // 4 waves
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -47,10 +46,11 @@ MICA_DEVICE float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408
 // outputs are rounded to bf16 after it)
 MICA_DEVICE float fsilu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + fexp(-x)); }
 
-// Sum of a value over the 4 lanes of each quad (DPP quad permutations [1,0,3,2] and [2,3,0,1]).
+// Sum of a value over the 4 lanes of each quad (DPP quad permutations [1,0,3,2] and [2,3,0,1]);
+// each move can fold into the add that follows it (v_add_f32 with a DPP source).
 MICA_DEVICE float quad_sum(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
     return v;
 }
 
@@ -193,16 +193,20 @@ MICA_DEVICE long chunk_id(const GdnParams &p, int b, int h, int c) { return ((lo
 
 // ---- prep: one workgroup per (chunk, value head, sequence) ------------------------------------
 // LDS (bytes): K rows, V rows (64 x 128 bf16, rows padded to 272 B), L (64 x 64 fp32, permuted for
-// the solve), T (64 x 64 bf16, rows padded to 144 B), W staging (64 x 128 bf16), G, exp(G), beta.
+// the solve), G, exp(G), beta.  T (64 x 64 bf16, rows padded to 144 B) reuses L's space once every
+// wave has finished the solve, and the W staging (64 x 128 bf16) reuses K's once W and U are done:
+// 52 KB, three workgroups per CU.
 constexpr int kRowP = 136;          // bf16 elements per padded 128-wide row
 constexpr int kRowC = 72;           // bf16 elements per padded 64-wide row
 constexpr int kPrepK = 0;
 constexpr int kPrepV = kPrepK + kC * kRowP * 2;
 constexpr int kPrepL = kPrepV + kC * kRowP * 2;
-constexpr int kPrepT = kPrepL + kC * kC * 4;
-constexpr int kPrepW = kPrepT + kC * kRowC * 2;
-constexpr int kPrepG = kPrepW + kC * kRowP * 2;
+constexpr int kPrepT = kPrepL;                     // after the solve
+constexpr int kPrepW = kPrepK;                     // after W and U
+constexpr int kPrepG = kPrepL + kC * kC * 4;
 constexpr int kPrepSmem = kPrepG + 3 * kC * 4;
+static_assert(kC * kRowC * 2 <= kC * kC * 4, "T fits in L's space");
+static_assert(3 * kPrepSmem <= 160 * 1024, "three prep workgroups per CU");
 
 __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
     __shared__ __attribute__((aligned(16))) int8_t smem[kPrepSmem];
@@ -283,30 +287,45 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
     }
     __syncthreads();
 
-    // ---- T = (I + L)^-1 by forward substitution: wave w solves columns 16 w .. 16 w + 15, four
-    // lanes per column; lane (j, q) holds T[4 s + q][j] for s = 0..15 and sums the terms m = 4 s + q
-    // of T[i][j] = delta_ij - sum_{m<i} L[i][m] T[m][j], the quad adds the four partial sums ----
+    // ---- T = (I + L)^-1 by forward substitution, four rows at a time: wave w solves columns
+    // 16 w .. 16 w + 15 with four lanes per column; lane (j, q) holds T[4 s + q][j], s = 0..15.
+    // For rows i .. i + 3 (i = 4 s0) the terms m < i of T[r][j] = delta_rj - sum_{m<r} L[r][m] T[m][j]
+    // are summed per lane (m = q mod 4) and over the quad; the terms i <= m < r are then a 4 x 4
+    // substitution done redundantly by all four lanes, which keep row i + q each. ----
     {
         const int j = wave * 16 + (lane >> 2), q = lane & 3;
         float t[16];
 #pragma unroll
         for (int s = 0; s < 16; ++s) t[s] = (4 * s + q == j) ? 1.0f : 0.0f;
 #pragma unroll
-        for (int i = 1; i < kC; ++i) {
-            const float *row = Lp + i * kC + q * 16;
-            const int ns = (i - 1) / 4 + 1; // s with 4 s <= i - 1 (terms with m >= i are zero in L)
-            float p0 = 0.0f, p1 = 0.0f; // two independent FMA chains
+        for (int s0 = 0; s0 < 16; ++s0) {
+            const int i = 4 * s0;
+            float S4[4];
 #pragma unroll
-            for (int s4 = 0; s4 < (ns + 3) / 4; ++s4) {
-                const float4 lv = *(const float4 *)(row + s4 * 4);
-                if (s4 * 4 + 0 < ns) p0 = __builtin_fmaf(lv.x, t[s4 * 4 + 0], p0);
-                if (s4 * 4 + 1 < ns) p1 = __builtin_fmaf(lv.y, t[s4 * 4 + 1], p1);
-                if (s4 * 4 + 2 < ns) p0 = __builtin_fmaf(lv.z, t[s4 * 4 + 2], p0);
-                if (s4 * 4 + 3 < ns) p1 = __builtin_fmaf(lv.w, t[s4 * 4 + 3], p1);
+            for (int a = 0; a < 4; ++a) {
+                const float *row = Lp + (i + a) * kC + q * 16;
+                float p0 = 0.0f, p1 = 0.0f; // two independent FMA chains
+#pragma unroll
+                for (int s4 = 0; s4 < (s0 + 3) / 4; ++s4) {
+                    const float4 lv = *(const float4 *)(row + s4 * 4);
+                    if (s4 * 4 + 0 < s0) p0 = __builtin_fmaf(lv.x, t[s4 * 4 + 0], p0);
+                    if (s4 * 4 + 1 < s0) p1 = __builtin_fmaf(lv.y, t[s4 * 4 + 1], p1);
+                    if (s4 * 4 + 2 < s0) p0 = __builtin_fmaf(lv.z, t[s4 * 4 + 2], p0);
+                    if (s4 * 4 + 3 < s0) p1 = __builtin_fmaf(lv.w, t[s4 * 4 + 3], p1);
+                }
+                S4[a] = quad_sum(p0 + p1);
             }
-            const float val = (i == j ? 1.0f : 0.0f) - quad_sum(p0 + p1);
-            if (q == (i & 3)) t[i >> 2] = val;
+            // L[i + a][i + b] sits at Lp[(i + a) * 64 + b * 16 + s0]
+            const float *lb = Lp + i * kC + s0;
+            const float l10 = lb[kC], l20 = lb[2 * kC], l21 = lb[2 * kC + 16];
+            const float l30 = lb[3 * kC], l31 = lb[3 * kC + 16], l32 = lb[3 * kC + 32];
+            const float x0 = (i == j ? 1.0f : 0.0f) - S4[0];
+            const float x1 = (i + 1 == j ? 1.0f : 0.0f) - S4[1] - l10 * x0;
+            const float x2 = (i + 2 == j ? 1.0f : 0.0f) - S4[2] - l20 * x0 - l21 * x1;
+            const float x3 = (i + 3 == j ? 1.0f : 0.0f) - S4[3] - l30 * x0 - l31 * x1 - l32 * x2;
+            t[s0] = q == 0 ? x0 : q == 1 ? x1 : q == 2 ? x2 : x3;
         }
+        __syncthreads(); // every wave is done reading L: T takes its place
 #pragma unroll
         for (int s = 0; s < 16; ++s) Ts[(4 * s + q) * kRowC + j] = f32_to_bf16(t[s]);
     }
@@ -353,10 +372,13 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
             uint16_t *dst = p.uf + cid * (kC * kDv) + ((mt * 4 + wave) * 64 + lane) * 16;
             *(u32x4 *)dst = lo;
             *(u32x4 *)(dst + 8) = hi;
-            // W: staged row-major, re-read below in the operand layout
+        }
+        __syncthreads(); // every wave is done reading K: the W staging takes its place
+        // W: staged row-major, re-read below in the operand layout
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) Ws[(mt * 32 + acc_row(r, lane)) * kRowP + col] = f32_to_bf16(aw[mt][r]);
-        }
     }
     __syncthreads();
     // W in the MFMA A-operand layout: fragment f = (row tile mt, k-step s) of 64 lanes x 8 values,
@@ -374,39 +396,52 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
     }
 }
 
-// ---- scan: one workgroup per (dv half, value head, sequence) ----------------------------------
-// LDS (bytes): S^T (64 dv rows x 128 dk, bf16, rows padded to 272 B); K rows of the chunk, two
-// buffers (alternate chunks); v_new^T and its decayed copy (64 dv x 64 tokens, bf16); P = masked
-// Q K^T (64 x 64 bf16, rows 144 B; also the per-wave output staging of waves 2-3); G, two buffers.
+// ---- scan: one workgroup of 8 waves per (value head, sequence) --------------------------------
+// Wave w: row role wr = w % 4 and dv half hf = w / 4.  The state S [128 dk x 128 dv] is spread so
+// that wave w holds dk rows 32 wr .. 32 wr + 31 of dv half hf (two 32 x 32 accumulator tiles).
+// Per chunk, X = [W; Q] S (rows 0-63 from W for wr = 0, 1; rows 64-127 from Q for wr = 2, 3),
+// P^T = K Q^T (waves 0-3, one tile each), v_new = U - W S (wr = 0, 1), o (wr = 2, 3) and the state
+// update (all waves).  Each operand held in registers is re-loaded for the next chunk right after
+// its last use in this one, so the loads overlap the rest of the chunk.
+// LDS (bytes): S^T (128 dv rows x 128 dk, bf16, 272 B rows); K rows of the chunk, two buffers
+// (alternate chunks); v_new^T and its decayed copy (128 dv x 64 tokens, 144 B rows); P = masked
+// Q K^T (64 x 64, 144 B rows); output staging (32 x 64 per output wave); G, two buffers.
+constexpr int kScanThreads = 512;
 constexpr int kScanS = 0;
-constexpr int kScanK = kScanS + kDvb * kRowP * 2;
+constexpr int kScanK = kScanS + kDv * kRowP * 2;
 constexpr int kScanVn = kScanK + 2 * kC * kRowP * 2;
-constexpr int kScanVd = kScanVn + kDvb * kRowC * 2;
-constexpr int kScanP = kScanVd + kDvb * kRowC * 2;
-constexpr int kScanG = kScanP + kC * kRowC * 2;
+constexpr int kScanVd = kScanVn + kDv * kRowC * 2;
+constexpr int kScanP = kScanVd + kDv * kRowC * 2;
+constexpr int kScanO = kScanP + kC * kRowC * 2;
+constexpr int kScanG = kScanO + 4 * 32 * kRowC * 2;
 constexpr int kScanSmem = kScanG + 2 * kC * 4;
-static_assert(2 * kScanSmem <= 160 * 1024, "two scan workgroups per CU");
+static_assert(kScanSmem <= 160 * 1024, "scan LDS");
 
-__global__ __launch_bounds__(kGdnThreads, 2) void gdn_scan_kernel(GdnParams p) {
+__global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
     __shared__ __attribute__((aligned(16))) int8_t smem[kScanSmem];
     uint16_t *Sst = (uint16_t *)(smem + kScanS);
     uint16_t *Vn = (uint16_t *)(smem + kScanVn);
     uint16_t *Vd = (uint16_t *)(smem + kScanVd);
     uint16_t *Ps = (uint16_t *)(smem + kScanP);
 
-    const int blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int h = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, hf = wave >> 2;
     const int hk = h / (p.HV / p.HK);
     const int l32 = lane & 31, kh = (lane >> 5) * 8;
     const long bh = (long)b * p.HV + h;
+    const bool w_rows = wr < 2;                    // X rows from W (v_new); otherwise from Q (output)
+    const bool needs_q = wave < 4 || wave >= 6;    // Q tile for P^T (waves 0-3) and/or X (wr = 2, 3)
+    const int mq = wave < 4 ? (wave & 1) : (wave - 6); // that Q tile
+    const int mk = wave >> 1;                      // K tile of this wave's P^T tile (waves 0-3)
 
-    // state: wave w holds S[dk = 32 w .. 32 w + 31][dv = 64 blk + 32 dvt .. + 31], dvt = 0, 1
+    // state: S[dk = 32 wr + acc_row][dv = 64 hf + 32 dvt + l32]
     f32x16 S[2];
 #pragma unroll
     for (int dvt = 0; dvt < 2; ++dvt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int dk = wave * 32 + acc_row(r, lane), dv = blk * kDvb + dvt * 32 + l32;
+            const int dk = wr * 32 + acc_row(r, lane), dv = hf * 64 + dvt * 32 + l32;
             S[dvt][r] = p.h0 ? p.h0[(bh * kDk + dk) * kDv + dv] : 0.0f;
         }
     auto store_state_bf16 = [&]() {
@@ -414,92 +449,81 @@ __global__ __launch_bounds__(kGdnThreads, 2) void gdn_scan_kernel(GdnParams p) {
         for (int dvt = 0; dvt < 2; ++dvt)
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const int dk = wave * 32 + 8 * r4 + 4 * (lane >> 5);
+                const int dk = wr * 32 + 8 * r4 + 4 * (lane >> 5);
                 u32x2 w2;
                 w2[0] = pack_bf16x2(S[dvt][4 * r4], S[dvt][4 * r4 + 1]);
                 w2[1] = pack_bf16x2(S[dvt][4 * r4 + 2], S[dvt][4 * r4 + 3]);
-                *(u32x2 *)(Sst + (dvt * 32 + l32) * kRowP + dk) = w2;
+                *(u32x2 *)(Sst + (hf * 64 + dvt * 32 + l32) * kRowP + dk) = w2;
             }
     };
     store_state_bf16();
 
-    const int mq = wave & 1;  // Q row tile of this wave (P^T column tile; o rows for waves 2, 3)
-    const int mk = wave >> 1; // K row tile of this wave's P^T tile
-    // L2 prefetch: one dword of each 128-byte line the next chunk reads (K and Q rows, W, this
-    // workgroup's U tiles: 448 lines, two per thread), consumed one chunk later so no wait stalls
-    auto prefetch_line = [&](int c, int i) -> uint32_t {
-        if (c >= p.NT) return 0u;
-        const int t0 = c * kC;
-        const long cid = chunk_id(p, b, h, c);
-        if (i < 128) { // K rows: 2 lines per row
-            const int t = t0 + (i >> 1);
-            return t < p.T ? *(const uint32_t *)(p.k + b * p.sbk + (long)t * p.ldk + hk * kDk + (i & 1) * 64) : 0u;
+    // ---- per-chunk operand loads into registers ----
+    u32x4 kreg[2];
+    float gn = 0.0f;
+    bf16x8 qf[8], wfr[8];
+    u32x4 uf[2][2];
+    auto load_k = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int piece = tid + i * kScanThreads; // 64 rows x 16 pieces of 16 bytes
+            const int t = c * kC + (piece >> 4);
+            kreg[i] = u32x4{0u, 0u, 0u, 0u};
+            if (t < p.T) kreg[i] = *(const u32x4 *)(p.k + b * p.sbk + (long)t * p.ldk + hk * kDk + (piece & 15) * 8);
         }
-        if (i < 256) {
-            const int t = t0 + ((i - 128) >> 1);
-            return t < p.T ? *(const uint32_t *)(p.q + b * p.sbq + (long)t * p.ldq + hk * kDk + (i & 1) * 64) : 0u;
-        }
-        if (i < 384) return *(const uint32_t *)(p.wf + cid * (kC * kDk) + (i - 256) * 64);
-        const int u = i - 384; // 64 lines: tiles (mt, blk * 2 + dvt), 16 lines each
-        const int tile = (u >> 5) * 4 + blk * 2 + ((u >> 4) & 1);
-        return *(const uint32_t *)(p.uf + cid * (kC * kDv) + tile * 1024 + (u & 15) * 64);
+        if (tid < kC) gn = p.gc[bh * p.NT * kC + c * kC + tid];
     };
-    uint32_t pf0 = prefetch_line(0, tid), pf1 = tid < 192 ? prefetch_line(0, tid + 256) : 0u, sink = 0u;
+    auto load_q = [&](int c) {
+        const int t = c * kC + mq * 32 + l32;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (t < p.T) v = *(const u32x4 *)(p.q + b * p.sbq + (long)t * p.ldq + hk * kDk + s * 16 + kh);
+            qf[s] = as_bf16x8(v);
+        }
+    };
+    auto load_w = [&](int c) {
+        const uint16_t *src = p.wf + chunk_id(p, b, h, c) * (kC * kDk) + ((long)(wr * 8) * 64 + lane) * 8;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) wfr[s] = ld_frag(src + s * 64 * 8);
+    };
+    auto load_u = [&](int c) {
+#pragma unroll
+        for (int dvt = 0; dvt < 2; ++dvt) {
+            const uint16_t *src = p.uf + chunk_id(p, b, h, c) * (kC * kDv) + ((wr * 4 + hf * 2 + dvt) * 64 + lane) * 16;
+            uf[dvt][0] = *(const u32x4 *)src;
+            uf[dvt][1] = *(const u32x4 *)(src + 8);
+        }
+    };
+    load_k(0);
+    if (needs_q) load_q(0);
+    if (w_rows) { load_w(0); load_u(0); }
+
     for (int c = 0; c < p.NT; ++c) {
         const int tbase = c * kC;
-        const long cid = chunk_id(p, b, h, c);
+        const bool more = c + 1 < p.NT;
         uint16_t *Ks = (uint16_t *)(smem + kScanK) + (c & 1) * kC * kRowP;
         float *Gs = (float *)(smem + kScanG) + (c & 1) * kC;
-        // ---- loads: K rows -> LDS, G -> LDS, Q rows / W and U fragments -> registers ----
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int piece = tid + i * kGdnThreads;
-            const int r = piece >> 4, col = (piece & 15) * 8;
-            const int t = tbase + r;
-            u32x4 kv = {0u, 0u, 0u, 0u};
-            if (t < p.T) kv = *(const u32x4 *)(p.k + b * p.sbk + (long)t * p.ldk + hk * kDk + col);
-            *(u32x4 *)(Ks + r * kRowP + col) = kv;
+        for (int i = 0; i < 2; ++i) {
+            const int piece = tid + i * kScanThreads;
+            *(u32x4 *)(Ks + (piece >> 4) * kRowP + (piece & 15) * 8) = kreg[i];
         }
-        if (tid < kC) Gs[tid] = p.gc[bh * p.NT * kC + tbase + tid];
-        bf16x8 qf[8];
-        {
-            const int t = tbase + mq * 32 + l32;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (t < p.T) v = *(const u32x4 *)(p.q + b * p.sbq + (long)t * p.ldq + hk * kDk + s * 16 + kh);
-                qf[s] = as_bf16x8(v);
-            }
-        }
-        bf16x8 wfr[8];
-        u32x4 uf[2][2];
-        if (wave < 2) {
-            const uint16_t *wsrc = p.wf + cid * (kC * kDk) + ((long)(wave * 8) * 64 + lane) * 8;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) wfr[s] = ld_frag(wsrc + s * 64 * 8);
-#pragma unroll
-            for (int dvt = 0; dvt < 2; ++dvt) {
-                const uint16_t *usrc = p.uf + cid * (kC * kDv) + ((wave * 4 + blk * 2 + dvt) * 64 + lane) * 16;
-                uf[dvt][0] = *(const u32x4 *)usrc;
-                uf[dvt][1] = *(const u32x4 *)(usrc + 8);
-            }
-        }
-        sink ^= pf0 ^ pf1; // the lines of this chunk, fetched a chunk ago
-        pf0 = prefetch_line(c + 1, tid);
-        pf1 = tid < 192 ? prefetch_line(c + 1, tid + 256) : 0u;
+        if (tid < kC) Gs[tid] = gn;
         __syncthreads(); // (A) K rows, G and the state S^T visible to every wave
 
-        // ---- X = [W; Q] S: waves 0-1 rows of W (tile = wave), waves 2-3 rows of Q (tile = wave - 2) ----
+        // ---- X = [W; Q] S for this wave's 32 rows and dv half ----
         f32x16 X[2] = {};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const bf16x8 a = wave < 2 ? wfr[s] : qf[s];
+            const bf16x8 a = w_rows ? wfr[s] : qf[s];
 #pragma unroll
             for (int dvt = 0; dvt < 2; ++dvt)
-                X[dvt] = mfma(a, ld_frag(Sst + (dvt * 32 + l32) * kRowP + s * 16 + kh), X[dvt]);
+                X[dvt] = mfma(a, ld_frag(Sst + (hf * 64 + dvt * 32 + l32) * kRowP + s * 16 + kh), X[dvt]);
         }
+        if (w_rows && more) load_w(c + 1);
         // ---- P^T tile (K rows mk) x (Q rows mq): P[i][j] = (q_i . k_j) exp(G_i - G_j), j <= i ----
-        {
+        if (wave < 4) {
             f32x16 pt = {};
 #pragma unroll
             for (int s = 0; s < 8; ++s) pt = mfma(ld_frag(Ks + (mk * 32 + l32) * kRowP + s * 16 + kh), qf[s], pt);
@@ -517,15 +541,16 @@ __global__ __launch_bounds__(kGdnThreads, 2) void gdn_scan_kernel(GdnParams p) {
                 *(u32x2 *)(Ps + i * kRowC + j0) = w2;
             }
         }
-        // ---- v_new = U - W S (waves 0-1), stored transposed, plain and decayed by exp(G_63 - G_m) ----
-        if (wave < 2) {
+        if (needs_q && more) load_q(c + 1);
+        // ---- v_new = U - W S (wr = 0, 1), stored transposed, plain and decayed by exp(G_63 - G_m) ----
+        if (w_rows) {
             const float glast = Gs[kC - 1];
 #pragma unroll
             for (int dvt = 0; dvt < 2; ++dvt) {
-                const int dv = dvt * 32 + l32;
+                const int dv = hf * 64 + dvt * 32 + l32;
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) {
-                    const int m0 = wave * 32 + 8 * r4 + 4 * (lane >> 5);
+                    const int m0 = wr * 32 + 8 * r4 + 4 * (lane >> 5);
                     const uint32_t u01 = uf[dvt][r4 >> 1][(r4 & 1) * 2], u23 = uf[dvt][r4 >> 1][(r4 & 1) * 2 + 1];
                     float vn[4] = {bf16_lo(u01) - X[dvt][4 * r4], bf16_hi(u01) - X[dvt][4 * r4 + 1],
                                    bf16_lo(u23) - X[dvt][4 * r4 + 2], bf16_hi(u23) - X[dvt][4 * r4 + 3]};
@@ -541,44 +566,46 @@ __global__ __launch_bounds__(kGdnThreads, 2) void gdn_scan_kernel(GdnParams p) {
                     *(u32x2 *)(Vd + dv * kRowC + m0) = d2;
                 }
             }
+            if (more) load_u(c + 1);
         }
-        __syncthreads(); // (B) v_new, P visible; every wave is done reading S^T
+        __syncthreads(); // (B) v_new, P visible; every wave is done reading S^T and the previous K buffer
+        if (more) load_k(c + 1);
 
-        // ---- o = scale (exp(G_i) (Q S)_i + P v_new) for the rows of waves 2-3 ----
-        if (wave >= 2) {
+        // ---- o = scale (exp(G_i) (Q S)_i + P v_new) for the rows of wr = 2, 3 ----
+        if (!w_rows) {
+            const int mo = wr - 2; // output row tile
             f32x16 O[2] = {};
 #pragma unroll
             for (int s = 0; s < kC / 16; ++s) {
-                const bf16x8 a = ld_frag(Ps + (mq * 32 + l32) * kRowC + s * 16 + kh);
+                const bf16x8 a = ld_frag(Ps + (mo * 32 + l32) * kRowC + s * 16 + kh);
 #pragma unroll
                 for (int dvt = 0; dvt < 2; ++dvt)
-                    O[dvt] = mfma(a, ld_frag(Vn + (dvt * 32 + l32) * kRowC + s * 16 + kh), O[dvt]);
+                    O[dvt] = mfma(a, ld_frag(Vn + (hf * 64 + dvt * 32 + l32) * kRowC + s * 16 + kh), O[dvt]);
             }
-            // stage this wave's 32 x 64 block over its own rows of P (no other wave reads them now)
-            uint16_t *ost = Ps + mq * 32 * kRowC;
+            uint16_t *ost = (uint16_t *)(smem + kScanO) + (hf * 2 + mo) * 32 * kRowC;
 #pragma unroll
             for (int dvt = 0; dvt < 2; ++dvt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int ml = acc_row(r, lane);
-                    const float y = X[dvt][r] * fexp(Gs[mq * 32 + ml]) * p.scale + O[dvt][r] * p.scale;
+                    const float y = X[dvt][r] * fexp(Gs[mo * 32 + ml]) * p.scale + O[dvt][r] * p.scale;
                     ost[ml * kRowC + dvt * 32 + l32] = f32_to_bf16(y);
                 }
             // write out: 32 rows x 128 bytes, 8 lanes per row
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 const int ml = it * 8 + (lane >> 3), cc = (lane & 7) * 8;
-                const int t = tbase + mq * 32 + ml;
+                const int t = tbase + mo * 32 + ml;
                 const u32x4 v = *(const u32x4 *)(ost + ml * kRowC + cc);
-                if (t < p.T) *(u32x4 *)(p.o + (((long)b * p.T + t) * p.HV + h) * kDv + blk * kDvb + cc) = v;
+                if (t < p.T) *(u32x4 *)(p.o + (((long)b * p.T + t) * p.HV + h) * kDv + hf * 64 + cc) = v;
             }
         }
-        // ---- S <- exp(G_63) S + K^T (decayed v_new): wave w updates dk rows 32 w .. 32 w + 31 ----
+        // ---- S <- exp(G_63) S + K^T (decayed v_new) ----
         {
             const float dl = fexp(Gs[kC - 1]);
 #pragma unroll
             for (int dvt = 0; dvt < 2; ++dvt) S[dvt] *= dl;
-            const int dk = wave * 32 + l32;
+            const int dk = wr * 32 + l32;
 #pragma unroll
             for (int s = 0; s < kC / 16; ++s) {
                 const int m0 = s * 16 + kh;
@@ -588,7 +615,7 @@ __global__ __launch_bounds__(kGdnThreads, 2) void gdn_scan_kernel(GdnParams p) {
                     kt[e] = (uint32_t)Ks[(m0 + 2 * e) * kRowP + dk] | ((uint32_t)Ks[(m0 + 2 * e + 1) * kRowP + dk] << 16);
 #pragma unroll
                 for (int dvt = 0; dvt < 2; ++dvt)
-                    S[dvt] = mfma(as_bf16x8(kt), ld_frag(Vd + (dvt * 32 + l32) * kRowC + s * 16 + kh), S[dvt]);
+                    S[dvt] = mfma(as_bf16x8(kt), ld_frag(Vd + (hf * 64 + dvt * 32 + l32) * kRowC + s * 16 + kh), S[dvt]);
             }
         }
         store_state_bf16(); // read after barrier (A) of the next chunk
@@ -598,12 +625,10 @@ __global__ __launch_bounds__(kGdnThreads, 2) void gdn_scan_kernel(GdnParams p) {
         for (int dvt = 0; dvt < 2; ++dvt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int dk = wave * 32 + acc_row(r, lane), dv = blk * kDvb + dvt * 32 + l32;
+                const int dk = wr * 32 + acc_row(r, lane), dv = hf * 64 + dvt * 32 + l32;
                 p.hT[(bh * kDk + dk) * kDv + dv] = S[dvt][r];
             }
     }
-    // keeps the prefetch loads alive; never true (B >= 1 whenever this kernel runs)
-    if (p.B < 0) p.o[tid] = (uint16_t)(sink ^ pf0 ^ pf1);
 }
 
 // ================================================================================================
@@ -792,7 +817,7 @@ extern "C" int mica_gdn_chunk(const void *q, long long sbq, int ldq, const void 
     hipLaunchKernelGGL(gdn_prep_kernel, dim3(p.NT, HV, B), dim3(kGdnThreads), 0, st, p);
     int rc = mica_err(hipGetLastError());
     if (rc) return rc;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3(kDv / kDvb, HV, B), dim3(kGdnThreads), 0, st, p);
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(HV, B), dim3(kScanThreads), 0, st, p);
     return mica_err(hipGetLastError());
 }
 

@@ -166,3 +166,68 @@ def test_ctypes_signature_arity_matches_header():
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
         assert len(params) == len(args), name
     assert ctypes.sizeof(ctypes.c_void_p) == 8
+
+
+def test_causal_conv1d_rejects():
+    lib = _lib.load()
+    # (x, sbx, ldx, w, bias, w_dtype, width, init, final, y, sby, ldy, B, T, C, silu, n_norm, eps)
+    ok = [A16, 64 * 8, 64, A16, None, 0, 4, None, None, A16, 64 * 8, 64, 2, 8, 64, 1, 0, 1e-6]
+
+    def with_(**kw):
+        a = list(ok)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return lib.mica_causal_conv1d(*a, None)
+
+    assert with_(a0=None) == 6            # NULL x
+    assert with_(a5=1) == 2               # fp16 weights
+    assert with_(a6=5) == 1               # width > 4
+    assert with_(a14=60) == 1             # C % 8
+    assert with_(a16=1) == 1              # a norm head wider than C
+    assert with_(a2=56) == 4              # token stride < C
+    assert with_(a1=100) == 4             # batch stride < T * ldx
+    assert with_(a9=A16 + 2) == 3         # misaligned y
+    assert with_(a13=0) == 0              # T = 0: nothing to do
+
+
+def test_gdn_chunk_rejects():
+    lib = _lib.load()
+    D = 128
+    # (q, sbq, ldq, k, sbk, ldk, v, sbv, ldv, g, beta, beta_dtype, h0, hT, o, scale, B, T, HK, HV, ws, ws_bytes)
+    ok = [A16, 8 * 2 * D, 2 * D, A16, 8 * 2 * D, 2 * D, A16, 8 * 4 * D, 4 * D, A16, A16, 0, None, None, A16, 0.1,
+          1, 8, 2, 4, A16, 1 << 30]
+
+    def with_(**kw):
+        a = list(ok)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return lib.mica_gdn_chunk(*a, None)
+
+    assert with_(a11=1) == 2              # fp16 beta
+    assert with_(a19=3) == 1              # HV not a multiple of HK
+    assert with_(a2=D) == 4               # q token stride < HK * 128
+    assert with_(a0=None) == 6            # NULL q with tokens to scan
+    assert with_(a14=A16 + 8) == 3        # misaligned o
+    assert with_(a20=None) == 6           # no workspace
+    assert with_(a21=16) == 6             # workspace too small
+    assert with_(a16=0) == 0              # no sequences
+    assert lib.mica_gdn_workspace_bytes(8, 2048, 32) == 8 * 32 * 32 * (2 * 64 * 128 * 2 + 64 * 4)
+
+
+def test_gated_rmsnorm_quant_rejects():
+    lib = _lib.load()
+    # (x, ldx, z, ldz, w, eps, y, ldy, q, ldq, s, M, N)
+    ok = [A16, 4096, A16, 4096, A16, 1e-6, None, 0, A16, 4096, A16, 4, 4096]
+
+    def with_(**kw):
+        a = list(ok)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return lib.mica_gated_rmsnorm_quant(*a, None)
+
+    assert with_(a8=None) == 6            # no int8 output
+    assert with_(a12=1536) == 1           # N / 512 not a power of two
+    assert with_(a12=16384) == 1          # N > 8192
+    assert with_(a1=2048) == 4            # ldx < N
+    assert with_(a2=A16 + 4) == 3         # misaligned z
+    assert with_(a11=0) == 0              # M = 0
