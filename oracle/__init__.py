@@ -9,6 +9,8 @@ HIP kernels against, and the CPU baseline bench.py times.  Nothing in ``mica_amd
 Modules
   w8a8      numpy restatement (bf16 as uint16 bit patterns, explicit fp32 steps); every function
             cites the reference file:line it follows.
+  gdn       float64 restatement of the GDN token mixer (causal conv + SiLU, l2norm, the gated delta rule
+            per token and in chunked WY form, the gated RMSNorm); pinned in tests/test_gdn_oracle.py.
   cpu_path  the reference's own CPU code path (int8_quant.quant_act -> torch._int_mm -> epilogue,
             eager RMSNorm, F.silu) restated with the same torch calls; used as the timed baseline
             and cross-checked bit-for-bit against ``w8a8``.
