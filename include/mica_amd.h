@@ -160,6 +160,20 @@ int mica_gather_logits(const void *h, int ldh, int n_rows, const int *rows, int 
                        int K, float *logits, const int *lo, const int *cnt, float *probs, int ldp,
                        mica_stream_t stream);
 
+/*
+ * Rotary position embedding in place on the first n_heads heads of each token row (the q and k heads
+ * of a fused QKV projection output), in bf16 arithmetic as transformers' apply_rotary_pos_emb
+ * computes it for the attention layers: for i < h = head_dim / 2,
+ *   y[i] = bf16(bf16(x[i] cos[p][i]) + bf16(x[i + h] (-sin[p][i])))
+ *   y[i + h] = bf16(bf16(x[i + h] cos[p][i]) + bf16(x[i] sin[p][i]))
+ * x: bf16 rows of ldx elements (T rows); cos_tab / sin_tab: bf16 [n_pos][h]; position p of row t is
+ * pos[t] (int32, device) or t % period when pos is NULL.  head_dim % 16 == 0.  Rows whose position
+ * falls outside the tables are left unrotated.  No counterpart in the reference's W8A8 launchers: it
+ * replaces the torch elementwise RoPE of the attention layers around them.
+ */
+int mica_rope_inplace(void *x, long long ldx, int n_heads, int head_dim, const void *cos_tab, const void *sin_tab,
+                      int n_pos, const int *pos, int period, int T, mica_stream_t stream);
+
 /* ---- gated delta net (GDN) token mixer ------------------------------------------------------- */
 
 /*

@@ -41,6 +41,7 @@ SIGNATURES = {
     "mica_swiglu": (_I, [_P, _P, _P, _LL, _I, _P]),
     "mica_gather_logits": (_I, [_P, _I, _I, _P, _I, _P, _I, _F, _F, _P, _I, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I,
                                 _P]),
+    "mica_rope_inplace": (_I, [_P, _LL, _I, _I, _P, _P, _I, _P, _I, _I, _P]),
     "mica_causal_conv1d": (_I, [_P, _LL, _I, _P, _P, _I, _I, _P, _P, _P, _LL, _I, _I, _I, _I, _I, _I, _F, _P]),
     "mica_gdn_chunk": (_I, [_P, _LL, _I, _P, _LL, _I, _P, _LL, _I, _P, _P, _I, _P, _P, _P, _F, _I, _I, _I, _I, _P,
                             _LL, _P]),

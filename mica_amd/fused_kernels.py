@@ -5,6 +5,7 @@ plus the fused RMSNorm + INT8 quantizer of the W8A8 hot path, on the gfx950 HIP 
   swi_glu(gate, up)                                  fused_kernels.py:85-96
   rms_norm_quant(x, weight, eps, ...)                new: the norm and QLinear's act_quant in one pass
   rms_norm_quant_multi(x, weight, eps, inv_smooths)  new: one norm, quantized for up to 4 consumers
+  rope_inplace(rows, n_heads, head_dim, cos, sin, period)  new: bf16 RoPE on QKV output rows, in place
 
 The reference runs Triton here on a GPU and torch formulas on the CPU; this build has no CPU compute
 path: a CPU tensor raises ValueError (the reference raises ValueError for unsupported layouts, :57-58).
@@ -176,3 +177,34 @@ def swi_glu(gate, up):
         raise ValueError(f"swi_glu does not support this input ({_lib.status_name(rc)})")
     _launched()
     return y
+
+
+def rope_inplace(rows, n_heads: int, head_dim: int, cos_tab, sin_tab, period: int | None = None, pos=None):
+    """Rotate the first n_heads heads of every row of ``rows`` ([T, >= n_heads * head_dim] bf16, unit
+    feature stride) in place: bf16(bf16(x cos) + bf16(rotate_half(x) sin)) as transformers'
+    apply_rotary_pos_emb computes it in bf16.  cos_tab / sin_tab: bf16 [n_pos, head_dim / 2].
+    Row t has position pos[t] (int32 tensor) or t % period."""
+    if not rows.is_cuda:
+        raise ValueError("mica_amd RoPE runs on the GPU only (got a CPU tensor)")
+    if rows.dim() != 2 or rows.dtype != torch.bfloat16 or rows.stride(1) != 1:
+        raise ValueError("rope_inplace expects bf16 [T, C] rows with unit feature stride")
+    if cos_tab.dtype != torch.bfloat16 or sin_tab.dtype != torch.bfloat16 or cos_tab.shape != sin_tab.shape or \
+            cos_tab.shape[1] != head_dim // 2 or not cos_tab.is_contiguous() or not sin_tab.is_contiguous():
+        raise ValueError("cos / sin tables must be contiguous bf16 [n_pos, head_dim / 2]")
+    if pos is not None and (pos.dtype != torch.int32 or not pos.is_contiguous() or pos.numel() != rows.shape[0]):
+        raise ValueError("pos must be a contiguous int32 [T] tensor")
+    if pos is None and not period:
+        raise ValueError("give pos or period")
+    dev = rows.device
+    if not _aligned(rows, cos_tab, sin_tab):
+        raise ValueError("rope_inplace requires 16-byte aligned rows and tables")
+    if not _gpu_ok(dev):
+        raise RuntimeError(f"mica_amd kernels need a gfx950 GPU (device {dev})")
+    L = _lib.load()
+    rc = _lib.check(_on(dev, lambda: L.mica_rope_inplace(
+        rows.data_ptr(), rows.stride(0), n_heads, head_dim, cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+        None if pos is None else pos.data_ptr(), int(period or 0), rows.shape[0], _stream(dev))), "mica_rope_inplace")
+    if rc:
+        raise ValueError(f"rope_inplace: unsupported input ({_lib.status_name(rc)})")
+    _launched()
+    return rows

@@ -25,7 +25,7 @@ import torch
 import torch.nn.functional as F
 
 from . import int8_kernels as aot
-from .fused_kernels import rms_norm_quant
+from .fused_kernels import rms_norm_quant, rope_inplace
 from .int8_runtime import GateUpQLinear, QLinear
 from .readout import LabelReadout
 
@@ -69,19 +69,18 @@ class Layer:
 
 
 def _rope(S, head_dim, theta, device):
-    """Rotate-half RoPE tables as bf16 [1, S, 1, head_dim]: (cos, cos) and (-sin, sin)."""
+    """RoPE tables (fp32 angles, then bf16 as the model's dtype): cos, sin as bf16 [S, head_dim / 2]."""
     inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
     ang = torch.arange(S, device=device, dtype=torch.float32)[:, None] * inv[None, :]
-    cos, sin = torch.cos(ang), torch.sin(ang)
-    cs = torch.cat((cos, cos), -1).to(torch.bfloat16)[None, :, None, :]
-    sn = torch.cat((-sin, sin), -1).to(torch.bfloat16)[None, :, None, :]
-    return cs, sn
+    return torch.cos(ang).to(torch.bfloat16).contiguous(), torch.sin(ang).to(torch.bfloat16).contiguous()
 
 
-def _apply_rope(x, cs, sn):
-    """x: [B, S, heads, d] (a view into the QKV output), in bf16 like the model's own attention:
-    x * (cos, cos) + rotate_half(x) * (-sin, sin)."""
+def _apply_rope(x, cos, sin):
+    """The same rotation as torch bf16 ops (a test reference for ``rope_inplace``): x [B, S, heads, d],
+    x * (cos, cos) + rotate_half(x) * (-sin, sin), each op rounded to bf16."""
     h = x.shape[-1] // 2
+    cs = torch.cat((cos, cos), -1)[None, :, None, :]
+    sn = torch.cat((-sin, sin), -1)[None, :, None, :]
     return x * cs + torch.cat((x[..., h:], x[..., :h]), -1) * sn
 
 
@@ -103,17 +102,18 @@ class W8A8Stack:
         self._rope = {}
 
     def _attention(self, qkv, B, S):
-        """Causal GQA attention per request on torch SDPA.  RoPE works on [B, S, heads, d] views of
-        the QKV output and SDPA reads them through transposed strides (enable_gqa shares each K/V
-        head with its group of query heads, no repeated copies); the output comes back
-        [B, S, heads, d]-contiguous, i.e. already the O projection's [T, heads * d] rows."""
+        """Causal GQA attention per request on torch SDPA.  RoPE rotates the q and k heads of the QKV
+        output in place (one kernel), and SDPA reads [B, S, heads, d] views of it through transposed
+        strides (enable_gqa shares each K/V head with its group of query heads, no repeated copies);
+        the output comes back [B, S, heads, d]-contiguous, i.e. already the O projection's
+        [T, heads * d] rows."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
-        q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
         if S not in self._rope:
             self._rope[S] = _rope(S, d, cfg.rope_theta, qkv.device)
-        cs, sn = self._rope[S]
-        q, k = _apply_rope(q, cs, sn), _apply_rope(k, cs, sn)
+        cos, sin = self._rope[S]
+        rope_inplace(qkv, hq + hk, d, cos, sin, period=S)
+        q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
         a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
                                            scale=1.0 / math.sqrt(d), enable_gqa=True)
         return a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
@@ -122,6 +122,7 @@ class W8A8Stack:
         cfg = self.cfg
         q, s = rms_norm_quant(h, L.input_norm, cfg.eps, offset=0.0)
         qkv = L.qkv.forward_quantized(q, s)
+        qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
         a = self._attention(qkv, B, S)
         r = aot.act_quant(a)
         h1 = L.o.forward_quantized(*r, residual=h)
@@ -130,7 +131,7 @@ class W8A8Stack:
         qh, sh = aot.act_quant(g)
         h2 = L.down.forward_quantized(qh, sh, residual=h1)
         if trace is not None:
-            trace.append(dict(h=h, q=q, s=s, qkv=qkv, a=a, qa=r[0], sa=r[1], h1=h1, q2=q2, s2=s2, g=g, qh=qh,
+            trace.append(dict(h=h, q=q, s=s, qkv=qkv_out, qkv_rope=qkv, a=a, qa=r[0], sa=r[1], h1=h1, q2=q2, s2=s2, g=g, qh=qh,
                               sh=sh, h2=h2))
         return h2
 

@@ -230,3 +230,16 @@ def option_probs(logits: np.ndarray, kind: str, n: int | None = None) -> np.ndar
     question, [2:2+n] otherwise."""
     z = logits[..., :2] if kind == "noul" else logits[..., 2:2 + n]
     return softmax(z)
+
+
+def rope(x_bits: np.ndarray, cos_bits: np.ndarray, sin_bits: np.ndarray) -> np.ndarray:
+    """Rotate-half rotary embedding in bf16 arithmetic, as transformers' apply_rotary_pos_emb computes
+    it for bf16 q / k (q * cos + rotate_half(q) * sin; each product and the sum rounded to bf16).
+    x: bf16 bits [..., d]; cos / sin: bf16 bits broadcastable to [..., d / 2].  Returns bf16 bits."""
+    x = bf16_to_f32(x_bits)
+    h = x.shape[-1] // 2
+    x1, x2 = x[..., :h], x[..., h:]
+    c, s = bf16_to_f32(cos_bits), bf16_to_f32(sin_bits)
+    y1 = round_bf16(x1 * c) + round_bf16(x2 * -s)
+    y2 = round_bf16(x2 * c) + round_bf16(x1 * s)
+    return f32_to_bf16(np.concatenate([y1, y2], -1).astype(np.float32))

@@ -530,3 +530,29 @@ def test_readout_bad_indices_give_nan_not_a_fault(gpu):
 
 def test_no_fallbacks_were_taken(gpu):
     assert not int8_kernels.STATS["fallback"], int8_kernels.STATS["fallback"]
+
+
+def test_rope_inplace_positions_and_period(gpu):
+    """rope_inplace against the oracle's bf16 RoPE, with an explicit position array (ragged requests)
+    and with period-derived positions; heads past n_heads and out-of-table positions stay as they were."""
+    from mica_amd.fused_kernels import rope_inplace
+    print("[case] rope", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(77)
+    T, H, d, n_heads, n_pos = 300, 6, 128, 4, 256
+    x = (torch.randn(T, H * d, generator=g) * 3).to(torch.bfloat16)
+    ang = torch.rand(n_pos, d // 2, generator=g) * 6.3
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    pos = torch.cat([torch.arange(100), torch.arange(150), torch.arange(50) + 230]).to(torch.int32)  # 20 past n_pos
+    xb = bits_of(x).reshape(T, H, d)
+    for use_pos in (True, False):
+        y = x.to(gpu)
+        rope_inplace(y, n_heads, d, cos.to(gpu), sin.to(gpu), period=None if use_pos else 64,
+                     pos=pos.to(gpu) if use_pos else None)
+        torch.cuda.synchronize()
+        p = pos.numpy() if use_pos else np.arange(T) % 64
+        want = xb.copy()
+        ok = p < n_pos
+        pc = np.minimum(p, n_pos - 1)
+        rot = O.rope(xb[:, :n_heads], bits_of(cos)[pc][:, None, :], bits_of(sin)[pc][:, None, :])
+        want[ok, :n_heads] = rot[ok]
+        assert np.array_equal(bits_of(y.cpu()).reshape(T, H, d), want)

@@ -55,6 +55,14 @@ def test_small_stack_stage_by_stage(gpu):
         # QKV GEMM from the kernel's q, s
         qkv = O.epilogue(O.int_gemm(q, L.qkv.qweight.cpu().numpy()), s, L.qkv.wscale.cpu().numpy())
         assert np.array_equal(bits(t["qkv"]), qkv), f"layer {li}: qkv"
+        # in-place RoPE on the q and k heads: bit-exact bf16 arithmetic
+        hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        cos, sin = st._rope[S]
+        pos = np.arange(B * S) % S
+        xr = qkv.reshape(B * S, hq + 2 * hk, d)
+        want = xr.copy()
+        want[:, :hq + hk] = O.rope(xr[:, :hq + hk], bits(cos)[pos][:, None, :], bits(sin)[pos][:, None, :])
+        assert np.array_equal(bits(t["qkv_rope"]), want.reshape(B * S, -1)), f"layer {li}: rope"
         # O projection + residual from the kernel's attention output
         qa, sa = O.quant_act(O.bf16_to_f32(bits(t["a"])))
         assert np.array_equal(t["qa"].cpu().numpy(), qa) and np.array_equal(t["sa"].cpu().numpy(), sa)

@@ -282,3 +282,24 @@ def _kat_failures(kat, monkey):
 def test_planted_mistakes_are_caught(kat, monkeypatch, name, fn):
     monkeypatch._plant = {name: fn}
     assert _kat_failures(kat, monkeypatch) >= 1, f"a wrong {name} passed every known-answer check"
+
+
+def test_rope_matches_torch_bf16_ops_and_closed_forms():
+    """bf16 RoPE: bit-exact against the same formula as torch bf16 tensor ops on the CPU (the model's
+    own attention arithmetic); position 0 (cos 1, sin 0) is the identity; a quarter turn maps
+    (x1, x2) to (-x2, x1) exactly."""
+    rng = np.random.default_rng(31)
+    x = O.f32_to_bf16(rng.standard_normal((7, 3, 64)).astype(np.float32) * 4)
+    ang = rng.uniform(0, 6.3, (7, 1, 32)).astype(np.float32)
+    cb, sb = O.f32_to_bf16(np.cos(ang)), O.f32_to_bf16(np.sin(ang))
+    got = O.rope(x, cb, sb)
+    tx, tc, ts = (_torch_from_bf16(a) for a in (x, cb, sb))
+    cs = torch.cat((tc, tc), -1)
+    sn = torch.cat((-ts, ts), -1)
+    ref = tx * cs + torch.cat((tx[..., 32:], tx[..., :32]), -1) * sn
+    assert np.array_equal(got, _bf16_from_torch(ref))
+    one, zero = O.f32_to_bf16(np.ones((1, 1, 32), np.float32)), O.f32_to_bf16(np.zeros((1, 1, 32), np.float32))
+    assert np.array_equal(O.rope(x, one, zero), x)
+    quarter = O.rope(x, zero, one)
+    assert np.array_equal(O.bf16_to_f32(quarter[..., :32]), -O.bf16_to_f32(x[..., 32:]))
+    assert np.array_equal(quarter[..., 32:], x[..., :32])
