@@ -1,0 +1,266 @@
+// Causal grouped-query attention forward on gfx950, head dim 256 (the full-attention layers of the 4B
+// model: 16 query heads sharing 4 key/value heads).  Replaces the reference's attention kernel
+// (kernel_src/kernels.py:71-124, launched by int8_kernels.attn_fwd, int8_kernels.py:409-481) and the
+// torch SDPA fallback the attention layers use without it.
+//
+//   o[t, h] = sum_{u <= t} softmax_u(scale q[t, h] . k[u, g(h)]) v[u, g(h)],   g(h) = h / (HQ / HK)
+//
+// Work split: one workgroup of 4 waves per (sequence, key/value head, block of 32 query positions);
+// wave w handles query head 4 g + w, so every K / V tile brought into LDS serves the 4 query heads of
+// its group.  Per tile of 32 keys, each wave computes S^T = K Q^T (32 keys x 32 queries) with
+// v_mfma_f32_32x32x16_bf16: a lane then holds 16 of the 32 scores of one query (its partner lane
+// l ^ 32 the other 16), so the online softmax needs one cross-lane exchange.  P^T (bf16) is used as the
+// B operand of O^T += V^T P^T directly from the accumulator layout: the contraction runs over the keys
+// in the order the accumulator rows hold them, and the V^T fragments are read in that same order.
+// O^T (256 x 32, fp32, 128 accumulators per lane) is rescaled only when a query's running maximum grows
+// by more than 2^8 (the exponentials stay <= 256; the final division makes the result exact).
+//
+// Data movement: Q fragments stay in registers for the whole workgroup.  K tiles arrive by LDS DMA
+// (buffer_load ... lds), 16-byte chunks XOR-swizzled by row so the operand reads are conflict-free;
+// V^T tiles are DMA'd from an image that v_transpose_kernel writes beforehand in exactly the LDS
+// layout.  Two LDS stages: the DMA of tile j + 1 overlaps the MFMAs of tile j.
+
+#include "common.h"
+
+namespace {
+
+constexpr int kD = 256;              // head dim
+constexpr int kBQ = 32;              // query positions per workgroup
+constexpr int kBK = 32;              // keys per tile
+constexpr int kFaWaves = 4;          // = query heads per key/value head
+constexpr int kFaThreads = 64 * kFaWaves;
+constexpr int kKBytes = kBK * kD * 2;    // 16 KB: 32 key rows x 512 B
+constexpr int kVBytes = kD * kBK * 2;    // 16 KB: 256 dim rows x 64 B
+constexpr int kStage = kKBytes + kVBytes;
+constexpr int kFaSmem = 2 * kStage;      // also the output staging (4 waves x 32 x 512 B) after the loop
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kBufferFlags = 0x00020000;   // raw buffer, 32-bit data format (gfx9)
+
+MICA_DEVICE f32x16 mfma_bf16(const bf16x8 &a, const bf16x8 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+template <int N>
+MICA_DEVICE void fa_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// V^T tile image: element (d, key k) of a tile at d * 32 + (((k / 4) ^ vt_swz(d)) * 4) + k % 4 (bf16);
+// XOR of the 8-byte unit by an even value keeps the 16-byte pairs the DMA moves intact
+MICA_DEVICE int vt_swz(int d) { return 2 * (d & 3); }
+
+struct FaParams {
+    const uint16_t *q; long long sbq, ldq;  // q head h of position t of sequence b: q + b sbq + t ldq + h 256
+    const uint16_t *k; long long sbk, ldk;
+    const uint16_t *v; long long sbv, ldv;
+    uint16_t *vt;                           // V^T images [B][HK][ntiles][256][32]
+    uint16_t *o; long long sbo, ldo;
+    int B, S, HQ, HK, ntiles;
+    float scale_log2;                       // softmax scale x log2(e)
+};
+
+// ---- V -> V^T tile images: one workgroup per (tile, sequence x head); thread = 8 dims x 4 keys ----
+__global__ __launch_bounds__(256) void v_transpose_kernel(FaParams p) {
+    const int tile = blockIdx.x, bh = blockIdx.y;
+    const int b = bh / p.HK, hk = bh % p.HK;
+    const int d0 = (threadIdx.x >> 3) * 8, u = threadIdx.x & 7; // dims d0 .. d0 + 7, keys 4 u .. 4 u + 3
+    u32x4 rows[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int t = tile * kBK + 4 * u + e;
+        rows[e] = u32x4{0u, 0u, 0u, 0u};
+        if (t < p.S) rows[e] = *(const u32x4 *)(p.v + b * p.sbv + (long long)t * p.ldv + hk * kD + d0);
+    }
+    uint16_t *dst = p.vt + (((long long)bh * p.ntiles + tile) * kD) * kBK;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int d = d0 + i;
+        u32x2 w;
+        const int sh = 16 * (i & 1);
+        w[0] = ((rows[0][i >> 1] >> sh) & 0xffffu) | (((rows[1][i >> 1] >> sh) & 0xffffu) << 16);
+        w[1] = ((rows[2][i >> 1] >> sh) & 0xffffu) | (((rows[3][i >> 1] >> sh) & 0xffffu) << 16);
+        *(u32x2 *)(dst + d * kBK + ((u ^ vt_swz(d)) * 4)) = w;
+    }
+}
+
+__global__ __launch_bounds__(kFaThreads, 2) void fa_fwd_kernel(FaParams p) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kFaSmem];
+    const int qblk = p.ntiles - 1 - (int)blockIdx.x; // longest rows first
+    const int hk = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int head = hk * kFaWaves + wave;
+    const int q0 = qblk * kBQ;
+    const int last = qblk; // key tiles 0 .. qblk (tile qblk holds the diagonal)
+
+    // operand buffers: K rows of sequence b (rows >= S read as zeros), the V^T images of (b, hk)
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.k + b * p.sbk), 0, (int)((long long)p.S * p.ldk * 2), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.vt + ((long long)(b * p.HK + hk) * p.ntiles) * kD * kBK), 0, p.ntiles * kVBytes, kBufferFlags);
+    auto dma_tile = [&](int j, int st) {
+        int8_t *ks = smem + st * kStage;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // K: 1 KB block (wave, i) = rows 2 (4 wave + i) + lane / 32; lane writes physical chunk l % 32,
+            // which holds logical chunk (l % 32) ^ row
+            const int row = (wave * 4 + i) * 2 + hi;
+            const int lc = l32 ^ row;
+            const int off = (int)((long long)(j * kBK + row) * p.ldk * 2 + (hk * kD + lc * 8) * 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(ks + (wave * 4 + i) * 1024), 16, off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int off = j * kVBytes + (wave * 4 + i) * 1024 + lane * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16, off, 0,
+                                                     0, 0);
+        }
+    };
+
+    // Q fragments (B operand of S^T): lane holds query q0 + l % 32, dims 16 s + 8 (l / 32) .. + 7
+    bf16x8 qf[kD / 16];
+    {
+        const int t = q0 + l32;
+#pragma unroll
+        for (int s = 0; s < kD / 16; ++s) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (t < p.S) v = *(const u32x4 *)(p.q + b * p.sbq + (long long)t * p.ldq + head * kD + s * 16 + hi * 8);
+            qf[s] = __builtin_bit_cast(bf16x8, v);
+        }
+    }
+    f32x16 O[kD / 32];
+#pragma unroll
+    for (int dt = 0; dt < kD / 32; ++dt) O[dt] = f32x16{};
+    float m_used = -__builtin_inff(), lsum = 0.0f;
+    const int query = q0 + l32;
+
+    dma_tile(0, 0);
+    for (int j = 0; j <= last; ++j) {
+        fa_wait_vmcnt<0>();   // this wave's DMA of tile j (and, at j = 0, its Q loads) landed ...
+        __syncthreads();      // ... and every wave's; nobody reads the other stage any more
+        if (j < last) dma_tile(j + 1, (j + 1) & 1);
+        const int8_t *ks = smem + (j & 1) * kStage;
+        const int8_t *vs = ks + kKBytes;
+        // ---- S^T = K Q^T: rows = keys j*32 + acc_row, column = query l % 32 ----
+        f32x16 sacc = {};
+#pragma unroll
+        for (int s = 0; s < kD / 16; ++s) {
+            const int lc = 2 * s + hi;
+            const bf16x8 a = __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + l32 * 512 + ((lc ^ l32) * 16)));
+            sacc = mfma_bf16(a, qf[s], sacc);
+        }
+        // scores in log2 units, masked above the diagonal, in place
+        float mloc = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = j * kBK + 8 * (r >> 2) + 4 * hi + (r & 3);
+            sacc[r] = key <= query ? sacc[r] * p.scale_log2 : -__builtin_inff();
+            mloc = __builtin_fmaxf(mloc, sacc[r]);
+        }
+        mloc = __builtin_fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        // lazy rescale: move the reference maximum only when the new one exceeds it by more than 8
+        const bool grow = mloc > m_used + 8.0f;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - mloc) : 1.0f;
+        if (grow) m_used = mloc;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+            for (int dt = 0; dt < kD / 32; ++dt) O[dt] *= alpha;
+            lsum *= alpha;
+        }
+        bf16x8 pb[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p0 = __builtin_amdgcn_exp2f(sacc[8 * s + 2 * e] - m_used);
+                const float p1 = __builtin_amdgcn_exp2f(sacc[8 * s + 2 * e + 1] - m_used);
+                lsum += p0 + p1;
+                w[e] = pack_bf16x2(p0, p1);
+            }
+            pb[s] = __builtin_bit_cast(bf16x8, w);
+        }
+        // ---- O^T += V^T P^T: lane's keys for step s are rows 8 s .. 8 s + 7 of the accumulator, i.e.
+        // key units 4 s + hi and 4 s + 2 + hi (4 keys each) ----
+#pragma unroll
+        for (int dt = 0; dt < kD / 32; ++dt) {
+            const int d = dt * 32 + l32;
+            const int8_t *vrow = vs + d * (kBK * 2);
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const u32x2 a0 = *(const u32x2 *)(vrow + ((4 * s + hi) ^ vt_swz(d)) * 8);
+                const u32x2 a1 = *(const u32x2 *)(vrow + ((4 * s + 2 + hi) ^ vt_swz(d)) * 8);
+                const u32x4 av = {a0[0], a0[1], a1[0], a1[1]};
+                O[dt] = mfma_bf16(__builtin_bit_cast(bf16x8, av), pb[s], O[dt]);
+            }
+        }
+    }
+    // ---- normalise, stage per wave in LDS (32 queries x 512 B), write 16-byte row pieces ----
+    const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+    const float inv = 1.0f / ltot;
+    __syncthreads(); // every wave is done with the operand stages
+    int8_t *ost = smem + wave * (kBQ * kD * 2);
+#pragma unroll
+    for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int d = dt * 32 + 8 * r4 + 4 * hi;
+            u32x2 w;
+            w[0] = pack_bf16x2(O[dt][4 * r4] * inv, O[dt][4 * r4 + 1] * inv);
+            w[1] = pack_bf16x2(O[dt][4 * r4 + 2] * inv, O[dt][4 * r4 + 3] * inv);
+            *(u32x2 *)(ost + l32 * (kD * 2) + d * 2) = w;
+        }
+#pragma unroll
+    for (int it = 0; it < (kBQ * kD * 2) / (64 * 16); ++it) {
+        const int piece = it * 64 + lane;
+        const int row = piece >> 5, c = piece & 31; // 32 pieces of 16 B per 512 B row
+        const int t = q0 + row;
+        const u32x4 v = *(const u32x4 *)(ost + row * (kD * 2) + c * 16);
+        if (t < p.S) *(u32x4 *)(p.o + b * p.sbo + (long long)t * p.ldo + head * kD + c * 8) = v;
+    }
+}
+
+}  // namespace
+
+extern "C" long long mica_attention_workspace_bytes(int B, int S, int HK) {
+    if (B < 0 || S < 0 || HK <= 0) return -1;
+    return (long long)B * HK * ((S + kBK - 1) / kBK) * kVBytes;
+}
+
+extern "C" int mica_attention_fwd(const void *q, long long sbq, long long ldq, const void *k, long long sbk,
+                                  long long ldk, const void *v, long long sbv, long long ldv, void *o, long long sbo,
+                                  long long ldo, int B, int S, int HQ, int HK, int head_dim, float scale, int causal,
+                                  void *workspace, long long workspace_bytes, mica_stream_t stream) {
+    if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || S < 0) return MICA_MISS_SHAPE;
+    if (!causal) return MICA_MISS_ARG;
+    if (B == 0 || S == 0) return 0;
+    if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || workspace == nullptr) return MICA_MISS_ARG;
+    if (ldq < (long long)HQ * kD || ldk < (long long)HK * kD || ldv < (long long)HK * kD || ldo < (long long)HQ * kD ||
+        ldq % 8 || ldk % 8 || ldv % 8 || ldo % 8 || sbq % 8 || sbk % 8 || sbv % 8 || sbo % 8 ||
+        (B > 1 && (sbq < S * ldq || sbk < S * ldk || sbv < S * ldv || sbo < S * ldo)))
+        return MICA_MISS_STRIDE;
+    if (!mica_aligned16(q) || !mica_aligned16(k) || !mica_aligned16(v) || !mica_aligned16(o) ||
+        !mica_aligned16(workspace))
+        return MICA_MISS_ALIGN;
+    const int ntiles = (S + kBK - 1) / kBK;
+    if ((long long)ntiles * kBK * ldk * 2 >= (1LL << 31) || (long long)ntiles * kVBytes >= (1LL << 31))
+        return MICA_MISS_RANGE;
+    if (workspace_bytes < mica_attention_workspace_bytes(B, S, HK)) return MICA_MISS_ARG;
+    FaParams p{};
+    p.q = (const uint16_t *)q; p.sbq = sbq; p.ldq = ldq;
+    p.k = (const uint16_t *)k; p.sbk = sbk; p.ldk = ldk;
+    p.v = (const uint16_t *)v; p.sbv = sbv; p.ldv = ldv;
+    p.vt = (uint16_t *)workspace; p.o = (uint16_t *)o; p.sbo = sbo; p.ldo = ldo;
+    p.B = B; p.S = S; p.HQ = HQ; p.HK = HK; p.ntiles = ntiles;
+    p.scale_log2 = scale * 1.44269504088896341f;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles, B * HK), dim3(256), 0, st, p);
+    int rc = mica_err(hipGetLastError());
+    if (rc) return rc;
+    hipLaunchKernelGGL(fa_fwd_kernel, dim3(ntiles, HK, B), dim3(kFaThreads), 0, st, p);
+    return mica_err(hipGetLastError());
+}

@@ -243,3 +243,22 @@ def rope(x_bits: np.ndarray, cos_bits: np.ndarray, sin_bits: np.ndarray) -> np.n
     y1 = round_bf16(x1 * c) + round_bf16(x2 * -s)
     y2 = round_bf16(x2 * c) + round_bf16(x1 * s)
     return f32_to_bf16(np.concatenate([y1, y2], -1).astype(np.float32))
+
+
+def causal_gqa_attention(q, k, v, scale: float) -> np.ndarray:
+    """float64 softmax(scale q k^T, causal) v per sequence and query head; q [B, S, HQ, D], k / v
+    [B, S, HK, D], query head h reads key/value head h // (HQ // HK) (the attention of the
+    full-attention layers; torch SDPA with enable_gqa computes the same)."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    B, S, HQ, D = q.shape
+    grp = HQ // k.shape[2]
+    out = np.zeros((B, S, HQ, D))
+    mask = np.triu(np.ones((S, S), bool), 1)
+    for b in range(B):
+        for h in range(HQ):
+            s = scale * q[b, :, h] @ k[b, :, h // grp].T
+            s[mask] = -np.inf
+            s -= s.max(1, keepdims=True)
+            p = np.exp(s)
+            out[b, :, h] = (p / p.sum(1, keepdims=True)) @ v[b, :, h // grp]
+    return out

@@ -556,3 +556,27 @@ def test_rope_inplace_positions_and_period(gpu):
         rot = O.rope(xb[:, :n_heads], bits_of(cos)[pc][:, None, :], bits_of(sin)[pc][:, None, :])
         want[ok, :n_heads] = rot[ok]
         assert np.array_equal(bits_of(y.cpu()).reshape(T, H, d), want)
+
+
+@pytest.mark.parametrize("B,S,HK", [(2, 100, 1), (1, 64, 2), (1, 33, 1), (2, 1, 1)])
+def test_causal_gqa_attention_matches_oracle(gpu, B, S, HK):
+    """Flash attention (head dim 256, 4 query heads per key/value head) against the float64 oracle on
+    the same bf16 inputs, q / k / v as strided views of one fused QKV buffer: relative Frobenius
+    error <= 1e-2 per (sequence, head) (P is rounded to bf16 for the PV product, as in the reference's
+    kernel and SDPA's flash path)."""
+    from mica_amd.attention import causal_gqa_attention
+    print(f"[case] attention B={B} S={S} HK={HK}", file=sys.stderr, flush=True)
+    HQ, D = 4 * HK, 256
+    g = torch.Generator().manual_seed(B * 100 + S)
+    qkv = (torch.randn(B, S, HQ + 2 * HK, D, generator=g) * 1.5).to(torch.bfloat16)
+    dq = qkv.to(gpu)
+    q, k, v = dq[:, :, :HQ], dq[:, :, HQ:HQ + HK], dq[:, :, HQ + HK:]
+    o = causal_gqa_attention(q, k, v)
+    torch.cuda.synchronize()
+    f = qkv.float().numpy()
+    ref = O.causal_gqa_attention(f[:, :, :HQ], f[:, :, HQ:HQ + HK], f[:, :, HQ + HK:], D ** -0.5)
+    got = o.float().cpu().numpy()
+    worst = max(np.linalg.norm(got[b, :, h] - ref[b, :, h]) / np.linalg.norm(ref[b, :, h])
+                for b in range(B) for h in range(HQ))
+    print(f"relative error {worst:.2e}", file=sys.stderr)
+    assert worst <= 1e-2

@@ -303,3 +303,21 @@ def test_rope_matches_torch_bf16_ops_and_closed_forms():
     quarter = O.rope(x, zero, one)
     assert np.array_equal(O.bf16_to_f32(quarter[..., :32]), -O.bf16_to_f32(x[..., 32:]))
     assert np.array_equal(quarter[..., 32:], x[..., :32])
+
+
+def test_attention_oracle_against_torch_and_closed_forms():
+    """Causal GQA attention: torch's math SDPA (float64, CPU) with enable_gqa; the first position
+    attends only to itself (o = v_0); equal keys give the running mean of v."""
+    import torch.nn.functional as F
+    rng = np.random.default_rng(41)
+    B, S, HQ, HK, D = 2, 19, 8, 2, 16
+    q, k, v = (rng.standard_normal((B, S, h, D)) for h in (HQ, HK, HK))
+    got = O.causal_gqa_attention(q, k, v, 0.25)
+    tq, tk, tv = (torch.tensor(a).transpose(1, 2) for a in (q, k, v))
+    ref = F.scaled_dot_product_attention(tq, tk, tv, is_causal=True, scale=0.25, enable_gqa=True).transpose(1, 2)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(got[:, 0], np.repeat(v[:, 0], HQ // HK, axis=1), rtol=1e-12)
+    k_same = np.repeat(k[:, :1], S, axis=1)
+    mean = np.cumsum(v, axis=1) / np.arange(1, S + 1)[None, :, None, None]
+    np.testing.assert_allclose(O.causal_gqa_attention(q, k_same, v, 0.25), np.repeat(mean, HQ // HK, axis=2),
+                               rtol=1e-10, atol=1e-12)
