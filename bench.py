@@ -302,6 +302,7 @@ def main():
                          "epilogue, requant of h, down(+residual); attention (a torch op) not included")
         extra["layer_T4096"] = layer
         extra["gdn_8x2048"] = gdn_token_mixer(torch, dev, timer, args)
+        extra["attention_8x2048"] = attention_extra(torch, dev, timer, args)
         result["extra"] = extra
         result["prefill_tokens_per_s"] = layer["hot_path_tokens_per_s_36_layers"]
 
@@ -359,9 +360,35 @@ def gdn_token_mixer(torch, dev, timer, args):
     return out
 
 
+def attention_extra(torch, dev, timer, args):
+    """Causal GQA attention of the full-attention layers (16 query / 4 K/V heads of 256) on 8 x 2048
+    tokens, q / k / v as views of one fused QKV buffer: the flash-attention kernel against torch SDPA
+    on the same views.  FLOPs: 4 B HQ D S^2 / 2 (the causal half of QK^T and PV)."""
+    import math
+
+    import torch.nn.functional as F
+
+    from mica_amd.attention import causal_gqa_attention
+
+    B, S, HQ, HK, D = 8, 2048, 16, 4, 256
+    g = torch.Generator(device=dev).manual_seed(11)
+    qkv = torch.randn(B * S, (HQ + 2 * HK) * D, device=dev, generator=g).to(torch.bfloat16)
+    q, k, v = qkv.view(B, S, HQ + 2 * HK, D).split((HQ, HK, HK), dim=2)
+    flops = 4.0 * B * HQ * D * S * S / 2
+    steps = max(args.steps // 20, 5)
+    ms = timer.run(lambda: causal_gqa_attention(q, k, v), steps, args.warmup)
+    ms_ref = timer.run(lambda: F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                                              is_causal=True, scale=1 / math.sqrt(D), enable_gqa=True),
+                       steps, args.warmup)
+    t = flops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "TFLOP/s": round(t, 1), "frac_bf16_peak": round(t / PEAK_BF16_TFLOPS, 4),
+            "sdpa_us": round(ms_ref * 1e3, 1), "speedup_vs_sdpa": round(ms_ref / ms, 2), "flops": flops}
+
+
 def stack_prefill(torch, dev, reps=3):
     """Config 4: the 36-layer 4B-shaped W8A8 stack on 8 requests x 2048 packed tokens, readout of 255
-    option ids at each request's last position.  Attention is torch SDPA (bf16)."""
+    option ids at each request's last position.  Attention (16 query / 4 K/V heads of 256) runs on the
+    flash-attention kernel; RoPE on the in-place kernel."""
     from mica_amd.model import StackConfig, W8A8Stack
 
     st = W8A8Stack(StackConfig(), device=dev, seed=0)
@@ -380,8 +407,8 @@ def stack_prefill(torch, dev, reps=3):
     ok = bool(torch.isfinite(probs).all()) and bool(torch.allclose(probs.sum(1), torch.ones(B, device=dev)))
     del st
     torch.cuda.empty_cache()
-    return {"workload": "36 layers, hidden 2560, inter 9728, QKV 6144, vocab 151936; 8 requests x 2048 tokens "
-                        "packed; last-position readout over 255 option ids + softmax",
+    return {"workload": "36 layers, hidden 2560, inter 9728, QKV 6144 (16 / 4 heads of 256), vocab 151936; "
+                        "8 requests x 2048 tokens packed; last-position readout over 255 option ids + softmax",
             "ms_per_prefill": round(ms, 2), "tokens_per_s": round(B * S / (ms * 1e-3), 1),
             "w8a8_linear_TOP": round(ops / 1e12, 2), "linear_TOPS_incl_attention_time": round(ops / (ms * 1e-3) / 1e12, 1),
             "probs_valid": ok, "reps": reps}

@@ -176,20 +176,22 @@ int mica_rope_inplace(void *x, long long ldx, int n_heads, int head_dim, const v
 
 /*
  * Causal grouped-query attention forward, head dim 256, HQ = 4 HK (query head h reads key/value head
- * h / 4).  Replaces the attention of the full-attention layers: the reference's Triton kernel
- * (kernel_src/kernels.py:71-124, int8_kernels.attn_fwd, int8_kernels.py:409-481) and torch SDPA.
- *   o[b, t, h] = sum_{u <= t} softmax_u(scale q[b, t, h] . k[b, u, h / 4]) v[b, u, h / 4]
- * q / k / v / o: bf16, head j of position t of sequence b at ptr + b sb + t ld + j 256 (elements);
+ * h / 4), Sq queries over Sk >= Sq keys (the queries are the last Sq positions).  Replaces the
+ * reference's attn_fwd (int8_kernels.py:409-481, Triton kernel kernel_src/kernels.py:71-124) and the
+ * torch SDPA path of the full-attention layers.
+ *   o[b, t, h] = sum_{u <= t + Sk - Sq} softmax_u(scale q[b, t, h] . k[b, u, h / 4]) v[b, u, h / 4]
+ * q / k / v / o: bf16; head j of row t of sequence b at ptr + b sb + j sh + t ld (elements, all % 8).
  * fp32 softmax and accumulation, bf16 products.  causal must be 1.  workspace:
- * mica_attention_workspace_bytes(B, S, HK) bytes (V^T tile images), 16-byte aligned.
+ * mica_attention_workspace_bytes(B, Sk, HK) bytes (V^T tile images), 16-byte aligned.
  */
-int mica_attention_fwd(const void *q, long long sbq, long long ldq, const void *k, long long sbk, long long ldk,
-                       const void *v, long long sbv, long long ldv, void *o, long long sbo, long long ldo, int B, int S,
-                       int HQ, int HK, int head_dim, float scale, int causal, void *workspace,
-                       long long workspace_bytes, mica_stream_t stream);
+int mica_attention_fwd(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
+                       long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv, void *o,
+                       long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ, int HK,
+                       int head_dim, float scale, int causal, void *workspace, long long workspace_bytes,
+                       mica_stream_t stream);
 
-/* bytes of mica_attention_fwd workspace: B x HK x ceil(S / 32) x 16 KiB */
-long long mica_attention_workspace_bytes(int B, int S, int HK);
+/* bytes of mica_attention_fwd workspace: B x HK x ceil(Sk / 32) x 16 KiB */
+long long mica_attention_workspace_bytes(int B, int Sk, int HK);
 
 /* ---- gated delta net (GDN) token mixer ------------------------------------------------------- */
 

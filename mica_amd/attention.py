@@ -20,42 +20,44 @@ HEAD_DIM = 256
 GROUP = 4
 
 
-def _view(t, name):
-    if t.dim() != 4 or t.dtype != torch.bfloat16 or t.shape[-1] != HEAD_DIM or t.stride(3) != 1 or \
-            t.stride(2) != HEAD_DIM:
-        raise ValueError(f"{name} must be bf16 [B, S, heads, 256] with contiguous heads")
-    return t.stride(0), t.stride(1)
-
-
-def causal_gqa_attention(q, k, v, scale: float | None = None, out=None):
-    """softmax(scale q k^T, causal) v per sequence and head; query head h reads key/value head h // 4."""
+def attention_fwd(q, k, v, q_layout: str, scale: float | None = None):
+    """Launch the kernel on q [B, Sq, HQ, 256] / k, v [B, Sk, HK, 256] ('bshd') or q [B, HQ, Sq, 256] /
+    k, v [B, HK, Sk, 256] ('bhsd') views with unit feature stride.  Returns o in q's layout
+    (contiguous [B, Sq, HQ, 256] memory), or raises ValueError on an unsupported input."""
     for t in (q, k, v):
         if not t.is_cuda:
             raise ValueError("mica_amd attention runs on the GPU only (got a CPU tensor)")
+        if t.dim() != 4 or t.dtype != torch.bfloat16 or t.shape[-1] != HEAD_DIM or t.stride(3) != 1:
+            raise ValueError("q / k / v must be bf16 4-D tensors with head dim 256 and unit feature stride")
     dev = q.device
     if not _gpu_ok(dev):
         raise RuntimeError(f"mica_amd kernels need a gfx950 GPU (device {dev})")
-    sbq, ldq = _view(q, "q")
-    sbk, ldk = _view(k, "k")
-    sbv, ldv = _view(v, "v")
-    B, S, HQ, _ = q.shape
-    HK = k.shape[2]
-    if k.shape[:2] != (B, S) or v.shape[:3] != (B, S, HK) or HQ != GROUP * HK:
-        raise ValueError("q / k / v shapes do not match (4 query heads per key/value head)")
-    o = out if out is not None else torch.empty((B, S, HQ, HEAD_DIM), dtype=torch.bfloat16, device=dev)
-    if o.shape != (B, S, HQ, HEAD_DIM) or not o.is_contiguous():
-        raise ValueError("out must be a contiguous bf16 [B, S, HQ, 256] tensor")
+    if q_layout == "bshd":
+        (B, Sq, HQ, _), (_, Sk, HK, _) = q.shape, k.shape
+        st = lambda t: (t.stride(0), t.stride(2), t.stride(1))  # noqa: E731  (batch, head, row)
+    else:
+        (B, HQ, Sq, _), (_, HK, Sk, _) = q.shape, k.shape
+        st = lambda t: (t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
+    if k.shape != v.shape or k.shape[0] != B or HQ != GROUP * HK or Sk < Sq:
+        raise ValueError("q / k / v shapes do not match (4 query heads per key/value head, Sk >= Sq)")
+    o = torch.empty((B, Sq, HQ, HEAD_DIM), dtype=torch.bfloat16, device=dev)
     L = _lib.load()
-    nbytes = int(L.mica_attention_workspace_bytes(B, S, HK))
+    nbytes = int(L.mica_attention_workspace_bytes(B, Sk, HK))
     ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=dev)
     if not _aligned(q, k, v, o, ws):
         raise ValueError("attention operands must be 16-byte aligned")
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else float(scale)
-    sbo, ldo = o.stride(0), o.stride(1)
+    o_st = (o.stride(0), o.stride(2), o.stride(1))
     rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd(
-        q.data_ptr(), sbq, ldq, k.data_ptr(), sbk, ldk, v.data_ptr(), sbv, ldv, o.data_ptr(), sbo, ldo,
-        B, S, HQ, HK, HEAD_DIM, scale, 1, ws.data_ptr(), nbytes, _stream(dev))), "mica_attention_fwd")
+        q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), o.data_ptr(), *o_st,
+        B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, ws.data_ptr(), nbytes, _stream(dev))), "mica_attention_fwd")
     if rc:
-        raise ValueError(f"causal_gqa_attention: unsupported input ({_lib.status_name(rc)})")
+        raise ValueError(f"attention: unsupported input ({_lib.status_name(rc)})")
     _launched()
-    return o
+    return o if q_layout == "bshd" else o.transpose(1, 2)
+
+
+def causal_gqa_attention(q, k, v, scale: float | None = None):
+    """softmax(scale q k^T, causal) v per sequence and head on [B, S, heads, 256] views (e.g. of the
+    fused QKV output); query head h reads key/value head h // 4.  Returns o [B, S, HQ, 256] bf16."""
+    return attention_fwd(q, k, v, "bshd", scale)

@@ -3,7 +3,9 @@
 // (kernel_src/kernels.py:71-124, launched by int8_kernels.attn_fwd, int8_kernels.py:409-481) and the
 // torch SDPA fallback the attention layers use without it.
 //
-//   o[t, h] = sum_{u <= t} softmax_u(scale q[t, h] . k[u, g(h)]) v[u, g(h)],   g(h) = h / (HQ / HK)
+//   o[t, h] = sum_{u <= t + Sk - Sq} softmax_u(scale q[t, h] . k[u, g(h)]) v[u, g(h)],  g(h) = h / (HQ / HK)
+//
+// (Sq queries over Sk >= Sq keys: the queries are the last Sq positions, as in the reference's kernel.)
 //
 // Work split: one workgroup of 4 waves per (sequence, key/value head, block of 32 query positions);
 // wave w handles query head 4 g + w, so every K / V tile brought into LDS serves the 4 query heads of
@@ -32,7 +34,14 @@ constexpr int kFaThreads = 64 * kFaWaves;
 constexpr int kKBytes = kBK * kD * 2;    // 16 KB: 32 key rows x 512 B
 constexpr int kVBytes = kD * kBK * 2;    // 16 KB: 256 dim rows x 64 B
 constexpr int kStage = kKBytes + kVBytes;
-constexpr int kFaSmem = 2 * kStage;      // also the output staging (4 waves x 32 x 512 B) after the loop
+#ifndef MICA_FA_STAGES
+#define MICA_FA_STAGES 2
+#endif
+#ifndef MICA_FA_OCC
+#define MICA_FA_OCC 2
+#endif
+constexpr int kNSt = MICA_FA_STAGES;     // LDS stages (tiles in flight: kNSt - 1 ahead)
+constexpr int kFaSmem = kNSt * kStage;   // also the output staging (4 waves x 32 x 512 B) after the loop
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -49,18 +58,19 @@ MICA_DEVICE void fa_wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// V^T tile image: element (d, key k) of a tile at d * 32 + (((k / 4) ^ vt_swz(d)) * 4) + k % 4 (bf16);
-// XOR of the 8-byte unit by an even value keeps the 16-byte pairs the DMA moves intact
-MICA_DEVICE int vt_swz(int d) { return 2 * (d & 3); }
+// V^T tile image: element (d, key k) of a tile at d * 32 + (((k / 4) ^ vt_swz(d)) * 4) + k % 4 (bf16).
+// Rows are 64 bytes, so 4 consecutive dims span the 64 banks; XOR-ing the 8-byte unit with d / 4 puts
+// the 32 lanes of an operand read (32 consecutive dims, one unit each) on 32 distinct bank pairs.
+MICA_DEVICE int vt_swz(int d) { return (d >> 2) & 7; }
 
 struct FaParams {
-    const uint16_t *q; long long sbq, ldq;  // q head h of position t of sequence b: q + b sbq + t ldq + h 256
-    const uint16_t *k; long long sbk, ldk;
-    const uint16_t *v; long long sbv, ldv;
-    uint16_t *vt;                           // V^T images [B][HK][ntiles][256][32]
-    uint16_t *o; long long sbo, ldo;
-    int B, S, HQ, HK, ntiles;
-    float scale_log2;                       // softmax scale x log2(e)
+    const uint16_t *q; long long sbq, shq, ldq; // head h of row t of sequence b: q + b sbq + h shq + t ldq
+    const uint16_t *k; long long sbk, shk, ldk;
+    const uint16_t *v; long long sbv, shv, ldv;
+    uint16_t *vt;                               // V^T images [B][HK][ntiles_k][256][32]
+    uint16_t *o; long long sbo, sho, ldo;
+    int B, Sq, Sk, HQ, HK, ntiles_q, ntiles_k;
+    float scale_log2;                           // softmax scale x log2(e)
 };
 
 // ---- V -> V^T tile images: one workgroup per (tile, sequence x head); thread = 8 dims x 4 keys ----
@@ -73,9 +83,9 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(FaParams p) {
     for (int e = 0; e < 4; ++e) {
         const int t = tile * kBK + 4 * u + e;
         rows[e] = u32x4{0u, 0u, 0u, 0u};
-        if (t < p.S) rows[e] = *(const u32x4 *)(p.v + b * p.sbv + (long long)t * p.ldv + hk * kD + d0);
+        if (t < p.Sk) rows[e] = *(const u32x4 *)(p.v + b * p.sbv + hk * p.shv + (long long)t * p.ldv + d0);
     }
-    uint16_t *dst = p.vt + (((long long)bh * p.ntiles + tile) * kD) * kBK;
+    uint16_t *dst = p.vt + (((long long)bh * p.ntiles_k + tile) * kD) * kBK;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int d = d0 + i;
@@ -87,21 +97,24 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(FaParams p) {
     }
 }
 
-__global__ __launch_bounds__(kFaThreads, 2) void fa_fwd_kernel(FaParams p) {
+__global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParams p) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[kFaSmem];
-    const int qblk = p.ntiles - 1 - (int)blockIdx.x; // longest rows first
-    const int hk = blockIdx.y, b = blockIdx.z;
+    // grid (HK, B, ntiles_q): every (sequence, head) pair's longest query blocks are dispatched first
+    const int qblk = p.ntiles_q - 1 - (int)blockIdx.z;
+    const int hk = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hi = lane >> 5;
     const int head = hk * kFaWaves + wave;
     const int q0 = qblk * kBQ;
-    const int last = qblk; // key tiles 0 .. qblk (tile qblk holds the diagonal)
+    const int off = p.Sk - p.Sq; // position of query row t is off + t
+    // key tiles 0 .. last: the last one holds the block's last query position
+    const int last = min(p.ntiles_k - 1, (off + q0 + kBQ - 1) / kBK);
 
-    // operand buffers: K rows of sequence b (rows >= S read as zeros), the V^T images of (b, hk)
+    // operand buffers: K rows of (b, hk) (rows >= Sk read as zeros), the V^T images of (b, hk)
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.k + b * p.sbk), 0, (int)((long long)p.S * p.ldk * 2), kBufferFlags);
+        (void *)(p.k + b * p.sbk + hk * p.shk), 0, (int)((long long)p.Sk * p.ldk * 2), kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.vt + ((long long)(b * p.HK + hk) * p.ntiles) * kD * kBK), 0, p.ntiles * kVBytes, kBufferFlags);
+        (void *)(p.vt + ((long long)(b * p.HK + hk) * p.ntiles_k) * kD * kBK), 0, p.ntiles_k * kVBytes, kBufferFlags);
     auto dma_tile = [&](int j, int st) {
         int8_t *ks = smem + st * kStage;
 #pragma unroll
@@ -110,13 +123,13 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd_kernel(FaParams p) {
             // which holds logical chunk (l % 32) ^ row
             const int row = (wave * 4 + i) * 2 + hi;
             const int lc = l32 ^ row;
-            const int off = (int)((long long)(j * kBK + row) * p.ldk * 2 + (hk * kD + lc * 8) * 2);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(ks + (wave * 4 + i) * 1024), 16, off, 0, 0, 0);
+            const int ko = (int)((long long)(j * kBK + row) * p.ldk * 2 + lc * 16);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(ks + (wave * 4 + i) * 1024), 16, ko, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int off = j * kVBytes + (wave * 4 + i) * 1024 + lane * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16, off, 0,
+            const int vo = j * kVBytes + (wave * 4 + i) * 1024 + lane * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16, vo, 0,
                                                      0, 0);
         }
     };
@@ -128,7 +141,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd_kernel(FaParams p) {
 #pragma unroll
         for (int s = 0; s < kD / 16; ++s) {
             u32x4 v = {0u, 0u, 0u, 0u};
-            if (t < p.S) v = *(const u32x4 *)(p.q + b * p.sbq + (long long)t * p.ldq + head * kD + s * 16 + hi * 8);
+            if (t < p.Sq) v = *(const u32x4 *)(p.q + b * p.sbq + head * p.shq + (long long)t * p.ldq + s * 16 + hi * 8);
             qf[s] = __builtin_bit_cast(bf16x8, v);
         }
     }
@@ -136,14 +149,20 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd_kernel(FaParams p) {
 #pragma unroll
     for (int dt = 0; dt < kD / 32; ++dt) O[dt] = f32x16{};
     float m_used = -__builtin_inff(), lsum = 0.0f;
-    const int query = q0 + l32;
+    const int query = off + q0 + l32; // position of this lane's query
 
-    dma_tile(0, 0);
+    // prologue: tiles 0 .. kNSt - 2 in flight
+#pragma unroll
+    for (int i = 0; i < kNSt - 1; ++i)
+        if (i <= last) dma_tile(i, i);
     for (int j = 0; j <= last; ++j) {
-        fa_wait_vmcnt<0>();   // this wave's DMA of tile j (and, at j = 0, its Q loads) landed ...
-        __syncthreads();      // ... and every wave's; nobody reads the other stage any more
-        if (j < last) dma_tile(j + 1, (j + 1) & 1);
-        const int8_t *ks = smem + (j & 1) * kStage;
+        // this wave's DMA of tile j landed: at most the DMA of tiles j + 1 .. j + kNSt - 2 (8 each) is
+        // younger; near the end fewer were issued, and waiting for all of them is exact too
+        if (kNSt > 2 && j + kNSt - 2 <= last) fa_wait_vmcnt<(kNSt > 2 ? (kNSt - 2) * 8 : 0)>();
+        else fa_wait_vmcnt<0>();
+        __syncthreads();      // ... in every wave; nobody reads stage (j - 1) % kNSt any more
+        if (j + kNSt - 1 <= last) dma_tile(j + kNSt - 1, (j + kNSt - 1) % kNSt);
+        const int8_t *ks = smem + (j % kNSt) * kStage;
         const int8_t *vs = ks + kKBytes;
         // ---- S^T = K Q^T: rows = keys j*32 + acc_row, column = query l % 32 ----
         f32x16 sacc = {};
@@ -220,47 +239,49 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd_kernel(FaParams p) {
         const int row = piece >> 5, c = piece & 31; // 32 pieces of 16 B per 512 B row
         const int t = q0 + row;
         const u32x4 v = *(const u32x4 *)(ost + row * (kD * 2) + c * 16);
-        if (t < p.S) *(u32x4 *)(p.o + b * p.sbo + (long long)t * p.ldo + head * kD + c * 8) = v;
+        if (t < p.Sq) *(u32x4 *)(p.o + b * p.sbo + head * p.sho + (long long)t * p.ldo + c * 8) = v;
     }
 }
 
 }  // namespace
 
-extern "C" long long mica_attention_workspace_bytes(int B, int S, int HK) {
-    if (B < 0 || S < 0 || HK <= 0) return -1;
-    return (long long)B * HK * ((S + kBK - 1) / kBK) * kVBytes;
+extern "C" long long mica_attention_workspace_bytes(int B, int Sk, int HK) {
+    if (B < 0 || Sk < 0 || HK <= 0) return -1;
+    return (long long)B * HK * ((Sk + kBK - 1) / kBK) * kVBytes;
 }
 
-extern "C" int mica_attention_fwd(const void *q, long long sbq, long long ldq, const void *k, long long sbk,
-                                  long long ldk, const void *v, long long sbv, long long ldv, void *o, long long sbo,
-                                  long long ldo, int B, int S, int HQ, int HK, int head_dim, float scale, int causal,
-                                  void *workspace, long long workspace_bytes, mica_stream_t stream) {
-    if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || S < 0) return MICA_MISS_SHAPE;
+extern "C" int mica_attention_fwd(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
+                                  long long shk, long long ldk, const void *v, long long sbv, long long shv,
+                                  long long ldv, void *o, long long sbo, long long sho, long long ldo, int B, int Sq,
+                                  int Sk, int HQ, int HK, int head_dim, float scale, int causal, void *workspace,
+                                  long long workspace_bytes, mica_stream_t stream) {
+    if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || Sq < 0 || Sk < Sq) return MICA_MISS_SHAPE;
     if (!causal) return MICA_MISS_ARG;
-    if (B == 0 || S == 0) return 0;
+    if (B == 0 || Sq == 0) return 0;
     if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || workspace == nullptr) return MICA_MISS_ARG;
-    if (ldq < (long long)HQ * kD || ldk < (long long)HK * kD || ldv < (long long)HK * kD || ldo < (long long)HQ * kD ||
-        ldq % 8 || ldk % 8 || ldv % 8 || ldo % 8 || sbq % 8 || sbk % 8 || sbv % 8 || sbo % 8 ||
-        (B > 1 && (sbq < S * ldq || sbk < S * ldk || sbv < S * ldv || sbo < S * ldo)))
-        return MICA_MISS_STRIDE;
+    const long long st[12] = {sbq, shq, ldq, sbk, shk, ldk, sbv, shv, ldv, sbo, sho, ldo};
+    for (long long x : st)
+        if (x < 0 || x % 8) return MICA_MISS_STRIDE;
+    if (ldq < kD && Sq > 1) return MICA_MISS_STRIDE;
     if (!mica_aligned16(q) || !mica_aligned16(k) || !mica_aligned16(v) || !mica_aligned16(o) ||
         !mica_aligned16(workspace))
         return MICA_MISS_ALIGN;
-    const int ntiles = (S + kBK - 1) / kBK;
-    if ((long long)ntiles * kBK * ldk * 2 >= (1LL << 31) || (long long)ntiles * kVBytes >= (1LL << 31))
+    const int ntiles_q = (Sq + kBQ - 1) / kBQ, ntiles_k = (Sk + kBK - 1) / kBK;
+    if ((long long)ntiles_k * kBK * ldk * 2 >= (1LL << 31) || (long long)ntiles_k * kVBytes >= (1LL << 31) ||
+        ntiles_q > 65535 || B > 65535)
         return MICA_MISS_RANGE;
-    if (workspace_bytes < mica_attention_workspace_bytes(B, S, HK)) return MICA_MISS_ARG;
+    if (workspace_bytes < mica_attention_workspace_bytes(B, Sk, HK)) return MICA_MISS_ARG;
     FaParams p{};
-    p.q = (const uint16_t *)q; p.sbq = sbq; p.ldq = ldq;
-    p.k = (const uint16_t *)k; p.sbk = sbk; p.ldk = ldk;
-    p.v = (const uint16_t *)v; p.sbv = sbv; p.ldv = ldv;
-    p.vt = (uint16_t *)workspace; p.o = (uint16_t *)o; p.sbo = sbo; p.ldo = ldo;
-    p.B = B; p.S = S; p.HQ = HQ; p.HK = HK; p.ntiles = ntiles;
+    p.q = (const uint16_t *)q; p.sbq = sbq; p.shq = shq; p.ldq = ldq;
+    p.k = (const uint16_t *)k; p.sbk = sbk; p.shk = shk; p.ldk = ldk;
+    p.v = (const uint16_t *)v; p.sbv = sbv; p.shv = shv; p.ldv = ldv;
+    p.vt = (uint16_t *)workspace; p.o = (uint16_t *)o; p.sbo = sbo; p.sho = sho; p.ldo = ldo;
+    p.B = B; p.Sq = Sq; p.Sk = Sk; p.HQ = HQ; p.HK = HK; p.ntiles_q = ntiles_q; p.ntiles_k = ntiles_k;
     p.scale_log2 = scale * 1.44269504088896341f;
-    hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles, B * HK), dim3(256), 0, st, p);
+    hipStream_t stream_ = (hipStream_t)stream;
+    hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles_k, B * HK), dim3(256), 0, stream_, p);
     int rc = mica_err(hipGetLastError());
     if (rc) return rc;
-    hipLaunchKernelGGL(fa_fwd_kernel, dim3(ntiles, HK, B), dim3(kFaThreads), 0, st, p);
+    hipLaunchKernelGGL(fa_fwd_kernel, dim3(HK, B, ntiles_q), dim3(kFaThreads), 0, stream_, p);
     return mica_err(hipGetLastError());
 }

@@ -254,15 +254,43 @@ def mm_i8_int32(qx, qw, split=False):
     return out if ok else None
 
 
-ATTN = {"enabled": False}
+ATTN = {"enabled": True}
 
 
 def attn_keys(device=None):
-    """No attention kernels ship in this build (attention runs as a torch op)."""
-    return []
+    """The attention configuration the gfx950 kernel serves, in the reference's key format
+    (int8_kernels.py:420-427): bf16, head dim 256, 16 query heads, 4 per key/value head, scale 1/16 (the
+    4B model's full-attention layers).  The kernel itself takes any scale and HQ = 4 HK."""
+    try:
+        dev = _dev(device)
+    except Exception:
+        return []
+    if dev.type != "cuda" or not _gpu_ok(dev):
+        return []
+    return ["attn|bf16|hd256|hq16|r4|s0.0625|m64"]
 
 
 def attn_fwd(q, k, v, scale):
-    """Always a miss: the causal GQA attention of the reference (kernel_src/kernels.py:71-124) is outside
-    this build's scope and stays on torch's scaled_dot_product_attention."""
-    return _miss("attn_unsupported")
+    """Causal GQA attention forward (int8_kernels.py:430-481): q [b, hq, n, d], k / v [b, hk, keys, d]
+    (keys >= n; the queries are the last n positions), bf16, unit feature stride.  Returns o [b, hq, n, d]
+    (a view of a [b, n, hq, d] tensor, as the reference returns), or None on a miss."""
+    if q.dim() != 4 or k.dim() != 4 or v.shape != k.shape or q.device.type != "cuda" or \
+            not q.dtype == k.dtype == v.dtype == torch.bfloat16:
+        return _miss("attn_input")
+    b, hq, n, d = q.shape
+    hk, keys = k.shape[1], k.shape[2]
+    if k.shape[0] != b or k.shape[3] != d or hq % hk or n < 1 or keys < n or k.device != q.device:
+        return _miss("attn_shape")
+    if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
+        return _miss("attn_stride")
+    if not _gpu_ok(q.device):
+        return _miss("no_container")
+    if d != 256 or hq != 4 * hk:
+        return _miss("attn_config")
+    if not _aligned(q, k, v) or any(s % 8 for t in (q, k, v) for s in t.stride()[:3]):
+        return _miss("align")
+    from .attention import attention_fwd
+    try:
+        return attention_fwd(q, k, v, "bhsd", float(scale))
+    except ValueError:
+        return _miss("attn_unsupported")

@@ -25,6 +25,7 @@ import torch
 import torch.nn.functional as F
 
 from . import int8_kernels as aot
+from .attention import GROUP as _FA_GROUP, HEAD_DIM as _FA_DIM, causal_gqa_attention
 from .fused_kernels import rms_norm_quant, rope_inplace
 from .int8_runtime import GateUpQLinear, QLinear
 from .readout import LabelReadout
@@ -35,9 +36,9 @@ class StackConfig:
     layers: int = 36
     hidden: int = 2560
     intermediate: int = 9728
-    heads: int = 32
-    kv_heads: int = 8
-    head_dim: int = 128
+    heads: int = 16       # the reference's full-attention layers: 16 query / 4 K/V heads of 256
+    kv_heads: int = 4     # (kernel_src/kernels.py:5, 71-124); QKV 6144 = (16 + 2 * 4) * 256
+    head_dim: int = 256
     vocab: int = 151936
     eps: float = 1e-6
     rope_theta: float = 1_000_000.0
@@ -87,8 +88,9 @@ def _apply_rope(x, cos, sin):
 class W8A8Stack:
     """Random-init 4B-shaped stack; `prefill(ids, batch)` returns option probabilities."""
 
-    def __init__(self, cfg: StackConfig = StackConfig(), device="cuda", seed=0):
+    def __init__(self, cfg: StackConfig = StackConfig(), device="cuda", seed=0, attention: str = "mica"):
         self.cfg = cfg
+        self.attention = attention
         self.device = torch.device(device)
         g = torch.Generator(device=self.device).manual_seed(seed)
         H = cfg.hidden
@@ -102,11 +104,11 @@ class W8A8Stack:
         self._rope = {}
 
     def _attention(self, qkv, B, S):
-        """Causal GQA attention per request on torch SDPA.  RoPE rotates the q and k heads of the QKV
-        output in place (one kernel), and SDPA reads [B, S, heads, d] views of it through transposed
-        strides (enable_gqa shares each K/V head with its group of query heads, no repeated copies);
-        the output comes back [B, S, heads, d]-contiguous, i.e. already the O projection's
-        [T, heads * d] rows."""
+        """Causal GQA attention per request.  RoPE rotates the q and k heads of the QKV output in place
+        (one kernel); the flash-attention kernel (head dim 256, 4 query heads per K/V head) then reads
+        [B, S, heads, d] views of it and writes [B, S, heads, d]-contiguous output, i.e. already the O
+        projection's [T, heads * d] rows.  Other head shapes, or attention="sdpa", use torch SDPA on the
+        same views (enable_gqa, transposed strides, no copies)."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
         if S not in self._rope:
@@ -114,6 +116,8 @@ class W8A8Stack:
         cos, sin = self._rope[S]
         rope_inplace(qkv, hq + hk, d, cos, sin, period=S)
         q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
+        if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
+            return causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d)).view(B * S, hq * d)
         a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
                                            scale=1.0 / math.sqrt(d), enable_gqa=True)
         return a.transpose(1, 2).reshape(B * S, hq * d).contiguous()

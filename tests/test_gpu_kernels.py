@@ -580,3 +580,32 @@ def test_causal_gqa_attention_matches_oracle(gpu, B, S, HK):
                 for b in range(B) for h in range(HQ))
     print(f"relative error {worst:.2e}", file=sys.stderr)
     assert worst <= 1e-2
+
+
+def test_attn_fwd_reference_selftest_cases(gpu):
+    """int8_kernels.attn_fwd under the reference's own attention self-test (int8_runtime.py:444-488):
+    its shapes (b, n, keys) with prefix keys, q as a transposed [b, n, hq, d] tensor and head-major k / v,
+    checked against the float64 oracle with the reference's row tolerance 0.02."""
+    print("[case] attn_fwd self-test cases", file=sys.stderr, flush=True)
+    hq, rep, d, scale = 16, 4, 256, 0.0625
+    hk = hq // rep
+    assert int8_kernels.attn_keys(gpu) == ["attn|bf16|hd256|hq16|r4|s0.0625|m64"]
+    g = torch.Generator().manual_seed(20261022)
+    worst = 0.0
+    for b, n, s in ((1, 1, 37), (2, 13, 13), (1, 48, 200), (1, 130, 130), (2, 70, 333)):
+        q = torch.randn(b, n, hq, d, generator=g).to(torch.bfloat16)
+        k = torch.randn(b, hk, s, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(b, hk, s, d, generator=g).to(torch.bfloat16)
+        o = int8_kernels.attn_fwd(q.to(gpu).transpose(1, 2), k.to(gpu), v.to(gpu), scale)
+        torch.cuda.synchronize()
+        assert o is not None and o.shape == (b, hq, n, d)
+        # oracle on the last n positions: pad the queries in front so query row i sits at position s - n + i
+        qp = torch.zeros(b, s, hq, d)
+        qp[:, s - n:] = q.float()
+        ref = O.causal_gqa_attention(qp.numpy(), k.float().transpose(1, 2).numpy(), v.float().transpose(1, 2).numpy(),
+                                     scale)[:, s - n:]
+        got = o.float().cpu().transpose(1, 2).numpy()
+        err = (np.linalg.norm(got - ref, axis=-1) / np.linalg.norm(ref, axis=-1)).max()
+        worst = max(worst, err)
+        assert err <= 0.02, (b, n, s, err)
+    print(f"worst row error {worst:.2e}", file=sys.stderr)

@@ -30,9 +30,13 @@ def test_cpu_inputs_miss_like_the_reference(lenient):
     assert lenient["fallback"]["mm_contiguous"] == 1
     assert int8_kernels.mm_i8(q, s.double(), q, s) is None
     assert lenient["fallback"]["mm_scales"] == 1
-    assert int8_kernels.attn_fwd(None, None, None, 1.0) is None
-    assert lenient["fallback"]["attn_unsupported"] == 1
-    assert int8_kernels.attn_keys() == []
+    qa = torch.zeros(1, 4, 8, 256, dtype=torch.bfloat16)
+    ka = torch.zeros(1, 1, 8, 256, dtype=torch.bfloat16)
+    assert int8_kernels.attn_fwd(qa, ka, ka, 0.0625) is None      # CPU tensors (int8_kernels.py:431-438)
+    assert lenient["fallback"]["attn_input"] == 1
+    assert int8_kernels.attn_fwd(qa, ka[:, :, :4], ka[:, :, :4], 0.0625) is None  # fewer keys than queries
+    assert lenient["fallback"]["attn_input"] == 2
+    assert int8_kernels.attn_keys() == []                          # no gfx950 device here
 
 
 def test_strict_mode_raises_on_a_miss(monkeypatch):
