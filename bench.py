@@ -405,13 +405,41 @@ def stack_prefill(torch, dev, reps=3):
     ms = s.elapsed_time(e) / reps
     ops = st.linear_ops_per_token() * B * S
     ok = bool(torch.isfinite(probs).all()) and bool(torch.allclose(probs.sum(1), torch.ones(B, device=dev)))
+    engine = engine_latency(torch, dev, st)
     del st
     torch.cuda.empty_cache()
     return {"workload": "36 layers, hidden 2560, inter 9728, QKV 6144 (16 / 4 heads of 256), vocab 151936; "
                         "8 requests x 2048 tokens packed; last-position readout over 255 option ids + softmax",
             "ms_per_prefill": round(ms, 2), "tokens_per_s": round(B * S / (ms * 1e-3), 1),
             "w8a8_linear_TOP": round(ops / 1e12, 2), "linear_TOPS_incl_attention_time": round(ops / (ms * 1e-3) / 1e12, 1),
-            "probs_valid": ok, "reps": reps}
+            "probs_valid": ok, "reps": reps, "engine": engine}
+
+
+def engine_latency(torch, dev, st, reps=5):
+    """The prefill engine (HIP-graph buckets, mica_amd.engine) on the 36-layer stack: per-call time of
+    one 512-token request (launch-bound when eager: ~430 launches) and of 8 x 2048 tokens, eager vs a
+    replayed graph (inputs copied in, outputs copied out)."""
+    from mica_amd.engine import PrefillEngine
+
+    out = {}
+    g = torch.Generator().manual_seed(5)
+    for B, S in ((1, 512), (8, 2048)):
+        reqs = [torch.randint(0, st.cfg.vocab, (S,), generator=g).to(dev) for _ in range(B)]
+        for mode in ("eager", "graph"):
+            eng = PrefillEngine(st, graph=mode == "graph")
+            eng(reqs)
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                eng(reqs)
+            e.record()
+            torch.cuda.synchronize()
+            ms = s.elapsed_time(e) / reps
+            out[f"{mode}_B{B}_S{S}"] = {"ms": round(ms, 3), "tokens_per_s": round(B * S / (ms * 1e-3), 1)}
+            del eng
+    torch.cuda.empty_cache()
+    return out
 
 
 def pmc_workload():

@@ -1,0 +1,103 @@
+"""Last-position prefill engine with HIP-graph buckets.
+
+The reference's PrefillEngine (v0.5/serving/lib/prefill_engine.py:171-418) runs a batch of requests
+through the model and keeps only each request's last position for the label readout; request widths
+are rounded up to a bucket, and each (bucket) shape is captured once as a CUDA graph and replayed with
+the token ids and the last positions copied into the graph's static inputs (capture :370-389, replay
+:391-409).  This engine does the same over ``mica_amd.model.W8A8Stack`` on HIP graphs
+(torch.cuda.CUDAGraph on ROCm): requests are padded at the end to a common width (causal attention
+keeps the padding out of every real position), packed [batch, width], and run by the stack's
+``forward_last``; the readout reads row b * width + len_b - 1.  Header/prefix-state reuse of the
+reference (:214-268) is not built: prefill-only scoring re-runs each request in full.
+"""
+from __future__ import annotations
+
+import torch
+
+BUCKET = 64          # width granularity (tokens)
+GRAPH_MAX = 4096     # widest bucket that is captured; wider batches run eagerly
+GRAPH_WARMUP = 2     # eager runs on a side stream before a capture (prefill_engine.py:375-378)
+
+
+class _Graph:
+    def __init__(self, batch, width, device):
+        self.ids = torch.zeros(batch * width, dtype=torch.long, device=device)
+        self.rows = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.lo = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.cnt = torch.ones(batch, dtype=torch.int32, device=device)
+        self.graph = None
+        self.out = None
+
+
+class PrefillEngine:
+    def __init__(self, stack, graph: bool = True, bucket: int = BUCKET, graph_max: int = GRAPH_MAX):
+        self.stack = stack
+        self.device = stack.device
+        self.graph = bool(graph) and self.device.type == "cuda"
+        self.bucket, self.graph_max = int(bucket), int(graph_max)
+        self.graphs, self.pool = {}, None
+        self.captures = 0
+
+    def plan(self, lengths):
+        """(batch, padded width, graphed) for requests of these lengths."""
+        if not lengths or min(lengths) < 1:
+            raise ValueError("every request needs at least one token")
+        width = -(-max(lengths) // self.bucket) * self.bucket
+        return len(lengths), width, self.graph and width <= self.graph_max
+
+    def _pack(self, requests, width, out=None):
+        ids = out if out is not None else torch.zeros(len(requests) * width, dtype=torch.long, device=self.device)
+        ids.zero_()
+        for b, r in enumerate(requests):
+            ids[b * width:b * width + r.numel()].copy_(r.reshape(-1))
+        return ids
+
+    def _inputs(self, lengths, width, kinds, n_choices):
+        rows = [b * width + n - 1 for b, n in enumerate(lengths)]
+        lo, cnt = self.stack.slices(kinds, n_choices, len(lengths), "cpu")
+        return torch.tensor(rows, dtype=torch.int32), lo, cnt
+
+    @torch.no_grad()
+    def run(self, requests, kinds=None, n_choices=None):
+        """Eager: pack, run, read out.  Returns (logits [B, 2 + n_options], probs [B, n_options])."""
+        lengths = [int(r.numel()) for r in requests]
+        B, width, _ = self.plan(lengths)
+        ids = self._pack(requests, width)
+        rows, lo, cnt = (t.to(self.device) for t in self._inputs(lengths, width, kinds, n_choices))
+        return self.stack.forward_last(ids, B, rows, lo, cnt)
+
+    def capture(self, batch, width):
+        g = _Graph(batch, width, self.device)
+        g.rows.copy_(torch.arange(batch, dtype=torch.int32, device=self.device) * width + (width - 1))
+        fn = lambda: self.stack.forward_last(g.ids, batch, g.rows, g.lo, g.cnt)  # noqa: E731
+        if self.pool is None:
+            self.pool = torch.cuda.graph_pool_handle()
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side), torch.no_grad():
+            for _ in range(GRAPH_WARMUP):
+                fn()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        g.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g.graph, pool=self.pool), torch.no_grad():
+            g.out = fn()
+        self.graphs[batch, width] = g
+        self.captures += 1
+        return g
+
+    @torch.no_grad()
+    def __call__(self, requests, kinds=None, n_choices=None):
+        """Prefill `requests` (1-D int token-id tensors on the device) and return their last-position
+        (logits, probs).  Graphed shapes return fresh copies of the graph's static outputs."""
+        lengths = [int(r.numel()) for r in requests]
+        B, width, graphed = self.plan(lengths)
+        if not graphed:
+            return self.run(requests, kinds, n_choices)
+        g = self.graphs.get((B, width)) or self.capture(B, width)
+        self._pack(requests, width, g.ids)
+        rows, lo, cnt = self._inputs(lengths, width, kinds, n_choices)
+        g.rows.copy_(rows, non_blocking=False)
+        g.lo.copy_(lo, non_blocking=False)
+        g.cnt.copy_(cnt, non_blocking=False)
+        g.graph.replay()
+        return g.out[0].clone(), g.out[1].clone()

@@ -144,19 +144,31 @@ class W8A8Stack:
         """ids: int [batch * S] packed token ids of `batch` equal-length requests.  Returns
         (logits [batch, 2 + n_options], probs [batch, width]) for the requests' last positions;
         kinds[b] == 'noul' softmaxes logits[:2], otherwise logits[2 : 2 + n_choices[b]]."""
-        T = ids.numel()
-        S = T // batch
-        h = self.embed.index_select(0, ids)
-        for L in self.layers:
-            h = self.layer_forward(L, h, batch, S, trace)
-        rows = torch.arange(batch, device=h.device, dtype=torch.int32) * S + (S - 1)
+        S = ids.numel() // batch
+        rows = torch.arange(batch, device=ids.device, dtype=torch.int32) * S + (S - 1)
+        lo, cnt = self.slices(kinds, n_choices, batch, ids.device)
+        return self.forward_last(ids, batch, rows, lo, cnt, trace)
+
+    def slices(self, kinds, n_choices, batch, device):
+        """The readout's softmax slices per request: [0, 2) for 'noul', [2, 2 + n) for a choice."""
         if kinds is None:
             kinds = ["choice"] * batch
         if n_choices is None:
             n_choices = [self.cfg.n_options] * batch
-        lo = torch.tensor([0 if k == "noul" else 2 for k in kinds], dtype=torch.int32, device=h.device)
-        cnt = torch.tensor([2 if k == "noul" else n for k, n in zip(kinds, n_choices)], dtype=torch.int32,
-                           device=h.device)
+        lo = torch.tensor([0 if k == "noul" else 2 for k in kinds], dtype=torch.int32, device=device)
+        cnt = torch.tensor([2 if k == "noul" else n for k, n in zip(kinds, n_choices)], dtype=torch.int32, device=device)
+        return lo, cnt
+
+    @torch.no_grad()
+    def forward_last(self, ids, batch, rows, lo, cnt, trace=None):
+        """The stack over `batch` packed requests of equal (padded) length S = ids.numel() / batch, then
+        the readout at the token rows `rows` (int32 [batch], device) with softmax slices lo / cnt.
+        Everything stays on the device and no tensor is built from host values, so a HIP graph can
+        capture the call (rows / lo / cnt / ids then act as the graph's static inputs)."""
+        S = ids.numel() // batch
+        h = self.embed.index_select(0, ids)
+        for L in self.layers:
+            h = self.layer_forward(L, h, batch, S, trace)
         logits, probs = self.readout(h, rows, self.final_norm, self.cfg.eps, offset=0.0, lo=lo, cnt=cnt,
                                      probs_width=self.cfg.n_options)
         if trace is not None:
