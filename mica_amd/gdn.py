@@ -197,3 +197,59 @@ def gated_rmsnorm_quant(x, z, weight, eps: float = 1e-6, want_y: bool = False):
         None if y is None else y.data_ptr(), N, q.data_ptr(), N, s.data_ptr(), M, N, _stream(dev))),
         "mica_gated_rmsnorm_quant")
     return (q, s, y) if want_y else (q, s)
+
+
+class GDNLayer(torch.nn.Module):
+    """The token-mixing half of a gated-delta-net decoder layer on the W8A8 path (fork.gdn_step and the
+    layer's residual around it, fork.py:20-149): h + out_proj(norm_z(GDN(conv(in_proj(rmsnorm(h)))))).
+
+      1. input RMSNorm, quantized per token once for the four projections (in_proj_qkv, in_proj_z,
+         in_proj_b, in_proj_a; each a QLinear with its own SmoothQuant factors)  -> 1 + 4 launches
+      2. causal conv + SiLU over the q / k / v channels, q / k l2-normalised  -> 1 launch
+      3. g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)  (fork.py:124-125; torch, [T, HV])
+      4. chunked gated delta rule  -> 2 launches
+      5. gated RMSNorm fused with out_proj's quantisation, out_proj GEMM with the residual add in its
+         epilogue  -> 2 launches
+    Input h: [B * T, hidden] bf16 rows of B sequences of T tokens each.  With keep=True the layer also
+    returns (conv state, recurrent state) for continuation."""
+
+    def __init__(self, norm_weight, eps, in_qkv, in_z, in_b, in_a, conv_weight, A_log, dt_bias, norm_z_weight,
+                 out_proj, num_k_heads: int, num_v_heads: int, norm_offset: float = 1.0, z_eps: float = 1e-6):
+        super().__init__()
+        from .int8_runtime import SharedNormQLinears
+
+        self.inproj = SharedNormQLinears(norm_weight, eps, [in_qkv, in_z, in_b, in_a], offset=norm_offset)
+        self.register_buffer("conv_weight", conv_weight.contiguous())
+        self.register_buffer("A_log", A_log.float().contiguous())
+        self.register_buffer("dt_bias", dt_bias.float().contiguous())
+        self.register_buffer("norm_z_weight", norm_z_weight.to(torch.bfloat16).contiguous())
+        self.out_proj = out_proj
+        self.hk, self.hv = int(num_k_heads), int(num_v_heads)
+        self.z_eps = float(z_eps)
+        if in_qkv.out_features != (2 * self.hk + self.hv) * HEAD_DIM or in_z.out_features != self.hv * HEAD_DIM:
+            raise ValueError("projection widths do not match the head counts (head dims 128)")
+
+    @torch.no_grad()
+    def forward(self, h, batch: int, initial=None, keep: bool = False, trace=None):
+        T = h.shape[0] // batch
+        mixed, z, b, a = self.inproj(h)
+        C = mixed.shape[-1]
+        init_conv = None if initial is None else initial[0]
+        conv = causal_conv1d_fn(mixed.view(batch, T, C).transpose(1, 2), self.conv_weight, activation="silu",
+                                initial_states=init_conv, return_final_states=keep, l2norm_heads=2 * self.hk)
+        conv, conv_state = conv if keep else (conv, None)
+        x = conv.transpose(1, 2)                            # [B, T, C] (contiguous memory)
+        kd = self.hk * HEAD_DIM
+        q = x[..., :kd].unflatten(-1, (self.hk, HEAD_DIM))
+        k = x[..., kd:2 * kd].unflatten(-1, (self.hk, HEAD_DIM))
+        v = x[..., 2 * kd:].unflatten(-1, (self.hv, HEAD_DIM))
+        g = -self.A_log.exp() * torch.nn.functional.softplus(a.float() + self.dt_bias)
+        beta = b.sigmoid()
+        o, rec = chunk_gated_delta_rule(q, k, v, g.view(batch, T, self.hv), beta.view(batch, T, self.hv),
+                                        initial_state=None if initial is None else initial[1],
+                                        output_final_state=keep)
+        qo, so = gated_rmsnorm_quant(o.view(batch * T, -1), z, self.norm_z_weight, self.z_eps)
+        out = self.out_proj.forward_quantized(qo, so, residual=h)
+        if trace is not None:
+            trace.update(mixed=mixed, z=z, b=b, a=a, conv=x, g=g, beta=beta, o=o, qo=qo, so=so, out=out)
+        return (out, (conv_state, rec)) if keep else out
