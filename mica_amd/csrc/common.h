@@ -53,16 +53,27 @@ MICA_DEVICE float round_to(float f, int dtype) {
 }
 
 // ---- wavefront (64 lanes) reductions -------------------------------------------------------
-MICA_DEVICE float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// 64-lane reductions (every lane must be active; every lane gets the same bits): DPP steps within
+// each 16-lane row (quad swaps, half-row mirror, row mirror: each lane of a pair adds the same two
+// values, so a row ends uniform), then the four row results are read into scalars and combined in
+// the same order in every lane.  No LDS traffic, a few cycles per step.
+template <bool MAX>
+MICA_DEVICE float wave_reduce(float v) {
+    auto op = [](float a, float b) { return MAX ? __builtin_fmaxf(a, b) : a + b; };
+#define MICA_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ctrl, 0xF, 0xF, true))
+    v = op(v, MICA_DPP(v, 0xB1));  // quad_perm [1, 0, 3, 2]
+    v = op(v, MICA_DPP(v, 0x4E));  // quad_perm [2, 3, 0, 1]
+    v = op(v, MICA_DPP(v, 0x141)); // row_half_mirror
+    v = op(v, MICA_DPP(v, 0x140)); // row_mirror
+#undef MICA_DPP
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return op(op(r0, r1), op(r2, r3));
 }
-MICA_DEVICE float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
+MICA_DEVICE float wave_sum(float v) { return wave_reduce<false>(v); }
+MICA_DEVICE float wave_max(float v) { return wave_reduce<true>(v); }
 
 // Pack four int8 values (given as int) into one dword, element 0 in the low byte.
 MICA_DEVICE uint32_t pack_i8x4(int a, int b, int c, int d) {
@@ -72,6 +83,36 @@ MICA_DEVICE uint32_t pack_i8x4(int a, int b, int c, int d) {
 
 // scale of a row from its absmax: max(amax, 1e-8) / 127 (int8_quant.py:68, EPS :13, QMAX :11)
 MICA_DEVICE float row_scale(float amax) { return __builtin_fmaxf(amax, 1e-8f) / 127.0f; }
+
+// The multiplier of the one-FMA half-even quantizer for a row of bf16 values x with a bf16 absmax
+// a (|x| <= a), s = row_scale(a), inv = 1 / s:  q = low byte of fmaf(x, r, 1.5 * 2^23), which
+// rounds the exact product x r to an integer in one step.  r is inv, moved one ulp toward the
+// reference's answer for x = a / 2 when rint(x r) and rint(x / s) (IEEE quotient) disagree there;
+// with that, q == clamp(rint(x / s), -127, 127) for every bf16 pair (x, a) (checked exhaustively
+// on the CPU, tests/native/fma_quotient_check.c).  Costs two divisions per row, saves three
+// instructions per element against the corrected quotient.
+constexpr float kMagicRne = 12582912.0f; // 1.5 * 2^23
+MICA_DEVICE float fma_quant_recip(float a, float s, float inv) {
+    const float h = a * 0.5f;
+    const float qh = __builtin_rintf(h / s);
+    const float qf = __builtin_fmaf(h, inv, kMagicRne) - kMagicRne;
+    const int dir = qh > qf ? 1 : (qh < qf ? -1 : 0);
+    return __uint_as_float(__float_as_uint(inv) + (uint32_t)dir);
+}
+// 8 values -> 8 int8 (element 0 in the low byte) with the multiplier above
+MICA_DEVICE u32x2 fma_quant8(const float (&x)[8], float r) {
+    uint32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = __float_as_uint(__builtin_fmaf(x[j], r, kMagicRne));
+    u32x2 q;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t lo = __builtin_amdgcn_perm(b[4 * h + 1], b[4 * h], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(b[4 * h + 3], b[4 * h + 2], 0x0c0c0400u);
+        q[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+    return q;
+}
 
 // ---- host-side helpers ---------------------------------------------------------------------
 static inline bool mica_aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }

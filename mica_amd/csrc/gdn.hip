@@ -693,29 +693,17 @@ __global__ __launch_bounds__(64 * kGnWaves) void gated_norm_quant_kernel(GatedNo
     }
     amax = wave_max(amax);
     const float s = row_scale(amax);
-    const float r = 1.0f / s;
+    // bf16 y with a bf16 row maximum: the one-FMA half-even quantizer (exact against the IEEE
+    // quotient for every such pair, tests/native/fma_quotient_check.c)
+    const float r = fma_quant_recip(amax, s, 1.0f / s);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int col = i * 512 + lane * 8;
         if (p.y) *(u32x4 *)(p.y + (long)row * p.ldy + col) = yr[i];
-        // y / s as y r plus one correction step, then half-even rounding from the low byte of
-        // v + 1.5 * 2^23: for bf16 y and a bf16 row maximum this gives the integer of the IEEE
-        // quotient and |v| < 127.5 (checked exhaustively on the CPU, tests/native/quotient_check.c)
-        uint32_t bq[8];
+        float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float x = (e & 1) ? bf16_hi(yr[i][e >> 1]) : bf16_lo(yr[i][e >> 1]);
-            const float y0 = x * r;
-            bq[e] = __float_as_uint(__builtin_fmaf(__builtin_fmaf(-y0, s, x), r, y0) + 12582912.0f);
-        }
-        u32x2 qq;
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-            const uint32_t lo = __builtin_amdgcn_perm(bq[4 * h2 + 1], bq[4 * h2], 0x0c0c0400u);
-            const uint32_t hi = __builtin_amdgcn_perm(bq[4 * h2 + 3], bq[4 * h2 + 2], 0x0c0c0400u);
-            qq[h2] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-        }
-        *(u32x2 *)(p.q + (long)row * p.ldq + col) = qq;
+        for (int e = 0; e < 8; ++e) x[e] = (e & 1) ? bf16_hi(yr[i][e >> 1]) : bf16_lo(yr[i][e >> 1]);
+        *(u32x2 *)(p.q + (long)row * p.ldq + col) = fma_quant8(x, r);
     }
     if (lane == 0) p.s[row] = s;
 }

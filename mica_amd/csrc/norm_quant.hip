@@ -102,7 +102,8 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
 // (MICA_ROUND_EVEN / MICA_ROUND_AWAY, or 2: the one given at run time).
 //
 // The quotient is y = x * r corrected once: y + fma(-y, s, x) * r.  For bf16 x with a bf16 absmax
-// (kFast: unsmoothed bf16 rows) its rounded integer equals the IEEE quotient's for every input
+// (kFast: unsmoothed bf16 rows; the row kernels take this path for half-away rounding, and the
+// one-FMA quantizer of common.h for half even) its rounded integer equals the IEEE quotient's for every input
 // (tests/native/quotient_check.c, exhaustive).  For other values (SmoothQuant-scaled rows, fp16 and
 // fp32 activations) the corrected quotient stays within one ulp of the IEEE one, so the integers can
 // only differ near a rounding boundary: lanes whose quotient lies within 2^-13 of k + 0.5 recompute
@@ -300,14 +301,19 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
             if (lane == 0) p.s[o][row] = sc;
             int8_t *qr = p.q[o] + (long)row * p.ldq[o];
             const bool smoothed = HAS_INV && inv != nullptr;
+            // unsmoothed bf16 rows rounded half even: one FMA per element (fma_quant_recip)
+            const bool one_fma = kFast && !smoothed && (RND == 2 ? p.rounding : RND) == MICA_ROUND_EVEN;
+            const float rf = one_fma ? fma_quant_recip(amax, sc, r) : r;
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 float t[kChunk];
                 chunk(c, t);
                 if (!live(c)) continue;
+                int8_t *dst = qr + c * kRowStep + lane * kChunk;
+                if (one_fma) __builtin_nontemporal_store(fma_quant8(t, rf), (u32x2 *)dst);
                 // smoothed values are fp32 products (not bf16): IEEE quotient
-                if (smoothed) quant_store8r<false, RND>(t, sc, r, p.rounding, qr + c * kRowStep + lane * kChunk);
-                else quant_store8r<kFast, RND>(t, sc, r, p.rounding, qr + c * kRowStep + lane * kChunk);
+                else if (smoothed) quant_store8r<false, RND>(t, sc, r, p.rounding, dst);
+                else quant_store8r<kFast, RND>(t, sc, r, p.rounding, dst);
             }
         }
     };
