@@ -1,17 +1,24 @@
 """A 4B-shaped decoder stack whose linear layers run on the W8A8 hot path, for prefill-only scoring.
 
 Shape (the benchmark's synthetic 4B configuration): 36 layers, hidden 2560, MLP intermediate 9728,
-32 query heads and 8 K/V heads of dim 128 (QKV projection N = 4096 + 2 x 1024), vocabulary 151936.
-Weights are random int8 with per-output-channel fp32 scales; norms are gamma-style RMSNorm weights.
+16 query heads and 4 K/V heads of dim 256 (QKV projection N = 4096 + 2 x 1024 = 6144), vocabulary
+151936.  Weights are random int8 with per-output-channel fp32 scales; norms are gamma-style RMSNorm
+weights.  With ``full_attention_interval = k > 0`` the stack is the hybrid layout of the reference's
+model instead (Qwen3.5: three gated-delta-net layers, then one full-attention layer, repeated).
 
-Per layer (the call pattern of the reference's fork.layer_step, v0.5/serving/lib/fork.py:394-422):
+Per full-attention layer (the call pattern of the reference's fork.layer_step,
+v0.5/serving/lib/fork.py:394-422):
   q, s   = rms_norm_quant(h, input_norm)                     1 launch
   qkv    = QKV W8A8 GEMM                                     1 launch
-  a      = causal GQA attention on each request (RoPE + torch SDPA, bf16; outside the W8A8 path)
+  a      = causal GQA attention per request: RoPE in place on the q / k heads, then the
+           flash-attention kernel (head dim 256, 4 query heads per K/V head)   3 launches
   h      = h + O W8A8(a)          (residual in the epilogue)  2 launches (act_quant + GEMM)
   q, s   = rms_norm_quant(h, post_attention_norm)            1 launch
   g      = fused gate+up GEMM, SiLU(gate) * up epilogue      1 launch
   h      = h + down W8A8(act_quant(g))                       2 launches
+A gated-delta-net layer replaces the first four steps with mica_amd.gdn.GDNLayer (fork.gdn_step,
+fork.py:20-149: one norm + quant for the four input projections, conv, gate, chunked scan, gated
+norm fused with out_proj's quantisation, out_proj with the residual).
 Then, as PrefillEngine.final + the readout do (prefill_engine.py:280-304, release_runtime.py:298-306,
 :509-517), only each request's last position is normed and dotted with the allowed label rows, and
 the option slice is softmaxed.  Requests are packed back to back, all of the same length.
@@ -27,6 +34,7 @@ import torch.nn.functional as F
 from . import int8_kernels as aot
 from .attention import GROUP as _FA_GROUP, HEAD_DIM as _FA_DIM, causal_gqa_attention
 from .fused_kernels import rms_norm_quant, rope_inplace
+from .gdn import HEAD_DIM as _GDN_DIM, GDNLayer
 from .int8_runtime import GateUpQLinear, QLinear
 from .readout import LabelReadout
 
@@ -43,6 +51,15 @@ class StackConfig:
     eps: float = 1e-6
     rope_theta: float = 1_000_000.0
     n_options: int = 255   # option labels after the No / Yes pair (mica/codebook.py:19)
+    # 0: every layer is full attention.  k > 0: layer i is full attention when (i + 1) % k == 0 and a
+    # gated-delta-net layer otherwise (the reference's model: k = 4, 16 key / 32 value heads of 128)
+    full_attention_interval: int = 0
+    linear_k_heads: int = 16
+    linear_v_heads: int = 32
+    conv_width: int = 4
+
+    def is_gdn(self, i: int) -> bool:
+        return self.full_attention_interval > 0 and (i + 1) % self.full_attention_interval != 0
 
 
 def _rand_qlinear(n, k, g, device):
@@ -56,6 +73,8 @@ def _rand_norm(n, g, device):
 
 
 class Layer:
+    """A full-attention decoder layer's weights."""
+
     def __init__(self, cfg: StackConfig, g, device):
         H = cfg.hidden
         self.cfg = cfg
@@ -63,10 +82,36 @@ class Layer:
         self.post_norm = _rand_norm(H, g, device)
         self.qkv = _rand_qlinear((cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim, H, g, device)
         self.o = _rand_qlinear(H, cfg.heads * cfg.head_dim, g, device)
-        gate = _rand_qlinear(cfg.intermediate, H, g, device)
-        up = _rand_qlinear(cfg.intermediate, H, g, device)
-        self.gate_up = GateUpQLinear(gate, up)
-        self.down = _rand_qlinear(H, cfg.intermediate, g, device)
+        _mlp_weights(self, cfg, g, device)
+
+
+def _mlp_weights(layer, cfg, g, device):
+    gate = _rand_qlinear(cfg.intermediate, cfg.hidden, g, device)
+    up = _rand_qlinear(cfg.intermediate, cfg.hidden, g, device)
+    layer.gate_up = GateUpQLinear(gate, up)
+    layer.down = _rand_qlinear(cfg.hidden, cfg.intermediate, g, device)
+
+
+class GDNBlock:
+    """A gated-delta-net decoder layer's weights: the token mixer (a GDNLayer with random int8
+    projections, conv taps, decay parameters and gated-norm weight) and the same MLP."""
+
+    def __init__(self, cfg: StackConfig, g, device):
+        H, D = cfg.hidden, _GDN_DIM
+        hk, hv = cfg.linear_k_heads, cfg.linear_v_heads
+        C = (2 * hk + hv) * D
+        self.cfg = cfg
+        self.mixer = GDNLayer(
+            norm_weight=_rand_norm(H, g, device), eps=cfg.eps,
+            in_qkv=_rand_qlinear(C, H, g, device), in_z=_rand_qlinear(hv * D, H, g, device),
+            in_b=_rand_qlinear(hv, H, g, device), in_a=_rand_qlinear(hv, H, g, device),
+            conv_weight=(torch.randn(C, cfg.conv_width, generator=g, device=device) * 0.5).to(torch.bfloat16),
+            A_log=torch.rand(hv, generator=g, device=device) * 2 - 1,
+            dt_bias=torch.randn(hv, generator=g, device=device) * 0.5,
+            norm_z_weight=_rand_norm(D, g, device), out_proj=_rand_qlinear(H, hv * D, g, device),
+            num_k_heads=hk, num_v_heads=hv, norm_offset=0.0, z_eps=cfg.eps)
+        self.post_norm = _rand_norm(H, g, device)
+        _mlp_weights(self, cfg, g, device)
 
 
 def _rope(S, head_dim, theta, device):
@@ -95,7 +140,7 @@ class W8A8Stack:
         g = torch.Generator(device=self.device).manual_seed(seed)
         H = cfg.hidden
         self.embed = (torch.randn(cfg.vocab, H, generator=g, device=self.device) * 0.5).to(torch.bfloat16)
-        self.layers = [Layer(cfg, g, self.device) for _ in range(cfg.layers)]
+        self.layers = [(GDNBlock if cfg.is_gdn(i) else Layer)(cfg, g, self.device) for i in range(cfg.layers)]
         self.final_norm = _rand_norm(H, g, self.device)
         self.lm_head = (torch.randn(cfg.vocab, H, generator=g, device=self.device) * 0.02).to(torch.bfloat16)
         ids = torch.randperm(cfg.vocab, generator=torch.Generator().manual_seed(seed))[: 2 + cfg.n_options]
@@ -122,21 +167,28 @@ class W8A8Stack:
                                            scale=1.0 / math.sqrt(d), enable_gqa=True)
         return a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
 
-    def layer_forward(self, L: Layer, h, B, S, trace=None):
+    def layer_forward(self, L, h, B, S, trace=None):
         cfg = self.cfg
-        q, s = rms_norm_quant(h, L.input_norm, cfg.eps, offset=0.0)
-        qkv = L.qkv.forward_quantized(q, s)
-        qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
-        a = self._attention(qkv, B, S)
-        r = aot.act_quant(a)
-        h1 = L.o.forward_quantized(*r, residual=h)
+        if isinstance(L, GDNBlock):
+            t = {} if trace is not None else None
+            h1 = L.mixer(h, B, trace=t)
+            t = dict(kind="gdn", h=h, mixer=t, h1=h1) if trace is not None else None
+        else:
+            q, s = rms_norm_quant(h, L.input_norm, cfg.eps, offset=0.0)
+            qkv = L.qkv.forward_quantized(q, s)
+            qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
+            a = self._attention(qkv, B, S)
+            r = aot.act_quant(a)
+            h1 = L.o.forward_quantized(*r, residual=h)
+            t = dict(kind="attention", h=h, q=q, s=s, qkv=qkv_out, qkv_rope=qkv, a=a, qa=r[0], sa=r[1],
+                     h1=h1) if trace is not None else None
         q2, s2 = rms_norm_quant(h1, L.post_norm, cfg.eps, offset=0.0)
         g = L.gate_up.forward_quantized(q2, s2)
         qh, sh = aot.act_quant(g)
         h2 = L.down.forward_quantized(qh, sh, residual=h1)
         if trace is not None:
-            trace.append(dict(h=h, q=q, s=s, qkv=qkv_out, qkv_rope=qkv, a=a, qa=r[0], sa=r[1], h1=h1, q2=q2, s2=s2, g=g, qh=qh,
-                              sh=sh, h2=h2))
+            t.update(q2=q2, s2=s2, g=g, qh=qh, sh=sh, h2=h2)
+            trace.append(t)
         return h2
 
     @torch.no_grad()
@@ -178,7 +230,10 @@ class W8A8Stack:
     def linear_ops_per_token(self):
         """int8 ops per token of the W8A8 linears (2 N K per projection), final readout excluded."""
         c = self.cfg
-        qkv = (c.heads + 2 * c.kv_heads) * c.head_dim * c.hidden
-        o = c.hidden * c.heads * c.head_dim
+        attn = ((c.heads + 2 * c.kv_heads) * c.head_dim * c.hidden    # QKV
+                + c.hidden * c.heads * c.head_dim)                   # O
+        hk, hv, D = c.linear_k_heads, c.linear_v_heads, _GDN_DIM
+        gdn = ((2 * hk + hv) * D + hv * D + 2 * hv) * c.hidden + c.hidden * hv * D  # in_proj qkv / z / b / a, out
         mlp = 3 * c.intermediate * c.hidden
-        return 2 * (qkv + o + mlp) * c.layers
+        n_gdn = sum(c.is_gdn(i) for i in range(c.layers))
+        return 2 * ((c.layers - n_gdn) * attn + n_gdn * gdn + c.layers * mlp)

@@ -29,6 +29,34 @@ def within_one_ulp(got, ref, min_exact=0.999):
     assert np.mean(got == ref) >= min_exact
 
 
+def _check_mlp(L, t, cfg, li):
+    """The post-attention norm + quant, fused gate+up SiLU, requant and down + residual of one layer,
+    each recomputed by the oracle from the kernel's own input to that stage."""
+    h1 = bits(t["h1"])
+    # post-attention norm + quant
+    g2 = O.bf16_to_f32(bits(L.post_norm))
+    y2, _ = O.rms_norm(h1, g2, cfg.eps, 0.0)
+    q2o, s2o = O.quant_act(O.bf16_to_f32(y2))
+    q2, s2 = t["q2"].cpu().numpy(), t["s2"].cpu().numpy()
+    assert (np.all(q2 == q2o, axis=1) & (s2 == s2o)).mean() > 0.97
+    # fused gate+up SiLU from the kernel's q2, s2 (packed weight: 64-row gate / up groups)
+    qp, sp = L.gate_up.qweight.cpu().numpy(), L.gate_up.wscale.cpu().numpy()
+    n = qp.shape[0] // 2
+    grp = qp.reshape(n // 64, 2, 64, -1)
+    sgr = sp.reshape(n // 64, 2, 64)
+    qg, qu = grp[:, 0].reshape(n, -1), grp[:, 1].reshape(n, -1)
+    sg, su = sgr[:, 0].reshape(n), sgr[:, 1].reshape(n)
+    gv = O.epilogue(O.int_gemm(q2, qg), s2, sg)
+    uv = O.epilogue(O.int_gemm(q2, qu), s2, su)
+    within_one_ulp(bits(t["g"]), O.silu_mul(gv, uv))
+    # requant of h and the down projection + residual
+    qho, sho = O.quant_act(O.bf16_to_f32(bits(t["g"])))
+    assert np.array_equal(t["qh"].cpu().numpy(), qho) and np.array_equal(t["sh"].cpu().numpy(), sho)
+    h2 = O.epilogue(O.int_gemm(qho, L.down.qweight.cpu().numpy()), sho, L.down.wscale.cpu().numpy())
+    h2 = O.f32_to_bf16(O.bf16_to_f32(h2) + O.bf16_to_f32(bits(t["h1"])))
+    assert np.array_equal(bits(t["h2"]), h2), f"layer {li}: down + residual"
+
+
 @pytest.fixture(autouse=True)
 def _strict(monkeypatch):
     monkeypatch.setattr(int8_kernels, "STRICT", True)
@@ -69,28 +97,7 @@ def test_small_stack_stage_by_stage(gpu):
         h1 = O.epilogue(O.int_gemm(qa, L.o.qweight.cpu().numpy()), sa, L.o.wscale.cpu().numpy())
         h1 = O.f32_to_bf16(O.bf16_to_f32(h1) + O.bf16_to_f32(hb))
         assert np.array_equal(bits(t["h1"]), h1), f"layer {li}: o_proj + residual"
-        # post-attention norm + quant
-        g2 = O.bf16_to_f32(bits(L.post_norm))
-        y2, _ = O.rms_norm(h1, g2, cfg.eps, 0.0)
-        q2o, s2o = O.quant_act(O.bf16_to_f32(y2))
-        q2, s2 = t["q2"].cpu().numpy(), t["s2"].cpu().numpy()
-        assert (np.all(q2 == q2o, axis=1) & (s2 == s2o)).mean() > 0.97
-        # fused gate+up SiLU from the kernel's q2, s2 (packed weight: 64-row gate / up groups)
-        qp, sp = L.gate_up.qweight.cpu().numpy(), L.gate_up.wscale.cpu().numpy()
-        n = qp.shape[0] // 2
-        grp = qp.reshape(n // 64, 2, 64, -1)
-        sgr = sp.reshape(n // 64, 2, 64)
-        qg, qu = grp[:, 0].reshape(n, -1), grp[:, 1].reshape(n, -1)
-        sg, su = sgr[:, 0].reshape(n), sgr[:, 1].reshape(n)
-        gv = O.epilogue(O.int_gemm(q2, qg), s2, sg)
-        uv = O.epilogue(O.int_gemm(q2, qu), s2, su)
-        within_one_ulp(bits(t["g"]), O.silu_mul(gv, uv))
-        # requant of h and the down projection + residual
-        qho, sho = O.quant_act(O.bf16_to_f32(bits(t["g"])))
-        assert np.array_equal(t["qh"].cpu().numpy(), qho) and np.array_equal(t["sh"].cpu().numpy(), sho)
-        h2 = O.epilogue(O.int_gemm(qho, L.down.qweight.cpu().numpy()), sho, L.down.wscale.cpu().numpy())
-        h2 = O.f32_to_bf16(O.bf16_to_f32(h2) + O.bf16_to_f32(bits(t["h1"])))
-        assert np.array_equal(bits(t["h2"]), h2), f"layer {li}: down + residual"
+        _check_mlp(L, t, cfg, li)
     fin = trace[-1]
     rows = fin["rows"].cpu().numpy()
     W = st.readout.weight.cpu().numpy()
@@ -112,3 +119,35 @@ def test_full_shape_stack_runs_one_layer(gpu):
     p = probs.cpu().numpy()
     assert np.isfinite(p).all() and np.allclose(p.sum(1), 1.0, atol=1e-5)
     assert st.linear_ops_per_token() == 2 * (6144 * 2560 + 2560 * 4096 + 3 * 9728 * 2560)
+
+
+def test_hybrid_stack_gdn_and_attention_layers(gpu):
+    """The hybrid layout (full_attention_interval 2: a gated-delta-net layer, then a full-attention
+    layer, twice): each GDN mixer output equals the GDN layer module run alone on the same input
+    (bit-identical; the module itself is checked stage by stage against the oracle in
+    test_gpu_gdn_layer.py), every MLP half is checked against the oracle as above, and the readout
+    gives finite probabilities that sum to one."""
+    print("[case] hybrid stack", file=sys.stderr, flush=True)
+    cfg = StackConfig(layers=4, hidden=512, intermediate=1024, heads=4, kv_heads=1, head_dim=256, vocab=4096,
+                      n_options=31, full_attention_interval=2, linear_k_heads=2, linear_v_heads=4)
+    st = W8A8Stack(cfg, device=gpu, seed=7)
+    assert [type(L).__name__ for L in st.layers] == ["GDNBlock", "Layer", "GDNBlock", "Layer"]
+    B, S = 2, 80
+    ids = torch.randint(0, cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(9)).to(gpu)
+    trace = []
+    logits, probs = st.prefill(ids, B, trace=trace)
+    torch.cuda.synchronize()
+    for li, (L, t) in enumerate(zip(st.layers, trace[:-1])):
+        assert t["kind"] == ("gdn" if li % 2 == 0 else "attention")
+        if t["kind"] == "gdn":
+            again = L.mixer(t["h"], B)
+            torch.cuda.synchronize()
+            assert torch.equal(again, t["h1"]), f"layer {li}: GDN mixer"
+        _check_mlp(L, t, cfg, li)
+    p = probs.cpu().numpy()
+    assert np.isfinite(p).all() and np.allclose(p.sum(1), 1.0, atol=1e-5)
+    hk, hv, H = 2, 4, 512
+    gdn_ops = ((2 * hk + hv) * 128 + hv * 128 + 2 * hv) * H + H * hv * 128
+    attn_ops = (4 + 2) * 256 * H + H * 4 * 256
+    assert st.linear_ops_per_token() == 2 * (2 * gdn_ops + 2 * attn_ops + 4 * 3 * 1024 * H)
+    assert not int8_kernels.STATS["fallback"]
