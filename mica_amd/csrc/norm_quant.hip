@@ -14,6 +14,8 @@
 // kernel), measured faster than cached stores on MI355X; cached loads measured faster than
 // non-temporal ones.
 
+#include <atomic>
+
 #include "common.h"
 
 namespace {
@@ -105,10 +107,11 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
 // (kFast: unsmoothed bf16 rows; the row kernels take this path for half-away rounding, and the
 // one-FMA quantizer of common.h for half even) its rounded integer equals the IEEE quotient's for every input
 // (tests/native/quotient_check.c, exhaustive).  For other values (SmoothQuant-scaled rows, fp16 and
-// fp32 activations) the corrected quotient stays within one ulp of the IEEE one, so the integers can
-// only differ near a rounding boundary: lanes whose quotient lies within 2^-13 of k + 0.5 recompute
-// it with the IEEE division (tests/native/guarded_quotient_check.c: 2^28 samples, no mismatch, the
-// slow path on ~5e-5 of the values).
+// fp32 activations) the plain product y = x * r is used: it is within 2^-16 of x / s for |x / s| <=
+// 127.5 (r's rounding and y's), so its integer can only differ from the IEEE quotient's near a rounding
+// boundary: lanes whose y lies within 2^-13 of k + 0.5 recompute it with the IEEE division
+// (tests/native/guarded_quotient_check.c: 2^28 samples, no mismatch, the slow path on ~5e-5 of the
+// values).
 //
 // Half even rounds with the 1.5 * 2^23 trick: for |t| < 2^22, t + 12582912 is an integer-valued
 // float (its rounding is the IEEE round-half-even of t), whose low mantissa byte is that integer in
@@ -122,7 +125,7 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
         const float y = v[j] * r;
-        t[j] = __builtin_fmaf(__builtin_fmaf(-y, s, v[j]), r, y);
+        t[j] = kFast ? __builtin_fmaf(__builtin_fmaf(-y, s, v[j]), r, y) : y;
     }
     if (!kFast) {
         bool near = false;
@@ -167,7 +170,7 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
 // fp32 once, and after the norm it stays in fp32 registers (already rounded to XT), so the
 // absmax and the quantizer work on registers.
 template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
-__global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
+MICA_DEVICE void row16_body(const RowParams &p) {
     constexpr bool kFast = XT == MICA_BF16; // the fast quotient is exact for unsmoothed bf16 rows
     const int lane = threadIdx.x & 63;
     const int nwaves = gridDim.x * (blockDim.x >> 6);
@@ -186,6 +189,28 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
     int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     u32x4 bufA[NCH], bufB[NCH <= 5 ? NCH : 1];
     if (row < p.M) load_row(bufA, row);
+
+    // rows of up to 2560 elements with smoothing factors: the workgroup copies every output's factors
+    // into LDS once (n_out x K fp32, dynamic shared memory), so the two passes of every row read them
+    // there instead of through the vector memory path.  Chunk ch = c * 64 + lane of output o sits at
+    // float4 pair ((o * NCH + c) * 64 + lane) * 2.
+    constexpr bool kInvLds = HAS_INV && NCH <= 5;
+    extern __shared__ float4 inv_sh[];
+    if (kInvLds) {
+        for (int o = 0; o < p.n_out; ++o) {
+            if (p.inv[o] == nullptr) continue;
+            for (int ch = threadIdx.x; ch < NCH * 64; ch += blockDim.x) {
+                float4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+                if (FULL || ch * kChunk < K) {
+                    a = ((const float4 *)(p.inv[o] + ch * kChunk))[0];
+                    b = ((const float4 *)(p.inv[o] + ch * kChunk))[1];
+                }
+                inv_sh[(o * NCH * 64 + ch) * 2] = a;
+                inv_sh[(o * NCH * 64 + ch) * 2 + 1] = b;
+            }
+        }
+        __syncthreads();
+    }
 
     // per-lane weight multipliers (offset + w), fp32, cached across the rows this wave visits
     float w1[NORM ? NCH : 1][kChunk];
@@ -208,7 +233,9 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
     // fp32 registers through the norm, the absmax and the quantizer; long rows stay packed and are
     // unpacked again in each pass, which keeps enough waves resident.
     constexpr bool kF32 = NCH <= 8;
-    constexpr bool kPrefetch = NCH <= 5; // long rows already keep enough bytes in flight per wave
+    // long rows already keep enough bytes in flight per wave; smoothed rows spend the registers on
+    // their factors' products instead
+    constexpr bool kPrefetch = NCH <= 5 && !HAS_INV;
     auto process = [&](u32x4 (&cur)[NCH], int row) {
         if (NORM && p.res != nullptr) {
             // v = (x + r) rounded to the activation dtype (fused_kernels.py:27-30, :52)
@@ -275,8 +302,16 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
                 }
                 if (HAS_INV && inv != nullptr) {
                     float iv[kChunk];
-                    if (live(c)) load_inv8(inv, c * kRowStep + lane * kChunk, iv);
-                    else for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
+                    if (kInvLds) {
+                        const float4 a = inv_sh[((o * NCH + c) * 64 + lane) * 2];
+                        const float4 b = inv_sh[((o * NCH + c) * 64 + lane) * 2 + 1];
+                        iv[0] = a.x; iv[1] = a.y; iv[2] = a.z; iv[3] = a.w;
+                        iv[4] = b.x; iv[5] = b.y; iv[6] = b.z; iv[7] = b.w;
+                    } else if (live(c)) {
+                        load_inv8(inv, c * kRowStep + lane * kChunk, iv);
+                    } else {
+                        for (int j = 0; j < kChunk; ++j) iv[j] = 0.0f;
+                    }
 #pragma unroll
                     for (int j = 0; j < kChunk; ++j) t[j] = t[j] * iv[j];
                 }
@@ -337,6 +372,24 @@ __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
             process(bufA, row);
         }
     }
+}
+
+template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
+__global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
+    row16_body<NCH, XT, NORM, HAS_INV, FULL, RND>(p);
+}
+
+// Smoothed rows of up to 2560 elements, held to 168 registers (a few spill) so that 3 waves per SIMD
+// stay resident, against 2 at the compiler's own choice (213 registers).
+template <int NCH, int XT, bool NORM, bool FULL, int RND>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void row16_smooth_kernel(RowParams p) {
+    row16_body<NCH, XT, NORM, true, FULL, RND>(p);
+}
+
+template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
+constexpr void (*row16_for())(RowParams) {
+    if constexpr (HAS_INV && NCH <= 5) return row16_smooth_kernel<NCH, XT, NORM, FULL, RND>;
+    else return row16_kernel<NCH, XT, NORM, HAS_INV, FULL, RND>;
 }
 
 // fp32 activations (act_quant only): same structure, two 16-byte loads per chunk.
@@ -431,11 +484,39 @@ int row_grid(int M) {
     return blocks < cap ? blocks : cap;
 }
 
+// dynamic LDS of a row16_kernel launch: the smoothing factors of rows of up to 2560 elements
+template <int NCH>
+unsigned inv_lds_bytes(const RowParams &p, bool has_inv) {
+    return (has_inv && NCH <= 5) ? (unsigned)(p.n_out * NCH * 64 * 2 * sizeof(float4)) : 0u;
+}
+
+// Launch a row kernel on a grid of at most MICA_ROW_BLOCKS_PER_CU workgroups per CU, fewer when its
+// registers or LDS let fewer be resident at once (a workgroup beyond that would only start when a
+// resident one ends, and its rows would then finish last).
+// The residency is queried once per kernel and output count (the LDS size depends on nothing else)
+// and kept; concurrent first calls store the same value.
+template <void (*Kernel)(RowParams)>
+int launch_rows(const RowParams &p, unsigned lds, hipStream_t st) {
+    static std::atomic<int> cached[kMaxOut + 1];
+    std::atomic<int> &slot = cached[lds ? p.n_out : 0];
+    int per_cu = slot.load(std::memory_order_relaxed);
+    if (per_cu <= 0) {
+        int occ = 0;
+        per_cu = MICA_ROW_BLOCKS_PER_CU;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, Kernel, 256, lds) == hipSuccess && occ > 0 &&
+            occ < per_cu)
+            per_cu = occ;
+        slot.store(per_cu, std::memory_order_relaxed);
+    }
+    const int blocks = (p.M + 3) / 4, cap = cu_count_of_current_device() * per_cu;
+    hipLaunchKernelGGL(Kernel, dim3(blocks < cap ? blocks : cap), dim3(256), lds, st, p);
+    return mica_err(hipGetLastError());
+}
+
 template <int NCH>
 int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st) {
-    dim3 grid(row_grid(p.M)), block(256);
 #define MICA_ROW16(XT_, NORM_, INV_) \
-    hipLaunchKernelGGL((row16_kernel<NCH, XT_, NORM_, INV_, false, 2>), grid, block, 0, st, p)
+    return launch_rows<row16_for<NCH, XT_, NORM_, INV_, false, 2>()>(p, inv_lds_bytes<NCH>(p, INV_), st)
     if (xt == MICA_BF16) {
         if (norm) { if (has_inv) MICA_ROW16(MICA_BF16, true, true); else MICA_ROW16(MICA_BF16, true, false); }
         else { if (has_inv) MICA_ROW16(MICA_BF16, false, true); else MICA_ROW16(MICA_BF16, false, false); }
@@ -444,22 +525,19 @@ int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st
         else { if (has_inv) MICA_ROW16(MICA_FP16, false, true); else MICA_ROW16(MICA_FP16, false, false); }
     }
 #undef MICA_ROW16
-    return mica_err(hipGetLastError());
 }
 
 // bf16 rows of exactly NCH * 512 elements (the hot widths): no masks, rounding fixed at compile time
 template <int NCH>
 int launch16_full(const RowParams &p, bool norm, bool has_inv, hipStream_t st) {
-    dim3 grid(row_grid(p.M)), block(256);
 #define MICA_ROWF(NORM_, INV_, RND_) \
-    hipLaunchKernelGGL((row16_kernel<NCH, MICA_BF16, NORM_, INV_, true, RND_>), grid, block, 0, st, p)
+    return launch_rows<row16_for<NCH, MICA_BF16, NORM_, INV_, true, RND_>()>(p, inv_lds_bytes<NCH>(p, INV_), st)
 #define MICA_ROWF2(NORM_, INV_) \
     if (p.rounding == MICA_ROUND_EVEN) MICA_ROWF(NORM_, INV_, MICA_ROUND_EVEN); else MICA_ROWF(NORM_, INV_, MICA_ROUND_AWAY);
     if (norm) { if (has_inv) { MICA_ROWF2(true, true) } else { MICA_ROWF2(true, false) } }
     else { if (has_inv) { MICA_ROWF2(false, true) } else { MICA_ROWF2(false, false) } }
 #undef MICA_ROWF2
 #undef MICA_ROWF
-    return mica_err(hipGetLastError());
 }
 
 template <int NCH>

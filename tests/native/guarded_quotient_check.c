@@ -1,17 +1,18 @@
 /*
  * CPU check of the guarded quotient the row kernels use for inputs outside the exhaustive bf16 proof
- * (SmoothQuant-scaled rows, fp16 and fp32 activations; quant8_guarded in
+ * (SmoothQuant-scaled rows, fp16 and fp32 activations; quant_store8r<false, ...> in
  * mica_amd/csrc/norm_quant.hip):
  *
  *     s = max(a, 1e-8f) / 127.0f,  r = 1.0f / s          a: the row's absmax of x
- *     v = fmaf(fmaf(-x * r, s, x), r, x * r)               the corrected quotient, as in the bf16 path
+ *     v = x * r                                            one rounded product
  *     if | |v - rint(v)| - 0.5 | <= 2^-13:  v = x / s      (IEEE division, only near a rounding boundary)
  *
  * The claim: rint(v) == rint(x / s) and trunc(v +- 0.5) == trunc(x / s +- 0.5) for every finite x with
- * |x| <= a.  It holds if |v_fast - x / s| stays far below the 2^-13 window, so this program samples
- * 2^28 (x, a) pairs (x = a bf16 value times a factor in [1e-4, 1e4], the SmoothQuant clamp range,
- * a >= |x| drawn around it), checks the claim on every one, and reports the largest gap between the
- * corrected and the IEEE quotient in units of the last place, and how often the slow path runs.
+ * |x| <= a.  It holds if |v_fast - x / s| stays far below the 2^-13 window (analytically |v - x / s| <=
+ * |x / s| 2^-24 + ulp(v) / 2 < 2^-16 for |x / s| <= 127.5), so this program samples 2^28 (x, a) pairs
+ * (x = a bf16 value times a factor in [1e-4, 1e4], the SmoothQuant clamp range, a >= |x| drawn around
+ * it), checks the claim on every one, and reports the largest gap between the fast and the IEEE
+ * quotient in units of the last place, and how often the slow path runs.
  *
  * Build: gcc -O2 -fopenmp -ffp-contract=off guarded_quotient_check.c -o guarded_quotient_check -lm
  * Output: "samples=<n> mismatch_even=<k> mismatch_away=<k> max_gap_ulp=<g> slow_fraction=<f>";
@@ -57,8 +58,7 @@ int main(void) {
         const float s = fmaxf(a, 1e-8f) / 127.0f;
         const float r = 1.0f / s;
         const float q = x / s;
-        const float y = x * r;
-        float v = fmaf(fmaf(-y, s, x), r, y);
+        float v = x * r;
         const double gap = fabs((double)v - (double)q) / ulp(q);
         if (gap > max_gap) max_gap = gap;
         if (fabsf(fabsf(v - rintf(v)) - 0.5f) <= 0x1p-13f) {

@@ -30,9 +30,10 @@ def test_fast_quotient_matches_ieee_division_exhaustively(tmp_path):
 
 @pytest.mark.slow
 def test_guarded_quotient_matches_ieee_division_sampled(tmp_path):
-    """The guarded quotient of smoothed / fp16 / fp32 rows: 2^28 sampled (x, absmax) pairs, no integer
-    differs from the IEEE quotient's, and the corrected quotient stays within 4 ulps of it (the guard
-    window is 2^-13, at least 16 ulps for every |x / s| <= 128)."""
+    """The guarded quotient of smoothed / fp16 / fp32 rows (x * (1 / s), with the IEEE division for
+    lanes within 2^-13 of a rounding boundary): 2^28 sampled (x, absmax) pairs, no integer differs from
+    the IEEE quotient's, and the product stays within 4 ulps of it (the guard window is 2^-13, at least
+    16 ulps for every |x / s| <= 128).  Without the guard the same samples give ~230 mismatches."""
     gcc = shutil.which("gcc")
     if gcc is None:
         pytest.skip("gcc not available")
