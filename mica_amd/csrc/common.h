@@ -58,7 +58,7 @@ MICA_DEVICE float round_to(float f, int dtype) {
 // values, so a row ends uniform), then the four row results are read into scalars and combined in
 // the same order in every lane.  No LDS traffic, a few cycles per step.
 template <bool MAX>
-MICA_DEVICE float wave_reduce(float v) {
+MICA_DEVICE float row16_reduce(float v) {
     auto op = [](float a, float b) { return MAX ? __builtin_fmaxf(a, b) : a + b; };
 #define MICA_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ctrl, 0xF, 0xF, true))
     v = op(v, MICA_DPP(v, 0xB1));  // quad_perm [1, 0, 3, 2]
@@ -66,6 +66,15 @@ MICA_DEVICE float wave_reduce(float v) {
     v = op(v, MICA_DPP(v, 0x141)); // row_half_mirror
     v = op(v, MICA_DPP(v, 0x140)); // row_mirror
 #undef MICA_DPP
+    return v;
+}
+// sum over each 16-lane row (lanes 16 r .. 16 r + 15, all active); every lane of a row gets the same bits
+MICA_DEVICE float row16_sum(float v) { return row16_reduce<false>(v); }
+
+template <bool MAX>
+MICA_DEVICE float wave_reduce(float v) {
+    auto op = [](float a, float b) { return MAX ? __builtin_fmaxf(a, b) : a + b; };
+    v = row16_reduce<MAX>(v);
     const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
     const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
     const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));

@@ -140,9 +140,8 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
         float ss = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += o[e] * o[e];
-        // the 16 threads of a 128-channel head are 16 consecutive lanes
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+        // the 16 threads of a 128-channel head are the 16 lanes of one DPP row
+        ss = row16_sum(ss);
         if (norm) {
             const float r = __builtin_amdgcn_rsqf(ss + p.eps);
 #pragma unroll
@@ -674,8 +673,7 @@ __global__ __launch_bounds__(64 * kGnWaves) void gated_norm_quant_kernel(GatedNo
         float ss = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+        ss = row16_sum(ss); // the head's 16 lanes: one DPP row
         const float rstd = 1.0f / sqrtf(ss / 128.0f + p.eps);
         float v[8];
 #pragma unroll
