@@ -159,18 +159,19 @@ def test_rmsnorm_quant_residual_and_smoothing(gpu):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
 
 
-@pytest.mark.parametrize("T,K", [(333, 2560), (64, 1000), (257, 9728)])
-def test_rmsnorm_quant_multi_consumers(gpu, T, K):
-    """One norm quantized for 3 consumers (unsmoothed, two different SmoothQuant factors): each output is
+@pytest.mark.parametrize("T,K,n", [(333, 2560, 3), (64, 1000, 3), (257, 9728, 3), (130, 2560, 4), (50, 512, 4)])
+def test_rmsnorm_quant_multi_consumers(gpu, T, K, n):
+    """One norm quantized for n consumers (one unsmoothed, the others with different SmoothQuant factors;
+    rows of up to 2560 keep the factors in LDS, 4 consumers being its largest size): each output is
     bit-identical to the single-consumer launch, and to the reference quantizer applied to the kernel's
     normed row times that consumer's factors."""
-    note(f"rmsnorm_quant_multi T={T} K={K}")
+    note(f"rmsnorm_quant_multi T={T} K={K} n={n}")
     rng = np.random.default_rng(T + K)
     xb, rb = act_bits(rng, (T, K)), act_bits(rng, (T, K), outliers=0)
     x, r = to_gpu_bf16(xb), to_gpu_bf16(rb)
     w = O.round_bf16(rng.normal(0.0, 0.1, K).astype(np.float32))
     wt = to_gpu_bf16(O.f32_to_bf16(w))
-    invs = [None] + [rng.uniform(0.3, 3.0, K).astype(np.float32) for _ in range(2)]
+    invs = [None] + [rng.uniform(0.3, 3.0, K).astype(np.float32) for _ in range(n - 1)]
     tinvs = [None if v is None else torch.from_numpy(v).cuda() for v in invs]
     outs, v = fused_kernels.rms_norm_quant_multi(x, wt, 1e-6, tinvs, residual=r)
     _, _, y, v1 = fused_kernels.rms_norm_quant(x, wt, 1e-6, residual=r, return_normed=True)
