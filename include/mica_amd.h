@@ -245,6 +245,17 @@ long long mica_gdn_workspace_bytes(int B, int T, int HV);
 int mica_gated_rmsnorm_quant(const void *x, int ldx, const void *z, int ldz, const void *w, float eps, void *y,
                              int ldy, int8_t *q, int ldq, float *s, int M, int N, mica_stream_t stream);
 
+/*
+ * The GDN layer's gate (fork.py:124-125): per token m and value head h,
+ *   g[m][h]    = -exp(A_log[h]) * softplus(f32(a[m][h]) + dt_bias[h])    fp32, softplus threshold 20
+ *   beta[m][h] = bf16(sigmoid(f32(b[m][h])))
+ * a, b: bf16 [M][HV] (lda / ldb, the in_proj_a / in_proj_b outputs); A_log, dt_bias: fp32 [HV];
+ * g: fp32 [M][HV], beta: bf16 [M][HV], both contiguous.  Replaces the reference's torch expressions
+ * (-self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias), b.sigmoid()).
+ */
+int mica_gdn_gate(const void *a, int lda, const void *b, int ldb, const float *A_log, const float *dt_bias, float *g,
+                  void *beta, int M, int HV, mica_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,7 @@ SIGNATURES = {
                             _LL, _P]),
     "mica_gdn_workspace_bytes": (_LL, [_I, _I, _I]),
     "mica_gated_rmsnorm_quant": (_I, [_P, _I, _P, _I, _P, _F, _P, _I, _P, _I, _P, _I, _I, _P]),
+    "mica_gdn_gate": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _P]),
 }
 
 _LIB = None

@@ -706,6 +706,23 @@ __global__ __launch_bounds__(64 * kGnWaves) void gated_norm_quant_kernel(GatedNo
     if (lane == 0) p.s[row] = s;
 }
 
+// The GDN layer's decay and write strength per token and value head (fork.py:124-125):
+//   g = -exp(A_log[h]) * softplus(f32(a) + dt_bias[h])   (softplus(x) = x above 20, else log1p(exp(x)),
+//                                                         torch's threshold), fp32
+//   beta = bf16(sigmoid(f32(b)))                         (torch's bf16 sigmoid: fp32 math, one rounding)
+// One thread per (token, head); a and b are the bf16 outputs of in_proj_a / in_proj_b.
+__global__ __launch_bounds__(256) void gate_kernel(const uint16_t *a, int lda, const uint16_t *b, int ldb,
+                                                   const float *A_log, const float *dt_bias, float *g,
+                                                   uint16_t *beta, int M, int HV) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)M * HV) return;
+    const int m = (int)(i / HV), h = (int)(i - (long)m * HV);
+    const float x = bf16_to_f32(a[(long)m * lda + h]) + dt_bias[h];
+    const float sp = x > 20.0f ? x : log1pf(expf(x));
+    g[i] = -expf(A_log[h]) * sp;
+    beta[i] = f32_to_bf16(1.0f / (1.0f + expf(-bf16_to_f32(b[(long)m * ldb + h]))));
+}
+
 // dst = src (or zeros when src is null): the final state of an empty scan
 __global__ void state_fill_kernel(const float *src, float *dst, long n) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -832,5 +849,20 @@ extern "C" int mica_gated_rmsnorm_quant(const void *x, int ldx, const void *z, i
     case 16: hipLaunchKernelGGL(gated_norm_quant_kernel<16>, grid, block, 0, st, p); break;
     default: return MICA_MISS_SHAPE;
     }
+    return mica_err(hipGetLastError());
+}
+
+extern "C" int mica_gdn_gate(const void *a, int lda, const void *b, int ldb, const float *A_log,
+                             const float *dt_bias, float *g, void *beta, int M, int HV, mica_stream_t stream) {
+    if (a == nullptr || b == nullptr || A_log == nullptr || dt_bias == nullptr || g == nullptr || beta == nullptr)
+        return MICA_MISS_ARG;
+    if (M < 0 || HV <= 0) return MICA_MISS_SHAPE;
+    if (lda < HV || ldb < HV) return MICA_MISS_STRIDE;
+    if ((long long)M * lda >= (1LL << 31) || (long long)M * ldb >= (1LL << 31) || (long long)M * HV >= (1LL << 31))
+        return MICA_MISS_RANGE;
+    if (M == 0) return 0;
+    const long long n = (long long)M * HV;
+    hipLaunchKernelGGL(gate_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)a, lda, (const uint16_t *)b, ldb, A_log, dt_bias, g, (uint16_t *)beta, M, HV);
     return mica_err(hipGetLastError());
 }

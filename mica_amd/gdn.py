@@ -11,6 +11,8 @@ The reference's GDN layer step (akivet/Mica v0.5/serving/lib/fork.py ``gdn_step`
       heads are read in place instead of repeat_interleave'd (fork.py:134-136)
   gated_rmsnorm_quant(x, z, weight, eps)                             fork.py:148 + out_proj's act_quant
       attn.norm(out, z) fused with the INT8 quantisation of out_proj's input
+  gdn_gate(a, b, A_log, dt_bias)                                     fork.py:124-125
+      the decay g and write strength beta from the in_proj_a / in_proj_b outputs
 
 Everything runs on the GPU through libmica_amd.so; there is no CPU path (a CPU tensor raises
 ValueError) and no fallback.
@@ -174,6 +176,31 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None, out
     return o, hT
 
 
+def gdn_gate(a, b, A_log, dt_bias):
+    """The GDN layer's decay and write strength (fork.py:124-125) in one launch:
+    g = -exp(A_log) * softplus(a + dt_bias) (fp32) and beta = sigmoid(b) (bf16), per token and value
+    head.  a, b: bf16 [..., HV] (rows may be strided); A_log, dt_bias: [HV].  Returns (g, beta) shaped
+    like a."""
+    dev = _need_gpu(a, b, A_log, dt_bias)
+    HV = a.shape[-1]
+    af, bf = a.reshape(-1, HV), b.reshape(-1, HV)
+    if af.dtype != torch.bfloat16 or bf.dtype != torch.bfloat16 or af.stride(1) != 1 or bf.stride(1) != 1 or \
+            bf.shape != af.shape:
+        raise ValueError("gdn_gate takes bf16 a and b of one shape [..., HV] with contiguous heads")
+    A = A_log.to(torch.float32).contiguous()
+    dt = dt_bias.to(torch.float32).contiguous()
+    if A.numel() != HV or dt.numel() != HV:
+        raise ValueError("A_log and dt_bias must have HV elements")
+    M = af.shape[0]
+    g = torch.empty((M, HV), dtype=torch.float32, device=dev)
+    beta = torch.empty((M, HV), dtype=torch.bfloat16, device=dev)
+    L = _lib.load()
+    _rc(_on(dev, lambda: L.mica_gdn_gate(af.data_ptr(), af.stride(0), bf.data_ptr(), bf.stride(0), A.data_ptr(),
+                                         dt.data_ptr(), g.data_ptr(), beta.data_ptr(), M, HV, _stream(dev))),
+        "mica_gdn_gate")
+    return g.view(a.shape), beta.view(a.shape)
+
+
 def gated_rmsnorm_quant(x, z, weight, eps: float = 1e-6, want_y: bool = False):
     """attn.norm(x, z) over 128-wide heads, then per-token INT8 (half-even) of the [.., HV * 128] row.
     Returns (q int8 [M, N], s fp32 [M]) or, with want_y, (q, s, y bf16 [M, N])."""
@@ -206,7 +233,7 @@ class GDNLayer(torch.nn.Module):
       1. input RMSNorm, quantized per token once for the four projections (in_proj_qkv, in_proj_z,
          in_proj_b, in_proj_a; each a QLinear with its own SmoothQuant factors)  -> 1 + 4 launches
       2. causal conv + SiLU over the q / k / v channels, q / k l2-normalised  -> 1 launch
-      3. g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)  (fork.py:124-125; torch, [T, HV])
+      3. g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)  (fork.py:124-125)  -> 1 launch
       4. chunked gated delta rule  -> 2 launches
       5. gated RMSNorm fused with out_proj's quantisation, out_proj GEMM with the residual add in its
          epilogue  -> 2 launches
@@ -243,8 +270,7 @@ class GDNLayer(torch.nn.Module):
         q = x[..., :kd].unflatten(-1, (self.hk, HEAD_DIM))
         k = x[..., kd:2 * kd].unflatten(-1, (self.hk, HEAD_DIM))
         v = x[..., 2 * kd:].unflatten(-1, (self.hv, HEAD_DIM))
-        g = -self.A_log.exp() * torch.nn.functional.softplus(a.float() + self.dt_bias)
-        beta = b.sigmoid()
+        g, beta = gdn_gate(a, b, self.A_log, self.dt_bias)
         o, rec = chunk_gated_delta_rule(q, k, v, g.view(batch, T, self.hv), beta.view(batch, T, self.hv),
                                         initial_state=None if initial is None else initial[1],
                                         output_final_state=keep)

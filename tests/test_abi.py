@@ -231,3 +231,20 @@ def test_gated_rmsnorm_quant_rejects():
     assert with_(a1=2048) == 4            # ldx < N
     assert with_(a2=A16 + 4) == 3         # misaligned z
     assert with_(a11=0) == 0              # M = 0
+
+
+def test_gdn_gate_rejects():
+    lib = _lib.load()
+    # (a, lda, b, ldb, A_log, dt_bias, g, beta, M, HV)
+    ok = [A16, 32, A16, 32, A16, A16, A16, A16, 4, 32]
+
+    def with_(**kw):
+        a = list(ok)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return lib.mica_gdn_gate(*a, None)
+
+    assert with_(a6=None) == 6            # no g output
+    assert with_(a9=0) == 1               # no heads
+    assert with_(a1=16) == 4              # lda < HV
+    assert with_(a8=0) == 0               # no tokens

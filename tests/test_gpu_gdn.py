@@ -162,3 +162,31 @@ def test_gated_rmsnorm_quant_matches_oracle(gpu, M, N):
     assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), rs)
     rq2, _ = O.quant_act(O.bf16_to_f32(ref_y))
     assert np.abs(q.cpu().numpy().astype(int) - rq2).max() <= 1
+
+
+@pytest.mark.parametrize("M,HV", [(300, 32), (7, 4), (1, 1)])
+def test_gdn_gate_matches_oracle(gpu, M, HV):
+    """g = -exp(A_log) softplus(a + dt_bias) within 1e-6 relative of the float64 formula applied to the
+    fp32 sum a + dt_bias (the reference adds in fp32, a.float() + self.dt_bias; below the threshold
+    softplus ~ exp passes that sum's rounding on as a relative error of up to |x| 2^-24, so the oracle
+    takes the same rounded sum), with fp32 exp and log1p a few ulps apart; values below 1e-30 compared
+    absolutely.  beta = sigmoid(b) within one bf16 ulp of the float64 value rounded to bf16; a spans
+    both sides of the softplus threshold 20."""
+    from mica_amd import gdn
+    g = torch.Generator().manual_seed(M * 31 + HV)
+    a = (torch.randn(M, HV, generator=g) * 12).to(torch.bfloat16)
+    b = (torch.randn(M, HV, generator=g) * 6).to(torch.bfloat16)
+    A_log = torch.rand(HV, generator=g) * 4 - 2
+    dt = torch.randn(HV, generator=g) * 2
+    gg, beta = gdn.gdn_gate(a.to(gpu), b.to(gpu), A_log.to(gpu), dt.to(gpu))
+    torch.cuda.synchronize()
+    x32 = (a.float() + dt).double().numpy()  # the reference's fp32 sum
+    rg, rb = G.gdn_gate(x32, _f64(b), A_log.double().numpy(), np.zeros(HV))
+    assert gg.dtype == torch.float32 and beta.dtype == torch.bfloat16
+    np.testing.assert_allclose(gg.cpu().double().numpy(), rg, rtol=1e-6, atol=1e-30)
+    ref_b = O.f32_to_bf16(rb.astype(np.float32))
+    assert (np.abs(O.bf16_to_f32(_bits(beta)).astype(np.float64) - O.bf16_to_f32(ref_b)) <= O.bf16_ulp(ref_b)).all()
+    # strided rows (the a / b columns of a wider projection output) give the same values
+    wide = torch.cat([a, b], 1).to(gpu)
+    g2, b2 = gdn.gdn_gate(wide[:, :HV], wide[:, HV:], A_log.to(gpu), dt.to(gpu))
+    assert torch.equal(g2, gg) and torch.equal(b2, beta)
