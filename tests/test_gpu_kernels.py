@@ -87,6 +87,7 @@ def test_act_quant_known_answers(gpu, kat):
     (7, 1000, False, "even", torch.bfloat16),        # K not a multiple of 512 (masked chunks)
     (333, 2560, True, "even", torch.bfloat16),       # smoothed, factors held in LDS
     (129, 1000, True, "away", torch.bfloat16),       # the same with masked chunks
+    (64, 2048, True, "even", torch.float16),         # fp16 rows on the LDS-factor path
 ])
 def test_act_quant_bit_exact(gpu, m, k, smooth, rounding, dtype):
     note(f"act_quant m={m} k={k} smooth={smooth} {rounding} {dtype}")
