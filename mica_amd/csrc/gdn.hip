@@ -276,12 +276,22 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
             acc = mfma(a, bb, acc);
         }
         const int j = tj * 32 + (lane & 31);
+        const float gj = Gs[j];
+        // rows i = ti 32 + 8 r4 + 4 (lane / 32) + u: four consecutive G and beta values per r4, read
+        // before any math (a masked select, not a branch, so the LDS reads are not serialised)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = ti * 32 + acc_row(r, lane);
-            const float l = j < i ? (Bs[i] * acc[r]) * fexp(Gs[i] - Gs[j]) : 0.0f;
-            // permuted: Lp[i][j % 4][j / 4], so a solving lane reads its 16 values contiguously
-            Lp[i * kC + (j & 3) * 16 + (j >> 2)] = l;
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int i0 = ti * 32 + 8 * r4 + 4 * (lane >> 5);
+            const float4 gi = *(const float4 *)(Gs + i0), bi = *(const float4 *)(Bs + i0);
+            const float ga[4] = {gi.x, gi.y, gi.z, gi.w}, ba[4] = {bi.x, bi.y, bi.z, bi.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u;
+                const float lv = (ba[u] * acc[4 * r4 + u]) * fexp(ga[u] - gj);
+                const float l = j < i ? lv : 0.0f;
+                // permuted: Lp[i][j % 4][j / 4], so a solving lane reads its 16 values contiguously
+                Lp[i * kC + (j & 3) * 16 + (j >> 2)] = l;
+            }
         }
     }
     __syncthreads();
@@ -531,9 +541,15 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int j0 = mk * 32 + 8 * r4 + 4 * (lane >> 5); // key tokens j0 .. j0 + 3
+                const float4 gj = *(const float4 *)(Gs + j0);
+                const float ga[4] = {gj.x, gj.y, gj.z, gj.w};
                 float e[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) e[u] = (j0 + u <= i) ? pt[4 * r4 + u] * fexp(gi - Gs[j0 + u]) : 0.0f;
+                for (int u = 0; u < 4; ++u) {
+                    // computed for every lane, then selected: a branch here would serialise the LDS reads
+                    const float ev = pt[4 * r4 + u] * fexp(gi - ga[u]);
+                    e[u] = (j0 + u <= i) ? ev : 0.0f;
+                }
                 u32x2 w2;
                 w2[0] = pack_bf16x2(e[0], e[1]);
                 w2[1] = pack_bf16x2(e[2], e[3]);
@@ -556,9 +572,9 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
                     u32x2 a2, d2;
                     a2[0] = pack_bf16x2(vn[0], vn[1]);
                     a2[1] = pack_bf16x2(vn[2], vn[3]);
-                    float dec[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) dec[u] = vn[u] * fexp(glast - Gs[m0 + u]);
+                    const float4 gm = *(const float4 *)(Gs + m0);
+                    const float dec[4] = {vn[0] * fexp(glast - gm.x), vn[1] * fexp(glast - gm.y),
+                                          vn[2] * fexp(glast - gm.z), vn[3] * fexp(glast - gm.w)};
                     d2[0] = pack_bf16x2(dec[0], dec[1]);
                     d2[1] = pack_bf16x2(dec[2], dec[3]);
                     *(u32x2 *)(Vn + dv * kRowC + m0) = a2;
@@ -582,12 +598,21 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
                     O[dvt] = mfma(a, ld_frag(Vn + (hf * 64 + dvt * 32 + l32) * kRowC + s * 16 + kh), O[dvt]);
             }
             uint16_t *ost = (uint16_t *)(smem + kScanO) + (hf * 2 + mo) * 32 * kRowC;
+            float eg[16]; // exp(G) of this lane's 16 output rows, read and computed before the stores
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const float4 g4 = *(const float4 *)(Gs + mo * 32 + 8 * r4 + 4 * (lane >> 5));
+                eg[4 * r4] = fexp(g4.x);
+                eg[4 * r4 + 1] = fexp(g4.y);
+                eg[4 * r4 + 2] = fexp(g4.z);
+                eg[4 * r4 + 3] = fexp(g4.w);
+            }
 #pragma unroll
             for (int dvt = 0; dvt < 2; ++dvt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int ml = acc_row(r, lane);
-                    const float y = X[dvt][r] * fexp(Gs[mo * 32 + ml]) * p.scale + O[dvt][r] * p.scale;
+                    const float y = X[dvt][r] * eg[r] * p.scale + O[dvt][r] * p.scale;
                     ost[ml * kRowC + dvt * 32 + l32] = f32_to_bf16(y);
                 }
             // write out: 32 rows x 128 bytes, 8 lanes per row
