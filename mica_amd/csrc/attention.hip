@@ -26,6 +26,18 @@
 
 namespace {
 
+// Combine a value with the one held by lane l ^ 32 (v_permlane32_swap: no LDS round trip).  With the
+// same register as both operands, the swap leaves (own, other) in lanes 0-31 and (other, own) in lanes
+// 32-63, so max and sum come out bit-identical in every lane.
+__device__ __forceinline__ float half_swap_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 constexpr int kD = 256;              // head dim
 constexpr int kBQ = 32;              // query positions per workgroup
 constexpr int kBK = 32;              // keys per tile
@@ -180,7 +192,7 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
             sacc[r] = key <= query ? sacc[r] * p.scale_log2 : -__builtin_inff();
             mloc = __builtin_fmaxf(mloc, sacc[r]);
         }
-        mloc = __builtin_fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = half_swap_max(mloc); // the other half of the wave holds the same queries' other keys
         // lazy rescale: move the reference maximum only when the new one exceeds it by more than 8
         const bool grow = mloc > m_used + 8.0f;
         const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - mloc) : 1.0f;
@@ -219,7 +231,7 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         }
     }
     // ---- normalise, stage per wave in LDS (32 queries x 512 B), write 16-byte row pieces ----
-    const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+    const float ltot = half_swap_sum(lsum);
     const float inv = 1.0f / ltot;
     __syncthreads(); // every wave is done with the operand stages
     int8_t *ost = smem + wave * (kBQ * kD * 2);
