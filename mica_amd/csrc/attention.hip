@@ -129,18 +129,24 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         (void *)(p.vt + ((long long)(b * p.HK + hk) * p.ntiles_k) * kD * kBK), 0, p.ntiles_k * kVBytes, kBufferFlags);
     auto dma_tile = [&](int j, int st) {
         int8_t *ks = smem + st * kStage;
+        // The per-lane offsets are recomputed at every call from an opaque copy of the thread id:
+        // hoisted out of the key loop they stay live across it, get spilled to scratch under the
+        // register pressure of this kernel, and every reload then stalls the DMA issue.
+        int t = tid;
+        __asm__ volatile("" : "+v"(t));
+        const int ln = t & 63, hi_ = ln >> 5, l32_ = ln & 31, w_ = t >> 6;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // K: 1 KB block (wave, i) = rows 2 (4 wave + i) + lane / 32; lane writes physical chunk l % 32,
             // which holds logical chunk (l % 32) ^ row
-            const int row = (wave * 4 + i) * 2 + hi;
-            const int lc = l32 ^ row;
+            const int row = (w_ * 4 + i) * 2 + hi_;
+            const int lc = l32_ ^ row;
             const int ko = (int)((long long)(j * kBK + row) * p.ldk * 2 + lc * 16);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(ks + (wave * 4 + i) * 1024), 16, ko, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int vo = j * kVBytes + (wave * 4 + i) * 1024 + lane * 16;
+            const int vo = j * kVBytes + (w_ * 4 + i) * 1024 + ln * 16;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16, vo, 0,
                                                      0, 0);
         }
