@@ -184,10 +184,20 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         const int8_t *vs = ks + kKBytes;
         // ---- S^T = K Q^T: rows = keys j*32 + acc_row, column = query l % 32 ----
         f32x16 sacc = {};
+        // K fragments read two steps ahead of their MFMA (the schedule is pinned: left to itself the
+        // compiler reads each fragment into one register quad right before its MFMA and waits)
+        auto kfrag = [&](int s) {
+            return __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + l32 * 512 + (((2 * s + hi) ^ l32) * 16)));
+        };
+        bf16x8 ka = kfrag(0), kb = kfrag(1);
 #pragma unroll
         for (int s = 0; s < kD / 16; ++s) {
-            const int lc = 2 * s + hi;
-            const bf16x8 a = __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + l32 * 512 + ((lc ^ l32) * 16)));
+            const bf16x8 a = (s & 1) ? kb : ka;
+            if (s + 2 < kD / 16) {
+                if (s & 1) kb = kfrag(s + 2);
+                else ka = kfrag(s + 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
             sacc = mfma_bf16(a, qf[s], sacc);
         }
         // scores in log2 units, masked above the diagonal, in place
