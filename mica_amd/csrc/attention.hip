@@ -202,11 +202,19 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         }
         // scores in log2 units, masked above the diagonal, in place
         float mloc = -__builtin_inff();
+        if (j * kBK + kBK - 1 <= off + q0) { // the whole tile lies at or below the block's diagonal
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = j * kBK + 8 * (r >> 2) + 4 * hi + (r & 3);
-            sacc[r] = key <= query ? sacc[r] * p.scale_log2 : -__builtin_inff();
-            mloc = __builtin_fmaxf(mloc, sacc[r]);
+            for (int r = 0; r < 16; ++r) {
+                sacc[r] = sacc[r] * p.scale_log2;
+                mloc = __builtin_fmaxf(mloc, sacc[r]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = j * kBK + 8 * (r >> 2) + 4 * hi + (r & 3);
+                sacc[r] = key <= query ? sacc[r] * p.scale_log2 : -__builtin_inff();
+                mloc = __builtin_fmaxf(mloc, sacc[r]);
+            }
         }
         mloc = half_swap_max(mloc); // the other half of the wave holds the same queries' other keys
         // lazy rescale: move the reference maximum only when the new one exceeds it by more than 8
