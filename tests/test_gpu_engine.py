@@ -13,15 +13,19 @@ from mica_amd.model import StackConfig, W8A8Stack
 pytestmark = pytest.mark.gpu
 
 
-def _stack(gpu):
+def _stack(gpu, hybrid=False):
     cfg = StackConfig(layers=2, hidden=512, intermediate=1024, heads=4, kv_heads=1, head_dim=256, vocab=4096,
-                      n_options=31)
+                      n_options=31, full_attention_interval=2 if hybrid else 0, linear_k_heads=2,
+                      linear_v_heads=4)
     return W8A8Stack(cfg, device=gpu, seed=7)
 
 
-def test_graph_replays_match_eager_and_single_requests(gpu):
-    print("[case] engine graph vs eager", file=sys.stderr, flush=True)
-    st = _stack(gpu)
+@pytest.mark.parametrize("hybrid", [False, True])
+def test_graph_replays_match_eager_and_single_requests(gpu, hybrid):
+    """hybrid: a gated-delta-net layer then an attention layer (conv, gate, chunked scan and gated
+    norm inside the graph; the GDN recurrence is causal, so end padding leaves real positions alone)."""
+    print(f"[case] engine graph vs eager hybrid={hybrid}", file=sys.stderr, flush=True)
+    st = _stack(gpu, hybrid)
     g = torch.Generator().manual_seed(3)
     lens = [37, 64, 5]
     reqs = [torch.randint(0, st.cfg.vocab, (n,), generator=g).to(gpu) for n in lens]
