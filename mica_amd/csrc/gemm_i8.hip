@@ -16,10 +16,10 @@
 //     16 bytes per lane) free of LDS bank conflicts; the DMA writes 1 KiB contiguous blocks.
 //
 // Schedule.  Tiles are numbered in an XCD-aware grouped order (tile_of).  The first dp_tiles run
-// whole, one per workgroup per round.  When the tile count leaves a partial last round, the
-// remaining sk_tiles are split along K over every workgroup of a persistent grid (stream-K):
-// workgroup g takes the contiguous range [g W / G, (g + 1) W / G) of the W = sk_tiles * nk
-// (tile, slab) iterations.  A workgroup that ends with part of a tile stores its int32 partial
+// whole, one per workgroup per round.  When the tile count leaves a partial last round of few
+// tiles with a long K, the remaining sk_tiles are split along K over the first sk_grid workgroups
+// (stream-K): workgroup g < G = sk_grid takes the contiguous range [g W / G, (g + 1) W / G) of the
+// W = sk_tiles * nk (tile, slab) iterations.  A workgroup that ends with part of a tile stores its int32 partial
 // accumulators to the workspace, publishes them (device-scope release) and counts itself in the
 // tile's arrival counter; the last of the tile's contributors to arrive adds the others' partials
 // to its own (integer addition: exact in any order) and runs the epilogue, then re-zeroes the
@@ -101,8 +101,8 @@ struct GemmParams {
     int vec_ok;           // ldc, ldr, N all multiples of 4: 4-column vector stores
     // schedule over the tiles in grouped order (tile_of): [0, dp_tiles) run whole, one per workgroup
     // per round; the next half_tiles run as two 256 x 128 halves each; the next sk_tiles are split
-    // along K over all gridDim.x workgroups (at most one of half_tiles, sk_tiles is nonzero)
-    int dp_tiles, half_tiles, sk_tiles;
+    // along K over workgroups [0, sk_grid) (at most one of half_tiles, sk_tiles is nonzero)
+    int dp_tiles, half_tiles, sk_tiles, sk_grid;
     v4i *partials; // [gridDim.x][2][kPartialVecs][kThreads]: a workgroup's partial accumulators
     int *arrivals; // [sk_tiles]: contributors arrived so far; zero between launches
 };
@@ -592,26 +592,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         }
     }
 
-    if (p.sk_tiles == 0) return;
+    if (p.sk_tiles == 0 || (int)blockIdx.x >= p.sk_grid) return;
     // ---- split tiles: this workgroup's stream-K range of (tile, slab) iterations.  A workgroup
     // ending with part of a tile publishes its partial sums; the tile's last contributor to
     // arrive adds the others' to its own and runs the epilogue ----
     int *flag = (int *)(smem + kFlagOff);
+    const int S = p.sk_grid;
     const long long W = (long long)p.sk_tiles * nk;
-    const long long my_begin = sk_begin(blockIdx.x, W, G);
-    const long long my_end = sk_begin(blockIdx.x + 1, W, G);
+    const long long my_begin = sk_begin(blockIdx.x, W, S);
+    const long long my_end = sk_begin(blockIdx.x + 1, W, S);
     // Partial sums move with device-scope (sc1) buffer stores and loads: written through to the
     // device's coherence point and read from it, so no cache-wide write-back or invalidation (a
     // device-scope fence) is needed, only the ordering below.
     constexpr int kDeviceScope = 16; // cache policy bits: sc1
     constexpr int kSlotBytes = CfgFull::kPartialVecs * kThreads * 16;
     const __amdgpu_buffer_rsrc_t rsrc_p =
-        __builtin_amdgcn_make_buffer_rsrc((void *)p.partials, 0, G * 2 * kSlotBytes, kBufferFlags);
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.partials, 0, S * 2 * kSlotBytes, kBufferFlags);
     auto slot_off = [&](int g, int seg) { return (g * 2 + seg) * kSlotBytes + tid * 16; };
     auto fixup = [&](int rel) -> bool {
         const long long tb = (long long)rel * nk;      // the tile's first iteration
         const int seg = tb > my_begin ? 1 : 0;          // first (0) or last (1) range segment of this workgroup
-        const int g0 = sk_owner(tb, W, G), g1 = sk_owner(tb + nk - 1, W, G);
+        const int g0 = sk_owner(tb, W, S), g1 = sk_owner(tb + nk - 1, W, S);
         const int mine = slot_off(blockIdx.x, seg);
 #pragma unroll
         for (int j = 0; j < CfgFull::NB; ++j)
@@ -630,7 +631,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         if (*flag != g1 - g0) return false; // a later contributor finishes the tile
         for (int g = g0; g <= g1; ++g) {
             if (g == (int)blockIdx.x) continue;
-            const int src = slot_off(g, tb > sk_begin(g, W, G) ? 1 : 0);
+            const int src = slot_off(g, tb > sk_begin(g, W, S) ? 1 : 0);
             // two halves of 64 registers each: the operand registers of the main loop are free
             // here, but not all 128 accumulators' worth on top of the accumulators themselves
 #pragma unroll
@@ -739,24 +740,32 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     // Schedule over a grid of at most one workgroup per CU.  Whole tiles, one per workgroup per
     // round; when the last round would be at most half full, its tiles run as two 256 x 128 halves
     // each instead (the halves fill up to one round; SCALE epilogue only).  With a workspace, a
-    // partial last round is instead split along K over all CUs, provided every workgroup gets at
-    // least kMinSlabs slabs.
-    constexpr int kMinSlabs = 4;
+    // partial last round of at most cus / kSplit tiles whose K has at least kSplit * kMinSplitSlabs
+    // slabs is instead split along K, kSplit workgroups per tile.  A split tile costs its last
+    // contributor a serial sum of the others' 256 KiB partials plus the partial-sum round trip
+    // (measured about 15 us + 3 us per partial), so the split pays only when a quarter of the tile's
+    // K still takes longer than that; with more contributors per tile the sum grows faster than
+    // the K share shrinks.
+    constexpr long long kSplit = 4;
+    constexpr long long kMinSplitSlabs = 32;
     p.dp_tiles = (int)tiles;
     p.half_tiles = 0;
     p.sk_tiles = 0;
+    p.sk_grid = 0;
     int grid = (int)tiles;
     int dev = 0;
     const int cus = hipGetDevice(&dev) == hipSuccess ? cu_count(dev) : 0;
     const long long nk = (K + BK - 1) / BK;
     const long long rem = cus > 0 ? tiles % cus : 0;
     if (rem != 0 && cus <= 1024) {
-        if (workspace != nullptr && workspace_bytes >= workspace_bytes_for(cus) && rem * nk >= (long long)kMinSlabs * cus) {
+        if (workspace != nullptr && workspace_bytes >= workspace_bytes_for(cus) && rem * kSplit <= cus &&
+            nk >= kSplit * kMinSplitSlabs) {
             p.dp_tiles = (int)(tiles - rem);
             p.sk_tiles = (int)rem;
+            p.sk_grid = (int)(rem * kSplit);
             p.arrivals = (int *)workspace;
             p.partials = (v4i *)((char *)workspace + kCounterBytes);
-            grid = cus;
+            grid = tiles > rem ? cus : p.sk_grid;
         } else if (epilogue == MICA_EPI_SCALE && 2 * rem <= cus) {
             p.dp_tiles = (int)(tiles - rem);
             p.half_tiles = (int)rem;

@@ -185,8 +185,9 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
     Extensions: ``residual`` ([M, N] of out_dtype) is added after the output rounding;
     ``epilogue='silu_mul'`` treats qw as gate/up rows interleaved in groups of 64
     (int8_runtime.pack_gate_up) and returns bf16(bf16(silu(gate)) * up) of shape [M, N / 2];
-    ``split=True`` lets the kernel split a partial last round of tiles along K over all CUs
-    (exact int32 partial sums through a per-stream workspace; same bits as the default schedule).
+    ``split=True`` lets the kernel split a partial last round of at most CUs / 4 tiles along K over four
+    workgroups each when K >= 8192 (exact int32 partial sums through a per-stream workspace; same bits
+    as the default schedule).
     """
     if qx.dim() != 2 or qw.dim() != 2 or qx.dtype != torch.int8 or qw.dtype != torch.int8 or out_dtype not in DT:
         return _miss("mm_input")

@@ -328,10 +328,11 @@ def test_gemm_headline_full_size(gpu):
 
 
 @pytest.mark.parametrize("m,n,k,epi", [
-    (4096, 9728, 2560, "none"),      # 608 tiles: 96 split over 256 CUs
-    (4096, 2560, 4096, "none"),      # 160 tiles: every tile split
-    (700, 2560, 9728, "residual"),   # 30 tiles, K = 9728: ~26 contributors per tile
-    (1000, 3072, 2560, "silu_mul"),  # the fused gate+up epilogue after a split
+    (4096, 4352, 8192, "none"),      # 272 tiles: 256 whole, then 16 split over 64 workgroups, 32 slabs each
+    (700, 2560, 9728, "residual"),   # 30 tiles split over 120 workgroups, 38 slabs each
+    (300, 3072, 8192, "silu_mul"),   # the fused gate+up epilogue after a split
+    (200, 2560, 8256, "none"),       # 129 slabs per tile: contributor ranges straddle tile boundaries
+    (512, 2560, 4096, "none"),       # K below the split threshold: half tiles, workspace unused
 ])
 def test_gemm_split_schedule_bit_exact(gpu, m, n, k, epi):
     """split=True (remainder tiles split along K, int32 partial sums through the workspace) gives the
