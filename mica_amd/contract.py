@@ -504,13 +504,18 @@ class EngineJudge:
     prompt text carries them), and the engine's stack must read out ``readout_token_ids`` of the same
     tokenizer in codebook order.  Rows whose prompt, kind and label count coincide are scored once
     (direct_backend.py:651-659); the rest run ``max_batch`` at a time, each batch one engine call.
-    Prefix sharing between rows (direct_backend.py:660-700) is not built: every prompt runs in full.
+    With ``share_prefix`` the prompts of a batch that start alike (several questions about one state)
+    share it (direct_backend.py:660-700): the common start, cut to a multiple of 64 tokens and short of
+    every prompt's last token, runs once into a ``PrefixState`` and each prompt continues it, with the
+    same bits as running the prompts in full.
     """
 
     def __init__(self, engine, tokenize: Callable[[str], Sequence[int]], max_length: int = 32768,
-                 max_batch: int = 8, tokenizer=None):
+                 max_batch: int = 8, tokenizer=None, share_prefix: bool = True):
         self.engine, self.tokenize = engine, tokenize
         self.max_length, self.max_batch = int(max_length), int(max_batch)
+        self.share_prefix = bool(share_prefix)
+        self.shared_tokens = 0              # prefix tokens the last call ran once instead of per prompt
         self.tokenizer = tokenizer          # renders prompts with its chat template when given
         n_opt = engine.stack.cfg.n_options
         if n_opt < 2:
@@ -543,14 +548,32 @@ class EngineJudge:
         unique = sorted(set(source))
         dists = {}
         dev = self.engine.device
+        self.shared_tokens = 0
         for s in range(0, len(unique), self.max_batch):
             win = unique[s:s + self.max_batch]
-            reqs = [torch.tensor(toks[i], dtype=torch.long).to(dev) for i in win]
-            _, probs = self.engine(reqs, [kinds[i] for i in win], [counts[i] for i in win])
+            cut, prefix = self._shared(win, toks), None
+            if cut:
+                prefix = self.engine.stack.prefix_state(torch.tensor(toks[win[0]][:cut], dtype=torch.long).to(dev))
+                self.shared_tokens += cut * (len(win) - 1)
+            reqs = [torch.tensor(toks[i][cut:], dtype=torch.long).to(dev) for i in win]
+            _, probs = self.engine(reqs, [kinds[i] for i in win], [counts[i] for i in win], prefix=prefix)
             probs = probs.float().cpu()
             for j, i in enumerate(win):
                 dists[i] = [float(v) for v in probs[j, :counts[i]].tolist()]
         return [list(dists[source[i]]) for i in range(len(rows))]
+
+    def _shared(self, win, toks) -> int:
+        """Tokens the prompts of a batch share from the start, cut to a multiple of PREFIX_ALIGN and
+        short of every prompt's last token (0: nothing worth sharing)."""
+        from .model import PREFIX_ALIGN
+
+        if not self.share_prefix or len(win) < 2:
+            return 0
+        first, n = toks[win[0]], min(len(toks[i]) for i in win) - 1
+        common = 0
+        while common < n and all(toks[i][common] == first[common] for i in win):
+            common += 1
+        return common // PREFIX_ALIGN * PREFIX_ALIGN
 
 
 def input_tokens(prompts) -> int:

@@ -130,6 +130,21 @@ def _apply_rope(x, cos, sin):
     return x * cs + torch.cat((x[..., h:], x[..., :h]), -1) * sn
 
 
+# A prompt prefix whose length is a multiple of this continues bit-identically: the GDN scan's chunks
+# (64 tokens) and the attention kernel's key tiles (32) fall on the same boundaries as in a full run.
+PREFIX_ALIGN = 64
+
+
+class PrefixState:
+    """What a prompt prefix of `length` tokens leaves in every layer, for the rest of the prompt to
+    continue from (the reference engine's header state, prefill_engine.py:218-226): an attention layer's
+    rotated keys and values [1, length, kv_heads, head_dim], a GDN layer's (conv state [1, C, W - 1],
+    recurrent state [1, HV, 128, 128] fp32).  Shared by any number of continuations."""
+
+    def __init__(self, length: int, layers: list):
+        self.length, self.layers = int(length), layers
+
+
 class W8A8Stack:
     """Random-init 4B-shaped stack; `prefill(ids, batch)` returns option probabilities."""
 
@@ -148,36 +163,73 @@ class W8A8Stack:
         self.readout = LabelReadout(self.lm_head, self.label_ids)
         self._rope = {}
 
-    def _attention(self, qkv, B, S):
+    def _tables(self, n, device):
+        if n not in self._rope:
+            self._rope[n] = _rope(n, self.cfg.head_dim, self.cfg.rope_theta, device)
+        return self._rope[n]
+
+    def _attention(self, qkv, B, S, past=None, keep=False):
         """Causal GQA attention per request.  RoPE rotates the q and k heads of the QKV output in place
         (one kernel); the flash-attention kernel (head dim 256, 4 query heads per K/V head) then reads
         [B, S, heads, d] views of it and writes [B, S, heads, d]-contiguous output, i.e. already the O
         projection's [T, heads * d] rows.  Other head shapes, or attention="sdpa", use torch SDPA on the
-        same views (enable_gqa, transposed strides, no copies)."""
+        same views (enable_gqa, transposed strides, no copies).
+
+        past: (k, v) of a prefix of P tokens; the S rows are then positions P .. P + S - 1 and attend to
+        the prefix's keys too (Sk = P + S keys, the queries being the last S).  keep: also return this
+        call's rotated (k, v), contiguous (batch 1: a prefix being recorded)."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
-        if S not in self._rope:
-            self._rope[S] = _rope(S, d, cfg.rope_theta, qkv.device)
-        cos, sin = self._rope[S]
-        rope_inplace(qkv, hq + hk, d, cos, sin, period=S)
+        P = 0 if past is None else past[0].shape[1]
+        if P == 0:
+            cos, sin = self._tables(S, qkv.device)
+            rope_inplace(qkv, hq + hk, d, cos, sin, period=S)
+        else:
+            cos, sin = self._tables(P + S, qkv.device)
+            key = ("pos", B, S, P)
+            if key not in self._rope:
+                self._rope[key] = (torch.arange(B * S, device=qkv.device, dtype=torch.int32) % S + P).contiguous()
+            rope_inplace(qkv, hq + hk, d, cos, sin, pos=self._rope[key])
         q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
+        state = (k.contiguous(), v.contiguous()) if keep else None
+        if P:
+            k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
+            v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
         if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
-            return causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d)).view(B * S, hq * d)
-        a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
-                                           scale=1.0 / math.sqrt(d), enable_gqa=True)
-        return a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
+            a = causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d)).view(B * S, hq * d)
+        else:
+            a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                               is_causal=P == 0, attn_mask=None if P == 0 else self._mask(S, P, q.device),
+                                               scale=1.0 / math.sqrt(d), enable_gqa=True)
+            a = a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
+        return (a, state) if keep else a
 
-    def layer_forward(self, L, h, B, S, trace=None):
+    @staticmethod
+    def _mask(S, P, device):
+        """Boolean [S, P + S] mask: query i (position P + i) sees keys 0 .. P + i."""
+        return torch.arange(P + S, device=device)[None, :] <= (torch.arange(S, device=device)[:, None] + P)
+
+    def layer_forward(self, L, h, B, S, trace=None, past=None, keep=False):
+        """One decoder layer over B packed sequences of S tokens.  past: this layer's part of a
+        PrefixState the sequences continue; keep: also return this layer's state (batch 1)."""
         cfg = self.cfg
+        state = None
         if isinstance(L, GDNBlock):
             t = {} if trace is not None else None
-            h1 = L.mixer(h, B, trace=t)
+            init = None
+            if past is not None:
+                init = tuple(x.expand(B, *x.shape[1:]) for x in past)
+            h1 = L.mixer(h, B, initial=init, keep=keep, trace=t)
+            if keep:
+                h1, state = h1
             t = dict(kind="gdn", h=h, mixer=t, h1=h1) if trace is not None else None
         else:
             q, s = rms_norm_quant(h, L.input_norm, cfg.eps, offset=0.0)
             qkv = L.qkv.forward_quantized(q, s)
             qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
-            a = self._attention(qkv, B, S)
+            a = self._attention(qkv, B, S, past, keep)
+            if keep:
+                a, state = a
             r = aot.act_quant(a)
             h1 = L.o.forward_quantized(*r, residual=h)
             t = dict(kind="attention", h=h, q=q, s=s, qkv=qkv_out, qkv_rope=qkv, a=a, qa=r[0], sa=r[1],
@@ -189,7 +241,22 @@ class W8A8Stack:
         if trace is not None:
             t.update(q2=q2, s2=s2, g=g, qh=qh, sh=sh, h2=h2)
             trace.append(t)
-        return h2
+        return (h2, state) if keep else h2
+
+    @torch.no_grad()
+    def prefix_state(self, ids) -> PrefixState:
+        """Run a prompt prefix (int [P] token ids, one sequence) through every layer and keep the
+        state the rest of a prompt continues from.  With P a multiple of PREFIX_ALIGN a continuation
+        gives the same bits as running the whole prompt."""
+        P = ids.numel()
+        if P < 1:
+            raise ValueError("an empty prefix has no state")
+        h = self.embed.index_select(0, ids.reshape(-1))
+        states = []
+        for L in self.layers:
+            h, st = self.layer_forward(L, h, 1, P, keep=True)
+            states.append(st)
+        return PrefixState(P, states)
 
     @torch.no_grad()
     def prefill(self, ids, batch, kinds=None, n_choices=None, trace=None):
@@ -212,15 +279,16 @@ class W8A8Stack:
         return lo, cnt
 
     @torch.no_grad()
-    def forward_last(self, ids, batch, rows, lo, cnt, trace=None):
+    def forward_last(self, ids, batch, rows, lo, cnt, trace=None, prefix: PrefixState | None = None):
         """The stack over `batch` packed requests of equal (padded) length S = ids.numel() / batch, then
         the readout at the token rows `rows` (int32 [batch], device) with softmax slices lo / cnt.
         Everything stays on the device and no tensor is built from host values, so a HIP graph can
-        capture the call (rows / lo / cnt / ids then act as the graph's static inputs)."""
+        capture the call (rows / lo / cnt / ids then act as the graph's static inputs).  With a prefix,
+        every request continues it: its tokens are positions prefix.length + 0 .. S - 1."""
         S = ids.numel() // batch
         h = self.embed.index_select(0, ids)
-        for L in self.layers:
-            h = self.layer_forward(L, h, batch, S, trace)
+        for i, L in enumerate(self.layers):
+            h = self.layer_forward(L, h, batch, S, trace, past=None if prefix is None else prefix.layers[i])
         logits, probs = self.readout(h, rows, self.final_norm, self.cfg.eps, offset=0.0, lo=lo, cnt=cnt,
                                      probs_width=self.cfg.n_options)
         if trace is not None:

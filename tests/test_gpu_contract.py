@@ -78,9 +78,9 @@ def test_duplicate_questions_scored_once(judge):
         def __init__(self, eng):
             self.eng, self.device, self.stack = eng, eng.device, eng.stack
 
-        def __call__(self, reqs, kinds, counts):
+        def __call__(self, reqs, kinds, counts, prefix=None):
             calls.append(len(reqs))
-            return engine_call(reqs, kinds, counts)
+            return engine_call(reqs, kinds, counts, prefix=prefix)
 
     j2 = C.EngineJudge(Counting(judge.engine), _tokenize, max_length=32768)
     out = C.answer(req, j2)
@@ -93,3 +93,18 @@ def test_input_too_long(judge):
     short = C.EngineJudge(judge.engine, _tokenize, max_length=64)
     with pytest.raises(C.InputTooLongError):
         C.answer({"state": "s", "questions": {"q": {"type": "noul", "instructions": "i"}}}, short)
+
+
+def test_questions_about_one_state_share_its_prefix(judge):
+    """Several questions about one long state: the prompts' common start (system message and state)
+    runs once, and every answer equals the one from its prompt run alone."""
+    state = "Inventory log. " + " ".join(f"item {i}: {i * 7 % 13} units" for i in range(60))
+    req = {"state": state, "questions": {
+        "a": {"type": "noul", "instructions": "Is item 3 in stock?"},
+        "b": {"type": "choice", "instructions": "Which item has most units?", "criteria": {"x": "item 1", "y": "item 2"}},
+        "c": {"type": "score", "instructions": "How full is the store?", "criteria": ["empty", "half", "full"]}}}
+    out = C.answer(req, judge)
+    assert judge.shared_tokens >= 2 * 512
+    for r in C.rows_from_request(req):
+        expect = C.response_envelope([r], [_alone(judge, r)], model=C.MODEL_NAME)["answers"][r["id"]]
+        assert out["answers"][r["id"]] == expect, r["id"]
