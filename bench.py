@@ -407,6 +407,7 @@ def stack_prefill(torch, dev, reps=3):
     ops = st.linear_ops_per_token() * B * S
     ok = bool(torch.isfinite(probs).all()) and bool(torch.allclose(probs.sum(1), torch.ones(B, device=dev)))
     engine = engine_latency(torch, dev, st)
+    engine["serve_8_questions_8k_state"] = serving_latency(torch, dev, st)
     del st
     torch.cuda.empty_cache()
     return {"workload": "36 layers, hidden 2560, inter 9728, QKV 6144 (16 / 4 heads of 256), vocab 151936; "
@@ -468,6 +469,45 @@ def engine_latency(torch, dev, st, reps=5):
             ms = s.elapsed_time(e) / reps
             out[f"{mode}_B{B}_S{S}"] = {"ms": round(ms, 3), "tokens_per_s": round(B * S / (ms * 1e-3), 1)}
             del eng
+    torch.cuda.empty_cache()
+    return out
+
+
+def serving_latency(torch, dev, st, reps=3):
+    """One /v1/systemone request end to end on the 36-layer stack (mica_amd.contract.answer: validation,
+    prompts, tokens, engine, typed answers): 8 questions (Noul, Choice, Score) about one synthetic state
+    of ~8 K tokens (UTF-8 bytes as tokens), with the prompts' common start run once (share_prefix) and
+    with every prompt run in full.  Wall time per request, host work included."""
+    from mica_amd import contract
+    from mica_amd.engine import PrefillEngine
+
+    state = " ".join(f"record {i}: value {i * 37 % 101}, status {'open' if i % 3 else 'closed'}." for i in range(220))
+    qs = {}
+    for i in range(8):
+        kind = ("noul", "choice", "score")[i % 3]
+        q = {"type": kind, "instructions": f"Question {i}: what does record {i * 11} say?"}
+        if kind == "choice":
+            q["criteria"] = {f"c{j}": f"value {j * 10}" for j in range(6)}
+        elif kind == "score":
+            q["criteria"] = ["low", "medium", "high", "very high"]
+        qs[f"q{i}"] = q
+    req = {"state": state, "questions": qs}
+    out = {}
+    for share in (True, False):
+        judge = contract.EngineJudge(PrefillEngine(st, graph=False), lambda t: list(t.encode("utf-8")),
+                                     share_prefix=share)
+        resp = contract.answer(req, judge)   # warm-up
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            resp = contract.answer(req, judge)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / reps * 1e3
+        out["shared_prefix" if share else "full_prompts"] = {
+            "ms": round(ms, 1), "prompt_tokens": sum(len(t) for t in judge.last_prompts),
+            "tokens_run": sum(len(t) for t in judge.last_prompts) - judge.shared_tokens,
+            "answers": len(resp["answers"])}
+        del judge
     torch.cuda.empty_cache()
     return out
 
