@@ -569,21 +569,34 @@ class EngineJudge:
 
         if not self.share_prefix or len(win) < 2:
             return 0
-        first, n = toks[win[0]], min(len(toks[i]) for i in win) - 1
-        common = 0
-        while common < n and all(toks[i][common] == first[common] for i in win):
-            common += 1
+        common = min(_common_prefix([toks[i] for i in win]), min(len(toks[i]) for i in win) - 1)
         return common // PREFIX_ALIGN * PREFIX_ALIGN
+
+
+def _common_prefix(seqs) -> int:
+    """Length of the longest common start of the sequences: that of their lexicographic minimum and
+    maximum (any sequence sorting between two that agree on a start shares it), so only one pair is
+    compared element by element."""
+    if not seqs:
+        return 0
+    lo, hi = min(seqs), max(seqs)
+    n = min(len(lo), len(hi))
+    # bisect on the first difference: lo[:m] == hi[:m] is monotone in m and compares in C
+    a, b = 0, n
+    while a < b:
+        m = (a + b + 1) // 2
+        if lo[:m] == hi[:m]:
+            a = m
+        else:
+            b = m - 1
+    return a
 
 
 def input_tokens(prompts) -> int:
     """Prefill tokens a request needs with the rows' common prefix counted once (server.py:42-52)."""
     if not prompts:
         return 0
-    common = 0
-    if len(prompts) > 1:
-        while all(common < len(t) for t in prompts) and len({t[common] for t in prompts}) == 1:
-            common += 1
+    common = _common_prefix([list(t) for t in prompts]) if len(prompts) > 1 else 0
     return sum(len(t) for t in prompts) - common * (len(prompts) - 1)
 
 

@@ -132,3 +132,20 @@ def test_escape_and_positional_ids():
 def test_input_tokens():
     assert C.input_tokens([[1, 2, 3, 4], [1, 2, 5]]) == 7 - 2
     assert C.input_tokens([[7, 8]]) == 2 and C.input_tokens([]) == 0
+
+
+def test_common_prefix_against_brute_force():
+    import random
+
+    def brute(seqs):
+        c = 0
+        while all(c < len(t) for t in seqs) and len({t[c] for t in seqs}) == 1:
+            c += 1
+        return c
+
+    rng = random.Random(0)
+    for _ in range(2000):
+        base = [rng.randint(0, 3) for _ in range(rng.randint(0, 12))]
+        seqs = [base[:rng.randint(0, len(base))] + [rng.randint(0, 3) for _ in range(rng.randint(0, 4))]
+                for _ in range(rng.randint(1, 5))]
+        assert C._common_prefix(seqs) == brute(seqs), seqs
