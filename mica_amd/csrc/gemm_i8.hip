@@ -71,8 +71,12 @@ struct Cfg {
 };
 using CfgFull = Cfg<256, 256>; // waves of 64 x 128: 2 x 4 MFMA tiles, 4 DMA per slab
 using CfgHalf = Cfg<256, 128>; // waves of 64 x 64: 2 x 2 MFMA tiles, 3 DMA per slab
+using CfgQuarter = Cfg<128, 128>; // waves of 32 x 64: 1 x 2 MFMA tiles, 2 DMA per slab
 static_assert(CfgFull::MB == 2 && CfgFull::NB == 4 && CfgFull::kABlk == 2 && CfgFull::kBBlk == 2, "schedule");
 static_assert(CfgHalf::MB == 2 && CfgHalf::NB == 2 && CfgHalf::kABlk == 2 && CfgHalf::kBBlk == 1, "schedule");
+static_assert(CfgQuarter::MB == 1 && CfgQuarter::NB == 2 && CfgQuarter::kABlk == 1 && CfgQuarter::kBBlk == 1,
+              "schedule");
+static_assert(CfgQuarter::kSmemMain <= CfgFull::kSmemMain, "LDS");
 // LDS: the larger configuration's stages / staging, then the tile's row scales, column scales and
 // bias (fp32, 3 x 256), then the arrival count a split tile's contributors read back
 constexpr int kSmemMain = CfgFull::kSmemMain > CfgHalf::kSmemMain ? CfgFull::kSmemMain : CfgHalf::kSmemMain;
@@ -100,9 +104,10 @@ struct GemmParams {
     int tiles_m, tiles_n; // 256 x 256 tiles
     int vec_ok;           // ldc, ldr, N all multiples of 4: 4-column vector stores
     // schedule over the tiles in grouped order (tile_of): [0, dp_tiles) run whole, one per workgroup
-    // per round; the next half_tiles run as two 256 x 128 halves each; the next sk_tiles are split
-    // along K over workgroups [0, sk_grid) (at most one of half_tiles, sk_tiles is nonzero)
-    int dp_tiles, half_tiles, sk_tiles, sk_grid;
+    // per round; the next half_tiles run as two 256 x 128 halves each, or the next quarter_tiles as
+    // four 128 x 128 quarters each; the next sk_tiles are split along K over workgroups [0, sk_grid)
+    // (at most one of half_tiles, quarter_tiles, sk_tiles is nonzero)
+    int dp_tiles, half_tiles, quarter_tiles, sk_tiles, sk_grid;
     v4i *partials; // [gridDim.x][2][kPartialVecs][kThreads]: a workgroup's partial accumulators
     int *arrivals; // [sk_tiles]: contributors arrived so far; zero between launches
 };
@@ -365,6 +370,26 @@ struct TileEngine {
                     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 }
+            } else if constexpr (MB == 1) {
+                // 6 reads, 2 DMA, 4 MFMA: 4 reads up front, then 2 x [M, R, M, D]
+                nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
+                nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
+                nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
+                nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
+                nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
+                nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
+                dma1(dslab, 0, 0);
+                dma1(dslab, 0, 1);
+                mfma_half(cur, 0);
+                mfma_half(cur, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
+                }
             } else {
                 // 8 reads, 3 DMA, 8 MFMA: 4 reads up front, then 3 x [M, R, M, D] + [M, R, M]
                 nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
@@ -590,6 +615,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(GemmParams p) {
                 half.epilogue(p, smem, tm * kTile, n0);
             }
         }
+        // ---- quarter tiles: the next quarter_tiles tiles, each as four 128 x 128 quarters (a
+        // quarter wholly past M or N is skipped: the branch is uniform over the workgroup) ----
+        if (p.quarter_tiles > 0) {
+            TileEngine<CfgQuarter, EPI, OUT, HAS_BIAS, HAS_RES> quarter;
+            for (int h = blockIdx.x; h < 4 * p.quarter_tiles; h += G) {
+                int tm, tn;
+                tile_of(p.dp_tiles + (h >> 2), p.tiles_m, p.tiles_n, tm, tn);
+                const int m0 = tm * kTile + ((h >> 1) & 1) * CfgQuarter::BM;
+                const int n0 = tn * kTile + (h & 1) * CfgQuarter::BN;
+                if (m0 >= p.M || n0 >= p.N) continue;
+                quarter.run(p, smem, rsrc_a, rsrc_b, m0, n0, 0, nk);
+                quarter.epilogue(p, smem, m0, n0);
+            }
+        }
     }
 
     if (p.sk_tiles == 0 || (int)blockIdx.x >= p.sk_grid) return;
@@ -738,18 +777,26 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     const long long tiles = (long long)p.tiles_m * p.tiles_n;
     if (tiles >= (1ll << 31)) return MICA_MISS_RANGE;
     // Schedule over a grid of at most one workgroup per CU.  Whole tiles, one per workgroup per
-    // round; when the last round would be at most half full, its tiles run as two 256 x 128 halves
-    // each instead (the halves fill up to one round; SCALE epilogue only).  With a workspace, a
-    // partial last round of at most cus / kSplit tiles whose K has at least kSplit * kMinSplitSlabs
-    // slabs is instead split along K, kSplit workgroups per tile.  A split tile costs its last
+    // round; when the last round would be at most a quarter full, its tiles run as four 128 x 128
+    // quarters each, and when at most half full, as two 256 x 128 halves (SCALE epilogue only; the
+    // pieces fill up to one round).  With a workspace, a partial last round of at most cus / kSplit
+    // tiles whose K has at least kSplit * kMinSplitSlabs slabs is instead split along K, kSplit
+    // workgroups per tile, where quarters do not serve better: for the SiLU epilogue, and for M <= 256,
+    // where a tile's lower quarters are mostly or wholly empty.  A split tile costs its last
     // contributor a serial sum of the others' 256 KiB partials plus the partial-sum round trip
     // (measured about 15 us + 3 us per partial), so the split pays only when a quarter of the tile's
     // K still takes longer than that; with more contributors per tile the sum grows faster than
-    // the K share shrinks.
+    // the K share shrinks.  Measured against quarters at K >= 8192: split 41.7 vs 44.4 us at
+    // M = 128, 43.1 vs 44.9 at M = 256; quarters 42.3 vs 43.3 at M = 512, 44.7 vs 52.2 at M = 1024.
+#ifndef MICA_GEMM_QUARTERS
+#define MICA_GEMM_QUARTERS 1
+#endif
+    constexpr bool kQuarters = MICA_GEMM_QUARTERS != 0;
     constexpr long long kSplit = 4;
     constexpr long long kMinSplitSlabs = 32;
     p.dp_tiles = (int)tiles;
     p.half_tiles = 0;
+    p.quarter_tiles = 0;
     p.sk_tiles = 0;
     p.sk_grid = 0;
     int grid = (int)tiles;
@@ -758,14 +805,20 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     const long long nk = (K + BK - 1) / BK;
     const long long rem = cus > 0 ? tiles % cus : 0;
     if (rem != 0 && cus <= 1024) {
+        const bool quarters = kQuarters && epilogue == MICA_EPI_SCALE && 4 * rem <= cus;
         if (workspace != nullptr && workspace_bytes >= workspace_bytes_for(cus) && rem * kSplit <= cus &&
-            nk >= kSplit * kMinSplitSlabs) {
+            nk >= kSplit * kMinSplitSlabs && !(quarters && M > 256)) {
             p.dp_tiles = (int)(tiles - rem);
             p.sk_tiles = (int)rem;
             p.sk_grid = (int)(rem * kSplit);
             p.arrivals = (int *)workspace;
             p.partials = (v4i *)((char *)workspace + kCounterBytes);
             grid = tiles > rem ? cus : p.sk_grid;
+        } else if (quarters) {
+            p.dp_tiles = (int)(tiles - rem);
+            p.quarter_tiles = (int)rem;
+            grid = cus < tiles ? cus : (int)tiles;
+            if (grid < 4 * rem) grid = (int)(4 * rem);
         } else if (epilogue == MICA_EPI_SCALE && 2 * rem <= cus) {
             p.dp_tiles = (int)(tiles - rem);
             p.half_tiles = (int)rem;

@@ -259,6 +259,7 @@ def _rand_gemm(rng, m, n, k):
     (1, 32, 2560),         # single row, the reference's N=32 projection
     (17, 300, 2576),       # K not a multiple of the 128-byte slab
     (258, 514, 16),        # K of one chunk
+    (130, 2704, 2576),     # 11 tiles as 128 x 128 quarters, cut by both the M and the N edge
 ])
 def test_gemm_int32_and_epilogue_bit_exact(gpu, m, n, k):
     note(f"gemm m={m} n={n} k={k}")
@@ -328,15 +329,17 @@ def test_gemm_headline_full_size(gpu):
 
 
 @pytest.mark.parametrize("m,n,k,epi", [
-    (4096, 4352, 8192, "none"),      # 272 tiles: 256 whole, then 16 split over 64 workgroups, 32 slabs each
-    (700, 2560, 9728, "residual"),   # 30 tiles split over 120 workgroups, 38 slabs each
-    (300, 3072, 8192, "silu_mul"),   # the fused gate+up epilogue after a split
-    (200, 2560, 8256, "none"),       # 129 slabs per tile: contributor ranges straddle tile boundaries
-    (512, 2560, 4096, "none"),       # K below the split threshold: half tiles, workspace unused
+    (4096, 4352, 8192, "none"),      # 272 tiles: 256 whole, then 16 as 128 x 128 quarters (M > 256)
+    (700, 2560, 9728, "residual"),   # 30 tiles as quarters, residual epilogue
+    (300, 3072, 8192, "silu_mul"),   # 24 tiles split along K over 96 workgroups, then the SiLU epilogue
+    (200, 2560, 8256, "none"),       # M <= 256: split; 129 slabs per tile, so ranges straddle tiles
+    (256, 2560, 9728, "none"),       # M <= 256: split, 4 contributors of 38 slabs per tile
+    (512, 2560, 4096, "none"),       # K below the split threshold: quarters, workspace unused
 ])
 def test_gemm_split_schedule_bit_exact(gpu, m, n, k, epi):
-    """split=True (remainder tiles split along K, int32 partial sums through the workspace) gives the
-    same bits as the oracle, twice in a row (the arrival counters must come back to zero)."""
+    """split=True (a workspace: remainder tiles split along K where that serves best, int32 partial sums
+    through the workspace) gives the same bits as the oracle, twice in a row (the arrival counters must
+    come back to zero)."""
     note(f"gemm split m={m} n={n} k={k} epi={epi}")
     rng = np.random.default_rng(m + n + k + 1)
     A, B, sa, sb = _rand_gemm(rng, m, n, k)
