@@ -38,7 +38,9 @@ def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # untimed launches before each timed block: after an idle host phase the first ~100 launches run
+    # ~10 % slower (113.5 us steady vs ~125 us for the headline GEMM) while the clocks come back up
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 36-layer prefill measurement")
@@ -584,12 +586,14 @@ def summarize(indir, out_txt, command="", top=16):
                 cur = (key, [d])
                 runs.append(cur)
         lines.append(f"# runs of >= 20 back-to-back dispatches, in launch order ({os.path.basename(f)})")
-        lines.append(f"{'run':>4} {'calls':>6} {'avg_us':>10} {'avg_last':>10} {'min_us':>10} {'max_us':>10} {'grid':>9}  kernel"
-                     f"  (avg_last: the last calls - 20, i.e. without the warm-up)")
+        lines.append(f"{'run':>4} {'calls':>6} {'avg_us':>10} {'avg_last':>10} {'avg_end50':>10} {'min_us':>10} "
+                     f"{'max_us':>10} {'grid':>9}  kernel  (avg_last: all calls but the first 20; avg_end50: the "
+                     f"last 50 calls, the timed ones of a --steps 50 run)")
         for i, (key, v) in enumerate(r_ for r_ in runs if len(r_[1]) >= 20):
             tail = v[20:] if len(v) > 20 else v
+            end = v[-50:]
             lines.append(f"{i:4d} {len(v):6d} {sum(v) / len(v) / 1e3:10.2f} {sum(tail) / len(tail) / 1e3:10.2f} "
-                         f"{min(v) / 1e3:10.2f} {max(v) / 1e3:10.2f} {key[1]:9d}  {key[0]}")
+                         f"{sum(end) / len(end) / 1e3:10.2f} {min(v) / 1e3:10.2f} {max(v) / 1e3:10.2f} {key[1]:9d}  {key[0]}")
         lines.append(f"# per-dispatch durations by kernel and launch shape ({os.path.basename(f)})")
         lines.append(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'grid':>9} {'wg':>5}  kernel")
         for (k, (gx, wx)), v in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
