@@ -122,9 +122,11 @@ int mica_rmsnorm_quant_multi(const void *x, int x_dtype, int ldx, const void *re
  *
  * workspace: NULL, or workspace_bytes >= mica_mm_i8_workspace_bytes(device) bytes of device memory,
  * 16-byte aligned, whose first 4 KiB are zero before its first use (every launch leaves them zero
- * again).  With it, when the last round of 256 x 256 tiles would hold at most CUs / 4 tiles and
- * K >= 8192, those tiles are split along K over four workgroups each; partial int32 sums go through
- * the workspace and are added exactly, so the result is bit-identical to the unsplit schedule.  Launches that
+ * again).  With it, when the last round of 256 x 256 tiles would hold at most CUs / 4 tiles,
+ * K >= 8192 and either M <= 256 or the SILU_MUL epilogue is asked for (elsewhere 128 x 128 quarter
+ * tiles, which need no workspace, serve such a round better), those tiles are split along K over four
+ * workgroups each; partial int32 sums go through the workspace and are added exactly, so the result is
+ * bit-identical to the unsplit schedule.  Launches that
  * share a workspace must be ordered (one stream); concurrent launches need one workspace each.
  * The workspace has no counterpart in the reference (its Triton GEMM has no split schedule).
  */

@@ -186,8 +186,9 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
     ``epilogue='silu_mul'`` treats qw as gate/up rows interleaved in groups of 64
     (int8_runtime.pack_gate_up) and returns bf16(bf16(silu(gate)) * up) of shape [M, N / 2];
     ``split=True`` lets the kernel split a partial last round of at most CUs / 4 tiles along K over four
-    workgroups each when K >= 8192 (exact int32 partial sums through a per-stream workspace; same bits
-    as the default schedule).
+    workgroups each when K >= 8192 and M <= 256 or the epilogue is 'silu_mul' (exact int32 partial sums
+    through a per-stream workspace; same bits as the default schedule, which runs such a round as
+    128 x 128 quarter tiles).
     """
     if qx.dim() != 2 or qw.dim() != 2 or qx.dtype != torch.int8 or qw.dtype != torch.int8 or out_dtype not in DT:
         return _miss("mm_input")
