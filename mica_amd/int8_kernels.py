@@ -179,7 +179,8 @@ def act_quant(x, inv_smooth=None, rounding="even"):
     return (q, s) if ok else None
 
 
-def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, epilogue="none", split=False):
+def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, epilogue="none", split=False,
+          requant=False):
     """C = (qx . qw^T)_i32 * sx[m] * sw[n] (+ bias[n]) -> out_dtype (int8_kernels.py:359-406).
 
     Extensions: ``residual`` ([M, N] of out_dtype) is added after the output rounding;
@@ -188,7 +189,10 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
     ``split=True`` lets the kernel split a partial last round of at most CUs / 4 tiles along K over four
     workgroups each when K >= 8192 and M <= 256 or the epilogue is 'silu_mul' (exact int32 partial sums
     through a per-stream workspace; same bits as the default schedule, which runs such a round as
-    128 x 128 quarter tiles).
+    128 x 128 quarter tiles).  ``requant=True`` returns the per-token int8 quantization (q, s) of the
+    output instead of the output (the next QLinear's input, e.g. h of the MLP for the down projection):
+    a second launch, because each row's scale needs the absmax of the whole row, which spans every
+    column tile of the GEMM.
     """
     if qx.dim() != 2 or qw.dim() != 2 or qx.dtype != torch.int8 or qw.dtype != torch.int8 or out_dtype not in DT:
         return _miss("mm_input")
@@ -227,7 +231,9 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
               sw.data_ptr(), None if bias is None else bias.data_ptr(),
               None if residual is None else residual.data_ptr(), n_out, out.data_ptr(), n_out, DT[out_dtype],
               m, n, k, EPILOGUE[epilogue], ws, ws_bytes)
-    return out if ok else None
+    if not ok:
+        return None
+    return act_quant(out) if requant else out
 
 
 def mm_i8_int32(qx, qw, split=False):

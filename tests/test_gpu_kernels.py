@@ -294,6 +294,23 @@ def test_gemm_extreme_accumulators(gpu):
     assert np.abs(acc).max() == k * 127 * 127
 
 
+def test_gemm_requant_output(gpu):
+    """mm_i8(..., requant=True): the per-token int8 quantization of the GEMM's output, bit-exact with the
+    oracle's quant_act of that output (the gate+up SiLU product h feeding the down projection, and a
+    plain bf16 output)."""
+    note("gemm requant")
+    rng = np.random.default_rng(21)
+    m, n, k = 300, 1024, 2560
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    tA, tB, tsa, tsb = (torch.from_numpy(v).cuda() for v in (A, B, sa, sb))
+    for epi in ("silu_mul", "none"):
+        out = int8_kernels.mm_i8(tA, tsa, tB, tsb, epilogue=epi)
+        q, s = int8_kernels.mm_i8(tA, tsa, tB, tsb, epilogue=epi, requant=True)
+        qo, so = O.quant_act(O.bf16_to_f32(bits_of(out)))
+        assert np.array_equal(q.cpu().numpy(), qo), epi
+        assert np.array_equal(s.cpu().numpy(), so), epi
+
+
 def test_gemm_residual_epilogue(gpu):
     note("gemm residual")
     rng = np.random.default_rng(3)
