@@ -69,3 +69,24 @@ class LabelReadout:
             raise ValueError(f"readout does not support this input ({_lib.status_name(rc)})")
         _launched()
         return logits, probs
+
+
+def gather_logits(h, last_idx, norm_w, eps, label_W, n_opts, offset=1.0):
+    """The readout as one function: the final RMSNorm of h at each request's last token (rows
+    last_idx of the packed [T, K] bf16 h), fp32 dots with the label rows label_W ([L, K] fp32 or bf16:
+    No, Yes, then the option labels, as gathered by release_runtime.py:298-302), and the softmax of
+    each request's slice (release_runtime.py:509-517): n_opts[b] == 0 reads the No / Yes pair, n > 0
+    the first n option labels.  n_opts is one int for every request or one per request.  Returns the
+    probabilities, fp32 [B, max slice] (zero past each request's slice); one kernel launch pair."""
+    if label_W.dtype not in (torch.float32, torch.bfloat16) or label_W.dim() != 2:
+        raise ValueError("label_W must be a 2-D fp32 or bf16 tensor")
+    ro = LabelReadout.__new__(LabelReadout)
+    ro.weight, ro.ids, ro.n_labels = label_W.contiguous(), None, int(label_W.shape[0])
+    B = int(torch.as_tensor(last_idx).numel())
+    ns = [int(n_opts)] * B if isinstance(n_opts, int) else [int(n) for n in n_opts]
+    if len(ns) != B or any(n < 0 or n > ro.n_labels - 2 for n in ns):
+        raise ValueError("n_opts must give 0 (No / Yes) or 1 .. L - 2 options for every request")
+    lo = torch.tensor([0 if n == 0 else 2 for n in ns], dtype=torch.int32)
+    cnt = torch.tensor([2 if n == 0 else n for n in ns], dtype=torch.int32)
+    _, probs = ro(h, last_idx, norm_w, eps, offset, lo=lo, cnt=cnt)
+    return probs

@@ -542,6 +542,28 @@ def test_readout_config4_shape(gpu, kat):
         np.testing.assert_allclose(pk.cpu().numpy()[0, :n], case["p"], atol=1e-6)
 
 
+def test_gather_logits_function(gpu):
+    """readout.gather_logits (fp32 and bf16 label rows; 0 = the No / Yes pair, n = the first n options)
+    against the oracle's readout and option softmax."""
+    from mica_amd.readout import gather_logits
+    note("gather_logits")
+    rng = np.random.default_rng(6)
+    T, K, L = 600, 2560, 257
+    h = act_bits(rng, (T, K), scale=0.5)
+    rows = np.array([99, 299, 599, 0])
+    norm_w = O.round_bf16(rng.normal(0, 0.1, K).astype(np.float32))
+    W = O.round_bf16(rng.normal(0, 0.02, (L, K)).astype(np.float32))
+    ns = [0, 255, 5, 0]
+    zo = O.readout(h, rows, norm_w, 1e-6, W)
+    for wt in (torch.from_numpy(W).cuda(), to_gpu_bf16(O.f32_to_bf16(W))):
+        p = gather_logits(to_gpu_bf16(h), torch.from_numpy(rows).cuda(), to_gpu_bf16(O.f32_to_bf16(norm_w)), 1e-6,
+                          wt, ns, offset=1.0).cpu().numpy()
+        for b, n in enumerate(ns):
+            kind, cnt = ("noul", 2) if n == 0 else ("choice", n)
+            np.testing.assert_allclose(p[b, :cnt], O.option_probs(zo[b], kind, cnt), atol=1e-3)
+            assert not p[b, cnt:].any()
+
+
 def test_readout_bad_indices_give_nan_not_a_fault(gpu):
     note("readout bad indices")
     h = torch.zeros(4, 64, dtype=torch.bfloat16, device=gpu)
