@@ -72,11 +72,14 @@ struct Cfg {
 using CfgFull = Cfg<256, 256>; // waves of 64 x 128: 2 x 4 MFMA tiles, 4 DMA per slab
 using CfgHalf = Cfg<256, 128>; // waves of 64 x 64: 2 x 2 MFMA tiles, 3 DMA per slab
 using CfgQuarter = Cfg<128, 128>; // waves of 32 x 64: 1 x 2 MFMA tiles, 2 DMA per slab
+using CfgHalfM = Cfg<128, 256>;   // waves of 32 x 128: 1 x 4 MFMA tiles, 3 DMA per slab (SiLU pairs intact)
 static_assert(CfgFull::MB == 2 && CfgFull::NB == 4 && CfgFull::kABlk == 2 && CfgFull::kBBlk == 2, "schedule");
 static_assert(CfgHalf::MB == 2 && CfgHalf::NB == 2 && CfgHalf::kABlk == 2 && CfgHalf::kBBlk == 1, "schedule");
 static_assert(CfgQuarter::MB == 1 && CfgQuarter::NB == 2 && CfgQuarter::kABlk == 1 && CfgQuarter::kBBlk == 1,
               "schedule");
 static_assert(CfgQuarter::kSmemMain <= CfgFull::kSmemMain, "LDS");
+static_assert(CfgHalfM::MB == 1 && CfgHalfM::NB == 4 && CfgHalfM::kABlk == 1 && CfgHalfM::kBBlk == 2 &&
+              CfgHalfM::WN == 128 && CfgHalfM::kSmemMain <= CfgFull::kSmemMain, "schedule");
 // LDS: the larger configuration's stages / staging, then the tile's row scales, column scales and
 // bias (fp32, 3 x 256), then the arrival count a split tile's contributors read back
 constexpr int kSmemMain = CfgFull::kSmemMain > CfgHalf::kSmemMain ? CfgFull::kSmemMain : CfgHalf::kSmemMain;
@@ -107,7 +110,8 @@ struct GemmParams {
     // per round; the next half_tiles run as two 256 x 128 halves each, or the next quarter_tiles as
     // four 128 x 128 quarters each; the next sk_tiles are split along K over workgroups [0, sk_grid)
     // (at most one of half_tiles, quarter_tiles, sk_tiles is nonzero)
-    int dp_tiles, half_tiles, quarter_tiles, sk_tiles, sk_grid;
+    // the next mhalf_tiles (SiLU epilogue) run as two 128 x 256 halves each along M
+    int dp_tiles, half_tiles, quarter_tiles, mhalf_tiles, sk_tiles, sk_grid;
     v4i *partials; // [gridDim.x][2][kPartialVecs][kThreads]: a workgroup's partial accumulators
     int *arrivals; // [sk_tiles]: contributors arrived so far; zero between launches
 };
@@ -339,7 +343,34 @@ struct TileEngine {
             __builtin_amdgcn_s_barrier();
             const int8_t *st = smem + ((k + 1) % NST) * C::kStage;
             const int dslab = k + NST;
-            if constexpr (NB == 4) {
+            if constexpr (NB == 4 && MB == 1) {
+                // 10 reads, 3 DMA, 8 MFMA: 4 reads up front, then 3 x [M, R, M, R, D] + [M, M]
+                nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
+                nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
+                nxt.x[0][0] = *(const v4i *)(st + x_rd[0][0]);
+                nxt.w[0][2] = *(const v4i *)(st + w_rd[2][0]);
+                nxt.w[0][3] = *(const v4i *)(st + w_rd[3][0]);
+                nxt.w[1][0] = *(const v4i *)(st + w_rd[0][1]);
+                nxt.w[1][1] = *(const v4i *)(st + w_rd[1][1]);
+                nxt.x[1][0] = *(const v4i *)(st + x_rd[0][1]);
+                nxt.w[1][2] = *(const v4i *)(st + w_rd[2][1]);
+                nxt.w[1][3] = *(const v4i *)(st + w_rd[3][1]);
+                dma1(dslab, 0, 0);
+                dma1(dslab, 0, 1);
+                dma1(dslab, 1, 1);
+                mfma_half(cur, 0);
+                mfma_half(cur, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); // 4 DS reads
+#pragma unroll
+                for (int r = 0; r < 3; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read (the LDS DMA)
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            } else if constexpr (NB == 4) {
                 // 12 reads, 4 DMA, 16 MFMA: 4 reads up front, then 4 x [M, R, M, R, M, D, M]
                 nxt.w[0][0] = *(const v4i *)(st + w_rd[0][0]);
                 nxt.w[0][1] = *(const v4i *)(st + w_rd[1][0]);
@@ -631,6 +662,23 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(GemmParams p) {
         }
     }
 
+    // ---- M-halves: the next mhalf_tiles tiles, each as two 128 x 256 halves along M (a half wholly
+    // past M is skipped: uniform over the workgroup); the SiLU epilogue's gate/up column pairs stay
+    // within one wave ----
+    if constexpr (EPI == MICA_EPI_SILU_MUL) {
+        if (p.mhalf_tiles > 0) {
+            TileEngine<CfgHalfM, EPI, OUT, HAS_BIAS, HAS_RES> mhalf;
+            for (int h = blockIdx.x; h < 2 * p.mhalf_tiles; h += G) {
+                int tm, tn;
+                tile_of(p.dp_tiles + (h >> 1), p.tiles_m, p.tiles_n, tm, tn);
+                const int m0 = tm * kTile + (h & 1) * CfgHalfM::BM;
+                if (m0 >= p.M) continue;
+                mhalf.run(p, smem, rsrc_a, rsrc_b, m0, tn * kTile, 0, nk);
+                mhalf.epilogue(p, smem, m0, tn * kTile);
+            }
+        }
+    }
+
     if (p.sk_tiles == 0 || (int)blockIdx.x >= p.sk_grid) return;
     // ---- split tiles: this workgroup's stream-K range of (tile, slab) iterations.  A workgroup
     // ending with part of a tile publishes its partial sums; the tile's last contributor to
@@ -778,8 +826,10 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     if (tiles >= (1ll << 31)) return MICA_MISS_RANGE;
     // Schedule over a grid of at most one workgroup per CU.  Whole tiles, one per workgroup per
     // round; when the last round would be at most a quarter full, its tiles run as four 128 x 128
-    // quarters each, and when at most half full, as two 256 x 128 halves (SCALE epilogue only; the
-    // pieces fill up to one round).  With a workspace, a partial last round of at most cus / kSplit
+    // quarters each, and when at most half full, as two 256 x 128 halves (SCALE epilogue; the pieces
+    // fill up to one round).  For the SiLU epilogue, whose waves need 128 columns (gate / up pairs), a
+    // last round at most half full runs as two 128 x 256 halves along M (measured: 36.2 -> 27.2 us at
+    // 128 x 19456 x 2560, 86.8 -> 73.8 us at M = 1024).  With a workspace, a partial last round of at most cus / kSplit
     // tiles whose K has at least kSplit * kMinSplitSlabs slabs is instead split along K, kSplit
     // workgroups per tile, where quarters do not serve better: for the SiLU epilogue, and for M <= 256,
     // where a tile's lower quarters are mostly or wholly empty.  A split tile costs its last
@@ -792,11 +842,16 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
 #define MICA_GEMM_QUARTERS 1
 #endif
     constexpr bool kQuarters = MICA_GEMM_QUARTERS != 0;
+#ifndef MICA_GEMM_MHALVES
+#define MICA_GEMM_MHALVES 1
+#endif
+    constexpr bool kMHalves = MICA_GEMM_MHALVES != 0;
     constexpr long long kSplit = 4;
     constexpr long long kMinSplitSlabs = 32;
     p.dp_tiles = (int)tiles;
     p.half_tiles = 0;
     p.quarter_tiles = 0;
+    p.mhalf_tiles = 0;
     p.sk_tiles = 0;
     p.sk_grid = 0;
     int grid = (int)tiles;
@@ -819,6 +874,11 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
             p.quarter_tiles = (int)rem;
             grid = cus < tiles ? cus : (int)tiles;
             if (grid < 4 * rem) grid = (int)(4 * rem);
+        } else if (kMHalves && epilogue == MICA_EPI_SILU_MUL && 2 * rem <= cus) {
+            p.dp_tiles = (int)(tiles - rem);
+            p.mhalf_tiles = (int)rem;
+            grid = cus < tiles ? cus : (int)tiles;
+            if (grid < 2 * rem) grid = (int)(2 * rem);
         } else if (epilogue == MICA_EPI_SCALE && 2 * rem <= cus) {
             p.dp_tiles = (int)(tiles - rem);
             p.half_tiles = (int)rem;

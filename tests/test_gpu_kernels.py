@@ -294,6 +294,22 @@ def test_gemm_extreme_accumulators(gpu):
     assert np.abs(acc).max() == k * 127 * 127
 
 
+@pytest.mark.parametrize("m", [1, 100, 128, 200, 300, 700])
+def test_gemm_silu_m_halves(gpu, m):
+    """The fused gate+up SiLU epilogue when the last round runs as 128 x 256 halves along M (a lower
+    half wholly past M skipped, one cut by it, or both full), within one bf16 ulp of the oracle."""
+    note(f"gemm silu m-halves m={m}")
+    rng = np.random.default_rng(m + 5)
+    n, k = 3072, 2560
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    grp = B.reshape(n // 128, 2, 64, k)
+    sgr = sb.reshape(n // 128, 2, 64)
+    gv = O.epilogue(O.int_gemm(A, grp[:, 0].reshape(n // 2, k)), sa, sgr[:, 0].reshape(n // 2))
+    uv = O.epilogue(O.int_gemm(A, grp[:, 1].reshape(n // 2, k)), sa, sgr[:, 1].reshape(n // 2))
+    y = int8_kernels.mm_i8(*(torch.from_numpy(v).cuda() for v in (A, sa, B, sb)), epilogue="silu_mul")
+    assert_within_one_ulp(bits_of(y), O.silu_mul(gv, uv))
+
+
 def test_gemm_requant_output(gpu):
     """mm_i8(..., requant=True): the per-token int8 quantization of the GEMM's output, bit-exact with the
     oracle's quant_act of that output (the gate+up SiLU product h feeding the down projection, and a
