@@ -450,13 +450,13 @@ def hybrid_prefill(torch, dev, reps=3):
 
 def engine_latency(torch, dev, st, reps=5):
     """The prefill engine (HIP-graph buckets, mica_amd.engine) on the 36-layer stack: per-call time of
-    one 512-token request (launch-bound when eager: ~430 launches) and of 8 x 2048 tokens, eager vs a
+    one 128-token and one 512-token request (~430 launches each) and of 8 x 2048 tokens, eager vs a
     replayed graph (inputs copied in, outputs copied out)."""
     from mica_amd.engine import PrefillEngine
 
     out = {}
     g = torch.Generator().manual_seed(5)
-    for B, S in ((1, 512), (8, 2048)):
+    for B, S in ((1, 128), (1, 512), (8, 2048)):
         reqs = [torch.randint(0, st.cfg.vocab, (S,), generator=g).to(dev) for _ in range(B)]
         for mode in ("eager", "graph"):
             eng = PrefillEngine(st, graph=mode == "graph")
