@@ -143,6 +143,16 @@ class PrefixState:
 
     def __init__(self, length: int, layers: list):
         self.length, self.layers = int(length), layers
+        self.positions = {}   # (batch, S) -> int32 [batch * S] RoPE positions of a continuation
+
+    def positions_for(self, batch: int, S: int, device):
+        """RoPE positions length + (t % S) of a packed continuation batch, made once per shape and kept
+        with the prefix (a graph that continues the prefix reads them on every replay)."""
+        key = (batch, S)
+        if key not in self.positions:
+            self.positions[key] = (torch.arange(batch * S, device=device, dtype=torch.int32) % S
+                                   + self.length).contiguous()
+        return self.positions[key]
 
 
 class W8A8Stack:
@@ -161,14 +171,22 @@ class W8A8Stack:
         ids = torch.randperm(cfg.vocab, generator=torch.Generator().manual_seed(seed))[: 2 + cfg.n_options]
         self.label_ids = ids.to(self.device)
         self.readout = LabelReadout(self.lm_head, self.label_ids)
-        self._rope = {}
+        self._rope = None     # (cos, sin) of positions 0 .. size - 1, grown by doubling
+        self._retired = []    # earlier tables: a captured graph may still read them
 
     def _tables(self, n, device):
-        if n not in self._rope:
-            self._rope[n] = _rope(n, self.cfg.head_dim, self.cfg.rope_theta, device)
-        return self._rope[n]
+        """cos / sin of positions 0 .. n - 1: the first n rows of one table, which is regrown (doubled)
+        when a longer sequence comes, so memory stays within twice the longest sequence seen.  Every
+        entry depends only on its position, so a row is the same in every table."""
+        if self._rope is None or self._rope[0].shape[0] < n:
+            size = max(n, 4096 if self._rope is None else 2 * self._rope[0].shape[0])
+            if self._rope is not None:
+                self._retired.append(self._rope)
+            self._rope = _rope(size, self.cfg.head_dim, self.cfg.rope_theta, device)
+        cos, sin = self._rope
+        return cos[:n], sin[:n]
 
-    def _attention(self, qkv, B, S, past=None, keep=False):
+    def _attention(self, qkv, B, S, past=None, keep=False, pos=None):
         """Causal GQA attention per request.  RoPE rotates the q and k heads of the QKV output in place
         (one kernel); the flash-attention kernel (head dim 256, 4 query heads per K/V head) then reads
         [B, S, heads, d] views of it and writes [B, S, heads, d]-contiguous output, i.e. already the O
@@ -176,8 +194,9 @@ class W8A8Stack:
         same views (enable_gqa, transposed strides, no copies).
 
         past: (k, v) of a prefix of P tokens; the S rows are then positions P .. P + S - 1 and attend to
-        the prefix's keys too (Sk = P + S keys, the queries being the last S).  keep: also return this
-        call's rotated (k, v), contiguous (batch 1: a prefix being recorded)."""
+        the prefix's keys too (Sk = P + S keys, the queries being the last S); pos: their int32 RoPE
+        positions (PrefixState.positions_for).  keep: also return this call's rotated (k, v),
+        contiguous (batch 1: a prefix being recorded)."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
         P = 0 if past is None else past[0].shape[1]
@@ -186,10 +205,7 @@ class W8A8Stack:
             rope_inplace(qkv, hq + hk, d, cos, sin, period=S)
         else:
             cos, sin = self._tables(P + S, qkv.device)
-            key = ("pos", B, S, P)
-            if key not in self._rope:
-                self._rope[key] = (torch.arange(B * S, device=qkv.device, dtype=torch.int32) % S + P).contiguous()
-            rope_inplace(qkv, hq + hk, d, cos, sin, pos=self._rope[key])
+            rope_inplace(qkv, hq + hk, d, cos, sin, pos=pos)
         q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
         state = (k.contiguous(), v.contiguous()) if keep else None
         if P:
@@ -209,7 +225,7 @@ class W8A8Stack:
         """Boolean [S, P + S] mask: query i (position P + i) sees keys 0 .. P + i."""
         return torch.arange(P + S, device=device)[None, :] <= (torch.arange(S, device=device)[:, None] + P)
 
-    def layer_forward(self, L, h, B, S, trace=None, past=None, keep=False):
+    def layer_forward(self, L, h, B, S, trace=None, past=None, keep=False, pos=None):
         """One decoder layer over B packed sequences of S tokens.  past: this layer's part of a
         PrefixState the sequences continue; keep: also return this layer's state (batch 1)."""
         cfg = self.cfg
@@ -227,7 +243,7 @@ class W8A8Stack:
             q, s = rms_norm_quant(h, L.input_norm, cfg.eps, offset=0.0)
             qkv = L.qkv.forward_quantized(q, s)
             qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
-            a = self._attention(qkv, B, S, past, keep)
+            a = self._attention(qkv, B, S, past, keep, pos)
             if keep:
                 a, state = a
             r = aot.act_quant(a)
@@ -287,8 +303,9 @@ class W8A8Stack:
         every request continues it: its tokens are positions prefix.length + 0 .. S - 1."""
         S = ids.numel() // batch
         h = self.embed.index_select(0, ids)
+        pos = None if prefix is None else prefix.positions_for(batch, S, ids.device)
         for i, L in enumerate(self.layers):
-            h = self.layer_forward(L, h, batch, S, trace, past=None if prefix is None else prefix.layers[i])
+            h = self.layer_forward(L, h, batch, S, trace, past=None if prefix is None else prefix.layers[i], pos=pos)
         logits, probs = self.readout(h, rows, self.final_norm, self.cfg.eps, offset=0.0, lo=lo, cnt=cnt,
                                      probs_width=self.cfg.n_options)
         if trace is not None:

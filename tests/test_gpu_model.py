@@ -85,7 +85,7 @@ def test_small_stack_stage_by_stage(gpu):
         assert np.array_equal(bits(t["qkv"]), qkv), f"layer {li}: qkv"
         # in-place RoPE on the q and k heads: bit-exact bf16 arithmetic
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
-        cos, sin = st._rope[S]
+        cos, sin = st._tables(S, st.device)
         pos = np.arange(B * S) % S
         xr = qkv.reshape(B * S, hq + 2 * hk, d)
         want = xr.copy()
