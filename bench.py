@@ -153,7 +153,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the hot path is a single-GPU "
-              f"kernel set; see DESIGN.md for how it would shard)", file=sys.stderr)
+              f"kernel set; requests shard across GPUs as independent processes)", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -7,7 +7,7 @@ plus the fused RMSNorm + INT8 quantizer of the W8A8 hot path, on the gfx950 HIP 
   rms_norm_quant_multi(x, weight, eps, inv_smooths)  new: one norm, quantized for up to 4 consumers
   rope_inplace(rows, n_heads, head_dim, cos, sin, period)  new: bf16 RoPE on QKV output rows, in place
 
-The reference runs Triton here on a GPU and torch formulas on the CPU; this build has no CPU compute
+The reference runs Triton here on a GPU and torch formulas on the CPU; mica_amd has no CPU compute
 path: a CPU tensor raises ValueError (the reference raises ValueError for unsupported layouts, :57-58).
 """
 from __future__ import annotations

@@ -15,8 +15,9 @@ Extensions used by the fused hot path: ``rounding='away'`` (the Triton kernel's 
 kernel_src/kernels.py:35), ``mm_i8(..., residual=, epilogue='silu_mul')``, ``mm_i8_int32`` (raw
 accumulators), and ``STRICT`` (env ``MICA_AMD_STRICT=1``) which turns a miss into an exception.
 
-Attention stays a torch op in this build: ``attn_fwd`` always misses with reason ``attn_unsupported``,
-exactly like the reference on a device whose container has no attention kernel.
+Attention: ``ATTN`` / ``attn_keys()`` / ``attn_fwd(q, k, v, scale)`` (:409-481) run the gfx950 flash-attention
+kernel for head dim 256 with 4 query heads per key/value head (key ``attn|bf16|hd256|hq16|r4|s0.0625|m64``);
+any other shape misses, as the reference does for a shape its container has no kernel for.
 """
 from __future__ import annotations
 

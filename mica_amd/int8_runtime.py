@@ -388,7 +388,7 @@ def _row_rel(a, b):
 
 
 def selftest(shapes, device, rows=SELFTEST_ROWS, seed=SELFTEST_SEED):
-    """The reference's acceptance test (int8_runtime.py:362-443), on this build's kernels.
+    """The reference's acceptance test (int8_runtime.py:362-443), on mica_amd's kernels.
 
     For every (N, K, has_bias) and every row count, with and without SmoothQuant factors: QLinear(x)
     must take exactly 2 kernel launches, be finite, and its row-relative L2 error against the fp32

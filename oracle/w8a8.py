@@ -176,7 +176,7 @@ def pack_gate_up(qg, sg, qu, su, group: int = 64):
     """Interleave gate and up weight rows in groups: [g0..g63, u0..u63, g64..g127, u64..u127, ...].
 
     Layout contract of the fused gate+up GEMM's SILU_MUL epilogue (the reference keeps separate
-    gate/up QLinears, fast_runtime.py:126-132; the fusion is this build's).
+    gate/up QLinears, fast_runtime.py:126-132; the fused GEMM is mica_amd's).
     """
     n, k = qg.shape
     assert n % group == 0 and qu.shape == qg.shape
