@@ -440,12 +440,26 @@ def hybrid_prefill(torch, dev, reps=3):
     ms = s.elapsed_time(e) / reps
     ops = st.linear_ops_per_token() * B * S
     ok = bool(torch.isfinite(probs).all()) and bool(torch.allclose(probs.sum(1), torch.ones(B, device=dev)))
+    # single requests (the GDN scan then has one workgroup per value head: 32)
+    single = {}
+    g = torch.Generator().manual_seed(6)
+    for S1 in (512, 4096):
+        ids1 = torch.randint(0, st.cfg.vocab, (S1,), generator=g).to(dev)
+        st.prefill(ids1, 1)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(reps):
+            st.prefill(ids1, 1)
+        e.record()
+        torch.cuda.synchronize()
+        ms1 = s.elapsed_time(e) / reps
+        single[f"B1_S{S1}"] = {"ms": round(ms1, 2), "tokens_per_s": round(S1 / (ms1 * 1e-3), 1)}
     del st
     torch.cuda.empty_cache()
     return {"workload": "32 layers (24 gated-delta-net + 8 full attention), hidden 2560, inter 9728; "
                         "8 requests x 2048 tokens packed; last-position readout over 255 option ids + softmax",
             "ms_per_prefill": round(ms, 2), "tokens_per_s": round(B * S / (ms * 1e-3), 1),
-            "w8a8_linear_TOP": round(ops / 1e12, 2), "probs_valid": ok, "reps": reps}
+            "w8a8_linear_TOP": round(ops / 1e12, 2), "probs_valid": ok, "reps": reps, "single_request": single}
 
 
 def engine_latency(torch, dev, st, reps=5):
