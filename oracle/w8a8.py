@@ -78,6 +78,18 @@ def quant_weight(w: np.ndarray):
     return q, s.astype(np.float32)
 
 
+def smooth_factors(act_amax: np.ndarray, w: np.ndarray, alpha: float = 0.5, lo: float = 1e-4, hi: float = 1e4):
+    """SmoothQuant factors per input channel, int8_quant.smooth_factors (int8_quant.py:80-85):
+    s = max(a, 1e-8)^alpha / max(wmax, 1e-8)^(1 - alpha) with wmax the column absmax of w [N, K];
+    1 where a or wmax is 0; clamped to [lo, hi].  fp32 throughout (pow as fp32 powf)."""
+    a = np.asarray(act_amax, np.float32)
+    wmax = np.abs(np.asarray(w, np.float32)).max(axis=0)
+    num = np.power(np.maximum(a, EPS), np.float32(alpha), dtype=np.float32)
+    den = np.power(np.maximum(wmax, EPS), np.float32(1.0 - alpha), dtype=np.float32)
+    s = np.where((a > 0) & (wmax > 0), (num / den).astype(np.float32), np.float32(1.0))
+    return np.clip(s, np.float32(lo), np.float32(hi)).astype(np.float32)
+
+
 # ---------------------------------------------------------------- GEMM
 def int_gemm(qa: np.ndarray, qw: np.ndarray) -> np.ndarray:
     """acc[m, n] = sum_k qa[m, k] * qw[n, k], exact int32 (int8_quant.int_gemm_exact, int8_quant.py:88-89).

@@ -108,6 +108,30 @@ def quant_cases():
     return out
 
 
+def weight_cases():
+    """quant_weight known answers (int8_quant.py:54-61): a weight matrix [N, K] quantized per output row,
+    i.e. quant_row applied to every row with half-even rounding.  The matrices are fp32 (offline weights
+    are fp32 after smoothing): exact .5 ties at s = 1 and s = 1/2, an all-zero row (s = 1e-8 / 127), a
+    single-element row, rows below the 1e-8 floor, a row of one repeated value (q = +-127 everywhere)."""
+    mats = [
+        [[127.0, 0.5, -0.5, 1.5, 2.5, -2.5, 126.5, -126.5],
+         [63.5, 0.25, -0.25, 0.75, 1.25, -1.25, 62.75, -0.0],
+         [0.0] * 8,
+         [1e-9, -3e-9, 5e-9, 0.0, 2e-10, -7e-9, 4e-9, 1e-9],
+         [-2.0] * 8],
+        [[5.0], [-0.0], [1e-12]],
+    ]
+    rnd = random.Random(20261202)
+    mats.append([[r32(rnd.gauss(0.0, 0.05)) for _ in range(24)] for _ in range(6)])
+    out = []
+    for w in mats:
+        w = [[r32(v) for v in row] for row in w]
+        qs = [quant_row(row, None, "even") for row in w]
+        out.append({"w_f32_bits": [[f32_bits(v) for v in row] for row in w], "q": [q for q, _ in qs],
+                    "s_bits": [f32_bits(s) for _, s in qs]})
+    return out
+
+
 def gemm_cases():
     rnd = random.Random(7)
     out = []
@@ -238,6 +262,7 @@ def main():
     data = {
         "note": "known answers for the W8A8 hot path; generated by tests/golden/make_golden.py",
         "quant": quant_cases(),
+        "quant_weight": weight_cases(),
         "gemm": gemm_cases(),
         "rms_norm": norm_cases(),
         "silu_mul": silu_cases(),

@@ -140,6 +140,8 @@ def test_rmsnorm_quant_config1(gpu, T, offset):
     same = np.all(yk == yo, axis=1)
     qe, se = O.quant_act(O.bf16_to_f32(yo))
     assert np.array_equal(q.cpu().numpy()[same], qe[same])
+    note(f"rmsnorm_quant T={T} offset={offset}: {same.mean():.5f} of rows equal the oracle's bf16 row, "
+         f"{np.mean(yk == yo):.7f} of elements")
     assert same.mean() > 0.95
 
 
@@ -431,6 +433,77 @@ def test_qlinear_config0_end_to_end(gpu):
     outs = lin.rows_forward(to_gpu_bf16(xb[:64]), [(0, 2048), (2048, 4096), (4096, 9728)])
     ref = O.qlinear(xb[:64], qw, sw)
     assert np.array_equal(np.concatenate([bits_of(o) for o in outs], 1), ref)
+
+
+def test_smoothed_qlinear_from_bf16_linear_on_device(gpu):
+    """A QLinear converted on the GPU from a random bf16 nn.Linear with SmoothQuant factors from synthetic
+    activation absmax (int8_runtime.py:108-127, int8_quant.py:54-61, 80-85): its int8 weights, scales and
+    inverse factors equal the oracle's weight quantizer on the smoothed fp32 weight, bit for bit, and
+    its forward equals oracle.qlinear with those buffers (quantize with inv_smooth, exact GEMM, epilogue
+    with bias)."""
+    note("smoothed qlinear convert")
+    torch.manual_seed(12)
+    N, K = 1024, 2560
+    lin = torch.nn.Linear(K, N, bias=True).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.mul_(20.0)
+    rng = np.random.default_rng(12)
+    amax = rng.uniform(0.05, 4.0, K).astype(np.float32)
+    amax[::61] *= 25.0
+    smooth = int8_runtime.smooth_factors(torch.from_numpy(amax), lin.weight.detach())     # on the CPU, once
+    q = int8_runtime.QLinear(lin.cuda(), smooth)
+    torch.cuda.synchronize()
+    s = smooth.numpy()
+    wf = lin.weight.detach().float().cpu().numpy() * s[None, :]
+    qo, so = O.quant_weight(wf)
+    inv = (np.float32(1) / s).astype(np.float32)
+    assert_equal_diag(q.qweight.cpu().numpy(), qo, "qweight")
+    assert_equal_diag(q.wscale.cpu().numpy().view(np.uint32), so.view(np.uint32), "wscale")
+    assert_equal_diag(q.inv_smooth.cpu().numpy().view(np.uint32), inv.view(np.uint32), "inv_smooth")
+    x = rng.standard_normal((300, K)).astype(np.float32) * (amax / 3)[None, :]
+    xb = O.f32_to_bf16(x)
+    bias = lin.bias.detach().float().cpu().numpy()
+    y = q(to_gpu_bf16(xb))
+    assert_equal_diag(bits_of(y), O.qlinear(xb, qo, so, bias=bias, inv_smooth=inv), "forward")
+
+
+def test_convert_body_on_device(gpu, tmp_path):
+    """int8_runtime.convert over a small body on the GPU with statistics read from a packed s.pt-layout
+    file: every target linear becomes a QLinear; smoothed exactly where the file has its absmax; each
+    one's forward equals the oracle's on its own buffers."""
+    note("convert body")
+    from torch import nn
+    torch.manual_seed(3)
+    H = 256
+    body = nn.Module()
+    body.layers = nn.ModuleList()
+    for i in range(2):
+        layer = nn.Module()
+        layer.mlp = nn.Module()
+        layer.mlp.gate_proj, layer.mlp.up_proj = nn.Linear(H, 512), nn.Linear(H, 512)
+        layer.mlp.down_proj = nn.Linear(512, H, bias=False)
+        body.layers.append(layer)
+    body = body.to(torch.bfloat16).cuda()
+    names = [n for n, *_ in int8_runtime.target_linears(body)]
+    rng = np.random.default_rng(3)
+    have = names[::2]
+    lens = [512 if n.endswith("down_proj") else H for n in have]
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    torch.save({"h": torch.tensor([int8_runtime.name_key(n) for n in have], dtype=torch.int64),
+                "o": torch.from_numpy(offs), "v": torch.from_numpy(rng.uniform(0.1, 20, offs[-1]).astype(np.float32))},
+               tmp_path / "s.pt")
+    stats = int8_runtime.load_stats(tmp_path / "s.pt")
+    assert int8_runtime.convert(body, stats) == (len(names), len(have))
+    for name, _, _, _ in [(n, None, None, None) for n in names]:
+        mod = body
+        for part in name.split("."):
+            mod = mod[int(part)] if part.isdigit() else getattr(mod, part)
+        assert isinstance(mod, int8_runtime.QLinear) and (mod.inv_smooth is not None) == (name in have), name
+        x = O.f32_to_bf16(rng.standard_normal((40, mod.in_features)).astype(np.float32) * 3)
+        inv = None if mod.inv_smooth is None else mod.inv_smooth.cpu().numpy()
+        bias = None if mod.bias is None else mod.bias.cpu().numpy()
+        ref = O.qlinear(x, mod.qweight.cpu().numpy(), mod.wscale.cpu().numpy(), bias=bias, inv_smooth=inv)
+        assert_equal_diag(bits_of(mod(to_gpu_bf16(x))), ref, name)
 
 
 def test_qlinear_reference_selftest(gpu):

@@ -46,6 +46,19 @@ def test_kat_quant(kat):
             assert s.view(np.uint32)[0] == case["s_bits"]
 
 
+def test_kat_quant_weight(kat):
+    """quant_weight (int8_quant.py:54-61) against pure-Python known answers: ties at s = 1 and 1/2, an
+    all-zero row, rows under the 1e-8 floor, single-element rows, a constant row; and row for row the
+    same bits as the activation quantizer applied to the weight's rows (the same formula per row)."""
+    for case in kat["quant_weight"]:
+        w = np.array(case["w_f32_bits"], np.uint32).view(np.float32)
+        q, s = O.quant_weight(w)
+        assert q.tolist() == case["q"], case
+        assert s.view(np.uint32).tolist() == case["s_bits"], case
+        qa, sa = O.quant_act(w)
+        assert np.array_equal(q, qa) and np.array_equal(s.view(np.uint32), sa.view(np.uint32))
+
+
 def test_kat_gemm(kat):
     for case in kat["gemm"]:
         A = np.array(case["A"], np.int8)
@@ -226,7 +239,20 @@ def _wrong_epilogue_order(acc, sa, sb, bias=None):
     return O.f32_to_bf16(y if bias is None else y + bias[None, :])
 
 
-_QUANT_ACT, _RMS_NORM = O.quant_act, O.rms_norm  # the originals, for the planted variants
+_QUANT_ACT, _RMS_NORM, _QUANT_WEIGHT = O.quant_act, O.rms_norm, O.quant_weight  # originals, for planting
+
+
+def _wrong_weight_round_away(w):
+    return _QUANT_ACT(np.asarray(w, np.float32), None, "away")
+
+
+def _wrong_weight_no_eps_floor(w):
+    return _wrong_no_eps_floor(w)
+
+
+def _wrong_weight_per_column(w):
+    q, s = _QUANT_WEIGHT(np.asarray(w, np.float32).T)
+    return q.T, s
 
 
 def _wrong_round_away(x, inv=None, rounding="even"):
@@ -260,7 +286,7 @@ def _wrong_norm_fused_scale(x_bits, w, eps, offset=1.0, residual_bits=None):
 def _kat_failures(kat, monkey):
     """Run the KAT checks with one oracle function replaced; return the number of failing checks."""
     fails = 0
-    for check in (test_kat_quant, test_kat_gemm, test_kat_rms_norm):
+    for check in (test_kat_quant, test_kat_quant_weight, test_kat_gemm, test_kat_rms_norm):
         with monkey.context() as mp:
             for name, fn in monkey._plant.items():
                 mp.setattr(O, name, fn)
@@ -278,6 +304,9 @@ def _kat_failures(kat, monkey):
     ("int_gemm", _wrong_transposed_gemm),
     ("rms_norm", _wrong_norm_no_offset),
     ("rms_norm", _wrong_norm_fused_scale),
+    ("quant_weight", _wrong_weight_round_away),
+    ("quant_weight", _wrong_weight_no_eps_floor),
+    ("quant_weight", _wrong_weight_per_column),
 ])
 def test_planted_mistakes_are_caught(kat, monkeypatch, name, fn):
     monkeypatch._plant = {name: fn}
