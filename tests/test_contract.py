@@ -129,6 +129,35 @@ def test_escape_and_positional_ids():
     assert "A) first\nB) second\nC) [open_door] third\n    why\n" in p
 
 
+def test_every_reference_control_token_is_escaped_as_the_reference_does():
+    """Each control token of the reference's prompt builder (tests/golden/control_tokens.json, taken from
+    its _SPECIAL_TEXT pattern) is broken by a zero-width space after its first character, alone and
+    inside text, and nothing else changes."""
+    tokens = json.loads((Path(__file__).parent / "golden" / "control_tokens.json").read_text())
+    assert len(tokens) == 33
+    for t in tokens:
+        want = t[0] + "\u200b" + t[1:]
+        assert C.escape_special(t) == want, t
+        assert C.escape_special(f"x {t}y{t}") == f"x {want}y{want}", t
+    assert C.escape_special("<b> <|im_star|> plain") == "<b> <|im_star|> plain"
+
+
+def test_register_special_tokens_extends_the_escape_set():
+    """A tokenizer's added and special tokens join the escaped set (lib/contract.py:280-297): tokens of
+    at least two characters that are not blank; single characters and whitespace are left alone."""
+    class Tok:
+        content = "[[SPECIAL_X]]"
+
+    class FakeTokenizer:
+        added_tokens_decoder = {1: Tok(), 2: "<extra_7>", 3: " ", 4: "Z"}
+        all_special_tokens = ["<|im_end|>", "@@sep@@"]
+
+    assert C.escape_special("[[SPECIAL_X]] <extra_7> @@sep@@") == "[[SPECIAL_X]] <extra_7> @@sep@@"
+    C.register_special_tokens(FakeTokenizer())
+    out = C.escape_special("[[SPECIAL_X]] <extra_7> @@sep@@ Z a b")
+    assert out == "[\u200b[SPECIAL_X]] <\u200bextra_7> @\u200b@sep@@ Z a b"
+
+
 def test_input_tokens():
     assert C.input_tokens([[1, 2, 3, 4], [1, 2, 5]]) == 7 - 2
     assert C.input_tokens([[7, 8]]) == 2 and C.input_tokens([]) == 0
