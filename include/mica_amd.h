@@ -208,7 +208,8 @@ long long mica_attention_workspace_bytes(int B, int Sk, int HK);
  * x, y: bf16 [B][T][C] with batch stride sbx / sby and token stride ldx / ldy (elements);
  * w: [C][width] of w_dtype (bf16 / fp32), bias: [C] of w_dtype or NULL; width <= 4.
  * init_state / final_state: bf16 [B][C][width - 1] (the inputs before t = 0 / the last width - 1
- * inputs, with history when T < width - 1), each optional.  C % 8 == 0, strides % 8 == 0.
+ * inputs, with history when T < width - 1), each optional; with T == 0 final_state receives
+ * init_state (zeros without one).  C % 8 == 0, strides % 8 == 0.
  */
 int mica_causal_conv1d(const void *x, long long sbx, int ldx, const void *w, const void *bias, int w_dtype, int width,
                        const void *init_state, void *final_state, void *y, long long sby, int ldy, int B, int T, int C,

@@ -754,6 +754,12 @@ __global__ void state_fill_kernel(const float *src, float *dst, long n) {
     if (i < n) dst[i] = src ? src[i] : 0.0f;
 }
 
+// the same for the conv's bf16 state: an empty sequence leaves the initial state (or zeros) unchanged
+__global__ void state_fill16_kernel(const uint16_t *src, uint16_t *dst, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src ? src[i] : (uint16_t)0;
+}
+
 long long gdn_ws_bytes(long long B, long long T, long long HV) {
     const long long NT = (T + kC - 1) / kC;
     return B * HV * NT * (2LL * kC * kDk * 2 + kC * 4);
@@ -766,7 +772,7 @@ extern "C" int mica_causal_conv1d(const void *x, long long sbx, int ldx, const v
                                   int w_dtype, int width, const void *init_state, void *final_state, void *y,
                                   long long sby, int ldy, int B, int T, int C, int silu, int n_norm, float eps,
                                   mica_stream_t stream) {
-    if (x == nullptr || w == nullptr || y == nullptr) return MICA_MISS_ARG;
+    if (w == nullptr || (T > 0 && (x == nullptr || y == nullptr))) return MICA_MISS_ARG;
     if (w_dtype != MICA_BF16 && w_dtype != MICA_FP32) return MICA_MISS_DTYPE;
     if (width < 1 || width > 4 || B < 0 || T < 0 || C <= 0 || C % 8 != 0 || n_norm < 0 || n_norm * 128 > C)
         return MICA_MISS_SHAPE;
@@ -774,7 +780,15 @@ extern "C" int mica_causal_conv1d(const void *x, long long sbx, int ldx, const v
         sbx % 8 != 0 || sby % 8 != 0)
         return MICA_MISS_STRIDE;
     if (!mica_aligned16(x) || !mica_aligned16(y)) return MICA_MISS_ALIGN;
-    if (B == 0 || T == 0) return 0;
+    if (B == 0) return 0;
+    if (T == 0) {
+        // no tokens: the final state is the initial one (zeros without one), as after the scan
+        if (final_state == nullptr || width == 1) return 0;
+        const long n = (long)B * C * (width - 1);
+        hipLaunchKernelGGL(state_fill16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t *)init_state, (uint16_t *)final_state, n);
+        return mica_err(hipGetLastError());
+    }
     ConvParams p{};
     p.x = (const uint16_t *)x; p.sbx = sbx; p.ldx = ldx;
     p.w = w; p.bias = bias; p.w_dtype = w_dtype; p.width = width;

@@ -139,11 +139,18 @@ _WS_LOCK = threading.Lock()
 def gemm_workspace(dev):
     """The GEMM's split-tile workspace for torch's current stream on ``dev``: allocated (zeroed) once
     per (device, stream) and kept for the life of the process, so a HIP graph that captured it
-    stays valid; every launch leaves its counters zero again.  Returns (pointer, bytes)."""
+    stays valid; every launch leaves its counters zero again.  Returns (pointer, bytes).  It cannot
+    be first allocated inside a HIP-graph capture (RuntimeError): allocate it on the stream before."""
     stream = torch.cuda.current_stream(dev)
     key = (dev.index, stream.cuda_stream)
     ws = _WORKSPACE.get(key)
     if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            # a buffer made during capture comes from the graph's pool and its zero fill is only
+            # recorded, not run: its arrival counters would hold garbage for other users of the key
+            raise RuntimeError("the GEMM split workspace must be allocated before HIP-graph capture: call "
+                               "int8_kernels.gemm_workspace(device) on the capturing stream first, or use "
+                               "split=False")
         with _WS_LOCK:
             ws = _WORKSPACE.get(key)
             if ws is None:

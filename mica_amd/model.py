@@ -6,8 +6,11 @@ Shape (the benchmark's synthetic 4B configuration): 36 layers, hidden 2560, MLP 
 weights.  With ``full_attention_interval = k > 0`` the stack is the hybrid layout of the reference's
 model instead (Qwen3.5: three gated-delta-net layers, then one full-attention layer, repeated).
 
-Per full-attention layer (the call pattern of the reference's fork.layer_step,
-v0.5/serving/lib/fork.py:394-422):
+The stack is a synthetic workload with the benchmark's shapes, not the reference model's computation:
+its full-attention layers have no q_proj output gate (o * sigmoid(gate)) and no per-head q / k
+RMSNorm, both of which the reference model's attention layers apply (fast_runtime.py:229-241), and all
+weights are random.  Per full-attention layer (the call pattern of the reference's fork.layer_step,
+v0.5/serving/lib/fork.py:394-422, without those two ops):
   q, s   = rms_norm_quant(h, input_norm)                     1 launch
   qkv    = QKV W8A8 GEMM                                     1 launch
   a      = causal GQA attention per request: RoPE in place on the q / k heads, then the
@@ -143,16 +146,19 @@ class PrefixState:
 
     def __init__(self, length: int, layers: list):
         self.length, self.layers = int(length), layers
-        self.positions = {}   # (batch, S) -> int32 [batch * S] RoPE positions of a continuation
+        self.positions = {}   # (batch, S) -> int32 [batch * S] RoPE positions of a captured continuation
 
     def positions_for(self, batch: int, S: int, device):
-        """RoPE positions length + (t % S) of a packed continuation batch, made once per shape and kept
-        with the prefix (a graph that continues the prefix reads them on every replay)."""
+        """RoPE positions length + (t % S) of a packed continuation batch.  Made during a HIP-graph
+        capture, they are kept with the prefix (the graph reads them on every replay), so the kept set
+        is bounded by the captured shapes; an eager run makes them for that call only."""
         key = (batch, S)
-        if key not in self.positions:
-            self.positions[key] = (torch.arange(batch * S, device=device, dtype=torch.int32) % S
-                                   + self.length).contiguous()
-        return self.positions[key]
+        if key in self.positions:
+            return self.positions[key]
+        pos = (torch.arange(batch * S, device=device, dtype=torch.int32) % S + self.length).contiguous()
+        if torch.device(device).type == "cuda" and torch.cuda.is_current_stream_capturing():
+            self.positions[key] = pos
+        return pos
 
 
 class W8A8Stack:

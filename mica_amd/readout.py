@@ -50,9 +50,16 @@ class LabelReadout:
         L = self.n_labels
         logits = torch.empty((B, L), dtype=torch.float32, device=dev)
         if lo is not None:
+            if probs_width is None:
+                # the width is read from host values only: a device tensor would need a synchronising
+                # read, which stalls the stream and cannot be captured in a HIP graph
+                if isinstance(cnt, torch.Tensor) and cnt.is_cuda:
+                    raise ValueError("give probs_width when cnt is a device tensor")
+                host = torch.as_tensor(cnt, dtype=torch.int64)
+                probs_width = int(host.max()) if host.numel() else 0
             lo = torch.as_tensor(lo, device=dev).to(torch.int32).contiguous()
             cnt = torch.as_tensor(cnt, device=dev).to(torch.int32).contiguous()
-            width = probs_width or int(cnt.max().item()) if B else 0
+            width = probs_width if B else 0
         else:
             width = L
         probs = torch.zeros((B, max(width, 1)), dtype=torch.float32, device=dev)
@@ -87,6 +94,7 @@ def gather_logits(h, last_idx, norm_w, eps, label_W, n_opts, offset=1.0):
     if len(ns) != B or any(n < 0 or n > ro.n_labels - 2 for n in ns):
         raise ValueError("n_opts must give 0 (No / Yes) or 1 .. L - 2 options for every request")
     lo = torch.tensor([0 if n == 0 else 2 for n in ns], dtype=torch.int32)
-    cnt = torch.tensor([2 if n == 0 else n for n in ns], dtype=torch.int32)
-    _, probs = ro(h, last_idx, norm_w, eps, offset, lo=lo, cnt=cnt)
+    cnt = [2 if n == 0 else n for n in ns]
+    _, probs = ro(h, last_idx, norm_w, eps, offset, lo=lo, cnt=torch.tensor(cnt, dtype=torch.int32),
+                  probs_width=max(cnt) if cnt else 0)
     return probs

@@ -14,6 +14,8 @@ Size-independent checks at the benchmark shape (8 x 2048 tokens, 16 key / 32 val
 split at a chunk boundary and continued from the returned state is bit-identical to the unsplit scan;
 one (sequence, head) pair is checked against the oracle.
 """
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -34,6 +36,25 @@ def _f64(t):
 
 def _rel(a, b):
     return np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+
+
+def test_causal_conv1d_empty_sequence_keeps_the_state(gpu):
+    """T = 0: no output rows, and the final state is the initial one (zeros without one), as the
+    scan's final state is for an empty input."""
+    from mica_amd import gdn
+    print("[case] conv T=0", file=sys.stderr, flush=True)
+    B, C = 2, 256
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn(C, 4, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    h0 = torch.randn(B, C, 3, generator=g).to(torch.bfloat16).to(gpu)
+    x = torch.empty(B, 0, C, dtype=torch.bfloat16, device=gpu).transpose(1, 2)
+    for init in (h0, None):
+        stale = torch.full((B, C, 3), 7.0, dtype=torch.bfloat16, device=gpu)
+        y, fin = gdn.causal_conv1d_fn(x, w, initial_states=init, return_final_states=True,
+                                      final_states_out=stale, activation="silu")
+        torch.cuda.synchronize()
+        assert y.shape == (B, C, 0)
+        assert torch.equal(fin, h0 if init is not None else torch.zeros_like(h0))
 
 
 @pytest.mark.parametrize("B,T,C,n_norm,init,bias", [(2, 37, 1024, 4, True, True), (1, 5, 8192, 32, False, False),

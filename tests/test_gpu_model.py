@@ -151,3 +151,94 @@ def test_hybrid_stack_gdn_and_attention_layers(gpu):
     attn_ops = (4 + 2) * 256 * H + H * 4 * 256
     assert st.linear_ops_per_token() == 2 * (2 * gdn_ops + 2 * attn_ops + 4 * 3 * 1024 * H)
     assert not int8_kernels.STATS["fallback"]
+
+
+def test_config4_full_stack_8x2048(gpu):
+    """Config 4 at its size: the 36-layer 4B-shaped stack (hidden 2560, intermediate 9728, QKV 6144,
+    vocab 151936) over 8 requests x 2048 packed tokens (M = 16384), logits only at each request's last
+    position over 2 + 255 label ids, softmaxed.  The probabilities are finite and sum to one; a second
+    run traced at the last layer gives the same bits; that layer's norm + quant, QKV, RoPE, O + residual,
+    SiLU epilogue, requant and down + residual are recomputed by the oracle on 64 sampled rows from the
+    kernels' own inputs to each stage, and the readout of the 8 last rows on all of them
+    (release_runtime.py:298-306, 509-517; prefill_engine.py:283-339)."""
+    print("[case] config 4: 36 layers, 8 x 2048 tokens", file=sys.stderr, flush=True)
+    cfg = StackConfig()
+    assert (cfg.layers, cfg.hidden, cfg.intermediate, cfg.vocab) == (36, 2560, 9728, 151936)
+    st = W8A8Stack(cfg, device=gpu, seed=4)
+    B, S = 8, 2048
+    ids = torch.randint(0, cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(44)).to(gpu)
+    logits, probs = st.prefill(ids, B)
+    torch.cuda.synchronize()
+    p = probs.cpu().numpy()
+    assert p.shape == (B, cfg.n_options)
+    assert np.isfinite(p).all() and np.allclose(p.sum(1), 1.0, atol=1e-5)
+
+    # the same run with the last layer traced (the trace only keeps tensors the run makes anyway)
+    rows_last = torch.arange(B, device=gpu, dtype=torch.int32) * S + (S - 1)
+    lo, cnt = st.slices(None, None, B, gpu)
+    h = st.embed.index_select(0, ids)
+    trace = []
+    for i, L in enumerate(st.layers):
+        h = st.layer_forward(L, h, B, S, trace if i == cfg.layers - 1 else None)
+    logits2, probs2 = st.readout(h, rows_last, st.final_norm, cfg.eps, offset=0.0, lo=lo, cnt=cnt,
+                                 probs_width=cfg.n_options)
+    torch.cuda.synchronize()
+    assert torch.equal(logits2, logits) and torch.equal(probs2, probs), "traced run differs from prefill"
+
+    L, t = st.layers[-1], trace[0]
+    rng = np.random.default_rng(4)
+    rows = np.unique(np.concatenate([rng.choice(B * S, 60, replace=False), [0, S - 1, S, B * S - 1]]))
+    trows = torch.from_numpy(rows).to(gpu)
+    sel = lambda x: x.index_select(0, trows)  # noqa: E731
+    hb = bits(sel(t["h"]))
+    # input norm + quant (the normed bf16 row may differ by one ulp: rows that agree quantize exactly)
+    yo, _ = O.rms_norm(hb, O.bf16_to_f32(bits(L.input_norm)), cfg.eps, 0.0)
+    qo, so = O.quant_act(O.bf16_to_f32(yo))
+    q, s = sel(t["q"]).cpu().numpy(), sel(t["s"]).cpu().numpy()
+    same = np.all(q == qo, axis=1) & (s == so)
+    print(f"[case] config 4 input norm+quant rows matching the oracle: {same.mean():.4f}", file=sys.stderr)
+    assert same.mean() >= 0.95
+    # QKV from the kernel's q, s: bit-exact
+    qkv = O.epilogue(O.int_gemm(q, L.qkv.qweight.cpu().numpy()), s, L.qkv.wscale.cpu().numpy())
+    assert np.array_equal(bits(sel(t["qkv"])), qkv), "qkv"
+    # RoPE in place on the q and k heads of those rows (positions t % S)
+    hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+    cos, sin = st._tables(S, gpu)
+    pos = rows % S
+    xr = qkv.reshape(rows.size, hq + 2 * hk, d)
+    want = xr.copy()
+    want[:, :hq + hk] = O.rope(xr[:, :hq + hk], bits(cos)[pos][:, None, :], bits(sin)[pos][:, None, :])
+    assert np.array_equal(bits(sel(t["qkv_rope"])), want.reshape(rows.size, -1)), "rope"
+    # O projection + residual from the kernel's attention output
+    qa, sa = O.quant_act(O.bf16_to_f32(bits(sel(t["a"]))))
+    assert np.array_equal(sel(t["qa"]).cpu().numpy(), qa) and np.array_equal(sel(t["sa"]).cpu().numpy(), sa)
+    h1 = O.epilogue(O.int_gemm(qa, L.o.qweight.cpu().numpy()), sa, L.o.wscale.cpu().numpy())
+    h1 = O.f32_to_bf16(O.bf16_to_f32(h1) + O.bf16_to_f32(hb))
+    assert np.array_equal(bits(sel(t["h1"])), h1), "o_proj + residual"
+    # post-attention norm + quant, SiLU epilogue, requant, down + residual
+    y2, _ = O.rms_norm(h1, O.bf16_to_f32(bits(L.post_norm)), cfg.eps, 0.0)
+    q2o, s2o = O.quant_act(O.bf16_to_f32(y2))
+    q2, s2 = sel(t["q2"]).cpu().numpy(), sel(t["s2"]).cpu().numpy()
+    same2 = np.all(q2 == q2o, axis=1) & (s2 == s2o)
+    print(f"[case] config 4 post norm+quant rows matching the oracle: {same2.mean():.4f}", file=sys.stderr)
+    assert same2.mean() >= 0.95
+    qp, sp = L.gate_up.qweight.cpu().numpy(), L.gate_up.wscale.cpu().numpy()
+    n = qp.shape[0] // 2
+    grp, sgr = qp.reshape(n // 64, 2, 64, -1), sp.reshape(n // 64, 2, 64)
+    gv = O.epilogue(O.int_gemm(q2, grp[:, 0].reshape(n, -1)), s2, sgr[:, 0].reshape(n))
+    uv = O.epilogue(O.int_gemm(q2, grp[:, 1].reshape(n, -1)), s2, sgr[:, 1].reshape(n))
+    g = bits(sel(t["g"]))
+    within_one_ulp(g, O.silu_mul(gv, uv))
+    qho, sho = O.quant_act(O.bf16_to_f32(g))
+    assert np.array_equal(sel(t["qh"]).cpu().numpy(), qho) and np.array_equal(sel(t["sh"]).cpu().numpy(), sho)
+    h2 = O.epilogue(O.int_gemm(qho, L.down.qweight.cpu().numpy()), sho, L.down.wscale.cpu().numpy())
+    h2 = O.f32_to_bf16(O.bf16_to_f32(h2) + O.bf16_to_f32(h1))
+    assert np.array_equal(bits(sel(t["h2"])), h2), "down + residual"
+    # readout of the 8 last rows over all 257 label rows, then the option softmax
+    last = rows_last.cpu().numpy()
+    W = st.readout.weight.cpu().numpy()
+    zo = O.readout(bits(h), last, O.bf16_to_f32(bits(st.final_norm)), cfg.eps, W, offset=0.0)
+    np.testing.assert_allclose(logits.cpu().numpy(), zo, rtol=1e-4, atol=1e-4)
+    for b in range(B):
+        np.testing.assert_allclose(p[b], O.option_probs(zo[b], "choice", cfg.n_options), atol=1e-3)
+    assert not int8_kernels.STATS["fallback"]

@@ -29,10 +29,15 @@ def test_rope_table_grows_by_doubling_and_keeps_rows():
     assert st._rope[0].shape[0] == 40000 and len(st._retired) == 3
 
 
-def test_prefix_positions_are_kept_per_shape():
+def test_prefix_positions_are_not_kept_for_eager_runs():
+    """Positions of an eager continuation are made per call: serving many request lengths eagerly does
+    not grow the prefix's memory (only shapes captured in a HIP graph are kept)."""
     pre = PrefixState(128, [])
     p = pre.positions_for(3, 64, "cpu")
     assert p.dtype == torch.int32 and p.numel() == 3 * 64
     assert torch.equal(p.view(3, 64), (torch.arange(64) + 128).int().expand(3, 64))
-    assert pre.positions_for(3, 64, "cpu") is p               # one tensor per shape, kept with the prefix
-    assert pre.positions_for(2, 64, "cpu") is not p
+    for S in range(1, 300):
+        pre.positions_for(2, S, "cpu")
+    assert pre.positions == {}
+    pre.positions[(3, 64)] = p                                 # a captured shape: served from the cache
+    assert pre.positions_for(3, 64, "cpu") is p
