@@ -103,33 +103,115 @@ def synthetic(torch, dev, M, K, N, seed):
     return x.to(torch.bfloat16).to(dev), qw.to(dev), sw.to(dev)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_time(fn, budget_s, min_reps=3, max_reps=30):
+    """Median wall time of fn after one warm-up, over at least min_reps runs or budget_s seconds."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline(torch, M, K, N):
-    """The reference's CPU path on the headline workload (oracle/cpu_path.qlinear), bounded to ~10 s."""
+    """The reference's CPU path (oracle/cpu_path: its torch calls restated), timed on this host's cores:
+    the headline W8A8 linear (the reported value), the eager RMSNorm of config 1 at T = 4096, and one
+    36-layer-stack layer of config 4 at M = 16384 tokens (extrapolated to the stack).  About 20 s."""
+    import math
+
+    import torch.nn.functional as F
+
     from oracle import cpu_path
 
-    torch.set_num_threads(os.cpu_count() or 1)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(1)
-    x = torch.randn(M, K, generator=g)
-    x[:, torch.randperm(K, generator=g)[:8]] *= 20.0
-    x = x.to(torch.bfloat16)
-    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
-    sw = torch.empty(N).uniform_(1e-3, 1e-2, generator=g)
-    cpu_path.qlinear(x, qw, sw)  # warm-up
-    times = []
-    t_end = time.perf_counter() + 10.0
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 30):
-        t0 = time.perf_counter()
-        cpu_path.qlinear(x, qw, sw)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {
+
+    def act(m, k):
+        x = torch.randn(m, k, generator=g)
+        x[:, torch.randperm(k, generator=g)[:8]] *= 20.0
+        return x.to(torch.bfloat16)
+
+    def weight(n, k):
+        return torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8), \
+            torch.empty(n).uniform_(1e-3, 1e-2, generator=g)
+
+    x = act(M, K)
+    qw, sw = weight(N, K)
+    med, reps = _cpu_time(lambda: cpu_path.qlinear(x, qw, sw), 10.0)
+    out = {
         "value": round(2.0 * M * N * K / med / 1e12, 4),
         "unit": "TOPS",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"W8A8 linear M={M} K={K} N={N}: quant_act (round half even) + torch._int_mm + fp32 scale "
-                   f"epilogue -> bf16 (oracle/cpu_path.qlinear), median of {len(times)} runs, {med * 1e3:.1f} ms"),
+                   f"epilogue -> bf16 (oracle/cpu_path.qlinear), median of {reps} runs, {med * 1e3:.1f} ms"),
+        "cpu_model": cpu_model(),
     }
+    # config 1's eager RMSNorm (fused_kernels.py:51-56) + quant_act at T = 4096
+    T = 4096
+    h, nw = act(T, K), (torch.randn(K, generator=g) * 0.1 + 1.0).to(torch.bfloat16)
+    med_n, reps_n = _cpu_time(lambda: cpu_path.rms_norm(h, nw, 1e-6, offset=0.0), 3.0)
+    med_q, reps_q = _cpu_time(lambda: cpu_path.quant_act(cpu_path.rms_norm(h, nw, 1e-6, offset=0.0)), 3.0)
+    nbytes = T * (2 * K + K + 4) + 2 * K
+    out["rmsnorm_T4096"] = {"rmsnorm_ms": round(med_n * 1e3, 2), "rmsnorm_then_quant_ms": round(med_q * 1e3, 2),
+                            "GB/s": round(nbytes / med_q / 1e9, 2),
+                            "note": f"eager RMSNorm (cpu_path.rms_norm), then quant_act; medians of {reps_n} / {reps_q}"}
+    # config 4: one layer of the 36-layer stack at M = 8 x 2048 tokens on the CPU path, attention (torch
+    # SDPA in fp32, causal, 16 / 4 heads of 256, per request) timed once; the stack = 36 layers
+    B, S, HQ, HK, D = 8, 2048, 16, 4, 256
+    Mt = B * S
+    hs = act(Mt, HIDDEN)
+    w_in, w_post = nw, nw
+    qkv_w, o_w = weight(QKV_N, HIDDEN), weight(HIDDEN, O_K)
+    gate_w, up_w, down_w = weight(INTER, HIDDEN), weight(INTER, HIDDEN), weight(HIDDEN, INTER)
+    t0 = time.perf_counter()
+    y = cpu_path.rms_norm(hs, w_in, 1e-6, offset=0.0)
+    qkv = cpu_path.qlinear(y, *qkv_w)
+    t_qkv = time.perf_counter()
+    q, k, v = qkv.view(B, S, HQ + 2 * HK, D).float().split((HQ, HK, HK), dim=2)
+    a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
+                                       scale=1 / math.sqrt(D), enable_gqa=True)
+    a = a.transpose(1, 2).reshape(Mt, HQ * D).to(torch.bfloat16)
+    t_att = time.perf_counter()
+    h1 = hs + cpu_path.qlinear(a, *o_w)
+    y2 = cpu_path.rms_norm(h1, w_post, 1e-6, offset=0.0)
+    h2 = h1 + cpu_path.qlinear(cpu_path.swi_glu(cpu_path.qlinear(y2, *gate_w), cpu_path.qlinear(y2, *up_w)), *down_w)
+    t1 = time.perf_counter()
+    del h2
+    linear_s = (t_qkv - t0) + (t1 - t_att)
+    layer_s = t1 - t0
+    out["c4_stack_extrapolated"] = {
+        "layer_ms": round(layer_s * 1e3, 1), "layer_linear_ms": round(linear_s * 1e3, 1),
+        "layer_attention_ms": round((t_att - t_qkv) * 1e3, 1),
+        "ms_per_prefill": round(LAYERS * layer_s * 1e3, 1),
+        "tokens_per_s": round(Mt / (LAYERS * layer_s), 1),
+        "note": ("one layer of the 36-layer stack at 8 x 2048 tokens on the reference's CPU path (eager RMSNorm, "
+                 "quant_act + torch._int_mm + epilogue per linear, F.silu(g) * u, fp32 SDPA per request), run "
+                 "once; x 36 layers (extrapolated), readout excluded")}
+    return out
 
 
 def traffic_from_profiles():
@@ -194,7 +276,7 @@ def main():
                                "int32 on MFMA, per-token x per-channel scale epilogue, bf16 out",
                    "M": M, "K": K, "N": N, "T": M, "parallelism": "none (1 GPU)"},
         "pct_int8_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
-        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(),
                      "note": "INT8 TOP/s (2 M N K per launch / mean launch time); peak = MI355X dense INT8 5.0 "
                              "POP/s"},
@@ -224,7 +306,7 @@ def main():
                                               "pct_peak": round(100 * ops / (ms_c * 1e-3) / 1e12 / PEAK_INT8_TOPS, 1),
                                               "launches": len(times), "note": "median; 512 MiB fill before each"}
         # fused RMSNorm + quant (config 1): T * (2K + K + 4) + 2K algorithmic bytes
-        for T in (4096, 32768):
+        for T in (256, 4096, 32768):
             g = torch.Generator().manual_seed(T)
             h = torch.randn(T, K, generator=g)
             h[:, torch.randperm(K, generator=g)[:8]] *= 20
@@ -303,6 +385,24 @@ def main():
         layer["note"] = ("per 4B layer at T=4096: 2 fused RMSNorm+quant, QKV, O(+residual), fused gate+up with SiLU "
                          "epilogue, requant of h, down(+residual); attention (a torch op) not included")
         extra["layer_T4096"] = layer
+        # config 2's gated MLP block at T = 4096: fused gate+up (SiLU epilogue), requant of h, down + residual
+        blk_us = layer["gate_up"]["us"] + layer["requant_h"]["us"] + layer["down"]["us"]
+        blk_ops = 2.0 * T * (2 * INTER) * HIDDEN + 2.0 * T * HIDDEN * INTER
+        extra["c2_gated_mlp_T4096"] = {"us": round(blk_us, 2), "TOPS": round(blk_ops / (blk_us * 1e-6) / 1e12, 1),
+                                       "frac_int8_peak": round(blk_ops / (blk_us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4),
+                                       "note": "sum of the three launches' times (gate_up, requant_h, down)"}
+        # config 0 (one W8A8 linear on 512 tokens) and config 3 (T = 32768 projections), GEMM launches alone
+        for tag, (m, n, k) in (("gemm_c0_512x2560x9728", (512, INTER, HIDDEN)),
+                               ("gemm_c3_qkv_32768x2560x6144", (32768, QKV_N, HIDDEN)),
+                               ("gemm_c3_o_32768x4096x2560", (32768, HIDDEN, O_K))):
+            xx, ww, ss = synthetic(torch, dev, m, k, n, seed=m + n + k)
+            qa, sa = int8_kernels.act_quant(xx)
+            o = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            ms_g = timer.run(gemm_launcher(torch, lib, qa, sa, ww, ss, o), max(args.steps // 4, 20), args.warmup)
+            t = 2.0 * m * n * k / (ms_g * 1e-3) / 1e12
+            extra[tag] = {"us": round(ms_g * 1e3, 2), "TOPS": round(t, 1), "frac_int8_peak": round(t / PEAK_INT8_TOPS, 4),
+                          "M": m, "K": k, "N": n}
+            del xx, ww, ss, qa, sa, o
         extra["gdn_8x2048"] = gdn_token_mixer(torch, dev, timer, args)
         extra["attention_8x2048"] = attention_extra(torch, dev, timer, args)
         result["extra"] = extra
