@@ -138,6 +138,24 @@ int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, const float *
 long long mica_mm_i8_workspace_bytes(int device);
 
 /*
+ * mica_mm_i8 for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments, checks, schedule and bits as mica_mm_i8 with a workspace, but the split schedule's
+ * workspace is a static device array of the library (mica_mm_i8_noalloc_scratch_bytes() = 32 MiB +
+ * 4 KiB per device, held until the process ends), so the call allocates nothing.  Limit: a split
+ * round of at most 16 tiles (64 workgroups); a call whose split round would need more returns
+ * MICA_MISS_RANGE.  Every call on a device shares that device's scratch: calls that overlap on one
+ * device (concurrent streams) race, so order them on one stream.  The first call on a device also
+ * clears the scratch's counters on its stream.
+ */
+int mica_mm_i8_noalloc(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
+                       const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M,
+                       int N, int K, int epilogue, mica_stream_t stream);
+
+/* bytes of the static scratch behind mica_mm_i8_noalloc (per device) */
+long long mica_mm_i8_noalloc_scratch_bytes(void);
+
+/*
  * Elementwise SwiGLU y = bf16(bf16(silu(f32(g))) * f32(u)) over n elements of bf16.
  * Replaces fused_kernels.swi_glu (v0.5/serving/lib/fused_kernels.py:85-96, Triton swiglu :36-42).
  */

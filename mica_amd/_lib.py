@@ -38,6 +38,8 @@ SIGNATURES = {
                                       _I, _P]),
     "mica_mm_i8": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _LL, _P]),
     "mica_mm_i8_workspace_bytes": (_LL, [_I]),
+    "mica_mm_i8_noalloc": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "mica_mm_i8_noalloc_scratch_bytes": (_LL, []),
     "mica_swiglu": (_I, [_P, _P, _P, _LL, _I, _P]),
     "mica_gather_logits": (_I, [_P, _I, _I, _P, _I, _P, _I, _F, _F, _P, _I, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I,
                                 _P]),

@@ -36,6 +36,8 @@
 // lane (see mica_amd.h).  The residual is added after that rounding.  16-bit outputs are staged
 // through LDS so every lane stores 16 contiguous bytes of a row.
 
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -782,18 +784,23 @@ int cu_count(int device) {
     return v;
 }
 
-}  // namespace
+// Scratch of the no-allocation entry point (mica_mm_i8_noalloc): the split schedule's arrival
+// counters, then two partial-sum slots for each of at most kScratchGroups split workgroups (16 split
+// tiles of 4 workgroups).  Every device the library runs on holds its own copy until the process ends.
+constexpr int kScratchGroups = 64;
+constexpr long long kScratchBytes = kCounterBytes + (long long)kScratchGroups * 2 * kSlotBytes; // 32 MiB + 4 KiB
 
-extern "C" long long mica_mm_i8_workspace_bytes(int device) {
-    const int cus = cu_count(device);
-    if (cus <= 0 || cus > 1024) return -(long long)hipErrorInvalidDevice;
-    return workspace_bytes_for(cus);
+__global__ void clear_counters_kernel(int *counters, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) counters[i] = 0;
 }
 
-extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
-                          const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M,
-                          int N, int K, int epilogue, void *workspace, long long workspace_bytes,
-                          mica_stream_t stream) {
+// Validation, schedule and launch shared by mica_mm_i8 and mica_mm_i8_noalloc.  `noalloc`: the
+// workspace is the static scratch (kScratchBytes), a split round needing more of it than that is
+// rejected (MICA_MISS_RANGE) instead of being run as quarter / half tiles.
+// Argument checks (no device call): 0 when the call is well-formed, else the miss code.
+int mm_i8_check(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
+                const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M, int N,
+                int K, int epilogue, const void *workspace, long long workspace_bytes) {
     if (A == nullptr || B == nullptr || sa == nullptr || sb == nullptr || C == nullptr) return MICA_MISS_ARG;
     if (epilogue != MICA_EPI_SCALE && epilogue != MICA_EPI_SILU_MUL) return MICA_MISS_ARG;
     if (out_dtype != MICA_BF16 && out_dtype != MICA_FP16 && out_dtype != MICA_FP32 && out_dtype != MICA_INT32)
@@ -815,7 +822,17 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
         (workspace && !mica_aligned16(workspace)))
         return MICA_MISS_ALIGN;
     if (workspace_bytes < 0) return MICA_MISS_ARG;
+    return 0;
+}
+
+int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
+              const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M, int N, int K,
+              int epilogue, void *workspace, long long workspace_bytes, bool noalloc, hipStream_t st) {
+    const int bad = mm_i8_check(A, lda, B, ldb, sa, sb, bias, residual, ldr, C, ldc, out_dtype, M, N, K, epilogue,
+                                workspace, workspace_bytes);
+    if (bad != 0) return bad;
     if (M == 0) return 0;
+    const int Nout = epilogue == MICA_EPI_SILU_MUL ? N / 2 : N;
     GemmParams p{};
     p.A = A; p.B = B; p.sa = sa; p.sb = sb; p.bias = bias; p.res = residual; p.C = C;
     p.lda = lda; p.ldb = ldb; p.ldr = ldr; p.ldc = ldc; p.M = M; p.N = N; p.K = K;
@@ -861,8 +878,13 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
     const long long rem = cus > 0 ? tiles % cus : 0;
     if (rem != 0 && cus <= 1024) {
         const bool quarters = kQuarters && epilogue == MICA_EPI_SCALE && 4 * rem <= cus;
-        if (workspace != nullptr && workspace_bytes >= workspace_bytes_for(cus) && rem * kSplit <= cus &&
-            nk >= kSplit * kMinSplitSlabs && !(quarters && M > 256)) {
+        const bool want_split = workspace != nullptr && rem * kSplit <= cus && nk >= kSplit * kMinSplitSlabs &&
+                                !(quarters && M > 256);
+        // the existing entry point splits with a workspace of mica_mm_i8_workspace_bytes(device); the
+        // no-allocation one with the scratch, which holds kScratchGroups split workgroups
+        const bool fits = noalloc ? rem * kSplit <= kScratchGroups : workspace_bytes >= workspace_bytes_for(cus);
+        if (want_split && noalloc && !fits) return MICA_MISS_RANGE;
+        if (want_split && fits) {
             p.dp_tiles = (int)(tiles - rem);
             p.sk_tiles = (int)rem;
             p.sk_grid = (int)(rem * kSplit);
@@ -886,11 +908,77 @@ extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, co
             if (grid < 2 * rem) grid = (int)(2 * rem);
         }
     }
-    hipStream_t st = (hipStream_t)stream;
     const bool hb = bias != nullptr, hr = residual != nullptr;
     if (epilogue == MICA_EPI_SILU_MUL) return launch_out<MICA_EPI_SILU_MUL, MICA_BF16>(p, grid, false, false, st);
     if (out_dtype == MICA_BF16) return launch_out<MICA_EPI_SCALE, MICA_BF16>(p, grid, hb, hr, st);
     if (out_dtype == MICA_FP16) return launch_out<MICA_EPI_SCALE, MICA_FP16>(p, grid, hb, hr, st);
     if (out_dtype == MICA_INT32) return launch_out<MICA_EPI_SCALE, MICA_INT32>(p, grid, false, false, st);
     return launch_out<MICA_EPI_SCALE, MICA_FP32>(p, grid, hb, hr, st);
+}
+
+}  // namespace
+
+// The scratch array.  In host code `scratch` names a host-side stand-in, not device memory: only the
+// per-device address hipGetSymbolAddress returns (scratch_on) is ever passed to a kernel.
+static __device__ __align__(256) int8_t scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// The scratch's device address on the current device, looked up once per device.  The first lookup
+// also clears the arrival counters on `st` (static storage starts zeroed; every split launch leaves
+// them zero again), so calls ordered after the first one see zero counters.
+int scratch_on(hipStream_t st, void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return -(int)e;
+    if (dev < 0 || dev >= kMaxDevices) return MICA_MISS_DEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return -(int)e;
+        if (ptr == nullptr) return -(int)hipErrorInvalidSymbol;
+        hipLaunchKernelGGL(clear_counters_kernel, dim3(1), dim3(256), 0, st, (int *)ptr, (int)(kCounterBytes / 4));
+        e = hipGetLastError();
+        if (e != hipSuccess) return -(int)e;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" long long mica_mm_i8_workspace_bytes(int device) {
+    const int cus = cu_count(device);
+    if (cus <= 0 || cus > 1024) return -(long long)hipErrorInvalidDevice;
+    return workspace_bytes_for(cus);
+}
+
+extern "C" int mica_mm_i8(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa, const float *sb,
+                          const float *bias, const void *residual, int ldr, void *C, int ldc, int out_dtype, int M,
+                          int N, int K, int epilogue, void *workspace, long long workspace_bytes,
+                          mica_stream_t stream) {
+    return mm_i8_run(A, lda, B, ldb, sa, sb, bias, residual, ldr, C, ldc, out_dtype, M, N, K, epilogue, workspace,
+                     workspace_bytes, false, (hipStream_t)stream);
+}
+
+extern "C" long long mica_mm_i8_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int mica_mm_i8_noalloc(const int8_t *A, int lda, const int8_t *B, int ldb, const float *sa,
+                                  const float *sb, const float *bias, const void *residual, int ldr, void *C, int ldc,
+                                  int out_dtype, int M, int N, int K, int epilogue, mica_stream_t stream) {
+    // arguments first (a rejected call touches no device), then the scratch of the current device
+    const int bad = mm_i8_check(A, lda, B, ldb, sa, sb, bias, residual, ldr, C, ldc, out_dtype, M, N, K, epilogue,
+                                nullptr, 0);
+    if (bad != 0 || M == 0) return bad;
+    void *ws = nullptr;
+    const int rc = scratch_on((hipStream_t)stream, &ws);
+    if (rc != 0) return rc;
+    return mm_i8_run(A, lda, B, ldb, sa, sb, bias, residual, ldr, C, ldc, out_dtype, M, N, K, epilogue, ws,
+                     kScratchBytes, true, (hipStream_t)stream);
 }

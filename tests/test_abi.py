@@ -70,6 +70,21 @@ def test_mm_i8_rejects_bad_workspace():
     assert lib.mica_mm_i8(*ok, A16, -1, None) == 6             # negative size
 
 
+@pytest.mark.parametrize("args,code", [
+    ((None, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0), 6),      # NULL A
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 40, 0), 1),       # K % 16
+    ((A16, 72, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0), 4),       # lda % 16
+    ((A16 + 8, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 8, 64, 64, 0), 3),   # misaligned A
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 1 << 30, 64, 64, 0), 5),  # M * lda >= 2^31
+    ((A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 0, 64, 64, 0), 0),       # M = 0: nothing to do
+])
+def test_mm_i8_noalloc_checks_arguments_before_any_device_call(args, code):
+    """The no-allocation GEMM validates its arguments as mica_mm_i8 does, before it looks up its scratch."""
+    lib = _lib.load()
+    assert lib.mica_mm_i8_noalloc(*args, None) == code
+    assert lib.mica_mm_i8_noalloc_scratch_bytes() == 4096 + 64 * 2 * 256 * 1024
+
+
 def test_mm_i8_empty_is_a_no_op():
     lib = _lib.load()
     assert lib.mica_mm_i8(A16, 64, A16, 64, A16, A16, None, None, 0, A16, 64, 0, 0, 64, 64, 0, None, 0, None) == 0

@@ -1,0 +1,98 @@
+"""mica_mm_i8_noalloc (the GEMM entry point that allocates nothing: its split schedule's workspace is a
+static device array of the library) against mica_mm_i8 with a workspace, both called through the C ABI.
+
+Bar: bit-identical outputs (int8 x int8 -> int32 accumulators, then the same epilogue).  Two calls in a
+row, the second smaller, so the shared scratch's arrival counters must come back to zero after each
+launch; a split round larger than the scratch is rejected with MICA_MISS_RANGE."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mica_amd import _lib, int8_kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[case] {msg}", file=sys.stderr, flush=True)
+
+
+def _operands(rng, m, n, k, dev):
+    A = torch.from_numpy(rng.integers(-127, 128, (m, k), dtype=np.int8)).to(dev)
+    B = torch.from_numpy(rng.integers(-127, 128, (n, k), dtype=np.int8)).to(dev)
+    sa = torch.from_numpy(rng.uniform(1e-3, 1e-2, m).astype(np.float32)).to(dev)
+    sb = torch.from_numpy(rng.uniform(1e-3, 1e-2, n).astype(np.float32)).to(dev)
+    return A, B, sa, sb
+
+
+def _call(noalloc, A, B, sa, sb, out, out_code, epi_code, residual=None):
+    L = _lib.load()
+    m, k = A.shape
+    n = B.shape[0]
+    n_out = out.shape[1]
+    stream = torch.cuda.current_stream().cuda_stream
+    res = None if residual is None else residual.data_ptr()
+    args = (A.data_ptr(), k, B.data_ptr(), k, sa.data_ptr(), sb.data_ptr(), None, res, n_out, out.data_ptr(), n_out,
+            out_code, m, n, k, epi_code)
+    if noalloc:
+        return L.mica_mm_i8_noalloc(*args, stream)
+    ws, ws_bytes = int8_kernels.gemm_workspace(A.device)
+    return L.mica_mm_i8(*args, ws, ws_bytes, stream)
+
+
+def _both(A, B, sa, sb, dtype, epi_code, n_out, residual=None):
+    code = {torch.bfloat16: _lib.BF16, torch.int32: _lib.INT32}[dtype]
+    outs = []
+    for noalloc in (False, True):
+        out = torch.full((A.shape[0], n_out), -1, dtype=dtype, device=A.device)  # no stale zeros
+        rc = _call(noalloc, A, B, sa, sb, out, code, epi_code, residual)
+        assert rc == 0, f"{'mica_mm_i8_noalloc' if noalloc else 'mica_mm_i8'} returned {rc} ({_lib.status_name(rc)})"
+        outs.append(out)
+    torch.cuda.synchronize()
+    return outs
+
+
+def _same(a, b, what):
+    ab, bb = a.view(torch.int16) if a.dtype == torch.bfloat16 else a, b.view(torch.int16) if b.dtype == torch.bfloat16 else b
+    diff = (ab != bb).sum().item()
+    assert diff == 0, f"{what}: {diff} of {a.numel()} outputs differ between mica_mm_i8_noalloc and mica_mm_i8"
+
+
+def test_scratch_size_is_stated(gpu):
+    assert _lib.load().mica_mm_i8_noalloc_scratch_bytes() == 4096 + 64 * 2 * 256 * 1024
+
+
+@pytest.mark.parametrize("calls", [
+    # (m, n, k, epilogue) per call; the second call of each pair is smaller
+    ((256, 2560, 9728, "scale"), (128, 1280, 8192, "scale")),       # split rounds of 10 then 5 tiles
+    ((200, 2048, 8192, "silu_mul"), (64, 1024, 8192, "silu_mul")),  # SiLU epilogue split, 8 then 4 tiles
+    ((512, 2560, 4096, "scale"), (300, 1000, 2576, "scale")),       # no split: quarter / half tiles
+])
+def test_noalloc_matches_mica_mm_i8_twice(gpu, calls):
+    rng = np.random.default_rng(7)
+    for i, (m, n, k, epi) in enumerate(calls):
+        note(f"noalloc call {i}: m={m} n={n} k={k} epi={epi}")
+        A, B, sa, sb = _operands(rng, m, n, k, gpu)
+        if epi == "silu_mul":
+            a, b = _both(A, B, sa, sb, torch.bfloat16, _lib.EPI_SILU_MUL, n // 2)
+            _same(a, b, f"silu call {i}")
+            continue
+        a, b = _both(A, B, sa, sb, torch.int32, _lib.EPI_SCALE, n)
+        _same(a, b, f"int32 call {i}")
+        res = torch.randn(m, n, device=gpu).to(torch.bfloat16)
+        a, b = _both(A, B, sa, sb, torch.bfloat16, _lib.EPI_SCALE, n, residual=res)
+        _same(a, b, f"bf16 + residual call {i}")
+
+
+def test_noalloc_rejects_a_split_round_beyond_the_scratch(gpu):
+    """24 SiLU tiles at K = 8192 would split over 96 workgroups: more than the scratch holds."""
+    note("noalloc reject m=300 n=3072 k=8192 silu")
+    rng = np.random.default_rng(3)
+    A, B, sa, sb = _operands(rng, 300, 3072, 8192, gpu)
+    out = torch.empty((300, 1536), dtype=torch.bfloat16, device=gpu)
+    assert _call(True, A, B, sa, sb, out, _lib.BF16, _lib.EPI_SILU_MUL) == 5  # MICA_MISS_RANGE
+    # the existing entry point serves it (its workspace is sized for every CU)
+    assert _call(False, A, B, sa, sb, out, _lib.BF16, _lib.EPI_SILU_MUL) == 0
+    torch.cuda.synchronize()
