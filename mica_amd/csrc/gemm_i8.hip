@@ -803,7 +803,12 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
     // K a multiple of 256 (an even number of 128-byte slabs) and no split: the wide kernel
     // (gemm_i8_wide.hip) runs the same schedule of whole tiles and tail pieces, with the same bits;
     // its grid stays persistent (one workgroup per CU) also when the tiles fill whole rounds
-    if (K % 256 == 0 && p.sk_tiles == 0) {
+    // (the operands addressable with 32-bit offsets one tile past their last row, and a 256-row span
+    // of C or of the residual)
+    const bool wide_ok = K % 256 == 0 && p.sk_tiles == 0 && (long long)(M + kTile) * lda < (1ll << 31) &&
+                         (long long)(N + kTile) * ldb < (1ll << 31) && (long long)kTile * ldc * 4 < (1ll << 31) &&
+                         (!residual || (long long)kTile * ldr * 4 < (1ll << 31));
+    if (wide_ok) {
         if (rem == 0 && cus > 0 && tiles > cus) grid = cus;
         return wide_launch(p, epilogue, out_dtype, grid, hb, hr, st);
     }

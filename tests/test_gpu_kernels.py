@@ -262,6 +262,9 @@ def _rand_gemm(rng, m, n, k):
     (17, 300, 2576),       # K not a multiple of the 128-byte slab
     (258, 514, 16),        # K of one chunk
     (130, 2704, 2576),     # 11 tiles as 128 x 128 quarters, cut by both the M and the N edge
+    (130, 2704, 2560),     # the same quarters with K a multiple of 256 (the 16x16x64 kernel)
+    (70, 1002, 512),       # N not a multiple of 4: element stores after the staged epilogue
+    (64, 260, 256),        # one pair of 128-byte slabs; N a multiple of 4 but not of 8
 ])
 def test_gemm_int32_and_epilogue_bit_exact(gpu, m, n, k):
     note(f"gemm m={m} n={n} k={k}")
@@ -329,10 +332,10 @@ def test_gemm_requant_output(gpu):
         assert np.array_equal(s.cpu().numpy(), so), epi
 
 
-def test_gemm_residual_epilogue(gpu):
-    note("gemm residual")
-    rng = np.random.default_rng(3)
-    m, n, k = 700, 2560, 9728
+@pytest.mark.parametrize("m,n,k", [(700, 2560, 9728), (130, 1004, 512)])
+def test_gemm_residual_epilogue(gpu, m, n, k):
+    note(f"gemm residual m={m} n={n} k={k}")
+    rng = np.random.default_rng(3 + m)
     A, B, sa, sb = _rand_gemm(rng, m, n, k)
     res = act_bits(rng, (m, n), outliers=0)
     y = int8_kernels.mm_i8(*(torch.from_numpy(v).cuda() for v in (A, sa, B, sb)), residual=to_gpu_bf16(res))
