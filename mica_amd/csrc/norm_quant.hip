@@ -169,7 +169,11 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
 // Each wave prefetches its next row while it works on the current one; the row is unpacked to
 // fp32 once, and after the norm it stays in fp32 registers (already rounded to XT), so the
 // absmax and the quantizer work on registers.
-template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
+// ONE: every wave owns exactly one row (the launch covers M with one wave per row, all resident at
+// once): no next row to prefetch, and the bf16 weights are loaded with the row and widened where
+// they are used instead of being held as fp32, which keeps the kernel within 4+ waves per SIMD
+// (measured at T = 4096, K = 2560 against weights formed once per workgroup in LDS: 6.0 vs 6.3 us).
+template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND, bool ONE = false>
 MICA_DEVICE void row16_body(const RowParams &p) {
     constexpr bool kFast = XT == MICA_BF16; // the fast quotient is exact for unsmoothed bf16 rows
     const int lane = threadIdx.x & 63;
@@ -187,8 +191,17 @@ MICA_DEVICE void row16_body(const RowParams &p) {
     };
     // the wave's first row is requested before the weights, so the two latencies overlap
     int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    u32x4 bufA[NCH], bufB[NCH <= 5 ? NCH : 1];
+    u32x4 bufA[NCH], bufB[NCH <= 5 && !ONE ? NCH : 1];
     if (row < p.M) load_row(bufA, row);
+    // ONE: the raw bf16 weights of this lane's chunks, widened at their use
+    u32x4 wraw[ONE && NORM ? NCH : 1];
+    if (ONE && NORM) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = c * kRowStep + lane * kChunk;
+            wraw[c] = live(c) ? *(const u32x4 *)((const uint16_t *)p.w + idx) : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
 
     // rows of up to 2560 elements with smoothing factors: the workgroup copies every output's factors
     // into LDS once (n_out x K fp32, dynamic shared memory), so the two passes of every row read them
@@ -213,8 +226,8 @@ MICA_DEVICE void row16_body(const RowParams &p) {
     }
 
     // per-lane weight multipliers (offset + w), fp32, cached across the rows this wave visits
-    float w1[NORM ? NCH : 1][kChunk];
-    if (NORM) {
+    float w1[NORM && !ONE ? NCH : 1][kChunk];
+    if (NORM && !ONE) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int idx = c * kRowStep + lane * kChunk;
@@ -235,7 +248,7 @@ MICA_DEVICE void row16_body(const RowParams &p) {
     constexpr bool kF32 = NCH <= 8;
     // long rows already keep enough bytes in flight per wave; smoothed rows spend the registers on
     // their factors' products instead
-    constexpr bool kPrefetch = NCH <= 5 && !HAS_INV;
+    constexpr bool kPrefetch = NCH <= 5 && !HAS_INV && !ONE;
     auto process = [&](u32x4 (&cur)[NCH], int row) {
         if (NORM && p.res != nullptr) {
             // v = (x + r) rounded to the activation dtype (fused_kernels.py:27-30, :52)
@@ -279,8 +292,15 @@ MICA_DEVICE void row16_body(const RowParams &p) {
                 float t[kChunk];
                 if (!kF32) unpack8<XT>(cur[c], t);
                 float(&a)[kChunk] = kF32 ? v[kF32 ? c : 0] : t;
+                if (ONE) {
+                    float wv[kChunk];
+                    unpack8<MICA_BF16>(wraw[ONE && NORM ? c : 0], wv);
 #pragma unroll
-                for (int j = 0; j < kChunk; ++j) a[j] = (a[j] * rstd) * w1[c][j];
+                    for (int j = 0; j < kChunk; ++j) a[j] = (a[j] * rstd) * (p.offset + wv[j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < kChunk; ++j) a[j] = (a[j] * rstd) * w1[ONE ? 0 : c][j];
+                }
                 const u32x4 packed = pack8<XT>(a);
                 if (kF32) unpack8<XT>(packed, a);
                 else cur[c] = packed;
@@ -353,7 +373,9 @@ MICA_DEVICE void row16_body(const RowParams &p) {
         }
     };
 
-    if constexpr (kPrefetch) {
+    if constexpr (ONE) {
+        if (row < p.M) process(bufA, row);
+    } else if constexpr (kPrefetch) {
         // two row buffers used in turn (no registers are copied between rows); each wave's next
         // row is requested before the current one is worked on
         for (;;) {
@@ -377,6 +399,16 @@ MICA_DEVICE void row16_body(const RowParams &p) {
 template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
 __global__ __launch_bounds__(256) void row16_kernel(RowParams p) {
     row16_body<NCH, XT, NORM, HAS_INV, FULL, RND>(p);
+}
+
+// One row per wave (see row16_body): for a launch whose rows all fit the resident waves at once.
+#ifndef MICA_ONE_THREADS
+#define MICA_ONE_THREADS 256
+#endif
+constexpr int kOneThreads = MICA_ONE_THREADS;
+template <int NCH, int XT, bool NORM, bool FULL, int RND>
+__global__ __launch_bounds__(kOneThreads) void row16_one_kernel(RowParams p) {
+    row16_body<NCH, XT, NORM, false, FULL, RND, true>(p);
 }
 
 // Smoothed rows of up to 2560 elements, held to 168 registers (a few spill) so that 3 waves per SIMD
@@ -513,6 +545,24 @@ int launch_rows(const RowParams &p, unsigned lds, hipStream_t st) {
     return mica_err(hipGetLastError());
 }
 
+// Launch a one-row-per-wave kernel when every row fits the waves that can be resident at once
+// (measured at T = 4096, K = 2560: the grid-stride kernel at 3 workgroups per CU leaves a third of
+// its waves a second row); returns -1 when the rows do not fit, for the caller's grid-stride path.
+template <void (*Kernel)(RowParams)>
+int launch_one(const RowParams &p, hipStream_t st) {
+    static std::atomic<int> cached{0};
+    int per_cu = cached.load(std::memory_order_relaxed);
+    if (per_cu <= 0) {
+        int occ = 0;
+        per_cu = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, Kernel, kOneThreads, 0) == hipSuccess && occ > 0 ? occ : 1;
+        cached.store(per_cu, std::memory_order_relaxed);
+    }
+    const long long blocks = ((long long)p.M + kOneThreads / 64 - 1) / (kOneThreads / 64);
+    if (blocks > (long long)cu_count_of_current_device() * per_cu) return -1;
+    hipLaunchKernelGGL(Kernel, dim3((unsigned)blocks), dim3(kOneThreads), 0, st, p);
+    return mica_err(hipGetLastError());
+}
+
 template <int NCH>
 int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st) {
 #define MICA_ROW16(XT_, NORM_, INV_) \
@@ -530,6 +580,17 @@ int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st
 // bf16 rows of exactly NCH * 512 elements (the hot widths): no masks, rounding fixed at compile time
 template <int NCH>
 int launch16_full(const RowParams &p, bool norm, bool has_inv, hipStream_t st) {
+    // rows of up to 2560 elements without smoothing: one wave per row when they all fit
+    if constexpr (NCH <= 5) {
+        if (!has_inv && (!norm || p.w_dtype == MICA_BF16)) {
+            int rc = -1;
+            if (norm && p.rounding == MICA_ROUND_EVEN) rc = launch_one<row16_one_kernel<NCH, MICA_BF16, true, true, MICA_ROUND_EVEN>>(p, st);
+            else if (norm) rc = launch_one<row16_one_kernel<NCH, MICA_BF16, true, true, MICA_ROUND_AWAY>>(p, st);
+            else if (p.rounding == MICA_ROUND_EVEN) rc = launch_one<row16_one_kernel<NCH, MICA_BF16, false, true, MICA_ROUND_EVEN>>(p, st);
+            else rc = launch_one<row16_one_kernel<NCH, MICA_BF16, false, true, MICA_ROUND_AWAY>>(p, st);
+            if (rc >= 0) return rc;
+        }
+    }
 #define MICA_ROWF(NORM_, INV_, RND_) \
     return launch_rows<row16_for<NCH, MICA_BF16, NORM_, INV_, true, RND_>()>(p, inv_lds_bytes<NCH>(p, INV_), st)
 #define MICA_ROWF2(NORM_, INV_) \
