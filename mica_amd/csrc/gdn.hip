@@ -407,7 +407,11 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
 
 // ---- scan: one workgroup of 8 waves per (value head, sequence) --------------------------------
 // Wave w: row role wr = w % 4 and dv half hf = w / 4.  The state S [128 dk x 128 dv] is spread so
-// that wave w holds dk rows 32 wr .. 32 wr + 31 of dv half hf (two 32 x 32 accumulator tiles).
+// that wave w holds dk rows 32 wr .. 32 wr + 31 of dv half hf (DVT = two 32 x 32 accumulator tiles).
+// With fewer (sequence, head) pairs than CUs the dv columns are split over gridDim.z workgroups
+// (the columns of S, v_new and o are independent; every workgroup recomputes the chunk's P): 2 of 8
+// waves with one 32 x 32 tile each (DVT = 1), or 4 of 4 waves (wr only, DVT = 1).  The arithmetic of
+// every output element is the same in each split.
 // Per chunk, X = [W; Q] S (rows 0-63 from W for wr = 0, 1; rows 64-127 from Q for wr = 2, 3),
 // P^T = K Q^T (waves 0-3, one tile each), v_new = U - W S (wr = 0, 1), o (wr = 2, 3) and the state
 // update (all waves).  Each operand held in registers is re-loaded for the next chunk right after
@@ -415,7 +419,6 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
 // LDS (bytes): S^T (128 dv rows x 128 dk, bf16, 272 B rows); K rows of the chunk, two buffers
 // (alternate chunks); v_new^T and its decayed copy (128 dv x 64 tokens, 144 B rows); P = masked
 // Q K^T (64 x 64, 144 B rows); output staging (32 x 64 per output wave); G, two buffers.
-constexpr int kScanThreads = 512;
 constexpr int kScanS = 0;
 constexpr int kScanK = kScanS + kDv * kRowP * 2;
 constexpr int kScanVn = kScanK + 2 * kC * kRowP * 2;
@@ -426,7 +429,10 @@ constexpr int kScanG = kScanO + 4 * 32 * kRowC * 2;
 constexpr int kScanSmem = kScanG + 2 * kC * 4;
 static_assert(kScanSmem <= 160 * 1024, "scan LDS");
 
-__global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
+template <int DVT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
+    constexpr int kThr = 64 * WAVES;
+    constexpr int kPieces = kC * 16 / kThr; // 16-byte pieces of the chunk's K rows per thread
     __shared__ __attribute__((aligned(16))) int8_t smem[kScanSmem];
     uint16_t *Sst = (uint16_t *)(smem + kScanS);
     uint16_t *Vn = (uint16_t *)(smem + kScanVn);
@@ -438,6 +444,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
     const int wr = wave & 3, hf = wave >> 2;
     const int hk = h / (p.HV / p.HK);
     const int l32 = lane & 31, kh = (lane >> 5) * 8;
+    // this wave's first value column: the workgroup's dv range starts at blockIdx.z times its width
+    const int dvw = blockIdx.z * ((WAVES / 4) * 32 * DVT) + hf * 32 * DVT;
     const long bh = (long)b * p.HV + h;
     const bool w_rows = wr < 2;                    // X rows from W (v_new); otherwise from Q (output)
     const bool needs_q = wave < 4 || wave >= 6;    // Q tile for P^T (waves 0-3) and/or X (wr = 2, 3)
@@ -445,37 +453,37 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
     const int mk = wave >> 1;                      // K tile of this wave's P^T tile (waves 0-3)
 
     // state: S[dk = 32 wr + acc_row][dv = 64 hf + 32 dvt + l32]
-    f32x16 S[2];
+    f32x16 S[DVT];
 #pragma unroll
-    for (int dvt = 0; dvt < 2; ++dvt)
+    for (int dvt = 0; dvt < DVT; ++dvt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int dk = wr * 32 + acc_row(r, lane), dv = hf * 64 + dvt * 32 + l32;
+            const int dk = wr * 32 + acc_row(r, lane), dv = dvw + dvt * 32 + l32;
             S[dvt][r] = p.h0 ? p.h0[(bh * kDk + dk) * kDv + dv] : 0.0f;
         }
     auto store_state_bf16 = [&]() {
 #pragma unroll
-        for (int dvt = 0; dvt < 2; ++dvt)
+        for (int dvt = 0; dvt < DVT; ++dvt)
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int dk = wr * 32 + 8 * r4 + 4 * (lane >> 5);
                 u32x2 w2;
                 w2[0] = pack_bf16x2(S[dvt][4 * r4], S[dvt][4 * r4 + 1]);
                 w2[1] = pack_bf16x2(S[dvt][4 * r4 + 2], S[dvt][4 * r4 + 3]);
-                *(u32x2 *)(Sst + (hf * 64 + dvt * 32 + l32) * kRowP + dk) = w2;
+                *(u32x2 *)(Sst + (dvw + dvt * 32 + l32) * kRowP + dk) = w2;
             }
     };
     store_state_bf16();
 
     // ---- per-chunk operand loads into registers ----
-    u32x4 kreg[2];
+    u32x4 kreg[kPieces];
     float gn = 0.0f;
     bf16x8 qf[8], wfr[8];
-    u32x4 uf[2][2];
+    u32x4 uf[DVT][2];
     auto load_k = [&](int c) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int piece = tid + i * kScanThreads; // 64 rows x 16 pieces of 16 bytes
+        for (int i = 0; i < kPieces; ++i) {
+            const int piece = tid + i * kThr; // 64 rows x 16 pieces of 16 bytes
             const int t = c * kC + (piece >> 4);
             kreg[i] = u32x4{0u, 0u, 0u, 0u};
             if (t < p.T) kreg[i] = *(const u32x4 *)(p.k + b * p.sbk + (long)t * p.ldk + hk * kDk + (piece & 15) * 8);
@@ -498,8 +506,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
     };
     auto load_u = [&](int c) {
 #pragma unroll
-        for (int dvt = 0; dvt < 2; ++dvt) {
-            const uint16_t *src = p.uf + chunk_id(p, b, h, c) * (kC * kDv) + ((wr * 4 + hf * 2 + dvt) * 64 + lane) * 16;
+        for (int dvt = 0; dvt < DVT; ++dvt) {
+            const uint16_t *src = p.uf + chunk_id(p, b, h, c) * (kC * kDv) + ((wr * 4 + dvw / 32 + dvt) * 64 + lane) * 16;
             uf[dvt][0] = *(const u32x4 *)src;
             uf[dvt][1] = *(const u32x4 *)(src + 8);
         }
@@ -514,21 +522,21 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
         uint16_t *Ks = (uint16_t *)(smem + kScanK) + (c & 1) * kC * kRowP;
         float *Gs = (float *)(smem + kScanG) + (c & 1) * kC;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int piece = tid + i * kScanThreads;
+        for (int i = 0; i < kPieces; ++i) {
+            const int piece = tid + i * kThr;
             *(u32x4 *)(Ks + (piece >> 4) * kRowP + (piece & 15) * 8) = kreg[i];
         }
         if (tid < kC) Gs[tid] = gn;
         __syncthreads(); // (A) K rows, G and the state S^T visible to every wave
 
         // ---- X = [W; Q] S for this wave's 32 rows and dv half ----
-        f32x16 X[2] = {};
+        f32x16 X[DVT] = {};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const bf16x8 a = w_rows ? wfr[s] : qf[s];
 #pragma unroll
-            for (int dvt = 0; dvt < 2; ++dvt)
-                X[dvt] = mfma(a, ld_frag(Sst + (hf * 64 + dvt * 32 + l32) * kRowP + s * 16 + kh), X[dvt]);
+            for (int dvt = 0; dvt < DVT; ++dvt)
+                X[dvt] = mfma(a, ld_frag(Sst + (dvw + dvt * 32 + l32) * kRowP + s * 16 + kh), X[dvt]);
         }
         if (w_rows && more) load_w(c + 1);
         // ---- P^T tile (K rows mk) x (Q rows mq): P[i][j] = (q_i . k_j) exp(G_i - G_j), j <= i ----
@@ -561,8 +569,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
         if (w_rows) {
             const float glast = Gs[kC - 1];
 #pragma unroll
-            for (int dvt = 0; dvt < 2; ++dvt) {
-                const int dv = hf * 64 + dvt * 32 + l32;
+            for (int dvt = 0; dvt < DVT; ++dvt) {
+                const int dv = dvw + dvt * 32 + l32;
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) {
                     const int m0 = wr * 32 + 8 * r4 + 4 * (lane >> 5);
@@ -589,13 +597,13 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
         // ---- o = scale (exp(G_i) (Q S)_i + P v_new) for the rows of wr = 2, 3 ----
         if (!w_rows) {
             const int mo = wr - 2; // output row tile
-            f32x16 O[2] = {};
+            f32x16 O[DVT] = {};
 #pragma unroll
             for (int s = 0; s < kC / 16; ++s) {
                 const bf16x8 a = ld_frag(Ps + (mo * 32 + l32) * kRowC + s * 16 + kh);
 #pragma unroll
-                for (int dvt = 0; dvt < 2; ++dvt)
-                    O[dvt] = mfma(a, ld_frag(Vn + (hf * 64 + dvt * 32 + l32) * kRowC + s * 16 + kh), O[dvt]);
+                for (int dvt = 0; dvt < DVT; ++dvt)
+                    O[dvt] = mfma(a, ld_frag(Vn + (dvw + dvt * 32 + l32) * kRowC + s * 16 + kh), O[dvt]);
             }
             uint16_t *ost = (uint16_t *)(smem + kScanO) + (hf * 2 + mo) * 32 * kRowC;
             float eg[16]; // exp(G) of this lane's 16 output rows, read and computed before the stores
@@ -608,27 +616,28 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
                 eg[4 * r4 + 3] = fexp(g4.w);
             }
 #pragma unroll
-            for (int dvt = 0; dvt < 2; ++dvt)
+            for (int dvt = 0; dvt < DVT; ++dvt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int ml = acc_row(r, lane);
                     const float y = X[dvt][r] * eg[r] * p.scale + O[dvt][r] * p.scale;
                     ost[ml * kRowC + dvt * 32 + l32] = f32_to_bf16(y);
                 }
-            // write out: 32 rows x 128 bytes, 8 lanes per row
+            // write out: 32 rows x 64 DVT bytes, 4 DVT lanes per row
+            constexpr int kLpr = 4 * DVT, kRpi = 64 / kLpr;
 #pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                const int ml = it * 8 + (lane >> 3), cc = (lane & 7) * 8;
+            for (int it = 0; it < 32 / kRpi; ++it) {
+                const int ml = it * kRpi + lane / kLpr, cc = (lane % kLpr) * 8;
                 const int t = tbase + mo * 32 + ml;
                 const u32x4 v = *(const u32x4 *)(ost + ml * kRowC + cc);
-                if (t < p.T) *(u32x4 *)(p.o + (((long)b * p.T + t) * p.HV + h) * kDv + hf * 64 + cc) = v;
+                if (t < p.T) *(u32x4 *)(p.o + (((long)b * p.T + t) * p.HV + h) * kDv + dvw + cc) = v;
             }
         }
         // ---- S <- exp(G_63) S + K^T (decayed v_new) ----
         {
             const float dl = fexp(Gs[kC - 1]);
 #pragma unroll
-            for (int dvt = 0; dvt < 2; ++dvt) S[dvt] *= dl;
+            for (int dvt = 0; dvt < DVT; ++dvt) S[dvt] *= dl;
             const int dk = wr * 32 + l32;
 #pragma unroll
             for (int s = 0; s < kC / 16; ++s) {
@@ -638,18 +647,18 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnParams p) {
                 for (int e = 0; e < 4; ++e)
                     kt[e] = (uint32_t)Ks[(m0 + 2 * e) * kRowP + dk] | ((uint32_t)Ks[(m0 + 2 * e + 1) * kRowP + dk] << 16);
 #pragma unroll
-                for (int dvt = 0; dvt < 2; ++dvt)
-                    S[dvt] = mfma(as_bf16x8(kt), ld_frag(Vd + (hf * 64 + dvt * 32 + l32) * kRowC + s * 16 + kh), S[dvt]);
+                for (int dvt = 0; dvt < DVT; ++dvt)
+                    S[dvt] = mfma(as_bf16x8(kt), ld_frag(Vd + (dvw + dvt * 32 + l32) * kRowC + s * 16 + kh), S[dvt]);
             }
         }
         store_state_bf16(); // read after barrier (A) of the next chunk
     }
     if (p.hT) {
 #pragma unroll
-        for (int dvt = 0; dvt < 2; ++dvt)
+        for (int dvt = 0; dvt < DVT; ++dvt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int dk = wr * 32 + acc_row(r, lane), dv = hf * 64 + dvt * 32 + l32;
+                const int dk = wr * 32 + acc_row(r, lane), dv = dvw + dvt * 32 + l32;
                 p.hT[(bh * kDk + dk) * kDv + dv] = S[dvt][r];
             }
     }
@@ -859,7 +868,15 @@ extern "C" int mica_gdn_chunk(const void *q, long long sbq, int ldq, const void 
     hipLaunchKernelGGL(gdn_prep_kernel, dim3(p.NT, HV, B), dim3(kGdnThreads), 0, st, p);
     int rc = mica_err(hipGetLastError());
     if (rc) return rc;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3(HV, B), dim3(kScanThreads), 0, st, p);
+    // dv split of the scan when (sequence, head) pairs leave CUs idle
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    const long long pairs = (long long)B * HV;
+    if (pairs * 4 <= cus) hipLaunchKernelGGL((gdn_scan_kernel<1, 4>), dim3(HV, B, 4), dim3(256), 0, st, p);
+    else if (pairs * 2 <= cus) hipLaunchKernelGGL((gdn_scan_kernel<1, 8>), dim3(HV, B, 2), dim3(512), 0, st, p);
+    else hipLaunchKernelGGL((gdn_scan_kernel<2, 8>), dim3(HV, B, 1), dim3(512), 0, st, p);
     return mica_err(hipGetLastError());
 }
 

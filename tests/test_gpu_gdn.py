@@ -139,6 +139,22 @@ def test_scan_with_l2norm_in_kernel_and_empty_input(gpu):
     assert o0.shape == (1, 0, 2, 128) and torch.equal(h0out.cpu(), h0)
 
 
+def test_scan_dv_split_is_bit_identical(gpu):
+    """With fewer (sequence, head) pairs than CUs the scan splits the value columns over 2 or 4
+    workgroups per pair; every output element keeps its arithmetic, so a sequence scanned alone (4-way
+    split), with three others (2-way) or with seven others (no split) gives the same bits."""
+    from mica_amd import gdn
+    B, T, HK, HV = 8, 200, 16, 32
+    qb, kb, vb, gt, bt, h0 = _scan_inputs(17, B, T, HK, HV, True)
+    q, k, v, g, beta, s0 = (t.to(gpu) for t in (qb, kb, vb, gt, bt, h0))
+    o8, h8 = gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0, output_final_state=True)
+    for n in (1, 4):
+        o, hT = gdn.chunk_gated_delta_rule(q[:n], k[:n], v[:n], g[:n], beta[:n], initial_state=s0[:n],
+                                           output_final_state=True)
+        torch.cuda.synchronize()
+        assert torch.equal(o, o8[:n]) and torch.equal(hT, h8[:n]), n
+
+
 def test_scan_at_benchmark_shape_split_is_bit_identical(gpu):
     """8 sequences x 2048 tokens, 16 key / 32 value heads (the GDN layer of the 4B model at the prefill
     benchmark's shape).  Scanning tokens [0, 1024) then [1024, 2048) from the returned state gives the
