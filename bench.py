@@ -628,8 +628,17 @@ def serving_latency(torch, dev, st, reps=3):
     return out
 
 
+# the --pmc-workload runs, in launch order, 20 back-to-back launches each (the counter summaries label
+# the runs of >= 20 dispatches of one kernel with these names, in this order)
+PMC_WORKLOADS = (
+    "gemm_headline_4096x9728x2560", "gemm_qkv_4096x6144x2560", "gemm_o_residual_4096x2560x4096",
+    "gemm_gate_up_silu_4096x19456x2560", "gemm_down_residual_4096x2560x9728", "rmsnorm_quant_T4096",
+    "rmsnorm_quant_T32768", "act_quant_h_4096x9728", "copy_256MiB",
+)
+
+
 def pmc_workload():
-    """The kernels the committed counter summaries describe, each launched 20 times."""
+    """The kernels the committed counter summaries describe (PMC_WORKLOADS), each launched 20 times."""
     import torch
 
     from mica_amd import _lib, int8_kernels
@@ -637,26 +646,64 @@ def pmc_workload():
     dev = torch.device("cuda", torch.cuda.current_device())
     lib = _lib.load()
     st = torch.cuda.current_stream().cuda_stream
-    M, K, N = 4096, HIDDEN, INTER
-    x, qw, sw = synthetic(torch, dev, M, K, N, seed=0)
+    T = 4096
+    x, _, _ = synthetic(torch, dev, T, HIDDEN, 16, seed=0)
     qx, sx = int8_kernels.act_quant(x)
-    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    gemm = gemm_launcher(torch, lib, qx, sx, qw, sw, out)
-    T = 32768
-    h = torch.randn(T, K, device=dev).to(torch.bfloat16)
-    w = torch.ones(K, device=dev).to(torch.bfloat16)
-    q = torch.empty(T, K, dtype=torch.int8, device=dev)
-    s = torch.empty(T, dtype=torch.float32, device=dev)
-    a = (h.data_ptr(), _lib.BF16, K, None, K, w.data_ptr(), _lib.BF16, 0.0, 1e-6, None, q.data_ptr(), K,
-         s.data_ptr(), None, K, None, K, T, K, 0, st)
+    h = torch.randn(T, INTER, device=dev).to(torch.bfloat16)
+    qh, sh = int8_kernels.act_quant(h)
+    a4 = torch.randn(T, O_K, device=dev).to(torch.bfloat16)
+    qa, sa = int8_kernels.act_quant(a4)
+    res = torch.randn(T, HIDDEN, device=dev).to(torch.bfloat16)
+
+    def gemm(n, k, qa_, sa_, epilogue=0, residual=None):
+        g = torch.Generator(device="cpu").manual_seed(n + k)
+        qw = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
+        sw = torch.empty(n).uniform_(1e-3, 1e-2, generator=g).to(dev)
+        out = torch.empty(T, n // 2 if epilogue else n, dtype=torch.bfloat16, device=dev)
+        return gemm_launcher(torch, lib, qa_, sa_, qw, sw, out, residual=residual, epilogue=epilogue)
+
+    def norm(rows):
+        hx = torch.randn(rows, HIDDEN, device=dev).to(torch.bfloat16)
+        w = torch.ones(HIDDEN, device=dev).to(torch.bfloat16)
+        q = torch.empty(rows, HIDDEN, dtype=torch.int8, device=dev)
+        s = torch.empty(rows, dtype=torch.float32, device=dev)
+        args = (hx.data_ptr(), _lib.BF16, HIDDEN, None, HIDDEN, w.data_ptr(), _lib.BF16, 0.0, 1e-6, None,
+                q.data_ptr(), HIDDEN, s.data_ptr(), None, HIDDEN, None, HIDDEN, rows, HIDDEN, 0, st)
+
+        def run():
+            if lib.mica_rmsnorm_quant(*args) != 0:
+                raise RuntimeError("mica_rmsnorm_quant failed")
+        return run
+
+    qo = torch.empty(T, INTER, dtype=torch.int8, device=dev)
+    so = torch.empty(T, dtype=torch.float32, device=dev)
+    rq = (h.data_ptr(), _lib.BF16, INTER, None, qo.data_ptr(), INTER, so.data_ptr(), T, INTER, 0, st)
+
+    def requant():
+        if lib.mica_act_quant(*rq) != 0:
+            raise RuntimeError("mica_act_quant failed")
+
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(20):
-        gemm()
-        if lib.mica_rmsnorm_quant(*a) != 0:
-            raise RuntimeError("mica_rmsnorm_quant failed")
-        dst.copy_(src)  # 256 MiB read + 256 MiB written: the calibration of FETCH_SIZE / WRITE_SIZE
+    runs = {
+        "gemm_headline_4096x9728x2560": gemm(INTER, HIDDEN, qx, sx),
+        "gemm_qkv_4096x6144x2560": gemm(QKV_N, HIDDEN, qx, sx),
+        "gemm_o_residual_4096x2560x4096": gemm(HIDDEN, O_K, qa, sa, residual=res),
+        "gemm_gate_up_silu_4096x19456x2560": gemm(2 * INTER, HIDDEN, qx, sx, epilogue=1),
+        "gemm_down_residual_4096x2560x9728": gemm(HIDDEN, INTER, qh, sh, residual=res),
+        "rmsnorm_quant_T4096": norm(4096),
+        "rmsnorm_quant_T32768": norm(32768),
+        "act_quant_h_4096x9728": requant,
+        # 256 MiB read + 256 MiB written: the calibration of FETCH_SIZE / WRITE_SIZE
+        "copy_256MiB": lambda: dst.copy_(src),
+    }
+    marker = torch.zeros(1, device=dev)
     torch.cuda.synchronize()
+    for name in PMC_WORKLOADS:
+        marker.fill_(1.0)  # one other kernel between two runs, so that runs of the same kernel stay apart
+        for _ in range(20):
+            runs[name]()
+        torch.cuda.synchronize()
     print("pmc workload done", flush=True)
 
 
@@ -715,20 +762,44 @@ def summarize(indir, out_txt, command="", top=16):
                          f"{gx:9d} {wx:5d}  {k}")
     pmc = sorted(glob.glob(os.path.join(indir, "**", "*counter_collection.csv"), recursive=True))
     for f in pmc:
-        agg = defaultdict(list)
+        # dispatches in launch order; runs of >= 20 back-to-back dispatches of one kernel are the
+        # --pmc-workload's runs, labelled with PMC_WORKLOADS in order (other kernels keep their names)
+        disp = {}
         for r in csv.DictReader(open(f)):
-            agg[(r["Kernel_Name"][:150], r["Counter_Name"])].append(float(r["Counter_Value"]))
+            d = disp.setdefault(int(r["Dispatch_Id"]), {"kernel": r["Kernel_Name"][:150], "c": {}})
+            d["c"][r["Counter_Name"]] = float(r["Counter_Value"])
+        order = [disp[i] for i in sorted(disp)]
+        runs, cur = [], None
+        for d in order:
+            if cur is not None and cur[0] == d["kernel"]:
+                cur[1].append(d)
+            else:
+                cur = (d["kernel"], [d])
+                runs.append(cur)
+        long_runs = [r_ for r_ in runs if len(r_[1]) >= 20]
+        labels = {}
+        if len(long_runs) == len(PMC_WORKLOADS):
+            for (k, ds), name in zip(long_runs, PMC_WORKLOADS):
+                for d in ds:
+                    labels[id(d)] = f"[{name}] {k}"
+        agg = defaultdict(list)
+        for d in order:
+            key = labels.get(id(d), d["kernel"])
+            for c, v in d["c"].items():
+                agg[(key, c)].append(v)
         lines.append(f"# counters per dispatch, mean over dispatches ({os.path.basename(f)})")
         for (k, c), v in sorted(agg.items()):
             lines.append(f"{c:28s} {sum(v) / len(v):16.1f}  n={len(v):3d}  {k}")
+        labelled = any(k.startswith("[copy_256MiB]") for k, _ in agg)
         copy = {c: sum(v) / len(v) for (k, c), v in agg.items()
-                if ("copyBuffer" in k or "copy_kernel" in k) and c in ("FETCH_SIZE", "WRITE_SIZE") and sum(v) > 0}
+                if (k.startswith("[copy_256MiB]") if labelled else ("copyBuffer" in k or "copy_kernel" in k))
+                and c in ("FETCH_SIZE", "WRITE_SIZE") and sum(v) > 0}
         for c, kib in copy.items():
             factor = (256 << 20) / (kib * 1024.0)
             lines.append(f"# calibration: the 256 MiB copy (256 MiB read, 256 MiB written) counts {c} = {kib:.1f} KiB "
                          f"-> bytes = KiB x 1024 x {factor:.4f}")
             for (k, c2), v in sorted(agg.items()):
-                if c2 == c and "copyBuffer" not in k:
+                if c2 == c and "copyBuffer" not in k and not k.startswith("[copy_256MiB]"):
                     lines.append(f"{c2 + '_bytes':28s} {sum(v) / len(v) * 1024.0 * factor:16.0f}  {k}")
         # derived figures per kernel.  GRBM_GUI_ACTIVE comes summed over the XCCs; rocprofv3's own
         # MfmaUtil divides the SIMD-summed MFMA busy cycles by the per-XCC active cycles x SIMD count
