@@ -810,7 +810,19 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
                          (!residual || (long long)kTile * ldr * 4 < (1ll << 31));
     if (wide_ok) {
         if (rem == 0 && cus > 0 && tiles > cus) grid = cus;
-        return wide_launch(p, epilogue, out_dtype, grid, hb, hr, st);
+        // One partial round of whole tiles with no tail pieces (more than half the CUs busy, e.g.
+        // 4096 x 2560: 160 tiles on 256 CUs) runs as 256 x 160 tiles instead when those still fit one
+        // round (256 of them there): each costs about 0.65 of a whole tile and more CUs work.
+        const long long tiles160 = (long long)p.tiles_m * ((N + 159) / 160);
+        const bool narrow = epilogue == MICA_EPI_SCALE && (out_dtype == MICA_BF16 || out_dtype == MICA_FP16) &&
+                            cus > 0 && p.dp_tiles == tiles && tiles < cus && tiles160 > tiles && tiles160 <= cus &&
+                            (long long)(N + 160) * ldb < (1ll << 31);
+        if (narrow) {
+            p.tiles_n = (N + 159) / 160;
+            p.dp_tiles = (int)tiles160;
+            grid = (int)tiles160;
+        }
+        return wide_launch(p, epilogue, out_dtype, grid, hb, hr, narrow, st);
     }
     if (epilogue == MICA_EPI_SILU_MUL) return launch_out<MICA_EPI_SILU_MUL, MICA_BF16>(p, grid, false, false, st);
     if (out_dtype == MICA_BF16) return launch_out<MICA_EPI_SCALE, MICA_BF16>(p, grid, hb, hr, st);

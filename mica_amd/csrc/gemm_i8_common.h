@@ -28,7 +28,7 @@ struct GemmParams {
     void *C;
     int lda, ldb, ldr, ldc;
     int M, N, K;
-    int tiles_m, tiles_n; // 256 x 256 tiles
+    int tiles_m, tiles_n; // 256 x 256 tiles (the wide kernel's narrow schedule: 256 x 160)
     int vec_ok;           // ldc, ldr, N all multiples of 4: 4-column vector stores
     // schedule over the tiles in grouped order (tile_of): [0, dp_tiles) run whole, one per workgroup
     // per round; the next half_tiles run as two 256 x 128 halves each, or the next quarter_tiles as
@@ -121,7 +121,7 @@ MICA_DEVICE void load4_res(const void *R, long off, float (&v)[4], int valid, bo
 
 // the wide kernel's launcher (gemm_i8_wide.hip)
 int wide_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool has_bias, bool has_res,
-                hipStream_t st);
+                bool narrow, hipStream_t st);
 
 }  // namespace mica_gemm
 

@@ -54,13 +54,26 @@ struct WCfg {
     static constexpr int kBHalf = BN * WBK;                  // one stage of B
     static constexpr int kBBase = 2 * kAHalf;                // B stages follow both A stages
     static constexpr int kADma = BM / 8 / kWideWaves;        // 1 KiB DMA instructions per wave per slab
-    static constexpr int kBDma = BN / 8 / kWideWaves;
-    static constexpr int kDma = kADma + kBDma;
+    // B's 8-row blocks: the first kBWide waves take kBDma of them, the others kBDma - 1 (BN = 160: 3, 2)
+    static constexpr int kBBlocks = BN / 8;
+    static constexpr int kBDma = (kBBlocks + kWideWaves - 1) / kWideWaves;
+    static constexpr int kBWide = kBBlocks - (kBDma - 1) * kWideWaves;
+    static constexpr int kDma = kADma + kBDma;               // the most any wave issues per slab
+    static_assert(BM % (8 * kWideWaves) == 0 && BN % 8 == 0, "DMA blocks");
+    MICA_DEVICE static int bdma_count(int wave) {
+        if constexpr (kBWide == kWideWaves) return kBDma;
+        else return wave < kBWide ? kBDma : kBDma - 1;
+    }
+    MICA_DEVICE static int bdma_first(int wave) {
+        if constexpr (kBWide == kWideWaves) return wave * kBDma;
+        else return wave < kBWide ? wave * kBDma : kBWide * kBDma + (wave - kBWide) * (kBDma - 1);
+    }
 };
 using WFull = WCfg<256, 256>;   // waves of 64 x 128
 using WHalfN = WCfg<256, 128>;  // waves of 64 x 64 (SCALE tail)
 using WHalfM = WCfg<128, 256>;  // waves of 32 x 128 (SiLU tail)
 using WQuart = WCfg<128, 128>;  // waves of 32 x 64 (SCALE tail at most a quarter of a round)
+using W160 = WCfg<256, 160>;    // waves of 64 x 80: whole tiles for N = 2560 at M = 4096 (256 tiles)
 
 // LDS: A stages 0 and 1, then B stages 0 and 1 (every operand read of either stage then reaches
 // its data with the 16-bit offset of ds_read_b128 from one base register per operand and k-step).
@@ -103,7 +116,8 @@ struct WideTile {
     static constexpr int kPitch = kCols * 2 + 16;
     static constexpr int kPassRows = (WM * kPitch <= 64 * 144) ? WM : WM / 2;
     static constexpr int kPasses = WM / kPassRows;
-    static constexpr int kLanesPerRow = kCols / 8;   // lanes x 8 columns per row
+    // lanes per staged row (8 columns each; a power of 2, lanes past kCols / 8 idle: kCols = 80 -> 16)
+    static constexpr int kLanesPerRow = kCols / 8 <= 8 ? 8 : (kCols / 8 <= 16 ? 16 : 32);
     static constexpr int kRowsPerStore = 64 / kLanesPerRow;
     static constexpr int kReadsPerPass = kPassRows / kRowsPerStore;
     static constexpr int kStores = k16 ? WM / kRowsPerStore : 0;
@@ -113,6 +127,19 @@ struct WideTile {
     static_assert(C::kBBase + C::kBHalf + (kWideWaves - kLowWaves) * kRegion <= kWScale, "staging");
     static_assert(kPassRows % 16 == 0 && kPassRows % kRowsPerStore == 0, "passes");
     static_assert(C::kDma + kStores < 64, "vmcnt");
+    static_assert(kCols % 8 == 0 && kCols / 8 <= kLanesPerRow && kLanesPerRow <= 64, "staged rows");
+
+    // s_waitcnt until this wave has at most N + (its DMA instructions per slab) vector memory operations
+    // outstanding (the count differs between waves when B's blocks do not divide evenly)
+    template <int N>
+    MICA_DEVICE static void wait_dma_plus(int wave) {
+        if constexpr (C::kBWide == kWideWaves) {
+            wait_vmcnt<C::kDma + N>();
+        } else {
+            if (wave < C::kBWide) wait_vmcnt<C::kDma + N>();
+            else wait_vmcnt<C::kDma - 1 + N>();
+        }
+    }
 
     v4i acc[NB][MB];
 
@@ -134,16 +161,18 @@ struct WideTile {
                                      __amdgpu_buffer_rsrc_t rsrc_b, int wave, int m0, int n0, int slab, int stage) {
         const int lane = fresh_lane();
         const int kb = slab * WBK;
+        const int bfirst = C::bdma_first(wave), bcount = C::bdma_count(wave);
         const int a0 = dma_base(m0 + wave * C::kADma * 8, p.lda, lane);
-        const int b0 = dma_base(n0 + wave * C::kBDma * 8, p.ldb, lane);
+        const int b0 = dma_base(n0 + bfirst * 8, p.ldb, lane);
         int8_t *sa_ = smem + stage * C::kAHalf + wave * C::kADma * 1024;
-        int8_t *sb_ = smem + C::kBBase + stage * C::kBHalf + wave * C::kBDma * 1024;
+        int8_t *sb_ = smem + C::kBBase + stage * C::kBHalf + bfirst * 1024;
 #pragma unroll
         for (int j = 0; j < C::kADma; ++j)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void *)(sa_ + j * 1024), 16, a0 + j * 8 * p.lda, kb, 0, 0);
 #pragma unroll
         for (int j = 0; j < C::kBDma; ++j)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_void *)(sb_ + j * 1024), 16, b0 + j * 8 * p.ldb, kb, 0, 0);
+            if (j < bcount)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_void *)(sb_ + j * 1024), 16, b0 + j * 8 * p.ldb, kb, 0, 0);
     }
 
     // tile (m0, n0)'s scales into scale buffer buf by LDS DMA (no VGPRs held while they travel):
@@ -176,21 +205,23 @@ struct WideTile {
         const int wm = wave >> 1, wn = wave & 1;
         const int r16 = lane & 15, kq = lane >> 4;
         const int nk = p.K / WBK;  // even
+        const int bfirst = C::bdma_first(wave), bcount = C::bdma_count(wave);
         const int a0 = opaque(dma_base(m0 + wave * C::kADma * 8, p.lda, lane));
-        const int b0 = opaque(dma_base(n0 + wave * C::kBDma * 8, p.ldb, lane));
+        const int b0 = opaque(dma_base(n0 + bfirst * 8, p.ldb, lane));
         // the per-instruction offsets are formed at each DMA (one add each): held across the loop
         // they would cost 6 more VGPRs
         auto dma = [&](int slab) {
             const int kb = slab * WBK;
             const int a = opaque(a0), b = opaque(b0);
             int8_t *sa_ = smem + (slab & 1) * C::kAHalf + wave * C::kADma * 1024;
-            int8_t *sb_ = smem + C::kBBase + (slab & 1) * C::kBHalf + wave * C::kBDma * 1024;
+            int8_t *sb_ = smem + C::kBBase + (slab & 1) * C::kBHalf + bfirst * 1024;
 #pragma unroll
             for (int j = 0; j < C::kADma; ++j)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void *)(sa_ + j * 1024), 16, a + j * 8 * p.lda, kb, 0, 0);
 #pragma unroll
             for (int j = 0; j < C::kBDma; ++j)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_void *)(sb_ + j * 1024), 16, b + j * 8 * p.ldb, kb, 0, 0);
+                if (j < bcount)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (lds_void *)(sb_ + j * 1024), 16, b + j * 8 * p.ldb, kb, 0, 0);
         };
         // operand reads: k-step s of row r is chunk 4 s + kq.  The stage and the 16-row block are
         // compile-time offsets (they fit the 16-bit offset of ds_read_b128), so two base registers per
@@ -310,7 +341,10 @@ struct WideTile {
                                                   : C::kBBase + C::kBHalf + (wave - kLowWaves) * kRegion);
             const int col0 = EPI == MICA_EPI_SCALE ? n0 + wn * WN : (n0 >> 1) + wn * (WN / 2);
             const int ncols_out = EPI == MICA_EPI_SCALE ? N : (N >> 1);
-            const int cl = (lane % kLanesPerRow) * 8;  // local column of this lane's 8 values
+            // local column of this lane's 8 values (lanes past the wave's columns read a valid place and
+            // store nothing)
+            const bool lane_on = kCols / 8 == kLanesPerRow || (lane % kLanesPerRow) * 8 < kCols;
+            const int cl = lane_on ? (lane % kLanesPerRow) * 8 : kCols - 8;
             u32x4 outv[kStores];
 #pragma unroll
             for (int pass = 0; pass < kPasses; ++pass) {
@@ -359,7 +393,7 @@ struct WideTile {
             // output row of store s: mw + s * kRowsPerStore + lane / kLanesPerRow
             const bool fast = vec && (p.ldc % 8 == 0) && (!HAS_RES || p.ldr % 8 == 0) && (ncols_out % 8 == 0);
             const int rows_in = M - m0 < C::BM ? M - m0 : C::BM;  // valid rows of this tile
-            const bool col_ok = col0 + cl < ncols_out;             // with fast: all 8 columns, or none
+            const bool col_ok = lane_on && col0 + cl < ncols_out;  // with fast: all 8 columns, or none
             u32x4 rv[HAS_RES ? kStores : 1];
             if (fast && HAS_RES) {
                 const __amdgpu_buffer_rsrc_t rsrc_r = __builtin_amdgcn_make_buffer_rsrc(
@@ -399,7 +433,7 @@ struct WideTile {
                 }
             } else {
                 // unaligned output: element stores, then nothing left in flight
-                const int valid = ncols_out - (col0 + cl) < 8 ? (ncols_out - (col0 + cl) > 0 ? ncols_out - (col0 + cl) : 0) : 8;
+                const int valid = !lane_on ? 0 : ncols_out - (col0 + cl) < 8 ? (ncols_out - (col0 + cl) > 0 ? ncols_out - (col0 + cl) : 0) : 8;
 #pragma unroll
                 for (int s = 0; s < kStores; ++s) {
                     const int m = mw + s * kRowsPerStore + lane / kLanesPerRow;
@@ -497,7 +531,7 @@ MICA_DEVICE void run_phase(const GemmParams &p, int8_t *smem, __amdgpu_buffer_rs
     Tile::scales_dma(p, smem, wave, 0, m0, n0);
     Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 0, 0);
     Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 1, 1);
-    wait_vmcnt<C::kDma>();  // scales and slab 0 landed (slab 1 may be in flight)
+    Tile::template wait_dma_plus<0>(wave);  // scales and slab 0 landed (slab 1 may be in flight)
     __builtin_amdgcn_s_barrier();
     int buf = 0;
     for (;;) {
@@ -508,7 +542,7 @@ MICA_DEVICE void run_phase(const GemmParams &p, int8_t *smem, __amdgpu_buffer_rs
         t.epilogue(p, smem, rsrc_a, rsrc_b, wave, m0, n0, buf, has_next, m0n, n0n);
         if (!has_next) break;
         // the next tile's slab 0 and scales landed: all but this epilogue's stores and its slab 1
-        wait_vmcnt<C::kDma + Tile::kStores>();
+        Tile::template wait_dma_plus<Tile::kStores>(wave);
         __builtin_amdgcn_s_barrier();
         buf ^= 1;
         h = hn;
@@ -517,7 +551,7 @@ MICA_DEVICE void run_phase(const GemmParams &p, int8_t *smem, __amdgpu_buffer_rs
     }
 }
 
-template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES>
+template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES, bool NARROW>
 __global__ __launch_bounds__(kWideThreads, 1) void gemm_i8_wide_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[kWSmem];
     static_assert(EPI == MICA_EPI_SCALE || WFull::WN == 128, "the SiLU epilogue needs one 128-row gate/up group per wave");
@@ -526,6 +560,18 @@ __global__ __launch_bounds__(kWideThreads, 1) void gemm_i8_wide_kernel(GemmParam
     const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, p.N * p.ldb, kBufferFlags);
     const int tm_n = p.tiles_m, tn_n = p.tiles_n, dp = p.dp_tiles, M = p.M, N = p.N;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    if constexpr (NARROW) {
+        // 256 x 160 tiles only (tiles_n counts 160-column tiles)
+        run_phase<W160, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, dp, G,
+                                                     [&](int h, int &m0, int &n0) {
+                                                         int tm, tn;
+                                                         tile_of(h, tm_n, tn_n, tm, tn);
+                                                         m0 = tm * 256;
+                                                         n0 = tn * 160;
+                                                         return true;
+                                                     });
+        return;
+    }
     run_phase<WFull, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, dp, G,
                                                   [&](int h, int &m0, int &n0) {
                                                       int tm, tn;
@@ -569,11 +615,12 @@ __global__ __launch_bounds__(kWideThreads, 1) void gemm_i8_wide_kernel(GemmParam
     }
 }
 
-template <int EPI, int OUT>
+template <int EPI, int OUT, bool NARROW = false>
 int wide_launch_out(const GemmParams &p, int grid, bool has_bias, bool has_res, hipStream_t st) {
     dim3 g(grid), b(kWideThreads);
-#define MICA_W(B_, R_) hipLaunchKernelGGL((gemm_i8_wide_kernel<EPI, OUT, B_, R_>), g, b, 0, st, p)
+#define MICA_W(B_, R_) hipLaunchKernelGGL((gemm_i8_wide_kernel<EPI, OUT, B_, R_, NARROW>), g, b, 0, st, p)
     if constexpr (EPI == MICA_EPI_SILU_MUL || OUT == MICA_INT32) {
+        static_assert(!NARROW, "narrow tiles: SCALE epilogue with 16-bit outputs only");
         MICA_W(false, false);
     } else {
         if (has_bias && has_res) MICA_W(true, true);
@@ -590,8 +637,16 @@ int wide_launch_out(const GemmParams &p, int grid, bool has_bias, bool has_res, 
 // Launch of the wide kernel for the schedule in p (dp_tiles whole tiles, then half_tiles, quarter_tiles
 // or mhalf_tiles as pieces; no split).  Called by mica_mm_i8 after its checks, only for K % 256 == 0
 // and row pitches whose 256-row tile spans stay below 2^31 bytes (the buffer offsets of the stores).
+// narrow: dp_tiles 256 x 160 tiles and nothing else (SCALE epilogue, bf16 / fp16 outputs).
 int mica_gemm::wide_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool has_bias, bool has_res,
-                           hipStream_t st) {
+                           bool narrow, hipStream_t st) {
+    if (narrow) {
+        if (epilogue != MICA_EPI_SCALE || p.half_tiles || p.quarter_tiles || p.mhalf_tiles || p.sk_tiles)
+            return MICA_MISS_ARG;
+        if (out_dtype == MICA_BF16) return wide_launch_out<MICA_EPI_SCALE, MICA_BF16, true>(p, grid, has_bias, has_res, st);
+        if (out_dtype == MICA_FP16) return wide_launch_out<MICA_EPI_SCALE, MICA_FP16, true>(p, grid, has_bias, has_res, st);
+        return MICA_MISS_ARG;
+    }
     if (epilogue == MICA_EPI_SILU_MUL) return wide_launch_out<MICA_EPI_SILU_MUL, MICA_BF16>(p, grid, false, false, st);
     if (out_dtype == MICA_BF16) return wide_launch_out<MICA_EPI_SCALE, MICA_BF16>(p, grid, has_bias, has_res, st);
     if (out_dtype == MICA_FP16) return wide_launch_out<MICA_EPI_SCALE, MICA_FP16>(p, grid, has_bias, has_res, st);

@@ -344,6 +344,34 @@ def test_gemm_residual_epilogue(gpu, m, n, k):
     assert np.array_equal(bits_of(y), ref)
 
 
+@pytest.mark.parametrize("m,n,k,epi", [
+    (4096, 2560, 4096, "residual"),  # the O projection at T = 4096: 160 whole tiles -> 256 tiles of 256 x 160
+    (4096, 2560, 9728, "bias"),      # the down projection's shape
+    (3900, 2504, 2560, "residual"),  # both edges ragged; the last tile's upper half 24 columns wide
+    (3900, 2500, 512, "fp16"),       # N not a multiple of 8: element stores
+])
+def test_gemm_narrow_tiles_bit_exact(gpu, m, n, k, epi):
+    """One partial round of whole tiles (more than half the CUs busy) runs as 256 x 160 tiles when those
+    still fit one round.  Bit-exact with the oracle, int32 accumulators included."""
+    note(f"gemm narrow m={m} n={n} k={k} epi={epi}")
+    rng = np.random.default_rng(m * 7 + n + k)
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    tA, tB, tsa, tsb = (torch.from_numpy(v).cuda() for v in (A, B, sa, sb))
+    acc = O.int_gemm(A, B)
+    if epi == "residual":
+        res = act_bits(rng, (m, n), outliers=0)
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, residual=to_gpu_bf16(res))
+        ref = O.f32_to_bf16(O.bf16_to_f32(O.epilogue(acc, sa, sb)) + O.bf16_to_f32(res))
+        assert_equal_diag(bits_of(y), ref, "bf16 + residual")
+    elif epi == "bias":
+        bias = rng.uniform(-1, 1, n).astype(np.float32)
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, torch.from_numpy(bias).cuda())
+        assert_equal_diag(bits_of(y), O.epilogue(acc, sa, sb, bias), "bf16 + bias")
+    else:
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, out_dtype=torch.float16)
+        assert_equal_diag(y.cpu().numpy(), O.epilogue(acc, sa, sb, None, "fp16"), "fp16")
+
+
 def test_gemm_headline_full_size(gpu):
     """The benchmarked GEMM itself, M=4096 K=2560 N=9728 (every tile, including the partial last round
     of tiles), bit-exact: int32 accumulators and the bf16 output.  Then a size-independent property
