@@ -109,9 +109,15 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
 // (tests/native/quotient_check.c, exhaustive).  For other values (SmoothQuant-scaled rows, fp16 and
 // fp32 activations) the plain product y = x * r is used: it is within 2^-16 of x / s for |x / s| <=
 // 127.5 (r's rounding and y's), so its integer can only differ from the IEEE quotient's near a rounding
-// boundary: lanes whose y lies within 2^-13 of k + 0.5 recompute it with the IEEE division
-// (tests/native/guarded_quotient_check.c: 2^28 samples, no mismatch, the slow path on ~5e-5 of the
-// values).
+// boundary: lanes whose y lies within 2^-13 of k + 0.5 (|fract(y) - 0.5| <= 2^-13, v_fract_f32)
+// recompute it with the IEEE division (tests/native/guarded_quotient_check.c: 2^28 samples, no
+// mismatch, the slow path on ~5e-5 of the values).
+//
+// Half even without kFast is one step shorter: the exact product x r (one FMA with 1.5 * 2^23) is
+// rounded to an integer directly, and the guard looks at u = fma(x, r, 0.5 + 2^-13): x r within
+// 2^-16 of k + 0.5 puts fract(u) below 2^-12 (|x r - x / s| < 2^-17, u's own rounding < 2^-17), so
+// the lanes whose exact product lies within ~2^-13 of a tie take the IEEE division
+// (tests/native/guarded_quotient_check.c checks this form as well).
 //
 // Half even rounds with the 1.5 * 2^23 trick: for |t| < 2^22, t + 12582912 is an integer-valued
 // float (its rounding is the IEEE round-half-even of t), whose low mantissa byte is that integer in
@@ -121,6 +127,29 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
 // holding Inf or NaN yields 0 for those elements).
 template <bool kFast, int RND>
 MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int rounding, int8_t *dst) {
+    const int mode = RND == 2 ? rounding : RND;
+    if (!kFast && mode == MICA_ROUND_EVEN) {
+        uint32_t b[kChunk];
+        float low = 1.0f;
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            b[j] = __float_as_uint(__builtin_fmaf(v[j], r, kMagicRne));
+            low = __builtin_fminf(low, __builtin_amdgcn_fractf(__builtin_fmaf(v[j], r, 0.5f + 0x1p-13f)));
+        }
+        if (low < 0x1p-12f) {
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) b[j] = __float_as_uint(v[j] / s + kMagicRne);
+        }
+        u32x2 packed;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t lo = __builtin_amdgcn_perm(b[4 * h + 1], b[4 * h], 0x0c0c0400u);
+            const uint32_t hi = __builtin_amdgcn_perm(b[4 * h + 3], b[4 * h + 2], 0x0c0c0400u);
+            packed[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+        __builtin_nontemporal_store(packed, (u32x2 *)dst);
+        return;
+    }
     float t[kChunk];
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
@@ -128,17 +157,18 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
         t[j] = kFast ? __builtin_fmaf(__builtin_fmaf(-y, s, v[j]), r, y) : y;
     }
     if (!kFast) {
-        bool near = false;
+        // fract(y) - 0.5 is exact; v_fract_f32 returns at most 1 - 2^-24 (for tiny negative y), far
+        // from the window
+        float gap = 1.0f;
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j)
-            near = near || __builtin_fabsf(__builtin_fabsf(t[j] - __builtin_rintf(t[j])) - 0.5f) <= 0x1p-13f;
+        for (int j = 0; j < kChunk; ++j) gap = __builtin_fminf(gap, __builtin_fabsf(__builtin_amdgcn_fractf(t[j]) - 0.5f));
+        const bool near = gap <= 0x1p-13f;
         if (near) {
 #pragma unroll
             for (int j = 0; j < kChunk; ++j) t[j] = v[j] / s;
         }
     }
     u32x2 packed;
-    const int mode = RND == 2 ? rounding : RND;
     if (mode == MICA_ROUND_EVEN) {
         uint32_t b[kChunk];
 #pragma unroll
@@ -418,6 +448,124 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
     row16_body<NCH, XT, NORM, true, FULL, RND>(p);
 }
 
+// Smoothed bf16 rows of exactly NCH * 512 elements where each of the NOUT outputs has its own
+// factors, one row per wave with every row of the launch resident at once.  Against the grid-stride
+// kernel above: no next row held, the norm's multipliers offset + w formed once per workgroup in LDS
+// next to the factors, no run-time test of which outputs are smoothed, and each output's smoothed
+// row held in registers from its absmax to its quantizer.  Same arithmetic, same bits: the row
+// (+ residual, rounded to bf16), the norm (x * rstd) * (offset + w) rounded to bf16, t = x * inv in
+// fp32, s = max(absmax(t), 1e-8) / 127, q from the guarded quotient t / s.
+#ifndef MICA_SMOOTH_THREADS
+#define MICA_SMOOTH_THREADS 1024
+#endif
+constexpr int kSmoothThreads = MICA_SMOOTH_THREADS;  // a whole CU's 16 rows share one copy of the factors
+template <int NCH, bool NORM, int NOUT, int RND>
+__global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(4))) void smooth_one_kernel(RowParams p) {
+    constexpr int XT = MICA_BF16;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kSmoothThreads / 64) + (threadIdx.x >> 6);
+    const bool on = row < p.M;
+    const bool has_res = NORM && p.res != nullptr;
+    u32x4 cur[NCH], rc[NORM ? NCH : 1];
+    if (on) {
+        const uint16_t *xr = (const uint16_t *)p.x + (long)row * p.ldx;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) cur[c] = *(const u32x4 *)(xr + c * kRowStep + lane * kChunk);
+        if (has_res) {
+            const uint16_t *rr = (const uint16_t *)p.res + (long)row * p.ldr;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) rc[NORM ? c : 0] = *(const u32x4 *)(rr + c * kRowStep + lane * kChunk);
+        }
+    }
+    // every output's factors into LDS: chunk ch = c * 64 + lane of output o at float4 pair
+    // ((o * NCH + c) * 64 + lane) * 2; with the norm, the multipliers offset + w (fp32) after them as
+    // output NOUT
+    extern __shared__ float4 inv_sh[];
+#pragma unroll
+    for (int o = 0; o < NOUT; ++o) {
+        for (int ch = threadIdx.x; ch < NCH * 64; ch += kSmoothThreads) {
+            inv_sh[(o * NCH * 64 + ch) * 2] = ((const float4 *)(p.inv[o] + ch * kChunk))[0];
+            inv_sh[(o * NCH * 64 + ch) * 2 + 1] = ((const float4 *)(p.inv[o] + ch * kChunk))[1];
+        }
+    }
+    if (NORM) {
+        for (int ch = threadIdx.x; ch < NCH * 64; ch += kSmoothThreads) {
+            float wv[kChunk];
+            unpack8<MICA_BF16>(*(const u32x4 *)((const uint16_t *)p.w + ch * kChunk), wv);
+            inv_sh[(NOUT * NCH * 64 + ch) * 2] = float4{p.offset + wv[0], p.offset + wv[1], p.offset + wv[2], p.offset + wv[3]};
+            inv_sh[(NOUT * NCH * 64 + ch) * 2 + 1] = float4{p.offset + wv[4], p.offset + wv[5], p.offset + wv[6], p.offset + wv[7]};
+        }
+    }
+    __syncthreads();
+    if (!on) return;
+
+    float v[NCH][kChunk];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = c * kRowStep + lane * kChunk;
+        if (has_res) {
+            // v = (x + r) rounded to the activation dtype (fused_kernels.py:27-30, :52)
+            float b[kChunk];
+            unpack8<XT>(cur[c], v[c]);
+            unpack8<XT>(rc[NORM ? c : 0], b);
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) v[c][j] = v[c][j] + b[j];
+            cur[c] = pack8<XT>(v[c]);
+            if (p.sum != nullptr) *(u32x4 *)((uint16_t *)p.sum + (long)row * p.lds + idx) = cur[c];
+        }
+        unpack8<XT>(cur[c], v[c]);
+    }
+    auto factors = [&](int o, int c, float (&iv)[kChunk]) {
+        const float4 a = inv_sh[((o * NCH + c) * 64 + lane) * 2];
+        const float4 b = inv_sh[((o * NCH + c) * 64 + lane) * 2 + 1];
+        iv[0] = a.x; iv[1] = a.y; iv[2] = a.z; iv[3] = a.w;
+        iv[4] = b.x; iv[5] = b.y; iv[6] = b.z; iv[7] = b.w;
+    };
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) ss = __builtin_fmaf(v[c][j], v[c][j], ss);
+        ss = wave_sum(ss);
+        const float mean = ss / (float)p.K;
+        const float rstd = 1.0f / __builtin_sqrtf(mean + p.eps);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            float w1[kChunk];
+            factors(NOUT, c, w1);
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) v[c][j] = (v[c][j] * rstd) * w1[j];
+            const u32x4 packed = pack8<XT>(v[c]);
+            unpack8<XT>(packed, v[c]);
+            if (p.y != nullptr) *(u32x4 *)((uint16_t *)p.y + (long)row * p.ldy + c * kRowStep + lane * kChunk) = packed;
+        }
+    }
+    // one output at a time: its smoothed row t stays in registers from the absmax to the quantizer
+    // (the factors are read from LDS once per output)
+#pragma unroll
+    for (int o = 0; o < NOUT; ++o) {
+        float t[NCH][kChunk];
+        float am = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            float iv[kChunk];
+            factors(o, c, iv);
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) {
+                t[c][j] = v[c][j] * iv[j];
+                am = __builtin_fmaxf(am, __builtin_fabsf(t[c][j]));
+            }
+        }
+        const float sc = row_scale(wave_max(am));
+        const float rr = 1.0f / sc;
+        if (lane == 0) p.s[o][row] = sc;
+        int8_t *qrow = p.q[o] + (long)row * p.ldq[o] + lane * kChunk;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) quant_store8r<false, RND>(t[c], sc, rr, p.rounding, qrow + c * kRowStep);
+    }
+}
+
 template <int NCH, int XT, bool NORM, bool HAS_INV, bool FULL, int RND>
 constexpr void (*row16_for())(RowParams) {
     if constexpr (HAS_INV && NCH <= 5) return row16_smooth_kernel<NCH, XT, NORM, FULL, RND>;
@@ -577,6 +725,32 @@ int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st
 #undef MICA_ROW16
 }
 
+// smooth_one_kernel when every row of the launch fits the resident waves; -1 otherwise (the caller
+// then takes the grid-stride path)
+template <int NCH, bool NORM, int NOUT, int RND>
+int launch_smooth_one(const RowParams &p, hipStream_t st) {
+    constexpr auto kern = smooth_one_kernel<NCH, NORM, NOUT, RND>;
+    const unsigned lds = (unsigned)((NOUT + (NORM ? 1 : 0)) * NCH * 64 * 2 * sizeof(float4));
+    static std::atomic<int> cached{0};
+    int per_cu = cached.load(std::memory_order_relaxed);
+    if (per_cu <= 0) {
+        int occ = 0;
+        per_cu = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kSmoothThreads, lds) == hipSuccess && occ > 0 ? occ : 1;
+        cached.store(per_cu, std::memory_order_relaxed);
+    }
+    constexpr int kRows = kSmoothThreads / 64;
+    const long long blocks = ((long long)p.M + kRows - 1) / kRows;
+    if (blocks > (long long)cu_count_of_current_device() * per_cu) return -1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kSmoothThreads), lds, st, p);
+    return mica_err(hipGetLastError());
+}
+
+template <int NCH, bool NORM, int NOUT>
+int launch_smooth_one_rnd(const RowParams &p, hipStream_t st) {
+    if (p.rounding == MICA_ROUND_EVEN) return launch_smooth_one<NCH, NORM, NOUT, MICA_ROUND_EVEN>(p, st);
+    return launch_smooth_one<NCH, NORM, NOUT, MICA_ROUND_AWAY>(p, st);
+}
+
 // bf16 rows of exactly NCH * 512 elements (the hot widths): no masks, rounding fixed at compile time
 template <int NCH>
 int launch16_full(const RowParams &p, bool norm, bool has_inv, hipStream_t st) {
@@ -588,6 +762,22 @@ int launch16_full(const RowParams &p, bool norm, bool has_inv, hipStream_t st) {
             else if (norm) rc = launch_one<row16_one_kernel<NCH, MICA_BF16, true, true, MICA_ROUND_AWAY>>(p, st);
             else if (p.rounding == MICA_ROUND_EVEN) rc = launch_one<row16_one_kernel<NCH, MICA_BF16, false, true, MICA_ROUND_EVEN>>(p, st);
             else rc = launch_one<row16_one_kernel<NCH, MICA_BF16, false, true, MICA_ROUND_AWAY>>(p, st);
+            if (rc >= 0) return rc;
+        }
+        // every output smoothed (1 to 3 of them): one wave per row when they all fit
+        bool all_inv = has_inv && p.n_out <= 3 && (!norm || p.w_dtype == MICA_BF16);
+        for (int o = 0; o < p.n_out; ++o) all_inv = all_inv && p.inv[o] != nullptr;
+        if (all_inv) {
+            int rc = -1;
+            if (norm) {
+                if (p.n_out == 1) rc = launch_smooth_one_rnd<NCH, true, 1>(p, st);
+                else if (p.n_out == 2) rc = launch_smooth_one_rnd<NCH, true, 2>(p, st);
+                else rc = launch_smooth_one_rnd<NCH, true, 3>(p, st);
+            } else {
+                if (p.n_out == 1) rc = launch_smooth_one_rnd<NCH, false, 1>(p, st);
+                else if (p.n_out == 2) rc = launch_smooth_one_rnd<NCH, false, 2>(p, st);
+                else rc = launch_smooth_one_rnd<NCH, false, 3>(p, st);
+            }
             if (rc >= 0) return rc;
         }
     }

@@ -191,6 +191,44 @@ def test_rmsnorm_quant_multi_consumers(gpu, T, K, n):
         assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32)), f"consumer {i} vs oracle"
 
 
+@pytest.mark.parametrize("T,n,res,rounding", [
+    (4096, 3, True, "even"),    # q / k / v of a smoothed model at T = 4096: every row resident at once
+    (4096, 2, False, "even"),   # gate / up
+    (333, 3, True, "away"),
+    (5, 1, True, "even"),       # fewer rows than waves in a workgroup
+    (20000, 3, True, "even"),   # more rows than resident waves: the grid-stride kernel
+])
+def test_rmsnorm_quant_all_consumers_smoothed(gpu, T, n, res, rounding):
+    """Every consumer with its own SmoothQuant factors (K = 2560): each output is bit-exact with the
+    reference quantizer applied to the kernel's normed row times that consumer's factors; the normed
+    row is within one bf16 ulp of the oracle's and the residual sum exact."""
+    note(f"rmsnorm_quant all smoothed T={T} n={n} res={res} {rounding}")
+    rng = np.random.default_rng(T * 3 + n)
+    K = 2560
+    xb, rb = act_bits(rng, (T, K)), act_bits(rng, (T, K), outliers=0)
+    w = O.round_bf16(rng.normal(0.0, 0.1, K).astype(np.float32))
+    wt = to_gpu_bf16(O.f32_to_bf16(w))
+    invs = [rng.uniform(0.05, 20.0, K).astype(np.float32) for _ in range(n)]
+    tinvs = [torch.from_numpy(v).cuda() for v in invs]
+    outs = fused_kernels.rms_norm_quant_multi(to_gpu_bf16(xb), wt, 1e-6, tinvs,
+                                              residual=to_gpu_bf16(rb) if res else None, rounding=rounding)
+    if res:
+        outs, v = outs
+    got = fused_kernels.rms_norm_quant(to_gpu_bf16(xb), wt, 1e-6, residual=to_gpu_bf16(rb) if res else None,
+                                       return_normed=True)
+    y = got[2]
+    yo, vo = O.rms_norm(xb, w, 1e-6, 1.0, rb if res else None)
+    if res:
+        assert np.array_equal(bits_of(v), vo)
+        assert np.array_equal(bits_of(v), bits_of(got[3]))
+    yk = bits_of(y)
+    assert_within_one_ulp(yk, yo)
+    for i, ((q, s), inv) in enumerate(zip(outs, invs)):
+        qo, so = O.quant_act(O.bf16_to_f32(yk), inv, rounding)
+        assert_equal_diag(q.cpu().numpy(), qo, f"consumer {i} q")
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32)), f"consumer {i} s"
+
+
 def test_shared_norm_qlinears_match_separate_path(gpu):
     """SharedNormQLinears (one norm + quant launch for q/k/v-style consumers, then a GEMM each) gives the
     bits of the reference's call pattern: rms_norm, then each QLinear quantizing with its own factors."""
