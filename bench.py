@@ -593,7 +593,8 @@ def serving_latency(torch, dev, st, reps=3):
     """One /v1/systemone request end to end on the 36-layer stack (mica_amd.contract.answer: validation,
     prompts, tokens, engine, typed answers): 8 questions (Noul, Choice, Score) about one synthetic state
     of ~8 K tokens (UTF-8 bytes as tokens), with the prompts' common start run once (share_prefix) and
-    with every prompt run in full.  Wall time per request, host work included."""
+    with every prompt run in full; the shared start also with the continuations' attention split over
+    the prefix keys (W8A8Stack.split_keys).  Wall time per request, host work included."""
     from mica_amd import contract
     from mica_amd.engine import PrefillEngine
 
@@ -609,7 +610,8 @@ def serving_latency(torch, dev, st, reps=3):
         qs[f"q{i}"] = q
     req = {"state": state, "questions": qs}
     out = {}
-    for share in (True, False):
+    for share, split in ((True, False), (True, True), (False, False)):
+        st.split_keys = split  # the continuations' attention over the prefix keys split over workgroups
         judge = contract.EngineJudge(PrefillEngine(st, graph=False), lambda t: list(t.encode("utf-8")),
                                      share_prefix=share)
         resp = contract.answer(req, judge)   # warm-up
@@ -619,11 +621,12 @@ def serving_latency(torch, dev, st, reps=3):
             resp = contract.answer(req, judge)
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) / reps * 1e3
-        out["shared_prefix" if share else "full_prompts"] = {
+        out[("shared_prefix_split_keys" if split else "shared_prefix") if share else "full_prompts"] = {
             "ms": round(ms, 1), "prompt_tokens": sum(len(t) for t in judge.last_prompts),
             "tokens_run": sum(len(t) for t in judge.last_prompts) - judge.shared_tokens,
             "answers": len(resp["answers"])}
         del judge
+    st.split_keys = False
     torch.cuda.empty_cache()
     return out
 

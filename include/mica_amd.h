@@ -213,6 +213,28 @@ int mica_attention_fwd(const void *q, long long sbq, long long shq, long long ld
 /* bytes of mica_attention_fwd workspace: B x HK x ceil(Sk / 32) x 16 KiB */
 long long mica_attention_workspace_bytes(int B, int Sk, int HK);
 
+/*
+ * mica_attention_fwd with each query block's keys split over key_splits workgroups (1 to 64), for
+ * few query blocks over many keys (a continuation batch over a long prefix: Sq << Sk).  Each
+ * workgroup writes its partial softmax state (unnormalised O in fp32, running maximum and sum) to
+ * the workspace and a merge kernel combines them:
+ *   o = (sum_s 2^(m_s - M) O_s) / (sum_s 2^(m_s - M) l_s),  M = max_s m_s.
+ * The reference's kernel walks all key blocks of a query block in one program
+ * (kernel_src/kernels.py:71-124, the n_q < n_k shift at :92-98); this split changes only the fp32
+ * summation order, so o matches mica_attention_fwd within bf16 rounding, not bit for bit.
+ * key_splits = 1 is mica_attention_fwd itself.  workspace:
+ * mica_attention_split_workspace_bytes(B, Sq, Sk, HQ, HK, key_splits) bytes, 16-byte aligned.
+ */
+int mica_attention_fwd_split(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
+                             long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv,
+                             void *o, long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
+                             int HK, int head_dim, float scale, int causal, int key_splits, void *workspace,
+                             long long workspace_bytes, mica_stream_t stream);
+
+/* bytes of mica_attention_fwd_split workspace: the V^T images, then B x HQ x key_splits x
+ * 32 ceil(Sq / 32) rows of 1032 bytes (O, m, l); -1 for an invalid argument */
+long long mica_attention_split_workspace_bytes(int B, int Sq, int Sk, int HQ, int HK, int key_splits);
+
 /* ---- gated delta net (GDN) token mixer ------------------------------------------------------- */
 
 /*

@@ -20,10 +20,27 @@ HEAD_DIM = 256
 GROUP = 4
 
 
-def attention_fwd(q, k, v, q_layout: str, scale: float | None = None):
+MAX_KEY_SPLITS = 64
+
+
+def key_splits_for(B: int, Sq: int, Sk: int, HK: int, cus: int = 256, per_cu: int = 2, min_tiles: int = 8) -> int:
+    """A split count for few query blocks over many keys: enough workgroups for per_cu per CU, each
+    split keeping at least min_tiles key tiles of 32; 1 (no split) when the query blocks already fill
+    the GPU."""
+    blocks = HK * B * ((Sq + 31) // 32)
+    want = -(-per_cu * cus // max(blocks, 1))
+    most = max(1, ((Sk + 31) // 32) // min_tiles)
+    return int(max(1, min(want, most, MAX_KEY_SPLITS)))
+
+
+def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits: int = 1):
     """Launch the kernel on q [B, Sq, HQ, 256] / k, v [B, Sk, HK, 256] ('bshd') or q [B, HQ, Sq, 256] /
     k, v [B, HK, Sk, 256] ('bhsd') views with unit feature stride.  Returns o in q's layout
-    (contiguous [B, Sq, HQ, 256] memory), or raises ValueError on an unsupported input."""
+    (contiguous [B, Sq, HQ, 256] memory), or raises ValueError on an unsupported input.
+
+    key_splits > 1 divides each query block's keys over that many workgroups and merges their partial
+    softmax states (mica_attention_fwd_split): faster for few query blocks over many keys, equal to the
+    unsplit result within bf16 rounding but not bit for bit."""
     for t in (q, k, v):
         if not t.is_cuda:
             raise ValueError("mica_amd attention runs on the GPU only (got a CPU tensor)")
@@ -40,24 +57,36 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None):
         st = lambda t: (t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
     if k.shape != v.shape or k.shape[0] != B or HQ != GROUP * HK or Sk < Sq:
         raise ValueError("q / k / v shapes do not match (4 query heads per key/value head, Sk >= Sq)")
+    key_splits = int(key_splits)
+    if not 1 <= key_splits <= MAX_KEY_SPLITS:
+        raise ValueError(f"key_splits must be 1 .. {MAX_KEY_SPLITS}")
     o = torch.empty((B, Sq, HQ, HEAD_DIM), dtype=torch.bfloat16, device=dev)
     L = _lib.load()
-    nbytes = int(L.mica_attention_workspace_bytes(B, Sk, HK))
+    nbytes = int(L.mica_attention_split_workspace_bytes(B, Sq, Sk, HQ, HK, key_splits))
+    if nbytes < 0:
+        raise ValueError("attention: invalid sizes")
     ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=dev)
     if not _aligned(q, k, v, o, ws):
         raise ValueError("attention operands must be 16-byte aligned")
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else float(scale)
     o_st = (o.stride(0), o.stride(2), o.stride(1))
-    rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd(
-        q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), o.data_ptr(), *o_st,
-        B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, ws.data_ptr(), nbytes, _stream(dev))), "mica_attention_fwd")
+    if key_splits == 1:
+        rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd(
+            q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), o.data_ptr(), *o_st,
+            B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, ws.data_ptr(), nbytes, _stream(dev))), "mica_attention_fwd")
+    else:
+        rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd_split(
+            q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), o.data_ptr(), *o_st,
+            B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, key_splits, ws.data_ptr(), nbytes, _stream(dev))),
+            "mica_attention_fwd_split")
     if rc:
         raise ValueError(f"attention: unsupported input ({_lib.status_name(rc)})")
     _launched()
     return o if q_layout == "bshd" else o.transpose(1, 2)
 
 
-def causal_gqa_attention(q, k, v, scale: float | None = None):
+def causal_gqa_attention(q, k, v, scale: float | None = None, key_splits: int = 1):
     """softmax(scale q k^T, causal) v per sequence and head on [B, S, heads, 256] views (e.g. of the
-    fused QKV output); query head h reads key/value head h // 4.  Returns o [B, S, HQ, 256] bf16."""
-    return attention_fwd(q, k, v, "bshd", scale)
+    fused QKV output); query head h reads key/value head h // 4.  Returns o [B, S, HQ, 256] bf16.
+    With Sk > Sq the queries are the last Sq positions; key_splits as in attention_fwd."""
+    return attention_fwd(q, k, v, "bshd", scale, key_splits)

@@ -54,6 +54,7 @@ constexpr int kStage = kKBytes + kVBytes;
 #endif
 constexpr int kNSt = MICA_FA_STAGES;     // LDS stages (tiles in flight: kNSt - 1 ahead)
 constexpr int kFaSmem = kNSt * kStage;   // also the output staging (4 waves x 32 x 512 B) after the loop
+constexpr int kMaxKeySplits = 64;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -83,6 +84,11 @@ struct FaParams {
     uint16_t *o; long long sbo, sho, ldo;
     int B, Sq, Sk, HQ, HK, ntiles_q, ntiles_k;
     float scale_log2;                           // softmax scale x log2(e)
+    // split keys: each query block's key tiles are divided over nsplit workgroups, which write their
+    // unnormalised partial state (O fp32, running maximum m and sum l, all relative to m) for
+    // fa_merge_kernel; part_* rows are (b, head, split, query), sq_pad = ntiles_q * 32 of them each
+    int nsplit, sq_pad;
+    float *part_o, *part_m, *part_l;
 };
 
 // ---- V -> V^T tile images: one workgroup per (tile, sequence x head); thread = 8 dims x 4 keys ----
@@ -109,10 +115,12 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(FaParams p) {
     }
 }
 
+template <bool SPLIT>
 __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParams p) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[kFaSmem];
-    // grid (HK, B, ntiles_q): every (sequence, head) pair's longest query blocks are dispatched first
-    const int qblk = p.ntiles_q - 1 - (int)blockIdx.z;
+    // grid (HK, B, ntiles_q [x nsplit]): every (sequence, head) pair's longest query blocks are
+    // dispatched first
+    const int qblk = p.ntiles_q - 1 - (SPLIT ? (int)blockIdx.z / p.nsplit : (int)blockIdx.z);
     const int hk = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hi = lane >> 5;
@@ -121,6 +129,10 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
     const int off = p.Sk - p.Sq; // position of query row t is off + t
     // key tiles 0 .. last: the last one holds the block's last query position
     const int last = min(p.ntiles_k - 1, (off + q0 + kBQ - 1) / kBK);
+    // this workgroup's tiles first .. last_own (all of them without a split)
+    const int split = SPLIT ? (int)blockIdx.z % p.nsplit : 0;
+    const int first = SPLIT ? (int)((long long)split * (last + 1) / p.nsplit) : 0;
+    const int last_own = SPLIT ? (int)((long long)(split + 1) * (last + 1) / p.nsplit) - 1 : last;
 
     // operand buffers: K rows of (b, hk) (rows >= Sk read as zeros), the V^T images of (b, hk)
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
@@ -166,21 +178,23 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
     f32x16 O[kD / 32];
 #pragma unroll
     for (int dt = 0; dt < kD / 32; ++dt) O[dt] = f32x16{};
-    float m_used = -__builtin_inff(), lsum = 0.0f;
+    // a split's range may hold no key at or below some of its queries: with a finite start the
+    // exponentials of their masked scores are exp2(-inf) = 0 (not NaN) and their state stays (m, 0, 0)
+    float m_used = SPLIT ? -1e30f : -__builtin_inff(), lsum = 0.0f;
     const int query = off + q0 + l32; // position of this lane's query
 
-    // prologue: tiles 0 .. kNSt - 2 in flight
+    // prologue: tiles first .. first + kNSt - 2 in flight (tile j in stage (j - first) % kNSt)
 #pragma unroll
     for (int i = 0; i < kNSt - 1; ++i)
-        if (i <= last) dma_tile(i, i);
-    for (int j = 0; j <= last; ++j) {
+        if (first + i <= last_own) dma_tile(first + i, i);
+    for (int j = first; j <= last_own; ++j) {
         // this wave's DMA of tile j landed: at most the DMA of tiles j + 1 .. j + kNSt - 2 (8 each) is
         // younger; near the end fewer were issued, and waiting for all of them is exact too
-        if (kNSt > 2 && j + kNSt - 2 <= last) fa_wait_vmcnt<(kNSt > 2 ? (kNSt - 2) * 8 : 0)>();
+        if (kNSt > 2 && j + kNSt - 2 <= last_own) fa_wait_vmcnt<(kNSt > 2 ? (kNSt - 2) * 8 : 0)>();
         else fa_wait_vmcnt<0>();
         __syncthreads();      // ... in every wave; nobody reads stage (j - 1) % kNSt any more
-        if (j + kNSt - 1 <= last) dma_tile(j + kNSt - 1, (j + kNSt - 1) % kNSt);
-        const int8_t *ks = smem + (j % kNSt) * kStage;
+        if (j + kNSt - 1 <= last_own) dma_tile(j + kNSt - 1, (j - first + kNSt - 1) % kNSt);
+        const int8_t *ks = smem + ((j - first) % kNSt) * kStage;
         const int8_t *vs = ks + kKBytes;
         // ---- S^T = K Q^T: rows = keys j*32 + acc_row, column = query l % 32 ----
         f32x16 sacc = {};
@@ -254,8 +268,26 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
             }
         }
     }
-    // ---- normalise, stage per wave in LDS (32 queries x 512 B), write 16-byte row pieces ----
     const float ltot = half_swap_sum(lsum);
+    if constexpr (SPLIT) {
+        // the partial state: O (fp32, 4 dims per 16-byte store) of query row q0 + l % 32, m and l;
+        // rows past Sq (up to sq_pad) are written too and never read
+        const long long prow = ((long long)(b * p.HQ + head) * p.nsplit + split) * p.sq_pad + q0 + l32;
+        float *po = p.part_o + prow * kD;
+#pragma unroll
+        for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = dt * 32 + 8 * r4 + 4 * hi;
+                *(float4 *)(po + d) = float4{O[dt][4 * r4], O[dt][4 * r4 + 1], O[dt][4 * r4 + 2], O[dt][4 * r4 + 3]};
+            }
+        if (hi == 0) {
+            p.part_m[prow] = m_used;
+            p.part_l[prow] = ltot;
+        }
+        return;
+    }
+    // ---- normalise, stage per wave in LDS (32 queries x 512 B), write 16-byte row pieces ----
     const float inv = 1.0f / ltot;
     __syncthreads(); // every wave is done with the operand stages
     int8_t *ost = smem + wave * (kBQ * kD * 2);
@@ -279,6 +311,38 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
     }
 }
 
+// ---- merge of the split partial states: one wave per (sequence, query head, query row), 4 dims per
+// lane.  With M = max_s m_s, w_s = exp2(m_s - M): o = (sum_s w_s O_s) / (sum_s w_s l_s), rounded to
+// bf16 (a split whose keys are all masked for the row has l_s = 0 and O_s = 0) ----
+__global__ __launch_bounds__(256) void fa_merge_kernel(FaParams p) {
+    const long long r = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b * HQ + head) * Sq + t
+    const int lane = threadIdx.x & 63;
+    if (r >= (long long)p.B * p.HQ * p.Sq) return;
+    const int t = (int)(r % p.Sq);
+    const long long bh = r / p.Sq;
+    const int b = (int)(bh / p.HQ), head = (int)(bh % p.HQ);
+    const long long row0 = bh * p.nsplit * p.sq_pad + t;  // split s at row0 + s * sq_pad
+    float mx = -__builtin_inff();
+    for (int sp = 0; sp < p.nsplit; ++sp) mx = __builtin_fmaxf(mx, p.part_m[row0 + (long long)sp * p.sq_pad]);
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float l = 0.0f;
+    for (int sp = 0; sp < p.nsplit; ++sp) {
+        const long long pr = row0 + (long long)sp * p.sq_pad;
+        const float w = __builtin_amdgcn_exp2f(p.part_m[pr] - mx);
+        const float4 o = *(const float4 *)(p.part_o + pr * kD + lane * 4);
+        l += w * p.part_l[pr];
+        acc.x += w * o.x;
+        acc.y += w * o.y;
+        acc.z += w * o.z;
+        acc.w += w * o.w;
+    }
+    const float inv = 1.0f / l;
+    u32x2 out;
+    out[0] = pack_bf16x2(acc.x * inv, acc.y * inv);
+    out[1] = pack_bf16x2(acc.z * inv, acc.w * inv);
+    *(u32x2 *)(p.o + b * p.sbo + head * p.sho + (long long)t * p.ldo + lane * 4) = out;
+}
+
 }  // namespace
 
 extern "C" long long mica_attention_workspace_bytes(int B, int Sk, int HK) {
@@ -286,13 +350,23 @@ extern "C" long long mica_attention_workspace_bytes(int B, int Sk, int HK) {
     return (long long)B * HK * ((Sk + kBK - 1) / kBK) * kVBytes;
 }
 
-extern "C" int mica_attention_fwd(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
-                                  long long shk, long long ldk, const void *v, long long sbv, long long shv,
-                                  long long ldv, void *o, long long sbo, long long sho, long long ldo, int B, int Sq,
-                                  int Sk, int HQ, int HK, int head_dim, float scale, int causal, void *workspace,
-                                  long long workspace_bytes, mica_stream_t stream) {
+extern "C" long long mica_attention_split_workspace_bytes(int B, int Sq, int Sk, int HQ, int HK, int key_splits) {
+    if (B < 0 || Sq < 0 || Sk < 0 || HQ <= 0 || HK <= 0 || key_splits < 1 || key_splits > kMaxKeySplits) return -1;
+    const long long vt = mica_attention_workspace_bytes(B, Sk, HK);
+    if (key_splits == 1) return vt;
+    const long long rows = (long long)B * HQ * key_splits * ((Sq + kBQ - 1) / kBQ) * kBQ;
+    return vt + rows * (kD * 4 + 8);
+}
+
+namespace {
+
+int attention_launch(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
+                     long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv, void *o,
+                     long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ, int HK, int head_dim,
+                     float scale, int causal, int key_splits, void *workspace, long long workspace_bytes,
+                     mica_stream_t stream) {
     if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || Sq < 0 || Sk < Sq) return MICA_MISS_SHAPE;
-    if (!causal) return MICA_MISS_ARG;
+    if (!causal || key_splits < 1 || key_splits > kMaxKeySplits) return MICA_MISS_ARG;
     if (B == 0 || Sq == 0) return 0;
     if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || workspace == nullptr) return MICA_MISS_ARG;
     const long long st[12] = {sbq, shq, ldq, sbk, shk, ldk, sbv, shv, ldv, sbo, sho, ldo};
@@ -304,9 +378,9 @@ extern "C" int mica_attention_fwd(const void *q, long long sbq, long long shq, l
         return MICA_MISS_ALIGN;
     const int ntiles_q = (Sq + kBQ - 1) / kBQ, ntiles_k = (Sk + kBK - 1) / kBK;
     if ((long long)ntiles_k * kBK * ldk * 2 >= (1LL << 31) || (long long)ntiles_k * kVBytes >= (1LL << 31) ||
-        ntiles_q > 65535 || B > 65535)
+        (long long)ntiles_q * key_splits > 65535 || B > 65535)
         return MICA_MISS_RANGE;
-    if (workspace_bytes < mica_attention_workspace_bytes(B, Sk, HK)) return MICA_MISS_ARG;
+    if (workspace_bytes < mica_attention_split_workspace_bytes(B, Sq, Sk, HQ, HK, key_splits)) return MICA_MISS_ARG;
     FaParams p{};
     p.q = (const uint16_t *)q; p.sbq = sbq; p.shq = shq; p.ldq = ldq;
     p.k = (const uint16_t *)k; p.sbk = sbk; p.shk = shk; p.ldk = ldk;
@@ -314,10 +388,50 @@ extern "C" int mica_attention_fwd(const void *q, long long sbq, long long shq, l
     p.vt = (uint16_t *)workspace; p.o = (uint16_t *)o; p.sbo = sbo; p.sho = sho; p.ldo = ldo;
     p.B = B; p.Sq = Sq; p.Sk = Sk; p.HQ = HQ; p.HK = HK; p.ntiles_q = ntiles_q; p.ntiles_k = ntiles_k;
     p.scale_log2 = scale * 1.44269504088896341f;
+    p.nsplit = key_splits;
+    p.sq_pad = ntiles_q * kBQ;
+    if (key_splits > 1) {
+        // partial states after the V^T images: O rows (1 KiB each), then m, then l
+        const long long rows = (long long)B * HQ * key_splits * p.sq_pad;
+        char *base = (char *)workspace + mica_attention_workspace_bytes(B, Sk, HK);
+        p.part_o = (float *)base;
+        p.part_m = (float *)(base + rows * kD * 4);
+        p.part_l = p.part_m + rows;
+    }
     hipStream_t stream_ = (hipStream_t)stream;
     hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles_k, B * HK), dim3(256), 0, stream_, p);
     int rc = mica_err(hipGetLastError());
     if (rc) return rc;
-    hipLaunchKernelGGL(fa_fwd_kernel, dim3(HK, B, ntiles_q), dim3(kFaThreads), 0, stream_, p);
+    if (key_splits == 1) {
+        hipLaunchKernelGGL(fa_fwd_kernel<false>, dim3(HK, B, ntiles_q), dim3(kFaThreads), 0, stream_, p);
+        return mica_err(hipGetLastError());
+    }
+    hipLaunchKernelGGL(fa_fwd_kernel<true>, dim3(HK, B, ntiles_q * key_splits), dim3(kFaThreads), 0, stream_, p);
+    rc = mica_err(hipGetLastError());
+    if (rc) return rc;
+    const long long rows = (long long)B * HQ * Sq;
+    if ((rows + 3) / 4 >= (1LL << 31)) return MICA_MISS_RANGE;
+    hipLaunchKernelGGL(fa_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream_, p);
     return mica_err(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int mica_attention_fwd(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
+                                  long long shk, long long ldk, const void *v, long long sbv, long long shv,
+                                  long long ldv, void *o, long long sbo, long long sho, long long ldo, int B, int Sq,
+                                  int Sk, int HQ, int HK, int head_dim, float scale, int causal, void *workspace,
+                                  long long workspace_bytes, mica_stream_t stream) {
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
+                            head_dim, scale, causal, 1, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mica_attention_fwd_split(const void *q, long long sbq, long long shq, long long ldq, const void *k,
+                                        long long sbk, long long shk, long long ldk, const void *v, long long sbv,
+                                        long long shv, long long ldv, void *o, long long sbo, long long sho,
+                                        long long ldo, int B, int Sq, int Sk, int HQ, int HK, int head_dim, float scale,
+                                        int causal, int key_splits, void *workspace, long long workspace_bytes,
+                                        mica_stream_t stream) {
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
+                            head_dim, scale, causal, key_splits, workspace, workspace_bytes, stream);
 }

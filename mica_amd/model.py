@@ -35,7 +35,7 @@ import torch
 import torch.nn.functional as F
 
 from . import int8_kernels as aot
-from .attention import GROUP as _FA_GROUP, HEAD_DIM as _FA_DIM, causal_gqa_attention
+from .attention import GROUP as _FA_GROUP, HEAD_DIM as _FA_DIM, causal_gqa_attention, key_splits_for
 from .fused_kernels import rms_norm_quant, rope_inplace
 from .gdn import HEAD_DIM as _GDN_DIM, GDNLayer
 from .int8_runtime import GateUpQLinear, QLinear
@@ -63,6 +63,17 @@ class StackConfig:
 
     def is_gdn(self, i: int) -> bool:
         return self.full_attention_interval > 0 and (i + 1) % self.full_attention_interval != 0
+
+
+_CUS = {}
+
+
+def _cu_count(device) -> int:
+    """Compute units of a CUDA device (cached per device index)."""
+    i = torch.device(device).index or 0
+    if i not in _CUS:
+        _CUS[i] = torch.cuda.get_device_properties(i).multi_processor_count
+    return _CUS[i]
 
 
 def _rand_qlinear(n, k, g, device):
@@ -164,9 +175,14 @@ class PrefixState:
 class W8A8Stack:
     """Random-init 4B-shaped stack; `prefill(ids, batch)` returns option probabilities."""
 
-    def __init__(self, cfg: StackConfig = StackConfig(), device="cuda", seed=0, attention: str = "mica"):
+    def __init__(self, cfg: StackConfig = StackConfig(), device="cuda", seed=0, attention: str = "mica",
+                 split_keys: bool = False):
         self.cfg = cfg
         self.attention = attention
+        # continuations over a prefix (Sk > S): divide each query block's keys over several workgroups
+        # (attention.key_splits_for).  Off by default: the continuation then matches a full run within
+        # bf16 rounding instead of bit for bit.
+        self.split_keys = split_keys
         self.device = torch.device(device)
         g = torch.Generator(device=self.device).manual_seed(seed)
         H = cfg.hidden
@@ -218,7 +234,10 @@ class W8A8Stack:
             k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
             v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
         if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
-            a = causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d)).view(B * S, hq * d)
+            ks = 1
+            if P and self.split_keys:
+                ks = key_splits_for(B, S, P + S, hk, cus=_cu_count(qkv.device))
+            a = causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), key_splits=ks).view(B * S, hq * d)
         else:
             a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
                                                is_causal=P == 0, attn_mask=None if P == 0 else self._mask(S, P, q.device),

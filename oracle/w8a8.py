@@ -258,14 +258,18 @@ def rope(x_bits: np.ndarray, cos_bits: np.ndarray, sin_bits: np.ndarray) -> np.n
 
 
 def causal_gqa_attention(q, k, v, scale: float) -> np.ndarray:
-    """float64 softmax(scale q k^T, causal) v per sequence and query head; q [B, S, HQ, D], k / v
-    [B, S, HK, D], query head h reads key/value head h // (HQ // HK) (the attention of the
-    full-attention layers; torch SDPA with enable_gqa computes the same)."""
+    """float64 softmax(scale q k^T, causal) v per sequence and query head; q [B, Sq, HQ, D], k / v
+    [B, Sk, HK, D] with Sk >= Sq, query head h reads key/value head h // (HQ // HK) (the attention of
+    the full-attention layers; torch SDPA with enable_gqa computes the same).  The queries are the
+    last Sq positions: query t sees keys u <= t + Sk - Sq (kernel_src/kernels.py:92-98, the n_q < n_k
+    shift of the reference's kernel)."""
     q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
     B, S, HQ, D = q.shape
+    Sk = k.shape[1]
+    assert Sk >= S
     grp = HQ // k.shape[2]
     out = np.zeros((B, S, HQ, D))
-    mask = np.triu(np.ones((S, S), bool), 1)
+    mask = np.arange(Sk)[None, :] > (np.arange(S)[:, None] + (Sk - S))
     for b in range(B):
         for h in range(HQ):
             s = scale * q[b, :, h] @ k[b, :, h // grp].T

@@ -787,6 +787,42 @@ def test_causal_gqa_attention_matches_oracle(gpu, B, S, HK):
     assert worst <= 1e-2
 
 
+@pytest.mark.parametrize("B,Sq,Sk,HK,splits", [
+    (2, 64, 1000, 1, 4),     # a continuation over a prefix: few query blocks, many keys
+    (1, 33, 33, 1, 2),       # Sq == Sk: the diagonal tile's split holds keys above some queries
+    (3, 40, 300, 2, 7),      # splits of unequal length, ragged last tiles
+    (1, 1, 2048, 1, 64),     # one query row, the most splits
+    (1, 96, 100, 1, 5),      # more splits than some blocks have tiles (empty splits)
+])
+def test_attention_split_keys_matches_oracle(gpu, B, Sq, Sk, HK, splits):
+    """mica_attention_fwd_split (each query block's keys over several workgroups, partial softmax states
+    merged) against the float64 oracle with Sk > Sq: relative error <= 1e-2 per (sequence, head), and
+    at most twice the unsplit kernel's own error (+ 1e-3)."""
+    from mica_amd.attention import causal_gqa_attention
+    note(f"attention split B={B} Sq={Sq} Sk={Sk} HK={HK} splits={splits}")
+    HQ, D = 4 * HK, 256
+    g = torch.Generator().manual_seed(B * 1000 + Sq + Sk)
+    q = (torch.randn(B, Sq, HQ, D, generator=g) * 1.5).to(torch.bfloat16)
+    kv = (torch.randn(B, Sk, 2 * HK, D, generator=g) * 1.5).to(torch.bfloat16)
+    dq, dkv = q.to(gpu), kv.to(gpu)
+    k, v = dkv[:, :, :HK], dkv[:, :, HK:]
+    o = causal_gqa_attention(dq, k, v, key_splits=splits)
+    o1 = causal_gqa_attention(dq, k, v)
+    torch.cuda.synchronize()
+    f = kv.float().numpy()
+    ref = O.causal_gqa_attention(q.float().numpy(), f[:, :, :HK], f[:, :, HK:], D ** -0.5)
+    def worst(out):
+        got = out.float().cpu().numpy()
+        return max(np.linalg.norm(got[b, :, h] - ref[b, :, h]) / np.linalg.norm(ref[b, :, h])
+                   for b in range(B) for h in range(HQ))
+    w_split, w_one = worst(o), worst(o1)
+    note(f"relative error: split {w_split:.2e}, unsplit {w_one:.2e}")
+    assert w_split <= 1e-2
+    # P is rounded to bf16 against a different running maximum in each split, so the two kernels differ
+    # by rounding noise of the same size as the unsplit kernel's own error, not by a bias
+    assert w_split <= 2.0 * w_one + 1e-3
+
+
 def test_attn_fwd_reference_selftest_cases(gpu):
     """int8_kernels.attn_fwd under the reference's own attention self-test (int8_runtime.py:444-488):
     its shapes (b, n, keys) with prefix keys, q as a transposed [b, n, hq, d] tensor and head-major k / v,

@@ -350,3 +350,27 @@ def test_attention_oracle_against_torch_and_closed_forms():
     mean = np.cumsum(v, axis=1) / np.arange(1, S + 1)[None, :, None, None]
     np.testing.assert_allclose(O.causal_gqa_attention(q, k_same, v, 0.25), np.repeat(mean, HQ // HK, axis=2),
                                rtol=1e-10, atol=1e-12)
+
+
+def test_attention_oracle_queries_after_a_prefix():
+    """Sq < Sk (the queries are the last Sq positions): torch's math SDPA with the explicit mask
+    key u <= t + Sk - Sq; the same rows of the full Sk x Sk attention (queries padded in front);
+    a one-query row over Sk keys attends to all of them (plain softmax)."""
+    import torch.nn.functional as F
+    rng = np.random.default_rng(43)
+    B, Sq, Sk, HQ, HK, D = 2, 7, 30, 8, 2, 16
+    q = rng.standard_normal((B, Sq, HQ, D))
+    k, v = (rng.standard_normal((B, Sk, HK, D)) for _ in range(2))
+    got = O.causal_gqa_attention(q, k, v, 0.3)
+    mask = torch.arange(Sk)[None, :] <= (torch.arange(Sq)[:, None] + Sk - Sq)
+    tq, tk, tv = (torch.tensor(a).transpose(1, 2) for a in (q, k, v))
+    ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask, scale=0.3, enable_gqa=True).transpose(1, 2)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-10, atol=1e-12)
+    qp = np.zeros((B, Sk, HQ, D))
+    qp[:, Sk - Sq:] = q
+    np.testing.assert_allclose(got, O.causal_gqa_attention(qp, k, v, 0.3)[:, Sk - Sq:], rtol=1e-12, atol=1e-14)
+    one = O.causal_gqa_attention(q[:, -1:], k, v, 0.3)
+    s = 0.3 * np.einsum("bhd,bkhd->bhk", q[:, -1], np.repeat(k, HQ // HK, axis=2))
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    np.testing.assert_allclose(one[:, 0], np.einsum("bhk,bkhd->bhd", p, np.repeat(v, HQ // HK, axis=2)), rtol=1e-10)
