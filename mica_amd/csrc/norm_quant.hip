@@ -459,7 +459,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
 #define MICA_SMOOTH_THREADS 1024
 #endif
 constexpr int kSmoothThreads = MICA_SMOOTH_THREADS;  // a whole CU's 16 rows share one copy of the factors
-template <int NCH, bool NORM, int NOUT, int RND>
+// SMOOTH = false: the same kernel for unsmoothed outputs, whose int8 rows are then all equal: the
+// row is quantized once (the one-FMA half-even quantizer of common.h, exact for bf16 rows) and
+// stored to each output.
+template <int NCH, bool NORM, int NOUT, int RND, bool SMOOTH = true>
 __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(4))) void smooth_one_kernel(RowParams p) {
     constexpr int XT = MICA_BF16;
     const int lane = threadIdx.x & 63;
@@ -481,8 +484,9 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
     // ((o * NCH + c) * 64 + lane) * 2; with the norm, the multipliers offset + w (fp32) after them as
     // output NOUT
     extern __shared__ float4 inv_sh[];
+    constexpr int kSets = SMOOTH ? NOUT : 0;  // factor sets before the norm's multipliers
 #pragma unroll
-    for (int o = 0; o < NOUT; ++o) {
+    for (int o = 0; o < kSets; ++o) {
         for (int ch = threadIdx.x; ch < NCH * 64; ch += kSmoothThreads) {
             inv_sh[(o * NCH * 64 + ch) * 2] = ((const float4 *)(p.inv[o] + ch * kChunk))[0];
             inv_sh[(o * NCH * 64 + ch) * 2 + 1] = ((const float4 *)(p.inv[o] + ch * kChunk))[1];
@@ -492,8 +496,8 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
         for (int ch = threadIdx.x; ch < NCH * 64; ch += kSmoothThreads) {
             float wv[kChunk];
             unpack8<MICA_BF16>(*(const u32x4 *)((const uint16_t *)p.w + ch * kChunk), wv);
-            inv_sh[(NOUT * NCH * 64 + ch) * 2] = float4{p.offset + wv[0], p.offset + wv[1], p.offset + wv[2], p.offset + wv[3]};
-            inv_sh[(NOUT * NCH * 64 + ch) * 2 + 1] = float4{p.offset + wv[4], p.offset + wv[5], p.offset + wv[6], p.offset + wv[7]};
+            inv_sh[(kSets * NCH * 64 + ch) * 2] = float4{p.offset + wv[0], p.offset + wv[1], p.offset + wv[2], p.offset + wv[3]};
+            inv_sh[(kSets * NCH * 64 + ch) * 2 + 1] = float4{p.offset + wv[4], p.offset + wv[5], p.offset + wv[6], p.offset + wv[7]};
         }
     }
     __syncthreads();
@@ -533,13 +537,42 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             float w1[kChunk];
-            factors(NOUT, c, w1);
+            factors(kSets, c, w1);
 #pragma unroll
             for (int j = 0; j < kChunk; ++j) v[c][j] = (v[c][j] * rstd) * w1[j];
             const u32x4 packed = pack8<XT>(v[c]);
             unpack8<XT>(packed, v[c]);
             if (p.y != nullptr) *(u32x4 *)((uint16_t *)p.y + (long)row * p.ldy + c * kRowStep + lane * kChunk) = packed;
         }
+    }
+    if constexpr (!SMOOTH) {
+        float am = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) am = __builtin_fmaxf(am, __builtin_fabsf(v[c][j]));
+        am = wave_max(am);
+        const float sc = row_scale(am);
+        const float rr = 1.0f / sc;
+        const float rf = RND == MICA_ROUND_EVEN ? fma_quant_recip(am, sc, rr) : rr;
+        if (lane == 0) {
+#pragma unroll
+            for (int o = 0; o < NOUT; ++o) p.s[o][row] = sc;
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            if (RND == MICA_ROUND_EVEN) {
+                const u32x2 packed = fma_quant8(v[c], rf);
+#pragma unroll
+                for (int o = 0; o < NOUT; ++o)
+                    __builtin_nontemporal_store(packed, (u32x2 *)(p.q[o] + (long)row * p.ldq[o] + c * kRowStep + lane * kChunk));
+            } else {
+#pragma unroll
+                for (int o = 0; o < NOUT; ++o)
+                    quant_store8r<true, RND>(v[c], sc, rr, p.rounding, p.q[o] + (long)row * p.ldq[o] + c * kRowStep + lane * kChunk);
+            }
+        }
+        return;
     }
     // one output at a time: its smoothed row t stays in registers from the absmax to the quantizer
     // (the factors are read from LDS once per output)
@@ -727,10 +760,15 @@ int launch16(const RowParams &p, int xt, bool norm, bool has_inv, hipStream_t st
 
 // smooth_one_kernel when every row of the launch fits the resident waves; -1 otherwise (the caller
 // then takes the grid-stride path)
-template <int NCH, bool NORM, int NOUT, int RND>
+template <int NCH, bool NORM, int NOUT, int RND, bool SMOOTH = true>
 int launch_smooth_one(const RowParams &p, hipStream_t st) {
-    constexpr auto kern = smooth_one_kernel<NCH, NORM, NOUT, RND>;
-    const unsigned lds = (unsigned)((NOUT + (NORM ? 1 : 0)) * NCH * 64 * 2 * sizeof(float4));
+    constexpr auto kern = smooth_one_kernel<NCH, NORM, NOUT, RND, SMOOTH>;
+    const unsigned lds = (unsigned)(((SMOOTH ? NOUT : 0) + (NORM ? 1 : 0)) * NCH * 64 * 2 * sizeof(float4));
+    // the kernel writes exactly NOUT quantized rows and scales per row: never launch it for another
+    // output count (a norm-only call has n_out = 0 and no q / s at all)
+    if (lds == 0 || p.n_out != NOUT) return -1;
+    for (int o = 0; o < NOUT; ++o)
+        if (p.q[o] == nullptr || p.s[o] == nullptr || (SMOOTH && p.inv[o] == nullptr)) return -1;
     static std::atomic<int> cached{0};
     int per_cu = cached.load(std::memory_order_relaxed);
     if (per_cu <= 0) {
@@ -745,10 +783,10 @@ int launch_smooth_one(const RowParams &p, hipStream_t st) {
     return mica_err(hipGetLastError());
 }
 
-template <int NCH, bool NORM, int NOUT>
+template <int NCH, bool NORM, int NOUT, bool SMOOTH = true>
 int launch_smooth_one_rnd(const RowParams &p, hipStream_t st) {
-    if (p.rounding == MICA_ROUND_EVEN) return launch_smooth_one<NCH, NORM, NOUT, MICA_ROUND_EVEN>(p, st);
-    return launch_smooth_one<NCH, NORM, NOUT, MICA_ROUND_AWAY>(p, st);
+    if (p.rounding == MICA_ROUND_EVEN) return launch_smooth_one<NCH, NORM, NOUT, MICA_ROUND_EVEN, SMOOTH>(p, st);
+    return launch_smooth_one<NCH, NORM, NOUT, MICA_ROUND_AWAY, SMOOTH>(p, st);
 }
 
 // bf16 rows of exactly NCH * 512 elements (the hot widths): no masks, rounding fixed at compile time
@@ -756,6 +794,16 @@ template <int NCH>
 int launch16_full(const RowParams &p, bool norm, bool has_inv, hipStream_t st) {
     // rows of up to 2560 elements without smoothing: one wave per row when they all fit
     if constexpr (NCH <= 5) {
+#ifndef MICA_NORM_ONE_LDS
+#define MICA_NORM_ONE_LDS 1
+#endif
+        // one normed, quantized output: the kernel with the multipliers offset + w in LDS (measured at
+        // T = 4096, K = 2560: 5.65 against 6.0 us for the kernel below, which stays faster for several
+        // outputs: 8.0 against 8.3 us for three)
+        if (MICA_NORM_ONE_LDS && !has_inv && norm && p.w_dtype == MICA_BF16 && p.n_out == 1) {
+            const int rc = launch_smooth_one_rnd<NCH, true, 1, false>(p, st);
+            if (rc >= 0) return rc;
+        }
         if (!has_inv && (!norm || p.w_dtype == MICA_BF16)) {
             int rc = -1;
             if (norm && p.rounding == MICA_ROUND_EVEN) rc = launch_one<row16_one_kernel<NCH, MICA_BF16, true, true, MICA_ROUND_EVEN>>(p, st);
@@ -765,7 +813,7 @@ int launch16_full(const RowParams &p, bool norm, bool has_inv, hipStream_t st) {
             if (rc >= 0) return rc;
         }
         // every output smoothed (1 to 3 of them): one wave per row when they all fit
-        bool all_inv = has_inv && p.n_out <= 3 && (!norm || p.w_dtype == MICA_BF16);
+        bool all_inv = has_inv && p.n_out >= 1 && p.n_out <= 3 && (!norm || p.w_dtype == MICA_BF16);
         for (int o = 0; o < p.n_out; ++o) all_inv = all_inv && p.inv[o] != nullptr;
         if (all_inv) {
             int rc = -1;
