@@ -754,6 +754,10 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
 #define MICA_GEMM_MHALVES 1
 #endif
     constexpr bool kMHalves = MICA_GEMM_MHALVES != 0;
+#ifndef MICA_GEMM_AGPR
+#define MICA_GEMM_AGPR 1
+#endif
+    constexpr bool kAgpr = MICA_GEMM_AGPR != 0;
     constexpr long long kSplit = 4;
     constexpr long long kMinSplitSlabs = 32;
     p.dp_tiles = (int)tiles;
@@ -821,8 +825,17 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
             p.tiles_n = (N + 159) / 160;
             p.dp_tiles = (int)tiles160;
             grid = (int)tiles160;
+            return wide_launch(p, epilogue, out_dtype, grid, hb, hr, true, st);
         }
-        return wide_launch(p, epilogue, out_dtype, grid, hb, hr, narrow, st);
+        // 16-bit outputs in whole 16-byte row units and at least 4 slabs of K: the AGPR kernel
+        // (gemm_i8_agpr.hip), same schedule and bits, one wave per SIMD
+        // (measured faster from one whole round of tiles on; below that the tail pieces dominate, and
+        // the 8-wave kernel serves them better: 22.5 vs 21.2 us at 512 x 9728 x 2560)
+        const bool agpr_ok = kAgpr && K >= 512 && cus > 0 && tiles >= cus &&
+                             (out_dtype == MICA_BF16 || out_dtype == MICA_FP16) && ldc % 8 == 0 &&
+                             Nout % 8 == 0 && (!residual || ldr % 8 == 0);
+        if (agpr_ok) return agpr_launch(p, epilogue, out_dtype, grid, hb, hr, st);
+        return wide_launch(p, epilogue, out_dtype, grid, hb, hr, false, st);
     }
     if (epilogue == MICA_EPI_SILU_MUL) return launch_out<MICA_EPI_SILU_MUL, MICA_BF16>(p, grid, false, false, st);
     if (out_dtype == MICA_BF16) return launch_out<MICA_EPI_SCALE, MICA_BF16>(p, grid, hb, hr, st);

@@ -122,6 +122,9 @@ MICA_DEVICE void load4_res(const void *R, long off, float (&v)[4], int valid, bo
 // the wide kernel's launcher (gemm_i8_wide.hip)
 int wide_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool has_bias, bool has_res,
                 bool narrow, hipStream_t st);
+// the AGPR kernel's launcher (gemm_i8_agpr.hip): SCALE (bf16 / fp16) and SiLU (bf16) epilogues
+int agpr_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool has_bias, bool has_res,
+                hipStream_t st);
 
 }  // namespace mica_gemm
 
