@@ -213,9 +213,12 @@ struct QTile {
     // DMA instructions go out one per kDStride MFMAs: issued together after the barrier they back up
     // the address unit, and the stalled issue starves this wave's MFMA pipe (measured: 66 K -> 45 K
     // cycles per 256 x 256 x 2560 tile without any DMA in the loop)
-    static constexpr int kDStride = kMfma / C::kDma;
-    static_assert(kDStride >= 1 && kDStride * C::kDma <= kMfma, "DMA spread");
-    template <int M, bool READ, int OFFW, int OFFX, bool FIRST, bool DMA>
+    // (whole tiles issue all kDma in their k-step; smaller tiles, whose k-steps are shorter, issue
+    // the rest early in the next one)
+    static constexpr int kDStride = 4;
+    static constexpr int kDFirst = (kMfma + kDStride - 1) / kDStride < C::kDma ? (kMfma + kDStride - 1) / kDStride : C::kDma;
+    static_assert(C::kDma - kDFirst <= kDFirst, "DMA spread over at most two k-steps");
+    template <int M, bool READ, int OFFW, int OFFX, bool FIRST, int D0>
     MICA_DEVICE void ks_body(Ops &nx, const Ops &cur, uint32_t wa, uint32_t xa, const DmaPlan &dp) {
         if constexpr (M < kMfma) {
             if constexpr (READ && M < kReads) {
@@ -224,19 +227,22 @@ struct QTile {
                 else
                     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(nx.x[M - NB]) : "v"(xa), "i"(OFFX + (M - NB) * 16 * QBK));
             }
-            if constexpr (DMA && M % kDStride == 0 && M / kDStride < C::kDma) dp.issue(M / kDStride);
+            // D0 < 0: no DMA in this k-step; else instructions D0, D0 + 1, ... (below the slab's kDma
+            // and, in the first k-step, below kDFirst)
+            if constexpr (D0 >= 0 && M % kDStride == 0 && D0 + M / kDStride < (D0 == 0 ? kDFirst : C::kDma))
+                dp.issue(D0 + M / kDStride);
             mfma_one<M, FIRST>(cur);
             __builtin_amdgcn_sched_barrier(0);
-            ks_body<M + 1, READ, OFFW, OFFX, FIRST, DMA>(nx, cur, wa, xa, dp);
+            ks_body<M + 1, READ, OFFW, OFFX, FIRST, D0>(nx, cur, wa, xa, dp);
         }
     }
     // READ: the next k-step's fragments (stage ST) into nx, one ahead of each of the first kReads
-    // MFMAs; DMA: the plan's instructions spread over the k-step
-    template <bool READ, int ST, bool FIRST, bool DMA>
+    // MFMAs; D0 >= 0: the plan's instructions from D0 on, one per kDStride MFMAs
+    template <bool READ, int ST, bool FIRST, int D0>
     MICA_DEVICE void kstep(Ops &nx, const Ops &cur, uint32_t wa, uint32_t xa, const DmaPlan &dp) {
         // clear of MFMAs still reading registers the loads may reuse
         if constexpr (READ) asm volatile("s_nop 7\n\ts_nop 7");
-        ks_body<0, READ, ST * C::kBHalf, ST * C::kAHalf, FIRST, DMA>(nx, cur, wa, xa, dp);
+        ks_body<0, READ, ST * C::kBHalf, ST * C::kAHalf, FIRST, D0>(nx, cur, wa, xa, dp);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -268,10 +274,16 @@ struct QTile {
         // R1 alongside); B(k) = slab k + 1 landed (this wave's share) and every wave past its reads of
         // slab k: a barrier, the DMA into slab k's stage (DK: 1 = this tile's slab k + 2, 2 = the next
         // tile's slab 0), then k-step 1 of slab k with k-step 0 of slab k + 1 read into R0.
+        // the DMA that half_b started, continued in the next half_a when it has more instructions
+        constexpr int kDMore = C::kDma > kDFirst ? kDFirst : -1;
+        DmaPlan cont = own;
         auto half_a = [&](auto st_c, auto first_c) {
             wait_lgkmcnt0();   // k-step 0's fragments (read one k-step ago) are in registers
             __builtin_amdgcn_sched_barrier(0);
-            kstep<true, decltype(st_c)::value, decltype(first_c)::value, false>(R1, R0, wa[1], xa[1], own);
+            if constexpr (decltype(first_c)::value)
+                kstep<true, decltype(st_c)::value, true, -1>(R1, R0, wa[1], xa[1], own);
+            else
+                kstep<true, decltype(st_c)::value, false, kDMore>(R1, R0, wa[1], xa[1], cont);
         };
         auto half_b = [&](auto st_c, const DmaPlan &dp) {
             constexpr int ST = decltype(st_c)::value;
@@ -279,7 +291,8 @@ struct QTile {
             wait_lgkmcnt0();   // k-step 1's fragments are in registers
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
-            kstep<true, ST ^ 1, false, true>(R0, R1, wa[0], xa[0], dp);
+            cont = dp;
+            kstep<true, ST ^ 1, false, 0>(R0, R1, wa[0], xa[0], dp);
         };
         // the DMA of this tile's slab `slab` into its stage
         auto own_plan = [&](int slab) {
@@ -308,7 +321,7 @@ struct QTile {
         half_a(S1{}, F{});
         wait_lgkmcnt0();
         __builtin_amdgcn_sched_barrier(0);
-        kstep<false, 0, false, false>(R0, R1, wa[0], xa[0], own);
+        kstep<false, 0, false, -1>(R0, R1, wa[0], xa[0], own);
     }
 
     // 16 bytes of one output row from MFMA tiles ja and ja + 1 of row block i: lanes of rows kq, kq ^ 1
@@ -516,28 +529,31 @@ __global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_kernel(GemmParams p
         if (p.half_tiles > 0)
             run_qphase<QHalfN, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, 2 * p.half_tiles, G,
                                                             [&](int h, int &m0, int &n0) {
-                                                                int tm, tn;
-                                                                tile_of(dp + (h >> 1), tm_n, tn_n, tm, tn);
+                                                                int tm, tn, t, part;
+                                                                tail_piece(h, 2, dp, p.half_tiles, t, part);
+                                                                tile_of(t, tm_n, tn_n, tm, tn);
                                                                 m0 = tm * 256;
-                                                                n0 = tn * 256 + (h & 1) * 128;
+                                                                n0 = tn * 256 + part * 128;
                                                                 return n0 < N;
                                                             });
         if (p.quarter_tiles > 0)
             run_qphase<QQuart, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, 4 * p.quarter_tiles, G,
                                                             [&](int h, int &m0, int &n0) {
-                                                                int tm, tn;
-                                                                tile_of(dp + (h >> 2), tm_n, tn_n, tm, tn);
-                                                                m0 = tm * 256 + ((h >> 1) & 1) * 128;
-                                                                n0 = tn * 256 + (h & 1) * 128;
+                                                                int tm, tn, t, part;
+                                                                tail_piece(h, 4, dp, p.quarter_tiles, t, part);
+                                                                tile_of(t, tm_n, tn_n, tm, tn);
+                                                                m0 = tm * 256 + ((part >> 1) & 1) * 128;
+                                                                n0 = tn * 256 + (part & 1) * 128;
                                                                 return m0 < M && n0 < N;
                                                             });
     } else {
         if (p.mhalf_tiles > 0)
             run_qphase<QHalfM, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, 2 * p.mhalf_tiles, G,
                                                             [&](int h, int &m0, int &n0) {
-                                                                int tm, tn;
-                                                                tile_of(dp + (h >> 1), tm_n, tn_n, tm, tn);
-                                                                m0 = tm * 256 + (h & 1) * 128;
+                                                                int tm, tn, t, part;
+                                                                tail_piece(h, 2, dp, p.mhalf_tiles, t, part);
+                                                                tile_of(t, tm_n, tn_n, tm, tn);
+                                                                m0 = tm * 256 + part * 128;
                                                                 n0 = tn * 256;
                                                                 return m0 < M;
                                                             });

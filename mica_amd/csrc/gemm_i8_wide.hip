@@ -585,20 +585,22 @@ __global__ __launch_bounds__(kWideThreads, 1) void gemm_i8_wide_kernel(GemmParam
         if (p.half_tiles > 0)
             run_phase<WHalfN, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, 2 * p.half_tiles, G,
                                                            [&](int h, int &m0, int &n0) {
-                                                               int tm, tn;
-                                                               tile_of(dp + (h >> 1), tm_n, tn_n, tm, tn);
+                                                               int tm, tn, t, part;
+                                                               tail_piece(h, 2, dp, p.half_tiles, t, part);
+                                                               tile_of(t, tm_n, tn_n, tm, tn);
                                                                m0 = tm * 256;
-                                                               n0 = tn * 256 + (h & 1) * 128;
+                                                               n0 = tn * 256 + part * 128;
                                                                return n0 < N;
                                                            });
         // or the next quarter_tiles tiles as four 128 x 128 quarters each
         if (p.quarter_tiles > 0)
             run_phase<WQuart, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, 4 * p.quarter_tiles, G,
                                                            [&](int h, int &m0, int &n0) {
-                                                               int tm, tn;
-                                                               tile_of(dp + (h >> 2), tm_n, tn_n, tm, tn);
-                                                               m0 = tm * 256 + ((h >> 1) & 1) * 128;
-                                                               n0 = tn * 256 + (h & 1) * 128;
+                                                               int tm, tn, t, part;
+                                                               tail_piece(h, 4, dp, p.quarter_tiles, t, part);
+                                                               tile_of(t, tm_n, tn_n, tm, tn);
+                                                               m0 = tm * 256 + ((part >> 1) & 1) * 128;
+                                                               n0 = tn * 256 + (part & 1) * 128;
                                                                return m0 < M && n0 < N;
                                                            });
     } else {
@@ -606,9 +608,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void gemm_i8_wide_kernel(GemmParam
         if (p.mhalf_tiles > 0)
             run_phase<WHalfM, EPI, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, 2 * p.mhalf_tiles, G,
                                                            [&](int h, int &m0, int &n0) {
-                                                               int tm, tn;
-                                                               tile_of(dp + (h >> 1), tm_n, tn_n, tm, tn);
-                                                               m0 = tm * 256 + (h & 1) * 128;
+                                                               int tm, tn, t, part;
+                                                               tail_piece(h, 2, dp, p.mhalf_tiles, t, part);
+                                                               tile_of(t, tm_n, tn_n, tm, tn);
+                                                               m0 = tm * 256 + part * 128;
                                                                n0 = tn * 256;
                                                                return m0 < M;
                                                            });
