@@ -142,7 +142,8 @@ def test_rmsnorm_quant_config1(gpu, T, offset):
     assert np.array_equal(q.cpu().numpy()[same], qe[same])
     note(f"rmsnorm_quant T={T} offset={offset}: {same.mean():.5f} of rows equal the oracle's bf16 row, "
          f"{np.mean(yk == yo):.7f} of elements")
-    assert same.mean() > 0.95
+    # observed 0.988 (T = 256) to 0.991 of rows (rows whose fp32 sum of squares rounds the other way)
+    assert same.mean() > 0.98
 
 
 def test_rmsnorm_quant_residual_and_smoothing(gpu):
