@@ -42,32 +42,39 @@ constexpr int kQWaves = 4, kQThreads = 64 * kQWaves;
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// A BM x BN tile on 4 waves in a 2 (M) x 2 (N) grid.
-template <int BM_, int BN_>
+// A BM x BN tile on 4 waves in a 2 (M) x 2 (N) grid, NS LDS stages of one slab each.
+template <int BM_, int BN_, int NS_ = 2>
 struct QCfg {
-    static constexpr int BM = BM_, BN = BN_;
+    static constexpr int BM = BM_, BN = BN_, NS = NS_;
     static constexpr int WM = BM / 2, WN = BN / 2;
     static constexpr int MB = WM / 16, NB = WN / 16;
     static constexpr int kAHalf = BM * QBK;                 // one stage of A
     static constexpr int kBHalf = BN * QBK;                 // one stage of B
-    static constexpr int kBBase = 2 * kAHalf;               // B stages follow both A stages
+    static constexpr int kBBase = NS * kAHalf;              // B stages follow the A stages
     static constexpr int kADma = BM / 8 / kQWaves;          // 1 KiB DMA instructions per wave per slab
     static constexpr int kBDma = BN / 8 / kQWaves;
     static constexpr int kDma = kADma + kBDma;
     static_assert(BM % (8 * kQWaves) == 0 && BN % (8 * kQWaves) == 0, "DMA blocks");
     static_assert(NB % 2 == 0, "tile pairs for the 16-byte stores");
 };
-using QFull = QCfg<256, 256>;   // waves of 128 x 128
-using QHalfN = QCfg<256, 128>;  // waves of 128 x 64 (SCALE tail)
-using QHalfM = QCfg<128, 256>;  // waves of 64 x 128 (SiLU tail)
-using QQuart = QCfg<128, 128>;  // waves of 64 x 64 (SCALE tail at most a quarter of a round)
+// Tail pieces (one per workgroup: the launcher gives a tail at most one piece per CU) keep three slabs
+// in LDS, two in flight while one is read: they need 48 B of DMA per MFMA clock against 32 for whole
+// tiles, and with one slab of lookahead their loop ran 35 K cycles (256 x 128 x 2560) against 28 K
+// with every operand resident in L2.
+using QFull = QCfg<256, 256>;      // waves of 128 x 128
+using QHalfN = QCfg<256, 128, 3>;  // waves of 128 x 64 (SCALE tail)
+using QHalfM = QCfg<128, 256, 3>;  // waves of 64 x 128 (SiLU tail)
+using QQuart = QCfg<128, 128, 3>;  // waves of 64 x 64 (SCALE tail at most a quarter of a round)
 
-// LDS: A stages 0 and 1, B stages 0 and 1, then two buffers of tile scales (sa, sb, bias: 3 x 256
-// fp32), for this tile and the next.
-constexpr int kQScale = 2 * (256 + 256) * QBK;
+// LDS: the A stages, the B stages, then (at a fixed place past the largest stage set) two buffers of
+// tile scales (sa, sb, bias: 3 x 256 fp32), for this tile and the next.
+constexpr int kQScale = 144 * 1024;
 constexpr int kQScaleBuf = 3 * 256 * 4;
 constexpr int kQSmem = kQScale + 2 * kQScaleBuf;
 static_assert(kQSmem <= 160 * 1024, "LDS");
+template <class C>
+constexpr bool stages_fit = C::NS * (C::kAHalf + C::kBHalf) <= kQScale;
+static_assert(stages_fit<QFull> && stages_fit<QHalfN> && stages_fit<QHalfM> && stages_fit<QQuart>, "stages");
 
 // This lane's index, computed afresh where it is used (a few VALU operations per tile instead of a
 // register held across the persistent loop).  The wave index lives in an SGPR.
@@ -324,6 +331,85 @@ struct QTile {
         kstep<false, 0, false, -1>(R0, R1, wa[0], xa[0], own);
     }
 
+    // ---- the slabs of a tail piece (C::NS == 3, no next piece to prefetch for): on entry slab 0 is
+    // visible in stage 0 and slabs 1 and 2 are in flight into stages 1 and 2.  Slab s lives in stage
+    // s % 3; after the barrier of B(k) (slab k + 1 landed, slab k read by every wave) slab k + 3 goes
+    // into slab k's stage, so two slabs are in flight while one is read.  Stage offsets beyond the
+    // 16-bit offset of ds_read_b128 ride on the base registers.
+    MICA_DEVICE void run3(const GemmParams &p, int8_t *smem, int wave, int m0, int n0) {
+        static_assert(C::NS == 3, "three stages");
+        const int lane = lane_id();
+        const int wm = wave >> 1, wn = wave & 1;
+        const int r16 = lane & 15, kq = lane >> 4;
+        const int nk = p.K / QBK;  // even, at least 4
+        const uint32_t lds0 = lds_addr(smem);
+        uint32_t xa[2], wa[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int pos = ((4 * s + kq) ^ (r16 & 7)) << 4;
+            xa[s] = lds0 + (wm * WM + r16) * QBK + pos;
+            wa[s] = lds0 + C::kBBase + (wn * WN + r16) * QBK + pos;
+        }
+        constexpr int kDMore = C::kDma > kDFirst ? kDFirst : -1;
+        Ops R0, R1;
+        DmaPlan cont = tile_plan(p, smem, wave, lane, m0, n0, 0, 0, false);
+        // the plan for slab `slab` (stage ST = slab % 3): zero-sized past the last slab, so every wave
+        // issues the same instructions and the waits below count them
+        auto plan = [&](int slab, auto st_c) {
+            return tile_plan(p, smem, wave, lane, m0, n0, slab, decltype(st_c)::value, slab < nk);
+        };
+        // A: k-step 0 of the slab in stage ST (in R0), its k-step 1 read into R1
+        auto half_a = [&](auto st_c, auto first_c) {
+            constexpr int ST = decltype(st_c)::value;
+            wait_lgkmcnt0();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (decltype(first_c)::value)
+                kstep<true, 0, true, -1>(R1, R0, wa[1] + ST * C::kBHalf, xa[1] + ST * C::kAHalf, cont);
+            else
+                kstep<true, 0, false, kDMore>(R1, R0, wa[1] + ST * C::kBHalf, xa[1] + ST * C::kAHalf, cont);
+        };
+        // B: slab k + 1 (stage ST + 1) landed, only slab k + 2's instructions may be in flight
+        auto half_b = [&](auto st_c, const DmaPlan &dp) {
+            constexpr int ST = decltype(st_c)::value;
+            constexpr int SN = (ST + 1) % 3;
+            wait_vmcnt<C::kDma>();
+            wait_lgkmcnt0();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            cont = dp;
+            kstep<true, 0, false, 0>(R0, R1, wa[0] + SN * C::kBHalf, xa[0] + SN * C::kAHalf, dp);
+        };
+        using T = std::integral_constant<bool, true>;
+        using F = std::integral_constant<bool, false>;
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        frag_reads<0, NB>(R0.w, wa[0]);
+        frag_reads<0, MB>(R0.x, xa[0]);
+        half_a(S0{}, T{});
+        int k = 0;
+        for (; k + 3 <= nk - 1; k += 3) {
+            half_b(S0{}, plan(k + 3, S0{}));
+            half_a(S1{}, F{});
+            half_b(S1{}, plan(k + 4, S1{}));
+            half_a(S2{}, F{});
+            half_b(S2{}, plan(k + 5, S2{}));
+            half_a(S0{}, F{});
+        }
+        // the last nk - 1 - k (0 to 2) pairs, from stage 0
+        if (k + 1 <= nk - 1) {
+            half_b(S0{}, plan(k + 3, S0{}));
+            half_a(S1{}, F{});
+        }
+        if (k + 2 <= nk - 1) {
+            half_b(S1{}, plan(k + 4, S1{}));
+            half_a(S2{}, F{});
+        }
+        wait_lgkmcnt0();
+        __builtin_amdgcn_sched_barrier(0);
+        kstep<false, 0, false, -1>(R0, R1, wa[0], xa[0], cont);
+    }
+
     // 16 bytes of one output row from MFMA tiles ja and ja + 1 of row block i: lanes of rows kq, kq ^ 1
     // exchange their halves (v_permlane16_swap swaps the odd 16-lane rows of the first operand with the
     // even rows of the second), so lane (r16, kq) ends with columns 16 (ja + kq % 2) + 8 (kq / 2) + 0..7
@@ -481,6 +567,24 @@ MICA_DEVICE void run_qphase(const GemmParams &p, int8_t *smem, __amdgpu_buffer_r
     while (h < hend && !piece(h, m0, n0)) h += G;
     if (h >= hend) return;
     Tile t;
+    if constexpr (C::NS == 3) {
+        // tail pieces, each on its own: slabs 0 - 2 out, slab 0 and the scales waited for
+        for (; h < hend; h += G) {
+            if (!piece(h, m0, n0)) continue;
+            wait_vmcnt<0>();
+            wait_lgkmcnt0();
+            __builtin_amdgcn_s_barrier();
+            Tile::scales_dma(p, smem, wave, 0, m0, n0);
+            Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 0, 0);
+            Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 1, 1);
+            Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 2, 2);
+            wait_vmcnt<2 * C::kDma>();  // scales and slab 0 landed (slabs 1 and 2 may be in flight)
+            __builtin_amdgcn_s_barrier();
+            t.run3(p, smem, wave, m0, n0);
+            t.epilogue(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 0, false, 0, 0);
+        }
+        return;
+    }
     // the previous phase's last epilogue is finished with the stages and the scales
     wait_vmcnt<0>();
     wait_lgkmcnt0();
