@@ -829,9 +829,14 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
         }
         // 16-bit outputs in whole 16-byte row units and at least 4 slabs of K: the AGPR kernel
         // (gemm_i8_agpr.hip), same schedule and bits, one wave per SIMD
-        // (measured faster from one whole round of tiles on; below that the tail pieces dominate, and
-        // the 8-wave kernel serves them better: 22.5 vs 21.2 us at 512 x 9728 x 2560)
-        const bool agpr_ok = kAgpr && K >= 512 && cus > 0 && tiles >= cus &&
+        // Measured (same box, bit-identical): faster from one whole round of tiles on; below that,
+        // wherever tail pieces run with a long K or at M >= 512 or for the SiLU epilogue (1024 x 2560 x
+        // 9728: 33.1 vs 48.7 us; 512 x 9728 x 2560: 19.8 vs 21.5; 128 x 19456 x 2560 SiLU: 22.4 vs
+        // 24.9), but not for quarters at M <= 256 with K = 2560 (11.0 vs 10.6 us at 256 x 6144) nor
+        // for fewer whole tiles than CUs with no pieces (33.8 vs 33.2 at 2048 x 6144).
+        const bool pieces = p.dp_tiles < tiles;
+        const bool agpr_wins = tiles >= cus || (pieces && (K >= 4096 || M >= 512 || epilogue == MICA_EPI_SILU_MUL));
+        const bool agpr_ok = kAgpr && K >= 512 && cus > 0 && agpr_wins &&
                              (out_dtype == MICA_BF16 || out_dtype == MICA_FP16) && ldc % 8 == 0 &&
                              Nout % 8 == 0 && (!residual || ldr % 8 == 0);
         if (agpr_ok) return agpr_launch(p, epilogue, out_dtype, grid, hb, hr, st);
