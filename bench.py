@@ -53,6 +53,12 @@ def parse():
     return ap.parse_args()
 
 
+def extra_warmup(args):
+    """Untimed launches before each extra line's timed block: at least 100, so short kernels are timed
+    at the clocks of a busy GPU (the headline's own warmup is exactly --warmup)."""
+    return max(args.warmup, 100)
+
+
 class Timer:
     """HIP events on the current stream around a block of launches."""
 
@@ -262,7 +268,8 @@ def main():
     cpu = cpu_baseline(torch, M, K, N) if not args.no_cpu_baseline else None
 
     if not args.no_extra:
-        extra = {}
+        extra = {"timing": "each line: at least 100 untimed launches, then its timed block (HIP events); "
+                           "cold-cache line: median of single launches after a 512 MiB fill"}
         # the headline GEMM with cold caches: before each launch a 512 MiB fill evicts the operands from
         # L2 and the 256 MB Infinity Cache; each launch is timed on its own (events around the GEMM only)
         flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
@@ -298,7 +305,7 @@ def main():
             def norm(a=a):
                 if lib.mica_rmsnorm_quant(*a) != 0:
                     raise RuntimeError("mica_rmsnorm_quant failed")
-            ms_n = timer.run(norm, max(args.steps, 50), args.warmup)
+            ms_n = timer.run(norm, max(args.steps, 50), extra_warmup(args))
             nbytes = T * (2 * K + K + 4) + 2 * K
             gbs = nbytes / (ms_n * 1e-3) / 1e9
             extra[f"rmsnorm_quant_T{T}"] = {"us": round(ms_n * 1e3, 2), "GB/s": round(gbs, 1),
@@ -321,7 +328,7 @@ def main():
                     def norm3(a3=a3):
                         if lib.mica_rmsnorm_quant_multi(*a3) != 0:
                             raise RuntimeError("mica_rmsnorm_quant_multi failed")
-                    ms_3 = timer.run(norm3, 50, args.warmup)
+                    ms_3 = timer.run(norm3, 50, extra_warmup(args))
                     b3 = T * (2 * K + 3 * (K + 4)) + 2 * K + (12 * K if tag else 0)
                     extra[f"rmsnorm_quant_3consumers{tag}_T4096"] = {
                         "us": round(ms_3 * 1e3, 2), "GB/s": round(b3 / (ms_3 * 1e-3) / 1e9, 1),
@@ -338,7 +345,7 @@ def main():
             o = torch.empty(T, n // 2 if epi else n, dtype=torch.bfloat16, device=dev)
             res = torch.randn(T, n, device=dev).to(torch.bfloat16) if name in ("o", "down") else None
             fn = gemm_launcher(torch, lib, qa, sa, ww, ss, o, residual=res, epilogue=epi)
-            ms_g = timer.run(fn, max(args.steps // 4, 20), args.warmup)
+            ms_g = timer.run(fn, max(args.steps // 4, 20), extra_warmup(args))
             t = 2.0 * T * n * k / (ms_g * 1e-3) / 1e12
             layer[name] = {"us": round(ms_g * 1e3, 2), "TOPS": round(t, 1), "pct_peak": round(100 * t / PEAK_INT8_TOPS, 1)}
             bufs[name] = (qa, sa, ww, ss, o, res, fn)
@@ -352,7 +359,7 @@ def main():
         def requant():
             if lib.mica_act_quant(*ra) != 0:
                 raise RuntimeError("mica_act_quant failed")
-        ms_r = timer.run(requant, 50, args.warmup)
+        ms_r = timer.run(requant, 50, extra_warmup(args))
         rbytes = T * (2 * INTER + INTER + 4)
         layer["requant_h"] = {"us": round(ms_r * 1e3, 2), "GB/s": round(rbytes / (ms_r * 1e-3) / 1e9, 1)}
         ms_norm = extra["rmsnorm_quant_T4096"]["us"] / 1e3
@@ -375,7 +382,7 @@ def main():
             xx, ww, ss = synthetic(torch, dev, m, k, n, seed=m + n + k)
             qa, sa = int8_kernels.act_quant(xx)
             o = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-            ms_g = timer.run(gemm_launcher(torch, lib, qa, sa, ww, ss, o), max(args.steps // 4, 20), args.warmup)
+            ms_g = timer.run(gemm_launcher(torch, lib, qa, sa, ww, ss, o), max(args.steps // 4, 20), extra_warmup(args))
             t = 2.0 * m * n * k / (ms_g * 1e-3) / 1e12
             extra[tag] = {"us": round(ms_g * 1e3, 2), "TOPS": round(t, 1), "frac_int8_peak": round(t / PEAK_INT8_TOPS, 4),
                           "M": m, "K": k, "N": n}
@@ -449,19 +456,19 @@ def gdn_token_mixer(torch, dev, timer, args):
     out = {}
     steps = max(args.steps // 10, 10)
     ms = timer.run(lambda: gdn.causal_conv1d_fn(mixed.transpose(1, 2), w, activation="silu", l2norm_heads=2 * HK),
-                   steps, args.warmup)
+                   steps, extra_warmup(args))
     nb = 2 * B * T * C * 2 + C * 4 * 2
     out["conv_silu_l2norm"] = {"us": round(ms * 1e3, 1), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
                                "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": nb}
     ms = timer.run(lambda: gdn.chunk_gated_delta_rule(q, k, v, gg, beta, output_final_state=True), steps,
-                   args.warmup)
+                   extra_warmup(args))
     flops = 11.5e6 * B * HV * (T // 64)
     nb = B * T * (2 * HK * D * 2 + 2 * HV * D * 2 + HV * 6) + B * HV * D * D * 4
     out["chunk_gated_delta_rule"] = {"us": round(ms * 1e3, 1), "Mtokens/s": round(B * T / (ms * 1e-3) / 1e6, 2),
                                      "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
                                      "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                                      "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "flops": flops, "bytes": nb}
-    ms = timer.run(lambda: gdn.gated_rmsnorm_quant(v.reshape(B * T, HV * D), z, nw), steps, args.warmup)
+    ms = timer.run(lambda: gdn.gated_rmsnorm_quant(v.reshape(B * T, HV * D), z, nw), steps, extra_warmup(args))
     nb = B * T * HV * D * 5 + B * T * 4 + D * 2
     out["gated_rmsnorm_quant"] = {"us": round(ms * 1e3, 1), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
                                   "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": nb}
@@ -487,10 +494,10 @@ def attention_extra(torch, dev, timer, args):
     q, k, v = qkv.view(B, S, HQ + 2 * HK, D).split((HQ, HK, HK), dim=2)
     flops = 4.0 * B * HQ * D * S * S / 2
     steps = max(args.steps // 20, 5)
-    ms = timer.run(lambda: causal_gqa_attention(q, k, v), steps, args.warmup)
+    ms = timer.run(lambda: causal_gqa_attention(q, k, v), steps, extra_warmup(args))
     ms_ref = timer.run(lambda: F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
                                                               is_causal=True, scale=1 / math.sqrt(D), enable_gqa=True),
-                       steps, args.warmup)
+                       steps, extra_warmup(args))
     t = flops / (ms * 1e-3) / 1e12
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(t, 1), "frac_bf16_peak": round(t / PEAK_BF16_TFLOPS, 4),
             "sdpa_us": round(ms_ref * 1e3, 1), "speedup_vs_sdpa": round(ms_ref / ms, 2), "flops": flops}
