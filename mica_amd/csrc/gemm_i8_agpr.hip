@@ -100,11 +100,11 @@ MICA_DEVICE uint32_t lds_addr(const int8_t *p) {
 // N operand fragments (16 bytes per lane) at a + OFF + 2048 i, i < N, by ds_read_b128 written as inline
 // assembly: the destinations are plain VGPRs (the compiler's own LDS loads may target AGPRs, which
 // pushes accumulators out of the AGPRs into copies every k-step).  The compiler does not see these
-// loads: every use waits with an explicit s_waitcnt lgkmcnt and a scheduling barrier, and the
-// s_nops keep the first load clear of MFMAs still reading registers the load may reuse.
+// loads: every use waits with an explicit s_waitcnt lgkmcnt and a scheduling barrier.  (An LDS load
+// may overwrite a register an MFMA issued just before reads as srcA / srcB: the compiler itself emits
+// that order with no wait states for gfx950.)
 template <int OFF, int N, int I = 0>
 MICA_DEVICE void frag_reads(v4i (&r)[N], uint32_t a) {
-    if constexpr (I == 0) asm volatile("s_nop 7\n\ts_nop 7");
     if constexpr (I < N) {
         asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r[I]) : "v"(a), "i"(OFF + I * 16 * QBK));
         frag_reads<OFF, N, I + 1>(r, a);
@@ -247,8 +247,6 @@ struct QTile {
     // MFMAs; D0 >= 0: the plan's instructions from D0 on, one per kDStride MFMAs
     template <bool READ, int ST, bool FIRST, int D0>
     MICA_DEVICE void kstep(Ops &nx, const Ops &cur, uint32_t wa, uint32_t xa, const DmaPlan &dp) {
-        // clear of MFMAs still reading registers the loads may reuse
-        if constexpr (READ) asm volatile("s_nop 7\n\ts_nop 7");
         ks_body<0, READ, ST * C::kBHalf, ST * C::kAHalf, FIRST, D0>(nx, cur, wa, xa, dp);
         __builtin_amdgcn_sched_barrier(0);
     }
