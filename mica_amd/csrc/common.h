@@ -29,6 +29,24 @@ MICA_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
 // Round an fp32 value to the nearest bf16 and return it as fp32.
 MICA_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// bf16(silu(g)) for a bf16 value g, silu(g) = g / (1 + exp(-g)) as F.silu evaluates it on bf16 (fp32 exp,
+// fp32 quotient, rounded to bf16; fused_kernels.py:86-87): exp(-g) as v_exp_f32 of g * -log2(e), and
+// 1 / (1 + e) as v_rcp_f32 refined by one Newton step (0 once 1 + e overflows), times g.  v_rcp_f32
+// flushes results below 2^-126, so a denominator of 2^64 or more is scaled by 2^-64 first (exactly) and
+// the product scaled back.  For every finite bf16 g this rounds to the same bf16 as a float64 exp and an
+// IEEE fp32 quotient do, also with v_exp_f32 and v_rcp_f32 each one ulp off (exhaustive on the CPU with a
+// flushing reciprocal; the GPU suite runs all 65536 codes).  ~15 VALU operations against ~23 for expf
+// and an IEEE division.
+MICA_DEVICE float silu_bf16(float g) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    const float d = 1.0f + e;
+    const float s = d >= 0x1p64f ? 0x1p-64f : 1.0f;
+    const float ds = d * s;
+    const float r0 = __builtin_amdgcn_rcpf(ds);
+    const float r = ds < __builtin_inff() ? __builtin_fmaf(r0, __builtin_fmaf(-ds, r0, 1.0f), r0) : 0.0f;
+    return round_bf16((g * r) * s);
+}
+
 MICA_DEVICE float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // fp32 -> fp16, round to nearest even, of the fp32 value as rounded.  The empty asm keeps the
 // compiler from folding a preceding multiply into the conversion (v_fma_mix*_f16 would round the

@@ -399,7 +399,7 @@ struct TileEngine {
                             } else {
                                 const float gv = round_bf16(((float)acc[j][i][4 * q + t] * sav[i]) * s1[t]);
                                 const float uv = round_bf16(((float)acc[j + 2][i][4 * q + t] * sav[i]) * s2[t]);
-                                const float act = round_bf16(gv / (1.0f + expf(-gv)));
+                                const float act = silu_bf16(gv);
                                 y[t] = act * uv;
                             }
                         }

@@ -369,7 +369,7 @@ struct WideTile {
                             } else {
                                 const float gv = round_bf16(((float)acc[j][i][t] * sav[i]) * s1[t]);
                                 const float uv = round_bf16(((float)acc[j + NB / 2][i][t] * sav[i]) * s2[t]);
-                                const float act = round_bf16(gv / (1.0f + expf(-gv)));
+                                const float act = silu_bf16(gv);
                                 y[t] = act * uv;
                             }
                         }

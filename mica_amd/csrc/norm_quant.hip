@@ -659,14 +659,14 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *g, const ui
         unpack8<MICA_BF16>(uc, uv);
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            const float act = round_bf16(gv[j] / (1.0f + expf(-gv[j])));
+            const float act = silu_bf16(gv[j]);
             out[j] = act * uv[j];
         }
         *(u32x4 *)(y + i0) = pack8<MICA_BF16>(out);
     } else {
         for (long long i = i0; i < n; ++i) {
             const float gv = bf16_to_f32(g[i]);
-            const float act = round_bf16(gv / (1.0f + expf(-gv)));
+            const float act = silu_bf16(gv);
             y[i] = f32_to_bf16(act * bf16_to_f32(u[i]));
         }
     }

@@ -655,6 +655,20 @@ def test_swi_glu_op(gpu, kat):
     assert_within_one_ulp(bits_of(fused_kernels.swi_glu(to_gpu_bf16(g), to_gpu_bf16(u))), O.silu_mul(g, u))
 
 
+def test_silu_every_bf16_gate(gpu):
+    """The SiLU of every finite bf16 gate value (u = 1, so h = bf16(silu(g))) is bit-exact against the
+    oracle's float64 exp and IEEE fp32 quotient: the device formula (v_exp_f32, v_rcp_f32 + one Newton
+    step) that the swi_glu kernel shares with the GEMMs' SiLU epilogue, on this hardware."""
+    note("silu over all bf16 codes")
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    g = g[np.isfinite(O.bf16_to_f32(g))]
+    u = np.full(g.shape, O.f32_to_bf16(np.array([1.0], np.float32))[0], np.uint16)
+    ref = O.silu_mul(g, u)
+    got = bits_of(fused_kernels.swi_glu(to_gpu_bf16(g), to_gpu_bf16(u)))
+    bad = np.flatnonzero(got != ref)
+    assert bad.size == 0, f"{bad.size} gate codes differ, first {g[bad[:5]]}: got {got[bad[:5]]} want {ref[bad[:5]]}"
+
+
 # ------------------------------------------------------------------------------ readout
 def test_readout_config4_shape(gpu, kat):
     """8 requests x 2048 packed tokens, hidden 2560: final RMSNorm at each last position, fp32 dot with
