@@ -71,10 +71,17 @@ MICA_DEVICE void fa_wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// V^T tile image: element (d, key k) of a tile at d * 32 + (((k / 4) ^ vt_swz(d)) * 4) + k % 4 (bf16).
-// Rows are 64 bytes, so 4 consecutive dims span the 64 banks; XOR-ing the 8-byte unit with d / 4 puts
-// the 32 lanes of an operand read (32 consecutive dims, one unit each) on 32 distinct bank pairs.
-MICA_DEVICE int vt_swz(int d) { return (d >> 2) & 7; }
+// V^T tile image: dim d's 32 keys are a 64-byte row of four 16-byte chunks.  Chunk c = 2 s + h holds
+// key units (4 keys each) 4 s + h and 4 s + 2 + h: the 8 keys that a lane in half h of the wave feeds
+// to step s of O^T += V^T P^T (the order of the P^T accumulator rows), so each A operand is one
+// ds_read_b128.  Chunk c sits at position c ^ vt_swz(d): the 16 lanes of a read quarter (16
+// consecutive dims) then cover the 64 banks once.
+MICA_DEVICE int vt_swz(int d) { return (d >> 2) & 3; }
+// bf16 offset of key unit u (keys 4 u .. 4 u + 3) of dim d in the tile image
+MICA_DEVICE int vt_pos(int d, int u) {
+    const int c = 2 * (u >> 2) + (u & 1);
+    return d * kBK + ((c ^ vt_swz(d)) * 2 + ((u >> 1) & 1)) * 4;
+}
 
 struct FaParams {
     const uint16_t *q; long long sbq, shq, ldq; // head h of row t of sequence b: q + b sbq + h shq + t ldq
@@ -111,7 +118,7 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(FaParams p) {
         const int sh = 16 * (i & 1);
         w[0] = ((rows[0][i >> 1] >> sh) & 0xffffu) | (((rows[1][i >> 1] >> sh) & 0xffffu) << 16);
         w[1] = ((rows[2][i >> 1] >> sh) & 0xffffu) | (((rows[3][i >> 1] >> sh) & 0xffffu) << 16);
-        *(u32x2 *)(dst + d * kBK + ((u ^ vt_swz(d)) * 4)) = w;
+        *(u32x2 *)(dst + vt_pos(d, u)) = w;
     }
 }
 
@@ -261,9 +268,7 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
             const int8_t *vrow = vs + d * (kBK * 2);
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const u32x2 a0 = *(const u32x2 *)(vrow + ((4 * s + hi) ^ vt_swz(d)) * 8);
-                const u32x2 a1 = *(const u32x2 *)(vrow + ((4 * s + 2 + hi) ^ vt_swz(d)) * 8);
-                const u32x4 av = {a0[0], a0[1], a1[0], a1[1]};
+                const u32x4 av = *(const u32x4 *)(vrow + ((2 * s + hi) ^ vt_swz(d)) * 16);
                 O[dt] = mfma_bf16(__builtin_bit_cast(bf16x8, av), pb[s], O[dt]);
             }
         }
