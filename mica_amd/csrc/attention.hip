@@ -22,6 +22,8 @@
 // V^T tiles are DMA'd from an image that v_transpose_kernel writes beforehand in exactly the LDS
 // layout.  Two LDS stages: the DMA of tile j + 1 overlaps the MFMAs of tile j.
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -46,13 +48,10 @@ constexpr int kFaThreads = 64 * kFaWaves;
 constexpr int kKBytes = kBK * kD * 2;    // 16 KB: 32 key rows x 512 B
 constexpr int kVBytes = kD * kBK * 2;    // 16 KB: 256 dim rows x 64 B
 constexpr int kStage = kKBytes + kVBytes;
-#ifndef MICA_FA_STAGES
-#define MICA_FA_STAGES 2
-#endif
 #ifndef MICA_FA_OCC
 #define MICA_FA_OCC 2
 #endif
-constexpr int kNSt = MICA_FA_STAGES;     // LDS stages (tiles in flight: kNSt - 1 ahead)
+constexpr int kNSt = 2;                  // LDS stages: tile j + 1 in flight while tile j is read
 constexpr int kFaSmem = kNSt * kStage;   // also the output staging (4 waves x 32 x 512 B) after the loop
 constexpr int kMaxKeySplits = 64;
 
@@ -129,7 +128,7 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
     // dispatched first
     const int qblk = p.ntiles_q - 1 - (SPLIT ? (int)blockIdx.z / p.nsplit : (int)blockIdx.z);
     const int hk = blockIdx.x, b = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hi = lane >> 5;
     const int head = hk * kFaWaves + wave;
     const int q0 = qblk * kBQ;
@@ -146,29 +145,27 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         (void *)(p.k + b * p.sbk + hk * p.shk), 0, (int)((long long)p.Sk * p.ldk * 2), kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.vt + ((long long)(b * p.HK + hk) * p.ntiles_k) * kD * kBK), 0, p.ntiles_k * kVBytes, kBufferFlags);
+    // DMA of key tile j into stage ST.  K: 1 KB block (wave, i) = key rows 2 (4 wave + i) + lane / 32;
+    // the lane writes physical chunk l % 32 of its row, which holds logical chunk (l % 32) ^ row.  V^T:
+    // block (wave, i) of the tile image.  The per-lane offsets are recomputed at every call from an
+    // opaque copy of the lane id: hoisted out of the key loop they stay live across it and push the
+    // kernel's registers into scratch.  (The K offset carries the tile's rows: the per-lane offset is
+    // what the buffer range check sees, which turns rows past Sk into zeros.)
     auto dma_tile = [&](int j, int st) {
         int8_t *ks = smem + st * kStage;
-        // The per-lane offsets are recomputed at every call from an opaque copy of the thread id:
-        // hoisted out of the key loop they stay live across it, get spilled to scratch under the
-        // register pressure of this kernel, and every reload then stalls the DMA issue.
-        int t = tid;
-        __asm__ volatile("" : "+v"(t));
-        const int ln = t & 63, hi_ = ln >> 5, l32_ = ln & 31, w_ = t >> 6;
+        int ln = lane;
+        __asm__ volatile("" : "+v"(ln));
+        const int hi_ = ln >> 5, l32_ = ln & 31;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            // K: 1 KB block (wave, i) = rows 2 (4 wave + i) + lane / 32; lane writes physical chunk l % 32,
-            // which holds logical chunk (l % 32) ^ row
-            const int row = (w_ * 4 + i) * 2 + hi_;
-            const int lc = l32_ ^ row;
-            const int ko = (int)((long long)(j * kBK + row) * p.ldk * 2 + lc * 16);
+            const int row = (wave * 4 + i) * 2 + hi_;
+            const int ko = (int)((long long)(j * kBK + row) * p.ldk * 2 + ((l32_ ^ row) << 4));
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(ks + (wave * 4 + i) * 1024), 16, ko, 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int vo = j * kVBytes + (w_ * 4 + i) * 1024 + ln * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16, vo, 0,
-                                                     0, 0);
-        }
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16,
+                                                     ln * 16, j * kVBytes + (wave * 4 + i) * 1024, 0, 0);
     };
 
     // Q fragments (B operand of S^T): lane holds query q0 + l % 32, dims 16 s + 8 (l / 32) .. + 7
@@ -190,25 +187,28 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
     float m_used = SPLIT ? -1e30f : -__builtin_inff(), lsum = 0.0f;
     const int query = off + q0 + l32; // position of this lane's query
 
-    // prologue: tiles first .. first + kNSt - 2 in flight (tile j in stage (j - first) % kNSt)
+    // K fragment s of a stage (A operand of S^T, read two steps ahead of its MFMA: left to itself the
+    // compiler reads each fragment right before its MFMA and waits)
+    const int kfoff = l32 * 512;
+    // V^T operand (dims 32 dt + l % 32, step s) of a stage: vt_swz(d) does not depend on dt
+    int vfoff[2];
 #pragma unroll
-    for (int i = 0; i < kNSt - 1; ++i)
-        if (first + i <= last_own) dma_tile(first + i, i);
+    for (int s = 0; s < 2; ++s) vfoff[s] = l32 * (kBK * 2) + (((2 * s + hi) ^ vt_swz(l32)) << 4);
+    // tile j in stage (j - first) % 2, the other stage receiving tile j + 1
+    if (first <= last_own) dma_tile(first, 0);
     for (int j = first; j <= last_own; ++j) {
-        // this wave's DMA of tile j landed: at most the DMA of tiles j + 1 .. j + kNSt - 2 (8 each) is
-        // younger; near the end fewer were issued, and waiting for all of them is exact too
-        if (kNSt > 2 && j + kNSt - 2 <= last_own) fa_wait_vmcnt<(kNSt > 2 ? (kNSt - 2) * 8 : 0)>();
-        else fa_wait_vmcnt<0>();
-        __syncthreads();      // ... in every wave; nobody reads stage (j - 1) % kNSt any more
-        if (j + kNSt - 1 <= last_own) dma_tile(j + kNSt - 1, (j - first + kNSt - 1) % kNSt);
-        const int8_t *ks = smem + ((j - first) % kNSt) * kStage;
+        const int st = (j - first) & 1;
+        // this wave's DMA of tile j landed; after the barrier every wave's has, and nobody reads
+        // stage st ^ 1 (tile j - 1) any more
+        fa_wait_vmcnt<0>();
+        __syncthreads();
+        if (j + 1 <= last_own) dma_tile(j + 1, st ^ 1);
+        const int8_t *ks = smem + st * kStage;
         const int8_t *vs = ks + kKBytes;
         // ---- S^T = K Q^T: rows = keys j*32 + acc_row, column = query l % 32 ----
         f32x16 sacc = {};
-        // K fragments read two steps ahead of their MFMA (the schedule is pinned: left to itself the
-        // compiler reads each fragment into one register quad right before its MFMA and waits)
         auto kfrag = [&](int s) {
-            return __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + l32 * 512 + (((2 * s + hi) ^ l32) * 16)));
+            return __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + kfoff + (((2 * s + hi) ^ l32) * 16)));
         };
         bf16x8 ka = kfrag(0), kb = kfrag(1);
 #pragma unroll
@@ -221,23 +221,21 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
             __builtin_amdgcn_sched_barrier(0);
             sacc = mfma_bf16(a, qf[s], sacc);
         }
-        // scores in log2 units, masked above the diagonal, in place
+        // raw scores, masked above the diagonal; the maximum in log2 units (the scale is positive, so
+        // it commutes with the maximum and its rounding)
         float mloc = -__builtin_inff();
         if (j * kBK + kBK - 1 <= off + q0) { // the whole tile lies at or below the block's diagonal
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                sacc[r] = sacc[r] * p.scale_log2;
-                mloc = __builtin_fmaxf(mloc, sacc[r]);
-            }
+            for (int r = 0; r < 16; ++r) mloc = __builtin_fmaxf(mloc, sacc[r]);
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = j * kBK + 8 * (r >> 2) + 4 * hi + (r & 3);
-                sacc[r] = key <= query ? sacc[r] * p.scale_log2 : -__builtin_inff();
+                sacc[r] = key <= query ? sacc[r] : -__builtin_inff();
                 mloc = __builtin_fmaxf(mloc, sacc[r]);
             }
         }
-        mloc = half_swap_max(mloc); // the other half of the wave holds the same queries' other keys
+        mloc = half_swap_max(mloc) * p.scale_log2; // the other half of the wave holds the same queries' other keys
         // lazy rescale: move the reference maximum only when the new one exceeds it by more than 8
         const bool grow = mloc > m_used + 8.0f;
         const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - mloc) : 1.0f;
@@ -247,28 +245,27 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
             for (int dt = 0; dt < kD / 32; ++dt) O[dt] *= alpha;
             lsum *= alpha;
         }
+        // p = 2^(scale s - m), the scaling fused into the exponent's argument
         bf16x8 pb[2];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             u32x4 w;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float p0 = __builtin_amdgcn_exp2f(sacc[8 * s + 2 * e] - m_used);
-                const float p1 = __builtin_amdgcn_exp2f(sacc[8 * s + 2 * e + 1] - m_used);
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[8 * s + 2 * e], p.scale_log2, -m_used));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[8 * s + 2 * e + 1], p.scale_log2, -m_used));
                 lsum += p0 + p1;
                 w[e] = pack_bf16x2(p0, p1);
             }
             pb[s] = __builtin_bit_cast(bf16x8, w);
         }
         // ---- O^T += V^T P^T: lane's keys for step s are rows 8 s .. 8 s + 7 of the accumulator, i.e.
-        // key units 4 s + hi and 4 s + 2 + hi (4 keys each) ----
+        // key units 4 s + hi and 4 s + 2 + hi (4 keys each), one 16-byte chunk of the V^T image ----
 #pragma unroll
         for (int dt = 0; dt < kD / 32; ++dt) {
-            const int d = dt * 32 + l32;
-            const int8_t *vrow = vs + d * (kBK * 2);
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const u32x4 av = *(const u32x4 *)(vrow + ((2 * s + hi) ^ vt_swz(d)) * 16);
+                const u32x4 av = *(const u32x4 *)(vs + vfoff[s] + dt * 32 * (kBK * 2));
                 O[dt] = mfma_bf16(__builtin_bit_cast(bf16x8, av), pb[s], O[dt]);
             }
         }
