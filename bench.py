@@ -289,6 +289,17 @@ def main():
         extra["gemm_headline_cold_caches"] = {"us": round(ms_c * 1e3, 2), "TOPS": round(ops / (ms_c * 1e-3) / 1e12, 1),
                                               "pct_peak": round(100 * ops / (ms_c * 1e-3) / 1e12 / PEAK_INT8_TOPS, 1),
                                               "launches": len(times), "note": "median; 512 MiB fill before each"}
+        # the same shape through ROCm's own int8 GEMM (torch._int_mm: int32 out, no scale epilogue), for
+        # reference
+        try:
+            qwt = qw.t()
+            ms_v = timer.run(lambda: torch._int_mm(qx, qwt), max(args.steps // 4, 10), extra_warmup(args))
+            extra["vendor_int8_gemm_same_shape"] = {
+                "us": round(ms_v * 1e3, 2), "TOPS": round(ops / (ms_v * 1e-3) / 1e12, 1),
+                "note": "torch._int_mm(qx, qw.t()) on M=4096 K=2560 N=9728 (int32 out); the headline kernel "
+                        "also applies the scale epilogue and writes bf16"}
+        except RuntimeError as ex:
+            extra["vendor_int8_gemm_same_shape"] = {"error": str(ex)[:160]}
         # fused RMSNorm + quant (config 1): T * (2K + K + 4) + 2K algorithmic bytes
         for T in (256, 4096, 32768):
             g = torch.Generator().manual_seed(T)
