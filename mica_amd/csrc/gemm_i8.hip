@@ -825,6 +825,13 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
             p.tiles_n = (N + 159) / 160;
             p.dp_tiles = (int)tiles160;
             grid = (int)tiles160;
+            // the AGPR kernel's 4 x 1 wave grid on the same tiles and bits (16-byte output row units),
+            // when the tiles fill more than 3/4 of the CUs.  Measured (same box, bit-identical):
+            // 4096 x 2560 x 4096: 37.5 vs 40.4 us, 4096 x 2560 x 9728: 77.7 vs 81.4; with half the CUs
+            // or fewer busy the 8-wave kernel is ahead (2048 x 2560 x 4096: 26.4 vs 25.2 us).
+            if (kAgpr && K >= 512 && 4 * tiles160 > 3 * (long long)cus && ldc % 8 == 0 && Nout % 8 == 0 &&
+                (!residual || ldr % 8 == 0))
+                return agpr_narrow_launch(p, out_dtype, grid, hb, hr, st);
             return wide_launch(p, epilogue, out_dtype, grid, hb, hr, true, st);
         }
         // 16-bit outputs in whole 16-byte row units and at least 4 slabs of K: the AGPR kernel

@@ -42,11 +42,12 @@ constexpr int kQWaves = 4, kQThreads = 64 * kQWaves;
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// A BM x BN tile on 4 waves in a 2 (M) x 2 (N) grid, NS LDS stages of one slab each.
-template <int BM_, int BN_, int NS_ = 2>
+// A BM x BN tile on 4 waves in a WGM (M) x WGN (N) grid, NS LDS stages of one slab each.
+template <int BM_, int BN_, int NS_ = 2, int WGM_ = 2, int WGN_ = 2>
 struct QCfg {
-    static constexpr int BM = BM_, BN = BN_, NS = NS_;
-    static constexpr int WM = BM / 2, WN = BN / 2;
+    static constexpr int BM = BM_, BN = BN_, NS = NS_, WGM = WGM_, WGN = WGN_;
+    static_assert(WGM * WGN == kQWaves, "wave grid");
+    static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int MB = WM / 16, NB = WN / 16;
     static constexpr int kAHalf = BM * QBK;                 // one stage of A
     static constexpr int kBHalf = BN * QBK;                 // one stage of B
@@ -65,6 +66,9 @@ using QFull = QCfg<256, 256>;      // waves of 128 x 128
 using QHalfN = QCfg<256, 128, 3>;  // waves of 128 x 64 (SCALE tail)
 using QHalfM = QCfg<128, 256, 3>;  // waves of 64 x 128 (SiLU tail)
 using QQuart = QCfg<128, 128, 3>;  // waves of 64 x 64 (SCALE tail at most a quarter of a round)
+// One partial round of 256 x 256 tiles run as 256 x 160 tiles (e.g. N = 2560 at M = 4096: 160 tiles
+// become 256): waves of 64 x 160 stacked along M, 10 x 4 MFMA tiles = 160 accumulators per lane.
+using QNarrow = QCfg<256, 160, 2, 4, 1>;
 
 // LDS: the A stages, the B stages, then (at a fixed place past the largest stage set) two buffers of
 // tile scales (sa, sb, bias: 3 x 256 fp32), for this tile and the next.
@@ -74,7 +78,8 @@ constexpr int kQSmem = kQScale + 2 * kQScaleBuf;
 static_assert(kQSmem <= 160 * 1024, "LDS");
 template <class C>
 constexpr bool stages_fit = C::NS * (C::kAHalf + C::kBHalf) <= kQScale;
-static_assert(stages_fit<QFull> && stages_fit<QHalfN> && stages_fit<QHalfM> && stages_fit<QQuart>, "stages");
+static_assert(stages_fit<QFull> && stages_fit<QHalfN> && stages_fit<QHalfM> && stages_fit<QQuart> &&
+                  stages_fit<QNarrow>, "stages");
 
 // This lane's index, computed afresh where it is used (a few VALU operations per tile instead of a
 // register held across the persistent loop).  The wave index lives in an SGPR.
@@ -258,7 +263,7 @@ struct QTile {
     MICA_DEVICE void run(const GemmParams &p, int8_t *smem, __amdgpu_buffer_rsrc_t rsrc_a,
                          __amdgpu_buffer_rsrc_t rsrc_b, int wave, int m0, int n0, bool has_next, int m0n, int n0n) {
         const int lane = lane_id();
-        const int wm = wave >> 1, wn = wave & 1;
+        const int wm = wave / C::WGN, wn = wave % C::WGN;
         const int r16 = lane & 15, kq = lane >> 4;
         const int nk = p.K / QBK;  // even, at least 4
         const int a0 = opaque_off(dma_base(m0 + wave * C::kADma * 8, p.lda, lane));
@@ -337,7 +342,7 @@ struct QTile {
     MICA_DEVICE void run3(const GemmParams &p, int8_t *smem, int wave, int m0, int n0) {
         static_assert(C::NS == 3, "three stages");
         const int lane = lane_id();
-        const int wm = wave >> 1, wn = wave & 1;
+        const int wm = wave / C::WGN, wn = wave % C::WGN;
         const int r16 = lane & 15, kq = lane >> 4;
         const int nk = p.K / QBK;  // even, at least 4
         const uint32_t lds0 = lds_addr(smem);
@@ -436,7 +441,7 @@ struct QTile {
                               __amdgpu_buffer_rsrc_t rsrc_b, int wave, int m0, int n0, int buf, bool has_next,
                               int m0n, int n0n) {
         const int lane = lane_id();
-        const int wm = wave >> 1, wn = wave & 1;
+        const int wm = wave / C::WGN, wn = wave % C::WGN;
         const int r16 = lane & 15, kq = lane >> 4;
         const float *sc = (const float *)(smem + kQScale + buf * kQScaleBuf);  // sa, sb, bias
         // nothing of the epilogue moves up into the last k-steps (its registers would not fit there)
@@ -664,6 +669,39 @@ __global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_kernel(GemmParams p
     wait_vmcnt<0>();
 }
 
+// One round of 256 x 160 tiles (dp_tiles of them over tiles_m x tiles_n, one per workgroup), SCALE
+// epilogue.
+template <int OUT, bool HAS_BIAS, bool HAS_RES>
+__global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_narrow_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kQSmem];
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, p.M * p.lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, p.N * p.ldb, kBufferFlags);
+    const int tm_n = p.tiles_m, tn_n = p.tiles_n;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    run_qphase<QNarrow, MICA_EPI_SCALE, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, p.dp_tiles,
+                                                               gridDim.x, [&](int h, int &m0, int &n0) {
+                                                                   int tm, tn;
+                                                                   tile_of(h, tm_n, tn_n, tm, tn);
+                                                                   m0 = tm * 256;
+                                                                   n0 = tn * 160;
+                                                                   return true;
+                                                               });
+    // every store of this workgroup has left before the waves end
+    wait_vmcnt<0>();
+}
+
+template <int OUT>
+int agpr_narrow_out(const GemmParams &p, int grid, bool has_bias, bool has_res, hipStream_t st) {
+    dim3 g(grid), b(kQThreads);
+#define MICA_QN(B_, R_) hipLaunchKernelGGL((gemm_i8_agpr_narrow_kernel<OUT, B_, R_>), g, b, 0, st, p)
+    if (has_bias && has_res) MICA_QN(true, true);
+    else if (has_bias) MICA_QN(true, false);
+    else if (has_res) MICA_QN(false, true);
+    else MICA_QN(false, false);
+#undef MICA_QN
+    return mica_err(hipGetLastError());
+}
+
 template <int EPI, int OUT>
 int agpr_launch_out(const GemmParams &p, int grid, bool has_bias, bool has_res, hipStream_t st) {
     dim3 g(grid), b(kQThreads);
@@ -694,5 +732,14 @@ int mica_gemm::agpr_launch(const GemmParams &p, int epilogue, int out_dtype, int
     }
     if (out_dtype == MICA_BF16) return agpr_launch_out<MICA_EPI_SCALE, MICA_BF16>(p, grid, has_bias, has_res, st);
     if (out_dtype == MICA_FP16) return agpr_launch_out<MICA_EPI_SCALE, MICA_FP16>(p, grid, has_bias, has_res, st);
+    return MICA_MISS_ARG;
+}
+
+// Launch of the 256 x 160 AGPR kernel for one round of tiles (p.tiles_n counts 160-column tiles; SCALE
+// epilogue, 16-bit outputs; the same conditions as agpr_launch, and (N + 160) * ldb below 2^31).
+int mica_gemm::agpr_narrow_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res,
+                                  hipStream_t st) {
+    if (out_dtype == MICA_BF16) return agpr_narrow_out<MICA_BF16>(p, grid, has_bias, has_res, st);
+    if (out_dtype == MICA_FP16) return agpr_narrow_out<MICA_FP16>(p, grid, has_bias, has_res, st);
     return MICA_MISS_ARG;
 }

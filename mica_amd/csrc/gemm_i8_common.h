@@ -141,6 +141,7 @@ int wide_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool
 // the AGPR kernel's launcher (gemm_i8_agpr.hip): SCALE (bf16 / fp16) and SiLU (bf16) epilogues
 int agpr_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool has_bias, bool has_res,
                 hipStream_t st);
+int agpr_narrow_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res, hipStream_t st);
 
 }  // namespace mica_gemm
 

@@ -388,6 +388,7 @@ def test_gemm_residual_epilogue(gpu, m, n, k):
     (4096, 2560, 9728, "bias"),      # the down projection's shape
     (3900, 2504, 2560, "residual"),  # both edges ragged; the last tile's upper half 24 columns wide
     (3900, 2500, 512, "fp16"),       # N not a multiple of 8: element stores
+    (4096, 2504, 1024, "fp16"),      # fp16 rows in 16-byte units: the AGPR kernel's 4 x 1 wave grid
 ])
 def test_gemm_narrow_tiles_bit_exact(gpu, m, n, k, epi):
     """One partial round of whole tiles (more than half the CUs busy) runs as 256 x 160 tiles when those
