@@ -71,6 +71,10 @@ class Timer:
             fn()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # an untimed spin kernel ahead of the start event, long enough for the host to queue every timed
+        # launch behind it: the events then bracket back-to-back GPU work, not the host's launch rate
+        # (a 5 us kernel launched through ctypes otherwise waits on the host at the start of the block)
+        torch.cuda._sleep(int(2e9 * 20e-6 * steps) + 1_000_000)
         s.record()
         for _ in range(steps):
             fn()
@@ -268,7 +272,8 @@ def main():
     cpu = cpu_baseline(torch, M, K, N) if not args.no_cpu_baseline else None
 
     if not args.no_extra:
-        extra = {"timing": "each line: at least 100 untimed launches, then its timed block (HIP events); "
+        extra = {"timing": "each line: at least 100 untimed launches, then an untimed spin kernel while the host queues "
+                           "the timed block, then its timed block (HIP events); "
                            "cold-cache line: median of single launches after a 512 MiB fill"}
         # the headline GEMM with cold caches: before each launch a 512 MiB fill evicts the operands from
         # L2 and the 256 MB Infinity Cache; each launch is timed on its own (events around the GEMM only)
@@ -426,8 +431,9 @@ def main():
         "config": {"workload": "W8A8 GEMM M=4096 K=2560 N=9728 (4B MLP projection at T=4096), int8 x int8 -> "
                                "int32 on MFMA, per-token x per-channel scale epilogue, bf16 out",
                    "M": M, "K": K, "N": N, "T": M, "parallelism": "none (1 GPU)",
-                   "timing": "HIP events around the K timed launches, after the W warmup launches; measured "
-                             "after the other lines of this run (GPU clocks of a busy GPU)"},
+                   "timing": "HIP events around the K timed launches, after the W warmup launches and an untimed "
+                             "spin kernel that lets the host queue them; measured after the other lines of this run "
+                             "(GPU clocks of a busy GPU)"},
         "pct_int8_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(),
