@@ -469,38 +469,66 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
     const int row = blockIdx.x * (kSmoothThreads / 64) + (threadIdx.x >> 6);
     const bool on = row < p.M;
     const bool has_res = NORM && p.res != nullptr;
+    // every output's factors go to LDS: chunk ch = c * 64 + lane of output o at float4 pair
+    // ((o * NCH + c) * 64 + lane) * 2; with the norm, the multipliers offset + w (fp32) after them as
+    // output NOUT.  This thread's share is loaded first, the row second: the memory counter retires
+    // loads in issue order, so the LDS fill waits for the factors alone, and the barrier after it waits
+    // for LDS only -- each wave then starts on its row as soon as that row has arrived, instead of the
+    // whole workgroup waiting for its slowest row (which a full __syncthreads() fence would do).
+    extern __shared__ float4 inv_sh[];
+    constexpr int kSets = SMOOTH ? NOUT : 0;  // factor sets before the norm's multipliers
+    constexpr int kFill = (NCH * 64 + kSmoothThreads - 1) / kSmoothThreads;  // chunks per thread and set
+    float4 fin[kSets > 0 ? kSets : 1][kFill][2];
+    u32x4 win[NORM ? kFill : 1];
+    // (both loads are issued on every path, idle lanes re-reading the last valid chunk or row, so that
+    // the compiler's wait before the LDS fill counts only the loads issued after the factors')
+#pragma unroll
+    for (int i = 0; i < kFill; ++i) {
+        const int ch = (int)threadIdx.x + i * kSmoothThreads;
+        const int chc = ch < NCH * 64 ? ch : NCH * 64 - 1;
+#pragma unroll
+        for (int o = 0; o < kSets; ++o) {
+            fin[o][i][0] = ((const float4 *)(p.inv[o] + chc * kChunk))[0];
+            fin[o][i][1] = ((const float4 *)(p.inv[o] + chc * kChunk))[1];
+        }
+        if (NORM) win[i] = *(const u32x4 *)((const uint16_t *)p.w + chc * kChunk);
+    }
+    // the scheduler keeps the multiplier loads ahead of the row loads; with smoothing factors held too,
+    // pinning that order makes the compiler spill them, so it keeps its own order there
+    if constexpr (!SMOOTH) __builtin_amdgcn_sched_barrier(0);
     u32x4 cur[NCH], rc[NORM ? NCH : 1];
-    if (on) {
-        const uint16_t *xr = (const uint16_t *)p.x + (long)row * p.ldx;
+    const int rowc = on ? row : p.M - 1;  // a launched block holds at least one row (M >= 1)
+    {
+        const uint16_t *xr = (const uint16_t *)p.x + (long)rowc * p.ldx;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) cur[c] = *(const u32x4 *)(xr + c * kRowStep + lane * kChunk);
         if (has_res) {
-            const uint16_t *rr = (const uint16_t *)p.res + (long)row * p.ldr;
+            const uint16_t *rr = (const uint16_t *)p.res + (long)rowc * p.ldr;
 #pragma unroll
             for (int c = 0; c < NCH; ++c) rc[NORM ? c : 0] = *(const u32x4 *)(rr + c * kRowStep + lane * kChunk);
         }
     }
-    // every output's factors into LDS: chunk ch = c * 64 + lane of output o at float4 pair
-    // ((o * NCH + c) * 64 + lane) * 2; with the norm, the multipliers offset + w (fp32) after them as
-    // output NOUT
-    extern __shared__ float4 inv_sh[];
-    constexpr int kSets = SMOOTH ? NOUT : 0;  // factor sets before the norm's multipliers
 #pragma unroll
-    for (int o = 0; o < kSets; ++o) {
-        for (int ch = threadIdx.x; ch < NCH * 64; ch += kSmoothThreads) {
-            inv_sh[(o * NCH * 64 + ch) * 2] = ((const float4 *)(p.inv[o] + ch * kChunk))[0];
-            inv_sh[(o * NCH * 64 + ch) * 2 + 1] = ((const float4 *)(p.inv[o] + ch * kChunk))[1];
+    for (int i = 0; i < kFill; ++i) {
+        const int ch = (int)threadIdx.x + i * kSmoothThreads;
+        if (ch < NCH * 64) {
+#pragma unroll
+            for (int o = 0; o < kSets; ++o) {
+                inv_sh[(o * NCH * 64 + ch) * 2] = fin[o][i][0];
+                inv_sh[(o * NCH * 64 + ch) * 2 + 1] = fin[o][i][1];
+            }
+            if (NORM) {
+                float wv[kChunk];
+                unpack8<MICA_BF16>(win[i], wv);
+                inv_sh[(kSets * NCH * 64 + ch) * 2] = float4{p.offset + wv[0], p.offset + wv[1], p.offset + wv[2], p.offset + wv[3]};
+                inv_sh[(kSets * NCH * 64 + ch) * 2 + 1] = float4{p.offset + wv[4], p.offset + wv[5], p.offset + wv[6], p.offset + wv[7]};
+            }
         }
     }
-    if (NORM) {
-        for (int ch = threadIdx.x; ch < NCH * 64; ch += kSmoothThreads) {
-            float wv[kChunk];
-            unpack8<MICA_BF16>(*(const u32x4 *)((const uint16_t *)p.w + ch * kChunk), wv);
-            inv_sh[(kSets * NCH * 64 + ch) * 2] = float4{p.offset + wv[0], p.offset + wv[1], p.offset + wv[2], p.offset + wv[3]};
-            inv_sh[(kSets * NCH * 64 + ch) * 2 + 1] = float4{p.offset + wv[4], p.offset + wv[5], p.offset + wv[6], p.offset + wv[7]};
-        }
-    }
-    __syncthreads();
+    // LDS-only barrier: this wave's LDS stores are complete (lgkmcnt 0; vmcnt and expcnt left at their
+    // maxima), then every wave of the workgroup has passed that point
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+    __builtin_amdgcn_s_barrier();
     if (!on) return;
 
     float v[NCH][kChunk];
