@@ -525,10 +525,13 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
             }
         }
     }
-    // LDS-only barrier: this wave's LDS stores are complete (lgkmcnt 0; vmcnt and expcnt left at their
-    // maxima), then every wave of the workgroup has passed that point
-    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+    // LDS-only barrier: release and acquire fences of workgroup scope restricted to the LDS address
+    // space around the barrier.  They order the LDS stores above before, and the LDS loads below after,
+    // the barrier in the compiler's memory model, and lower to a wait on the LDS counter alone
+    // (lgkmcnt 0), leaving the row's global loads in flight
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     if (!on) return;
 
     float v[NCH][kChunk];

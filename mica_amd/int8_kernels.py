@@ -5,7 +5,8 @@ Same contract as the reference:
   * ``act_quant(x, inv_smooth=None) -> (q, s) | None`` (int8_kernels.py:325-353)
   * ``mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16) -> Tensor | None`` (:359-406)
   * ``available(device=None) -> (bool, str)`` (:146-159), ``preload(device=None) -> int`` (:217-224),
-    ``kernel_dir()`` (:83-84), ``STATS`` (:19), ``ATTN`` / ``attn_keys`` / ``attn_fwd`` (:409-481)
+    ``kernel_dir()`` (:83-84; MICA_W8A8_AOT_DIR when set, where the reference keeps ``s.pt``),
+    ``STATS`` (:19), ``ATTN`` / ``attn_keys`` / ``attn_fwd`` (:409-481)
   * an unsupported input returns ``None`` and counts the reason in ``STATS['fallback']`` (:22-24);
     every launch adds 1 to ``STATS['launch']`` (:310); a device error raises RuntimeError (:60-64).
   * outputs are allocated with torch on the input's device; kernels run on torch's current stream
@@ -55,7 +56,19 @@ def _launched():
         STATS["launch"] += 1
 
 
+ENV_DIR = "MICA_W8A8_AOT_DIR"   # int8_kernels.py:10
+
+
 def kernel_dir() -> Path:
+    """The directory the reference's callers read their kernel-side files from, the SmoothQuant
+    statistics ``s.pt`` among them (``decide`` and ``apply``, int8_runtime.py:227, 265): the directory
+    named by MICA_W8A8_AOT_DIR when it is set, as in the reference (int8_kernels.py:83-84), else that of
+    libmica_amd.so (lib_dir())."""
+    env = os.environ.get(ENV_DIR)
+    return Path(env) if env else lib_dir()
+
+
+def lib_dir() -> Path:
     """Directory holding libmica_amd.so (env MICA_AMD_LIB_DIR overrides)."""
     return _lib.lib_path().parent
 
@@ -91,7 +104,7 @@ def available(device=None):
     arch = _gfx(dev)
     if arch != 950:
         return (False, f"gfx{arch} is not gfx950")
-    return (True, f"gfx950 kernels from {kernel_dir()}")
+    return (True, f"gfx950 kernels from {lib_dir()}")
 
 
 def preload(device=None) -> int:

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import hashlib
 import json
-import re
+import struct
 import time
 import types
 from pathlib import Path
@@ -37,11 +37,26 @@ def _ieee_div(num: torch.Tensor, den: float) -> torch.Tensor:
     return num / torch.full((), den, dtype=num.dtype, device=num.device)
 
 
-def quant_weight(w: torch.Tensor):
-    """Per-output-channel symmetric int8 (int8_quant.quant_weight, int8_quant.py:54-61); offline.  The
-    scales are IEEE quotients max(amax, 1e-8) / 127 on any device (see _ieee_div)."""
+SCALE_DIVISION = ("ieee", "reciprocal")
+
+
+def quant_weight(w: torch.Tensor, division: str = "ieee"):
+    """Per-output-channel symmetric int8 (int8_quant.quant_weight, int8_quant.py:54-61); offline.
+
+    ``division`` picks how the scale max(amax, 1e-8) / 127 is rounded.  'ieee' (default): the IEEE fp32
+    quotient on any device (see _ieee_div), the bits of the reference's CPU path.  'reciprocal':
+    fl(amax * fl(1 / 127)), the bits torch produces on a GPU for the same expression (a division by a
+    Python scalar becomes a multiplication by its fp32 reciprocal), i.e. the bits of weights the reference
+    converts on the GPU (release_runtime.py:267-272 -> int8_runtime.apply -> convert).  The two differ by
+    one ulp on a few per cent of channels; q is then rounded from w / s with either s."""
+    if division not in SCALE_DIVISION:
+        raise ValueError(f"division must be one of {SCALE_DIVISION}, got {division!r}")
     wf = w.float()
-    s = _ieee_div(wf.abs().amax(1).clamp_min(EPS), QMAX)
+    amax = wf.abs().amax(1).clamp_min(EPS)
+    if division == "ieee":
+        s = _ieee_div(amax, QMAX)
+    else:
+        s = amax * torch.full((), 1.0, dtype=torch.float32, device=amax.device).div_(QMAX)
     q = torch.round(wf / s[:, None]).clamp(-127, 127).to(torch.int8)
     return q, s
 
@@ -76,7 +91,9 @@ class QLinear(nn.Module):
     int8 activations themselves (the fused RMSNorm + quantizer).
     """
 
-    def __init__(self, linear, smooth=None, backend="aot", keep_bf16=False):
+    def __init__(self, linear, smooth=None, backend="aot", keep_bf16=False, division="ieee"):
+        """From a bf16 linear (int8_runtime.py:109-127): SmoothQuant factors folded into the weight, which
+        is then quantized per output channel; ``division`` is quant_weight's scale rounding."""
         super().__init__()
         w = linear.weight.detach()
         self.register_buffer("w16", w.contiguous() if keep_bf16 else None)
@@ -89,7 +106,7 @@ class QLinear(nn.Module):
             self.register_buffer("inv_smooth", (torch.ones_like(smooth) / smooth).contiguous())
         else:
             self.inv_smooth = None
-        q, s = quant_weight(wf)
+        q, s = quant_weight(wf, division)
         self.register_buffer("qweight", q.contiguous())
         self.register_buffer("wscale", s.contiguous())
         self.register_buffer("bias", None if linear.bias is None else linear.bias.detach().float().contiguous())
@@ -325,27 +342,50 @@ def load_stats(path):
 
 
 MODULE_GROUPS = {"gdn": LINEAR_NAMES[:5], "attn": LINEAR_NAMES[5:9], "mlp": LINEAR_NAMES[9:]}  # int8_quant.py:6-9
+MODULE_GROUPS["ffn"] = MODULE_GROUPS["mlp"]
 MODULE_GROUPS["all"] = LINEAR_NAMES
+DEFAULT_LAYERS = range(0, 16)     # int8_quant.py:10
+
+
+def parse_modules(spec=None) -> tuple:
+    """The linear names a module spec selects (int8_quant.parse_modules, int8_quant.py:16-30): None is all
+    twelve; otherwise a comma-separated string or a sequence whose items are group names ('gdn', 'attn',
+    'mlp' or its alias 'ffn', 'all') or linear names, blank items ignored, expanded in order with
+    repeats dropped.  A name that is neither raises ValueError."""
+    if spec is None:
+        return LINEAR_NAMES
+    items = [str(x).strip() for x in (spec.split(",") if isinstance(spec, str) else spec)]
+    names = dict.fromkeys(n for item in items if item for n in MODULE_GROUPS.get(item, (item,)))
+    unknown = [n for n in names if n not in LINEAR_NAMES]
+    if unknown:
+        raise ValueError(f"unknown module names {unknown}; known {list(LINEAR_NAMES)}")
+    return tuple(names)
+
+
+def parse_layers(spec=None, n_layers=None) -> list:
+    """Sorted distinct layer indices of a layer spec (int8_quant.parse_layers, int8_quant.py:33-51): None is
+    layers 0-15 (DEFAULT_LAYERS); a string is comma-separated indices and inclusive ranges ('0-3,8');
+    anything else an iterable of indices.  With ``n_layers``, indices >= n_layers are dropped."""
+    if spec is None:
+        spec = DEFAULT_LAYERS
+    if isinstance(spec, str):
+        picked = set()
+        for part in filter(None, (p.strip() for p in spec.split(","))):
+            lo, sep, hi = part.partition("-")
+            picked.update(range(int(lo), int(hi) + 1) if sep else (int(part),))
+        spec = picked
+    out = sorted({int(i) for i in spec})
+    return out if n_layers is None else [i for i in out if i < n_layers]
 
 
 def target_linears(body, layers=None, modules=None):
-    """(qualified name, parent module, attribute, nn.Linear) of every linear named in ``modules`` (a group
-    name or attribute names; default all twelve) inside ``body.layers[i]`` for i in ``layers`` (default
-    all), in layer order and module-tree order; the qualified name is ``layers.{i}.{path}`` as the
-    statistics file keys it (int8_quant.target_linears, int8_quant.py:99-110)."""
-    if modules is None:
-        wanted = set(LINEAR_NAMES)
-    else:
-        wanted = set()
-        for m in ([modules] if isinstance(modules, str) else modules):
-            wanted |= set(MODULE_GROUPS.get(m, (m,)))
-        unknown = wanted - set(LINEAR_NAMES)
-        if unknown:
-            raise ValueError(f"unknown linear names {sorted(unknown)}; known {list(LINEAR_NAMES)}")
-    n = len(body.layers)
-    idx = range(n) if layers is None else sorted({int(i) for i in layers if int(i) < n})
+    """(qualified name, parent module, attribute, nn.Linear) of every linear ``modules`` selects
+    (parse_modules) inside ``body.layers[i]`` for the layers ``layers`` selects (parse_layers: None is
+    layers 0-15, as in the reference), in layer order and module-tree order; the qualified name is
+    ``layers.{i}.{path}`` as the statistics file keys it (int8_quant.target_linears, int8_quant.py:99-110)."""
+    wanted = set(parse_modules(modules))
     found = []
-    for i in idx:
+    for i in parse_layers(layers, len(body.layers)):
         for path, parent in body.layers[i].named_modules():
             for attr, child in parent.named_children():
                 if attr in wanted and isinstance(child, nn.Linear):
@@ -353,69 +393,92 @@ def target_linears(body, layers=None, modules=None):
     return found
 
 
-def convert(body, stats=None, alpha=ALPHA, layers=None, modules=None):
+def convert(body, stats=None, alpha=ALPHA, layers=None, modules=None, division="ieee"):
     """Replace the body's bf16 linears by W8A8 QLinears in place (int8_runtime.convert,
     int8_runtime.py:195-206): a linear whose input absmax is in ``stats`` (load_stats) is smoothed with
     SmoothQuant factors (alpha 0.5) folded into its weight before quantization, the others are quantized
-    as they are.  Returns (linears replaced, linears smoothed)."""
+    as they are.  ``layers`` None converts every layer, as the reference's convert does (it passes all of
+    them to target_linears); ``division`` is quant_weight's scale rounding.  Returns (linears replaced,
+    linears smoothed)."""
     replaced = smoothed = 0
+    layers = range(len(body.layers)) if layers is None else layers
     for name, parent, attr, child in target_linears(body, layers, modules):
         amax = None if stats is None else stats.get(name)
         smooth = None if amax is None else smooth_factors(amax, child.weight.detach(), alpha)
-        setattr(parent, attr, QLinear(child, smooth))
+        setattr(parent, attr, QLinear(child, smooth, division=division))
         replaced += 1
         smoothed += smooth is not None
     return replaced, smoothed
 
 
-def _safetensors_header(path):
-    """The JSON header of a .safetensors file (8-byte little-endian length, then JSON); no tensor data
-    is read."""
+def _tensor_shapes(path) -> dict:
+    """{tensor name: shape tuple} of a .safetensors file, read from its JSON header alone (an 8-byte
+    little-endian length, then the JSON); no tensor data is touched."""
     with open(path, "rb") as f:
-        n = int.from_bytes(f.read(8), "little")
-        if not 0 < n < (1 << 30):
+        (size,) = struct.unpack("<Q", f.read(8))
+        if not 0 < size < (1 << 30):
             raise ValueError(f"{path}: not a safetensors file")
-        return json.loads(f.read(n).decode("utf-8"))
+        header = json.loads(f.read(size))
+    return {name: tuple(entry["shape"]) for name, entry in header.items() if name != "__metadata__"}
+
+
+def _weight_sources(folder: Path):
+    """The files whose headers describe the linears, and the leaf name of a linear's matrix in them:
+    the int8 file and its ``qweight`` buffers when present; otherwise the bf16 ``weight`` matrices of the
+    shards that ``model.safetensors.index.json`` lists (those present in the folder), or of
+    ``model.safetensors`` when there is no index."""
+    if (folder / FILE).is_file():
+        return [folder / FILE], "qweight"
+    index = folder / "model.safetensors.index.json"
+    shards = {"model.safetensors"}
+    if index.is_file():
+        shards = set(json.loads(index.read_text(encoding="utf-8"))["weight_map"].values())
+    return [folder / name for name in sorted(shards) if (folder / name).is_file()], "weight"
+
+
+def _is_layer_linear(name: str, leaf: str) -> bool:
+    """True for ``<...>.layers.<i>.<...>.<linear>.<leaf>`` with <linear> one of LINEAR_NAMES, outside the
+    multi-token-prediction head (names starting with ``mtp``)."""
+    parts = name.split(".")
+    if name.startswith("mtp") or len(parts) < 3 or parts[-1] != leaf or parts[-2] not in LINEAR_NAMES:
+        return False
+    return any(a == "layers" and b.isdigit() for a, b in zip(parts[:-2], parts[1:-1]))
+
+
+def _qkv_row_ranges(folder: Path):
+    """(hidden, q/k width, v width) of the linear-attention in_proj_qkv from config.json (its
+    ``text_config`` when nested), or None when the file or a key is missing."""
+    try:
+        cfg = json.loads((folder / "config.json").read_text(encoding="utf-8"))
+        text = cfg.get("text_config", cfg)
+        return (text["hidden_size"], text["linear_num_key_heads"] * text["linear_key_head_dim"],
+                text["linear_num_value_heads"] * text["linear_value_head_dim"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def linear_shapes(folder):
-    """(N, K, has_bias) of every decoder-layer W8A8 linear in a checkpoint folder, from file headers only
-    (int8_runtime.linear_shapes, int8_runtime.py:312-355): the ``qweight`` buffers of a
-    ``model-int8.safetensors``, else the ``weight`` of the bf16 ``model*.safetensors`` shards.  The
-    linear-attention in_proj_qkv also contributes its q / k and v row ranges, which rows_forward runs
-    as separate GEMMs, when config.json gives the head sizes.  Multi-token-prediction layers (``mtp``)
-    are skipped.  These are the shapes the self-test checks before a model is served."""
+    """(N, K, has_bias) of every decoder-layer W8A8 linear in a checkpoint folder, sorted, from file
+    headers only: the shape set the self-test is run on before a model is served (the output of
+    int8_runtime.linear_shapes, int8_runtime.py:312-355).  A linear has a bias when ``<prefix>.bias`` is
+    in the same file.  When config.json gives the linear-attention head sizes and a bias-free
+    in_proj_qkv [2 KD + VD, H] is present, its q / k rows [KD, H] and v rows [VD, H] are added too:
+    rows_forward runs those ranges as GEMMs of their own."""
     folder = Path(folder)
-    if (folder / FILE).is_file():
-        files, leaf = [folder / FILE], "qweight"
-    else:
-        index = folder / "model.safetensors.index.json"
-        names = (sorted(set(json.loads(index.read_text(encoding="utf-8"))["weight_map"].values()))
-                 if index.is_file() else ["model.safetensors"])
-        files, leaf = [folder / n for n in names if (folder / n).is_file()], "weight"
-    layer = re.compile(r"(?:^|\.)layers\.\d+\.")
-    out = set()
+    files, leaf = _weight_sources(folder)
+    found = set()
     for path in files:
-        head = _safetensors_header(path)
-        for key, info in head.items():
-            if key == "__metadata__" or key.startswith("mtp") or not layer.search(key):
-                continue
-            parts = key.split(".")
-            if len(parts) < 2 or parts[-1] != leaf or parts[-2] not in LINEAR_NAMES or len(info["shape"]) != 2:
-                continue
-            n, k = info["shape"]
-            out.add((n, k, key[: -len(leaf)] + "bias" in head))
-    try:
-        cfg = json.loads((folder / "config.json").read_text(encoding="utf-8"))
-        cfg = cfg.get("text_config", cfg)
-        hidden = cfg["hidden_size"]
-        kd = cfg["linear_num_key_heads"] * cfg["linear_key_head_dim"]
-        vd = cfg["linear_num_value_heads"] * cfg["linear_value_head_dim"]
-        if (2 * kd + vd, hidden, False) in out:
-            out |= {(kd, hidden, False), (vd, hidden, False)}
-    except (OSError, KeyError, ValueError):
-        pass
-    return sorted(out)
+        shapes = _tensor_shapes(path)
+        for name, shape in shapes.items():
+            if len(shape) == 2 and _is_layer_linear(name, leaf):
+                prefix = name[: -len(leaf) - 1]
+                found.add((shape[0], shape[1], prefix + ".bias" in shapes))
+    widths = _qkv_row_ranges(folder)
+    if widths is not None:
+        hidden, kd, vd = widths
+        if (2 * kd + vd, hidden, False) in found:
+            found.update({(kd, hidden, False), (vd, hidden, False)})
+    return sorted(found)
 
 
 def load_linears(path, device="cuda"):
@@ -499,8 +562,10 @@ def _selftest_case(q, x, wd):
     return y, launches, _row_rel(y, exact), _row_rel(emulated, exact)
 
 
-def selftest(shapes, device, rows=SELFTEST_ROWS, seed=SELFTEST_SEED):
-    """The reference's acceptance test (int8_runtime.py:362-443), on mica_amd's kernels.
+def selftest(shapes, device, backend="aot", rows=SELFTEST_ROWS, seed=SELFTEST_SEED):
+    """The reference's acceptance test (int8_runtime.py:362-443), on mica_amd's kernels; same positional
+    signature, ``selftest(shapes, device, backend)``, which the reference's self-test child calls
+    (int8_runtime.py:292).  ``backend`` must be 'aot': there is no other backend here.
 
     For every (N, K, has_bias) and every row count, with and without SmoothQuant factors: QLinear(x)
     must take exactly 2 kernel launches, be finite, and its row-relative L2 error against the fp32
@@ -514,6 +579,9 @@ def selftest(shapes, device, rows=SELFTEST_ROWS, seed=SELFTEST_SEED):
     started = time.perf_counter()
     report = {"ok": False, "reason": "", "cases": 0, "max_err_vs_noise": 0.0}
     try:
+        if backend != "aot":
+            report["reason"] = f"backend {backend!r} is not available: mica_amd runs the 'aot' kernels only"
+            return report
         dev = torch.device(device)
         g = torch.Generator().manual_seed(seed)
         first_launch = aot.STATS["launch"]

@@ -122,3 +122,80 @@ def test_loaded_linear_runs_bit_exact(gpu, ckpt):
     ref = O.qlinear(x, t[pre + ".qweight"].numpy(), t[pre + ".wscale"].numpy(), bias=t[pre + ".bias"].numpy(),
                     inv_smooth=t[pre + ".inv_smooth"].numpy())
     assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+
+
+# ------------------------------------------------- linear_shapes on the bf16 checkpoint routes
+def _bf16_linear(t, prefix, n, k, bias=False):
+    t[prefix + ".weight"] = torch.zeros(n, k, dtype=torch.bfloat16)
+    if bias:
+        t[prefix + ".bias"] = torch.zeros(n, dtype=torch.bfloat16)
+
+
+def _config(folder, nested=True, **over):
+    cfg = {"hidden_size": H, "linear_num_key_heads": 2, "linear_key_head_dim": KD // 2,
+           "linear_num_value_heads": 3, "linear_value_head_dim": VD // 3}
+    cfg.update(over)
+    (folder / "config.json").write_text(json.dumps({"text_config": cfg} if nested else cfg))
+
+
+def test_linear_shapes_sharded_bf16(tmp_path):
+    """Shards named by model.safetensors.index.json: 'weight' leaves of decoder-layer linears only; a shard
+    the index lists but the folder lacks is skipped; a bias counts when it sits in the same shard."""
+    a, b = {}, {}
+    _bf16_linear(a, "model.language_model.layers.0.linear_attn.in_proj_qkv", 2 * KD + VD, H)
+    _bf16_linear(a, "model.language_model.layers.0.mlp.gate_proj", I, H)
+    _bf16_linear(a, "model.language_model.layers.3.self_attn.q_proj", H, H, bias=True)
+    a["model.language_model.layers.0.input_layernorm.weight"] = torch.zeros(H, dtype=torch.bfloat16)
+    a["model.language_model.embed_tokens.weight"] = torch.zeros(64, H, dtype=torch.bfloat16)
+    _bf16_linear(b, "model.language_model.layers.1.mlp.down_proj", H, I)
+    _bf16_linear(b, "mtp.layers.0.mlp.down_proj", H + 16, I)              # multi-token-prediction: skipped
+    _bf16_linear(b, "model.visual.blocks.0.mlp.up_proj", 48, 32)           # not under layers.<i>: skipped
+    _bf16_linear(b, "model.language_model.layers.2.self_attn.k_proj", 64, H)
+    b["model.language_model.layers.2.self_attn.k_proj.qweight"] = torch.zeros(8, H, dtype=torch.int8)  # wrong leaf
+    b["model.language_model.layers.2.mlp.gate_proj.weight"] = torch.zeros(I, dtype=torch.bfloat16)   # not 2-D
+    save_file(a, str(tmp_path / "model-00001-of-00003.safetensors"))
+    save_file(b, str(tmp_path / "model-00002-of-00003.safetensors"))
+    wm = {k: "model-00001-of-00003.safetensors" for k in a}
+    wm.update({k: "model-00002-of-00003.safetensors" for k in b})
+    wm["model.language_model.layers.5.mlp.up_proj.weight"] = "model-00003-of-00003.safetensors"  # absent shard
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": wm}))
+    _config(tmp_path)
+    assert int8_runtime.linear_shapes(tmp_path) == sorted({
+        (2 * KD + VD, H, False), (KD, H, False), (VD, H, False),    # in_proj_qkv and its q/k and v row ranges
+        (I, H, False), (H, H, True), (H, I, False), (64, H, False)})
+
+
+def test_linear_shapes_single_file_and_config_forms(tmp_path):
+    """No index: model.safetensors alone.  The in_proj_qkv split reads a flat config as well as a nested
+    text_config, and only applies to a bias-free [2 KD + VD, H] linear."""
+    t = {}
+    _bf16_linear(t, "model.layers.0.linear_attn.in_proj_qkv", 2 * KD + VD, H)
+    _bf16_linear(t, "model.layers.0.linear_attn.out_proj", H, VD)
+    save_file(t, str(tmp_path / "model.safetensors"))
+    _config(tmp_path, nested=False)
+    assert int8_runtime.linear_shapes(tmp_path) == sorted({(2 * KD + VD, H, False), (KD, H, False), (VD, H, False),
+                                                           (H, VD, False)})
+    _config(tmp_path, linear_num_value_heads=4)     # widths that do not add up to the stored linear: no split
+    assert int8_runtime.linear_shapes(tmp_path) == sorted({(2 * KD + VD, H, False), (H, VD, False)})
+    (tmp_path / "config.json").write_text(json.dumps({"hidden_size": H}))    # keys missing: no split, no error
+    assert int8_runtime.linear_shapes(tmp_path) == sorted({(2 * KD + VD, H, False), (H, VD, False)})
+    (tmp_path / "config.json").unlink()                                     # no config at all
+    assert int8_runtime.linear_shapes(tmp_path) == sorted({(2 * KD + VD, H, False), (H, VD, False)})
+    t2 = {}
+    _bf16_linear(t2, "model.layers.0.linear_attn.in_proj_qkv", 2 * KD + VD, H, bias=True)
+    save_file(t2, str(tmp_path / "model.safetensors"))
+    _config(tmp_path)
+    assert int8_runtime.linear_shapes(tmp_path) == [(2 * KD + VD, H, True)]   # biased: not split
+
+
+def test_linear_shapes_prefers_int8_file(ckpt):
+    """With model-int8.safetensors present, bf16 shards in the same folder are not read."""
+    folder, _ = ckpt
+    t = {}
+    _bf16_linear(t, "model.layers.0.mlp.gate_proj", 4 * I, H)
+    save_file(t, str(folder / "model.safetensors"))
+    assert (4 * I, H, False) not in int8_runtime.linear_shapes(folder)
+
+
+def test_linear_shapes_empty_folder(tmp_path):
+    assert int8_runtime.linear_shapes(tmp_path) == []

@@ -164,3 +164,65 @@ def test_convert_smooths_where_statistics_exist():
         qo, so = O.quant_weight(wf)
         assert np.array_equal(mod.qweight.numpy(), qo), name
         assert np.array_equal(mod.wscale.numpy().view(np.uint32), so.view(np.uint32)), name
+
+
+def test_parse_modules_specs():
+    """Module specs as int8_quant.parse_modules reads them (int8_quant.py:16-30)."""
+    assert R.parse_modules(None) == R.LINEAR_NAMES
+    assert R.parse_modules("attn,mlp") == ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                           "down_proj")
+    assert R.parse_modules("ffn") == R.parse_modules("mlp") == ("gate_proj", "up_proj", "down_proj")
+    assert R.parse_modules(" o_proj , ,mlp,o_proj") == ("o_proj", "gate_proj", "up_proj", "down_proj")
+    assert R.parse_modules(["gdn", "out_proj", "q_proj"]) == ("in_proj_qkv", "in_proj_z", "in_proj_a",
+                                                             "in_proj_b", "out_proj", "q_proj")
+    assert R.parse_modules("all") == R.LINEAR_NAMES
+    with pytest.raises(ValueError, match="lm_head"):
+        R.parse_modules("mlp,lm_head")
+
+
+def test_parse_layers_specs():
+    """Layer specs as int8_quant.parse_layers reads them (int8_quant.py:33-51)."""
+    assert R.parse_layers(None) == list(range(16))
+    assert R.parse_layers(None, 8) == list(range(8))
+    assert R.parse_layers("0-3, 8,2,,10-10") == [0, 1, 2, 3, 8, 10]
+    assert R.parse_layers([5, 1, 5, 30], 16) == [1, 5]
+    assert R.parse_layers(range(20, 40), 36) == list(range(20, 36))
+
+
+def test_target_linears_default_layers_and_string_specs():
+    torch.manual_seed(0)
+    body = nn.Module()
+    body.layers = nn.ModuleList([_Layer(16, attention=True) for _ in range(20)])
+    assert {n.split(".")[1] for n, *_ in R.target_linears(body)} == {str(i) for i in range(16)}
+    got = [n for n, *_ in R.target_linears(body, layers="17-18", modules="ffn,o_proj")]
+    assert got == [f"layers.{i}.{m}" for i in (17, 18)
+                   for m in ("self_attn.o_proj", "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")]
+    # convert with no layer spec converts every layer, as the reference's convert does
+    assert R.convert(body, None, modules="o_proj") == (20, 0)
+
+
+def test_weight_scale_division_modes():
+    """'ieee' (default) is the CPU path's quotient amax / 127; 'reciprocal' is fl(amax * fl(1/127)), what
+    torch computes for the same expression on a GPU.  Both pinned against numpy fp32; they differ on
+    some channels, so the option is not a no-op."""
+    rng = np.random.default_rng(11)
+    w = torch.from_numpy(rng.standard_normal((4096, 64)).astype(np.float32) * rng.uniform(0.01, 3, (4096, 1))
+                         .astype(np.float32))
+    amax = np.maximum(np.abs(w.numpy()).max(1), np.float32(1e-8)).astype(np.float32)
+    q_i, s_i = R.quant_weight(w)
+    q_r, s_r = R.quant_weight(w, division="reciprocal")
+    ieee = (amax / np.float32(127)).astype(np.float32)
+    recip = (amax * (np.float32(1) / np.float32(127))).astype(np.float32)
+    assert np.array_equal(s_i.numpy().view(np.uint32), ieee.view(np.uint32))
+    assert np.array_equal(s_r.numpy().view(np.uint32), recip.view(np.uint32))
+    assert 0 < np.count_nonzero(ieee != recip) < ieee.size // 4
+    qo, so = O.quant_weight(w.numpy())
+    assert np.array_equal(q_i.numpy(), qo) and np.array_equal(s_i.numpy(), so)
+    # q rounds w / s with the chosen s (IEEE quotient, half-even, clamp)
+    assert np.array_equal(q_r.numpy(), np.clip(np.rint(w.numpy() / s_r.numpy()[:, None]), -127, 127).astype(np.int8))
+    with pytest.raises(ValueError):
+        R.quant_weight(w, division="fast")
+    lin = nn.Linear(64, 4096, bias=False)
+    lin.weight.data = w.to(torch.bfloat16)
+    mod = R.QLinear(lin, division="reciprocal")
+    assert np.array_equal(mod.wscale.numpy(), R.quant_weight(w.to(torch.bfloat16), "reciprocal")[1].numpy())

@@ -4,13 +4,18 @@ static device array of the library) against mica_mm_i8 with a workspace, both ca
 Bar: bit-identical outputs (int8 x int8 -> int32 accumulators, then the same epilogue).  Two calls in a
 row, the second smaller, so the shared scratch's arrival counters must come back to zero after each
 launch; a split round larger than the scratch is rejected with MICA_MISS_RANGE."""
+import json
+import os
+import subprocess
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
 import torch
 
 from mica_amd import _lib, int8_kernels
+from oracle import w8a8 as O
 
 pytestmark = pytest.mark.gpu
 
@@ -81,6 +86,9 @@ def test_noalloc_matches_mica_mm_i8_twice(gpu, calls):
             continue
         a, b = _both(A, B, sa, sb, torch.int32, _lib.EPI_SCALE, n)
         _same(a, b, f"int32 call {i}")
+        rows = np.unique(np.r_[0, m - 1, rng.integers(0, m, 6)])   # noalloc's accumulators against the oracle
+        want = O.int_gemm(A.cpu().numpy()[rows], B.cpu().numpy())
+        assert np.array_equal(b.cpu().numpy()[rows], want), f"int32 call {i}: noalloc differs from the oracle"
         res = torch.randn(m, n, device=gpu).to(torch.bfloat16)
         a, b = _both(A, B, sa, sb, torch.bfloat16, _lib.EPI_SCALE, n, residual=res)
         _same(a, b, f"bf16 + residual call {i}")
@@ -96,3 +104,58 @@ def test_noalloc_rejects_a_split_round_beyond_the_scratch(gpu):
     # the existing entry point serves it (its workspace is sized for every CU)
     assert _call(False, A, B, sa, sb, out, _lib.BF16, _lib.EPI_SILU_MUL) == 0
     torch.cuda.synchronize()
+
+
+def _capture_child():
+    """Run in a fresh process: the process's first mica_mm_i8_noalloc calls are made inside a HIP-graph
+    capture (torch.cuda.graph) on a split shape, so the scratch lookup and its counter clear happen
+    under capture.  The graph is replayed three times, with eager work and synchronisation between the
+    replays, and every replay is compared with eager mica_mm_i8 (own workspace) and, for the int32
+    accumulators, with the oracle on sampled rows.  Prints one JSON line."""
+    dev = torch.device("cuda", 0)
+    L = _lib.load()
+    rng = np.random.default_rng(21)
+    m, n, k = 256, 2560, 9728                    # a split round of 10 tiles
+    A, B, sa, sb = _operands(rng, m, n, k, dev)
+    eager_i32 = torch.empty((m, n), dtype=torch.int32, device=dev)
+    eager_bf16 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    assert _call(False, A, B, sa, sb, eager_i32, _lib.INT32, _lib.EPI_SCALE) == 0
+    assert _call(False, A, B, sa, sb, eager_bf16, _lib.BF16, _lib.EPI_SCALE) == 0
+    out_i32 = torch.full((m, n), -1, dtype=torch.int32, device=dev)
+    out_bf16 = torch.full((m, n), -1, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = [_call(True, A, B, sa, sb, out_i32, _lib.INT32, _lib.EPI_SCALE),
+              _call(True, A, B, sa, sb, out_bf16, _lib.BF16, _lib.EPI_SCALE)]
+    result = {"rc": rc, "replays": []}
+    rows = np.unique(np.r_[0, m - 1, rng.integers(0, m, 6)])
+    want = O.int_gemm(A.cpu().numpy()[rows], B.cpu().numpy())
+    for r in range(3):
+        out_i32.fill_(-1)
+        out_bf16.fill_(-1)
+        (A.float() @ B[:64].float().t().contiguous()).sum().item()   # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        result["replays"].append({
+            "int32_differs": int((out_i32 != eager_i32).sum().item()),
+            "bf16_differs": int((out_bf16.view(torch.int16) != eager_bf16.view(torch.int16)).sum().item()),
+            "oracle_rows_equal": bool(np.array_equal(out_i32.cpu().numpy()[rows], want)),
+        })
+    print(json.dumps(result), flush=True)
+
+
+def test_noalloc_first_call_under_graph_capture(gpu):
+    """A caller under HIP-graph capture whose first noalloc call is the captured one (see _capture_child)."""
+    note("noalloc first call inside graph capture: m=256 n=2560 k=9728, child process")
+    here = Path(__file__).resolve().parent
+    code = f"import sys; sys.path[:0] = [{str(here.parent)!r}, {str(here)!r}]; import test_zz_no_alloc as t; t._capture_child()"
+    proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=240,
+                          env=dict(os.environ), cwd=str(here.parent))
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    r = json.loads(proc.stdout.strip().splitlines()[-1])
+    assert r["rc"] == [0, 0], r
+    assert len(r["replays"]) == 3
+    for i, rep in enumerate(r["replays"]):
+        assert rep == {"int32_differs": 0, "bf16_differs": 0, "oracle_rows_equal": True}, (i, r)
