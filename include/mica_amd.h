@@ -231,6 +231,22 @@ int mica_attention_fwd_split(const void *q, long long sbq, long long shq, long l
                              int HK, int head_dim, float scale, int causal, int key_splits, void *workspace,
                              long long workspace_bytes, mica_stream_t stream);
 
+/*
+ * mica_attention_fwd_split with a key count per sequence: kv_len (int32 [B], device memory) gives
+ * sequence b's number of keys, clamped to Sq .. Sk; its queries are the last Sq positions of those
+ * kv_len[b] keys, and keys kv_len[b] .. Sk - 1 are never read.  This is the key limit of the reference's
+ * last-position pass over requests padded to a common width (prefill_engine.py:298-304, 332-336:
+ * keys < limit); with one query per sequence it runs only the picked positions' attention.  Each
+ * query's arithmetic is that of mica_attention_fwd for the same query over the same keys, so with
+ * key_splits = 1 the result equals the unpadded run's row bit for bit.  workspace as for
+ * mica_attention_fwd_split.
+ */
+int mica_attention_fwd_kvlen(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
+                             long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv,
+                             void *o, long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
+                             int HK, int head_dim, float scale, int causal, int key_splits, const int *kv_len,
+                             void *workspace, long long workspace_bytes, mica_stream_t stream);
+
 /* bytes of mica_attention_fwd_split workspace: the V^T images, then B x HQ x key_splits x
  * 32 ceil(Sq / 32) rows of 1032 bytes (O, m, l); -1 for an invalid argument */
 long long mica_attention_split_workspace_bytes(int B, int Sq, int Sk, int HQ, int HK, int key_splits);

@@ -33,14 +33,18 @@ def key_splits_for(B: int, Sq: int, Sk: int, HK: int, cus: int = 256, per_cu: in
     return int(max(1, min(want, most, MAX_KEY_SPLITS)))
 
 
-def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits: int = 1):
+def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits: int = 1, kv_len=None):
     """Launch the kernel on q [B, Sq, HQ, 256] / k, v [B, Sk, HK, 256] ('bshd') or q [B, HQ, Sq, 256] /
     k, v [B, HK, Sk, 256] ('bhsd') views with unit feature stride.  Returns o in q's layout
     (contiguous [B, Sq, HQ, 256] memory), or raises ValueError on an unsupported input.
 
     key_splits > 1 divides each query block's keys over that many workgroups and merges their partial
     softmax states (mica_attention_fwd_split): faster for few query blocks over many keys, equal to the
-    unsplit result within bf16 rounding but not bit for bit."""
+    unsplit result within bf16 rounding but not bit for bit.
+
+    kv_len (int32 [B] on the device, optional): sequence b's key count, clamped to Sq .. Sk; its queries
+    are then the last Sq positions of its first kv_len[b] keys (mica_attention_fwd_kvlen), e.g. the last
+    real position of each request of a batch padded to a common width."""
     for t in (q, k, v):
         if not t.is_cuda:
             raise ValueError("mica_amd attention runs on the GPU only (got a CPU tensor)")
@@ -70,7 +74,14 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
         raise ValueError("attention operands must be 16-byte aligned")
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else float(scale)
     o_st = (o.stride(0), o.stride(2), o.stride(1))
-    if key_splits == 1:
+    if kv_len is not None:
+        if kv_len.dtype != torch.int32 or kv_len.device != dev or kv_len.numel() != B or not kv_len.is_contiguous():
+            raise ValueError("kv_len must be a contiguous int32 [B] tensor on q's device")
+        rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd_kvlen(
+            q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), o.data_ptr(), *o_st,
+            B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, key_splits, kv_len.data_ptr(), ws.data_ptr(), nbytes,
+            _stream(dev))), "mica_attention_fwd_kvlen")
+    elif key_splits == 1:
         rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd(
             q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), o.data_ptr(), *o_st,
             B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, ws.data_ptr(), nbytes, _stream(dev))), "mica_attention_fwd")
@@ -85,8 +96,8 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
     return o if q_layout == "bshd" else o.transpose(1, 2)
 
 
-def causal_gqa_attention(q, k, v, scale: float | None = None, key_splits: int = 1):
+def causal_gqa_attention(q, k, v, scale: float | None = None, key_splits: int = 1, kv_len=None):
     """softmax(scale q k^T, causal) v per sequence and head on [B, S, heads, 256] views (e.g. of the
     fused QKV output); query head h reads key/value head h // 4.  Returns o [B, S, HQ, 256] bf16.
-    With Sk > Sq the queries are the last Sq positions; key_splits as in attention_fwd."""
-    return attention_fwd(q, k, v, "bshd", scale, key_splits)
+    With Sk > Sq the queries are the last Sq positions; key_splits and kv_len as in attention_fwd."""
+    return attention_fwd(q, k, v, "bshd", scale, key_splits, kv_len)

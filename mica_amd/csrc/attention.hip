@@ -5,7 +5,10 @@
 //
 //   o[t, h] = sum_{u <= t + Sk - Sq} softmax_u(scale q[t, h] . k[u, g(h)]) v[u, g(h)],  g(h) = h / (HQ / HK)
 //
-// (Sq queries over Sk >= Sq keys: the queries are the last Sq positions, as in the reference's kernel.)
+// (Sq queries over Sk >= Sq keys: the queries are the last Sq positions, as in the reference's kernel.
+// With per-sequence key counts kv_len[b] (clamped to Sq .. Sk), sequence b's queries are the last Sq
+// positions of its first kv_len[b] keys: Sk becomes kv_len[b] in the sum's bound, and the keys past it
+// are never read -- the reference's key limit of the padded last-position pass, prefill_engine.py:332-336.)
 //
 // Work split: one workgroup of 4 waves per (sequence, key/value head, block of 32 query positions);
 // wave w handles query head 4 g + w, so every K / V tile brought into LDS serves the 4 query heads of
@@ -95,6 +98,7 @@ struct FaParams {
     // fa_merge_kernel; part_* rows are (b, head, split, query), sq_pad = ntiles_q * 32 of them each
     int nsplit, sq_pad;
     float *part_o, *part_m, *part_l;
+    const int *kv_len;                          // [B] per-sequence key counts, or null: Sk for every one
 };
 
 // ---- V -> V^T tile images: one workgroup per (tile, sequence x head); thread = 8 dims x 4 keys ----
@@ -132,7 +136,9 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
     const int l32 = lane & 31, hi = lane >> 5;
     const int head = hk * kFaWaves + wave;
     const int q0 = qblk * kBQ;
-    const int off = p.Sk - p.Sq; // position of query row t is off + t
+    // sequence b's key count (its queries are the last Sq of them); position of query row t: off + t
+    const int skb = p.kv_len ? min(max(p.kv_len[b], p.Sq), p.Sk) : p.Sk;
+    const int off = skb - p.Sq;
     // key tiles 0 .. last: the last one holds the block's last query position
     const int last = min(p.ntiles_k - 1, (off + q0 + kBQ - 1) / kBK);
     // this workgroup's tiles first .. last_own (all of them without a split)
@@ -365,8 +371,8 @@ namespace {
 int attention_launch(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
                      long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv, void *o,
                      long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ, int HK, int head_dim,
-                     float scale, int causal, int key_splits, void *workspace, long long workspace_bytes,
-                     mica_stream_t stream) {
+                     float scale, int causal, int key_splits, const int *kv_len, void *workspace,
+                     long long workspace_bytes, mica_stream_t stream) {
     if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || Sq < 0 || Sk < Sq) return MICA_MISS_SHAPE;
     if (!causal || key_splits < 1 || key_splits > kMaxKeySplits) return MICA_MISS_ARG;
     if (B == 0 || Sq == 0) return 0;
@@ -392,6 +398,7 @@ int attention_launch(const void *q, long long sbq, long long shq, long long ldq,
     p.scale_log2 = scale * 1.44269504088896341f;
     p.nsplit = key_splits;
     p.sq_pad = ntiles_q * kBQ;
+    p.kv_len = kv_len;
     if (key_splits > 1) {
         // partial states after the V^T images: O rows (1 KiB each), then m, then l
         const long long rows = (long long)B * HQ * key_splits * p.sq_pad;
@@ -425,7 +432,7 @@ extern "C" int mica_attention_fwd(const void *q, long long sbq, long long shq, l
                                   int Sk, int HQ, int HK, int head_dim, float scale, int causal, void *workspace,
                                   long long workspace_bytes, mica_stream_t stream) {
     return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
-                            head_dim, scale, causal, 1, workspace, workspace_bytes, stream);
+                            head_dim, scale, causal, 1, nullptr, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mica_attention_fwd_split(const void *q, long long sbq, long long shq, long long ldq, const void *k,
@@ -435,5 +442,16 @@ extern "C" int mica_attention_fwd_split(const void *q, long long sbq, long long 
                                         int causal, int key_splits, void *workspace, long long workspace_bytes,
                                         mica_stream_t stream) {
     return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
-                            head_dim, scale, causal, key_splits, workspace, workspace_bytes, stream);
+                            head_dim, scale, causal, key_splits, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mica_attention_fwd_kvlen(const void *q, long long sbq, long long shq, long long ldq, const void *k,
+                                        long long sbk, long long shk, long long ldk, const void *v, long long sbv,
+                                        long long shv, long long ldv, void *o, long long sbo, long long sho,
+                                        long long ldo, int B, int Sq, int Sk, int HQ, int HK, int head_dim, float scale,
+                                        int causal, int key_splits, const int *kv_len, void *workspace,
+                                        long long workspace_bytes, mica_stream_t stream) {
+    if (kv_len == nullptr) return MICA_MISS_ARG;
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
+                            head_dim, scale, causal, key_splits, kv_len, workspace, workspace_bytes, stream);
 }

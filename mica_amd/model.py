@@ -22,6 +22,13 @@ v0.5/serving/lib/fork.py:394-422, without those two ops):
 A gated-delta-net layer replaces the first four steps with mica_amd.gdn.GDNLayer (fork.gdn_step,
 fork.py:20-149: one norm + quant for the four input projections, conv, gate, chunked scan, gated
 norm fused with out_proj's quantisation, out_proj with the residual).
+The last layer runs last-only, as the reference's PrefillEngine does by default (last_only=True,
+prefill_engine.py:181, 283-339): its input norm + quant, K / V projection and RoPE of the keys cover
+every row (the picked queries attend to all of them), while the query projection, attention, O
+projection, post-attention norm and MLP run on the B picked rows only; a GDN last layer runs its mixer
+over every row and the MLP on the picked rows.  Each picked row's values are bit-identical to those of
+the full layer (rows of a GEMM are independent and the attention kernel's per-query arithmetic is the
+same; W8A8Stack(last_only=False) runs the full layer).
 Then, as PrefillEngine.final + the readout do (prefill_engine.py:280-304, release_runtime.py:298-306,
 :509-517), only each request's last position is normed and dotted with the allowed label rows, and
 the option slice is softmaxed.  Requests are packed back to back, all of the same length.
@@ -97,6 +104,10 @@ class Layer:
         self.qkv = _rand_qlinear((cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim, H, g, device)
         self.o = _rand_qlinear(H, cfg.heads * cfg.head_dim, g, device)
         _mlp_weights(self, cfg, g, device)
+        # the last-only pass's two projections: views of the fused weight's query rows and K / V rows
+        nq = cfg.heads * cfg.head_dim
+        self.q_rows = QLinear.from_quantized(self.qkv.qweight[:nq], self.qkv.wscale[:nq])
+        self.kv_rows = QLinear.from_quantized(self.qkv.qweight[nq:], self.qkv.wscale[nq:])
 
 
 def _mlp_weights(layer, cfg, g, device):
@@ -126,6 +137,15 @@ class GDNBlock:
             num_k_heads=hk, num_v_heads=hv, norm_offset=0.0, z_eps=cfg.eps)
         self.post_norm = _rand_norm(H, g, device)
         _mlp_weights(self, cfg, g, device)
+
+
+def _norm_quant(h, w, eps, keep_normed):
+    """The layer's fused RMSNorm (zero-centred weight: offset 0 on the stored 1 + w) + int8 quant:
+    (q, s, None), or (q, s, y) with the bf16 normed rows kept for a trace."""
+    if keep_normed:
+        return rms_norm_quant(h, w, eps, offset=0.0, return_normed=True)
+    q, s = rms_norm_quant(h, w, eps, offset=0.0)
+    return q, s, None
 
 
 def _rope(S, head_dim, theta, device):
@@ -176,9 +196,11 @@ class W8A8Stack:
     """Random-init 4B-shaped stack; `prefill(ids, batch)` returns option probabilities."""
 
     def __init__(self, cfg: StackConfig = StackConfig(), device="cuda", seed=0, attention: str = "mica",
-                 split_keys: bool = False):
+                 split_keys: bool = False, last_only: bool = True):
         self.cfg = cfg
         self.attention = attention
+        # the last layer at the picked rows only (prefill_engine.py:181, 283-339); same bits per row
+        self.last_only = last_only
         # continuations over a prefix (Sk > S): divide each query block's keys over several workgroups
         # (attention.key_splits_for).  Off by default: the continuation then matches a full run within
         # bf16 rounding instead of bit for bit.
@@ -245,6 +267,70 @@ class W8A8Stack:
             a = a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
         return (a, state) if keep else a
 
+    def _attention_rows(self, qr, kv, B, S, rows, past=None, pos=None):
+        """Attention of the last-only pass: one query per request, the picked row rows[b] (int32, a row
+        of the packed [B * S] batch), over its request's keys.  qr: the picked rows' query projection
+        [B, heads * d]; kv: every row's K / V projection [B * S, 2 * kv_heads * d].  RoPE rotates the
+        keys of every row (positions as in _attention) and each query at its own position; the query of
+        request b, at position p_b = rows[b] - b S (+ the prefix length), sees keys 0 .. p_b, i.e.
+        kv_len[b] = p_b + 1 (the reference's key limit, prefill_engine.py:332-336).  Returns
+        [B, heads * d]."""
+        cfg = self.cfg
+        hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        P = 0 if past is None else past[0].shape[1]
+        cos, sin = self._tables(P + S, kv.device)
+        if P == 0:
+            rope_inplace(kv, hk, d, cos, sin, period=S)
+        else:
+            rope_inplace(kv, hk, d, cos, sin, pos=pos)
+        qpos = (rows - torch.arange(B, device=rows.device, dtype=torch.int32) * S + P).to(torch.int32)
+        rope_inplace(qr, hq, d, cos, sin, pos=qpos)
+        k, v = kv.view(B, S, 2 * hk, d).split((hk, hk), dim=2)
+        if P:
+            k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
+            v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
+        q = qr.view(B, 1, hq, d)
+        kv_len = (qpos + 1).to(torch.int32)
+        if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
+            return causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), kv_len=kv_len).view(B, hq * d)
+        seen = torch.arange(P + S, device=q.device)[None, :] < kv_len[:, None]
+        a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                           attn_mask=seen[:, None, None, :], scale=1.0 / math.sqrt(d),
+                                           enable_gqa=True)
+        return a.transpose(1, 2).reshape(B, hq * d).contiguous()
+
+    def last_layer_forward(self, L, h, B, S, rows, trace=None, past=None, pos=None):
+        """The last layer at the picked rows only (prefill_engine.py:283-339): returns the layer's
+        output rows [B, hidden] for the packed rows ``rows`` (int32 [B], device), bit-identical to
+        layer_forward's output at those rows."""
+        cfg = self.cfg
+        t = {} if trace is not None else None
+        if isinstance(L, GDNBlock):
+            init = None if past is None else tuple(x.expand(B, *x.shape[1:]) for x in past)
+            full = L.mixer(h, B, initial=init)
+            h1 = full.index_select(0, rows)
+            if t is not None:
+                t.update(kind="gdn_last", h=h, mixer_out=full)
+        else:
+            q, s, y = _norm_quant(h, L.input_norm, cfg.eps, t is not None)
+            kv = L.kv_rows.forward_quantized(q, s)
+            qr = L.q_rows.forward_quantized(q.index_select(0, rows), s.index_select(0, rows))
+            if t is not None:
+                t.update(kind="attention_last", h=h, q=q, s=s, y=y, kv=kv.clone(), qr=qr.clone())
+            a = self._attention_rows(qr, kv, B, S, rows, past, pos)
+            r = aot.act_quant(a)
+            h1 = L.o.forward_quantized(*r, residual=h.index_select(0, rows))
+            if t is not None:
+                t.update(kv_rope=kv, qr_rope=qr, a=a, qa=r[0], sa=r[1])
+        q2, s2, y2 = _norm_quant(h1, L.post_norm, cfg.eps, t is not None)
+        g = L.gate_up.forward_quantized(q2, s2)
+        qh, sh = aot.act_quant(g)
+        h2 = L.down.forward_quantized(qh, sh, residual=h1)
+        if t is not None:
+            t.update(rows=rows, h1=h1, q2=q2, s2=s2, y2=y2, g=g, qh=qh, sh=sh, h2=h2)
+            trace.append(t)
+        return h2
+
     @staticmethod
     def _mask(S, P, device):
         """Boolean [S, P + S] mask: query i (position P + i) sees keys 0 .. P + i."""
@@ -265,7 +351,7 @@ class W8A8Stack:
                 h1, state = h1
             t = dict(kind="gdn", h=h, mixer=t, h1=h1) if trace is not None else None
         else:
-            q, s = rms_norm_quant(h, L.input_norm, cfg.eps, offset=0.0)
+            q, s, y = _norm_quant(h, L.input_norm, cfg.eps, trace is not None)
             qkv = L.qkv.forward_quantized(q, s)
             qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
             a = self._attention(qkv, B, S, past, keep, pos)
@@ -273,14 +359,14 @@ class W8A8Stack:
                 a, state = a
             r = aot.act_quant(a)
             h1 = L.o.forward_quantized(*r, residual=h)
-            t = dict(kind="attention", h=h, q=q, s=s, qkv=qkv_out, qkv_rope=qkv, a=a, qa=r[0], sa=r[1],
+            t = dict(kind="attention", h=h, q=q, s=s, y=y, qkv=qkv_out, qkv_rope=qkv, a=a, qa=r[0], sa=r[1],
                      h1=h1) if trace is not None else None
-        q2, s2 = rms_norm_quant(h1, L.post_norm, cfg.eps, offset=0.0)
+        q2, s2, y2 = _norm_quant(h1, L.post_norm, cfg.eps, trace is not None)
         g = L.gate_up.forward_quantized(q2, s2)
         qh, sh = aot.act_quant(g)
         h2 = L.down.forward_quantized(qh, sh, residual=h1)
         if trace is not None:
-            t.update(q2=q2, s2=s2, g=g, qh=qh, sh=sh, h2=h2)
+            t.update(q2=q2, s2=s2, y2=y2, g=g, qh=qh, sh=sh, h2=h2)
             trace.append(t)
         return (h2, state) if keep else h2
 
@@ -329,8 +415,14 @@ class W8A8Stack:
         S = ids.numel() // batch
         h = self.embed.index_select(0, ids)
         pos = None if prefix is None else prefix.positions_for(batch, S, ids.device)
-        for i, L in enumerate(self.layers):
-            h = self.layer_forward(L, h, batch, S, trace, past=None if prefix is None else prefix.layers[i], pos=pos)
+        past = (lambda i: None) if prefix is None else (lambda i: prefix.layers[i])  # noqa: E731
+        n = len(self.layers)
+        full = n - 1 if self.last_only and n else n
+        for i in range(full):
+            h = self.layer_forward(self.layers[i], h, batch, S, trace, past=past(i), pos=pos)
+        if full < n:
+            h = self.last_layer_forward(self.layers[-1], h, batch, S, rows, trace, past=past(n - 1), pos=pos)
+            rows = torch.arange(batch, device=h.device, dtype=torch.int32)   # h now holds the picked rows
         logits, probs = self.readout(h, rows, self.final_norm, self.cfg.eps, offset=0.0, lo=lo, cnt=cnt,
                                      probs_width=self.cfg.n_options)
         if trace is not None:

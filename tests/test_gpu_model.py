@@ -57,6 +57,18 @@ def _check_mlp(L, t, cfg, li):
     assert np.array_equal(bits(t["h2"]), h2), f"layer {li}: down + residual"
 
 
+def _check_norm_quant(h_bits, norm_w, cfg, y_bits, q, s, what):
+    """Fused norm + quant rows: the normed row y within one bf16 ulp of the oracle's norm of h (the fp32
+    sum-of-squares order is not pinned), and q, s bit-exact with the oracle's quantizer applied to the
+    kernel's own y -- on every row."""
+    yo, _ = O.rms_norm(h_bits, O.bf16_to_f32(bits(norm_w)), cfg.eps, 0.0)
+    within_one_ulp(y_bits, yo, min_exact=0.99)
+    qy, sy = O.quant_act(O.bf16_to_f32(y_bits))
+    assert np.array_equal(q, qy) and np.array_equal(s, sy), f"{what} norm + quant: int8 / scale vs the kernel's y"
+    same = np.all(q == O.quant_act(O.bf16_to_f32(yo))[0], axis=1)
+    print(f"[case] {what} norm+quant rows equal to the oracle's own: {same.mean():.4f}", file=sys.stderr)
+
+
 @pytest.fixture(autouse=True)
 def _strict(monkeypatch):
     monkeypatch.setattr(int8_kernels, "STRICT", True)
@@ -66,7 +78,7 @@ def test_small_stack_stage_by_stage(gpu):
     print("[case] small stack", file=sys.stderr, flush=True)
     cfg = StackConfig(layers=2, hidden=512, intermediate=1024, heads=8, kv_heads=2, head_dim=64, vocab=4096,
                       n_options=31)
-    st = W8A8Stack(cfg, device=gpu, seed=3)
+    st = W8A8Stack(cfg, device=gpu, seed=3, last_only=False)
     B, S = 2, 96
     ids = torch.randint(0, cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(5)).to(gpu)
     trace = []
@@ -130,7 +142,7 @@ def test_hybrid_stack_gdn_and_attention_layers(gpu):
     print("[case] hybrid stack", file=sys.stderr, flush=True)
     cfg = StackConfig(layers=4, hidden=512, intermediate=1024, heads=4, kv_heads=1, head_dim=256, vocab=4096,
                       n_options=31, full_attention_interval=2, linear_k_heads=2, linear_v_heads=4)
-    st = W8A8Stack(cfg, device=gpu, seed=7)
+    st = W8A8Stack(cfg, device=gpu, seed=7, last_only=False)
     assert [type(L).__name__ for L in st.layers] == ["GDNBlock", "Layer", "GDNBlock", "Layer"]
     B, S = 2, 80
     ids = torch.randint(0, cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(9)).to(gpu)
@@ -173,7 +185,8 @@ def test_config4_full_stack_8x2048(gpu):
     assert p.shape == (B, cfg.n_options)
     assert np.isfinite(p).all() and np.allclose(p.sum(1), 1.0, atol=1e-5)
 
-    # the same run with the last layer traced (the trace only keeps tensors the run makes anyway)
+    # the same run with the whole last layer (every row) traced: the prefill ran that layer last-only
+    # (its query side, attention, O and MLP at the 8 picked rows), which must give the same bits
     rows_last = torch.arange(B, device=gpu, dtype=torch.int32) * S + (S - 1)
     lo, cnt = st.slices(None, None, B, gpu)
     h = st.embed.index_select(0, ids)
@@ -183,7 +196,7 @@ def test_config4_full_stack_8x2048(gpu):
     logits2, probs2 = st.readout(h, rows_last, st.final_norm, cfg.eps, offset=0.0, lo=lo, cnt=cnt,
                                  probs_width=cfg.n_options)
     torch.cuda.synchronize()
-    assert torch.equal(logits2, logits) and torch.equal(probs2, probs), "traced run differs from prefill"
+    assert torch.equal(logits2, logits) and torch.equal(probs2, probs), "full last layer differs from last-only"
 
     L, t = st.layers[-1], trace[0]
     rng = np.random.default_rng(4)
@@ -191,13 +204,10 @@ def test_config4_full_stack_8x2048(gpu):
     trows = torch.from_numpy(rows).to(gpu)
     sel = lambda x: x.index_select(0, trows)  # noqa: E731
     hb = bits(sel(t["h"]))
-    # input norm + quant (the normed bf16 row may differ by one ulp: rows that agree quantize exactly)
-    yo, _ = O.rms_norm(hb, O.bf16_to_f32(bits(L.input_norm)), cfg.eps, 0.0)
-    qo, so = O.quant_act(O.bf16_to_f32(yo))
+    # input norm + quant: the kernel's normed bf16 row within one ulp of the oracle's, and its int8 row and
+    # scale bit-exact with the oracle's quantizer applied to that row, for every sampled row
     q, s = sel(t["q"]).cpu().numpy(), sel(t["s"]).cpu().numpy()
-    same = np.all(q == qo, axis=1) & (s == so)
-    print(f"[case] config 4 input norm+quant rows matching the oracle: {same.mean():.4f}", file=sys.stderr)
-    assert same.mean() >= 0.95
+    _check_norm_quant(hb, L.input_norm, cfg, bits(sel(t["y"])), q, s, "input")
     # QKV from the kernel's q, s: bit-exact
     qkv = O.epilogue(O.int_gemm(q, L.qkv.qweight.cpu().numpy()), s, L.qkv.wscale.cpu().numpy())
     assert np.array_equal(bits(sel(t["qkv"])), qkv), "qkv"
@@ -216,12 +226,8 @@ def test_config4_full_stack_8x2048(gpu):
     h1 = O.f32_to_bf16(O.bf16_to_f32(h1) + O.bf16_to_f32(hb))
     assert np.array_equal(bits(sel(t["h1"])), h1), "o_proj + residual"
     # post-attention norm + quant, SiLU epilogue, requant, down + residual
-    y2, _ = O.rms_norm(h1, O.bf16_to_f32(bits(L.post_norm)), cfg.eps, 0.0)
-    q2o, s2o = O.quant_act(O.bf16_to_f32(y2))
     q2, s2 = sel(t["q2"]).cpu().numpy(), sel(t["s2"]).cpu().numpy()
-    same2 = np.all(q2 == q2o, axis=1) & (s2 == s2o)
-    print(f"[case] config 4 post norm+quant rows matching the oracle: {same2.mean():.4f}", file=sys.stderr)
-    assert same2.mean() >= 0.95
+    _check_norm_quant(h1, L.post_norm, cfg, bits(sel(t["y2"])), q2, s2, "post-attention")
     qp, sp = L.gate_up.qweight.cpu().numpy(), L.gate_up.wscale.cpu().numpy()
     n = qp.shape[0] // 2
     grp, sgr = qp.reshape(n // 64, 2, 64, -1), sp.reshape(n // 64, 2, 64)
@@ -242,3 +248,122 @@ def test_config4_full_stack_8x2048(gpu):
     for b in range(B):
         np.testing.assert_allclose(p[b], O.option_probs(zo[b], "choice", cfg.n_options), atol=1e-3)
     assert not int8_kernels.STATS["fallback"]
+
+
+def _padded_batch(cfg, gpu, lengths, width, seed):
+    """Requests of these lengths padded at the end to a common width, as the engine packs them, and the
+    rows of their last real positions."""
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.zeros(len(lengths) * width, dtype=torch.long)
+    for b, n in enumerate(lengths):
+        ids[b * width:b * width + n] = torch.randint(0, cfg.vocab, (n,), generator=gen)
+    rows = torch.tensor([b * width + n - 1 for b, n in enumerate(lengths)], dtype=torch.int32)
+    return ids.to(gpu), rows.to(gpu)
+
+
+@pytest.mark.parametrize("interval", [0, 3])
+def test_last_only_equals_full_last_layer(gpu, interval):
+    """The last-only last layer (prefill_engine.py:283-339: K / V and the keys' RoPE over every row,
+    the query projection, attention, O projection and MLP at the picked rows) against the same stack
+    running the whole last layer: logits and probabilities bit-identical, for requests padded to a common
+    width (picked rows inside the batch, so each query sees only its own request's first keys), with and
+    without a prefix state.  interval 3 makes the last layer a gated-delta-net layer (mixer over every
+    row, MLP at the picked rows)."""
+    print(f"[case] last-only vs full last layer, interval {interval}", file=sys.stderr, flush=True)
+    cfg = StackConfig(layers=2, hidden=512, intermediate=1024, heads=4, kv_heads=1, head_dim=256, vocab=4096,
+                      n_options=31, full_attention_interval=interval, linear_k_heads=2, linear_v_heads=4)
+    last = W8A8Stack(cfg, device=gpu, seed=11)
+    full = W8A8Stack(cfg, device=gpu, seed=11, last_only=False)
+    assert type(last.layers[-1]).__name__ == ("GDNBlock" if interval == 3 else "Layer")
+    lengths, width = [128, 77, 100, 1], 128
+    ids, rows = _padded_batch(cfg, gpu, lengths, width, seed=12)
+    lo, cnt = last.slices(["choice", "noul", "choice", "choice"], [31, 2, 5, 31], len(lengths), gpu)
+    B = len(lengths)
+    a = last.forward_last(ids, B, rows, lo, cnt)
+    b = full.forward_last(ids, B, rows, lo, cnt)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), "last-only readout differs from the full layer's"
+    # continuations of a 64-token prefix
+    pre = torch.randint(0, cfg.vocab, (64,), generator=torch.Generator().manual_seed(13)).to(gpu)
+    pa, pb = last.prefix_state(pre), full.prefix_state(pre)
+    a = last.forward_last(ids, B, rows, lo, cnt, prefix=pa)
+    b = full.forward_last(ids, B, rows, lo, cnt, prefix=pb)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), "last-only continuation differs"
+    assert not int8_kernels.STATS["fallback"]
+
+
+def test_last_only_layer_stage_by_stage(gpu):
+    """The last-only layer's stages against the oracle from the kernels' own inputs: norm + quant of every
+    row, the K / V GEMM over every row and the query GEMM at the picked rows (bit-exact), RoPE of the keys
+    and of each query at its own position (bit-exact), then O + residual and the MLP at the picked rows."""
+    print("[case] last-only layer stage by stage", file=sys.stderr, flush=True)
+    cfg = StackConfig(layers=1, hidden=512, intermediate=1024, heads=4, kv_heads=1, head_dim=256, vocab=4096,
+                      n_options=31)
+    st = W8A8Stack(cfg, device=gpu, seed=21)
+    lengths, width = [96, 33, 64], 96
+    ids, rows = _padded_batch(cfg, gpu, lengths, width, seed=22)
+    B = len(lengths)
+    lo, cnt = st.slices(None, None, B, gpu)
+    trace = []
+    logits, probs = st.forward_last(ids, B, rows, lo, cnt, trace=trace)
+    torch.cuda.synchronize()
+    L, t = st.layers[0], trace[0]
+    assert t["kind"] == "attention_last"
+    hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+    hb = bits(t["h"])
+    q, s = t["q"].cpu().numpy(), t["s"].cpu().numpy()
+    _check_norm_quant(hb, L.input_norm, cfg, bits(t["y"]), q, s, "input")
+    W, sw = L.qkv.qweight.cpu().numpy(), L.qkv.wscale.cpu().numpy()
+    nq = hq * d
+    kv = O.epilogue(O.int_gemm(q, W[nq:]), s, sw[nq:])
+    assert np.array_equal(bits(t["kv"]), kv), "K / V GEMM over every row"
+    r = rows.cpu().numpy()
+    qr = O.epilogue(O.int_gemm(q[r], W[:nq]), s[r], sw[:nq])
+    assert np.array_equal(bits(t["qr"]), qr), "query GEMM at the picked rows"
+    cos, sin = (bits(x) for x in st._tables(width, gpu))
+    kpos = np.arange(B * width) % width
+    krot = kv.reshape(B * width, 2 * hk, d).copy()
+    krot[:, :hk] = O.rope(krot[:, :hk], cos[kpos][:, None, :], sin[kpos][:, None, :])
+    assert np.array_equal(bits(t["kv_rope"]), krot.reshape(B * width, -1)), "RoPE of the keys"
+    qpos = r - np.arange(B) * width
+    qrot = O.rope(qr.reshape(B, hq, d), cos[qpos][:, None, :], sin[qpos][:, None, :])
+    assert np.array_equal(bits(t["qr_rope"]), qrot.reshape(B, -1)), "RoPE of the queries at their positions"
+    # attention of each picked query over its own request's first keys (oracle, float64), then O + residual
+    kr = O.bf16_to_f32(krot.reshape(B, width, 2 * hk, d)[:, :, :hk])
+    vr = O.bf16_to_f32(kv.reshape(B, width, 2 * hk, d)[:, :, hk:])
+    a = O.bf16_to_f32(bits(t["a"])).reshape(B, hq, d)
+    for b in range(B):
+        n = qpos[b] + 1
+        want = O.causal_gqa_attention(O.bf16_to_f32(qrot[b])[None, None], kr[b:b + 1, :n], vr[b:b + 1, :n],
+                                      1.0 / 16)[0, 0]
+        np.testing.assert_allclose(a[b], want, rtol=2e-2, atol=2e-2)
+    qa, sa = O.quant_act(O.bf16_to_f32(bits(t["a"])))
+    assert np.array_equal(t["qa"].cpu().numpy(), qa) and np.array_equal(t["sa"].cpu().numpy(), sa)
+    h1 = O.epilogue(O.int_gemm(qa, L.o.qweight.cpu().numpy()), sa, L.o.wscale.cpu().numpy())
+    h1 = O.f32_to_bf16(O.bf16_to_f32(h1) + O.bf16_to_f32(hb[r]))
+    assert np.array_equal(bits(t["h1"]), h1), "O + residual at the picked rows"
+    q2, s2 = t["q2"].cpu().numpy(), t["s2"].cpu().numpy()
+    _check_norm_quant(h1, L.post_norm, cfg, bits(t["y2"]), q2, s2, "post-attention")
+    _check_mlp(L, t, cfg, 0)
+    fin = trace[-1]
+    zo = O.readout(bits(fin["h_final"]), fin["rows"].cpu().numpy(), O.bf16_to_f32(bits(st.final_norm)), cfg.eps,
+                   st.readout.weight.cpu().numpy(), offset=0.0)
+    np.testing.assert_allclose(logits.cpu().numpy(), zo, rtol=1e-4, atol=1e-4)
+    assert not int8_kernels.STATS["fallback"]
+
+
+def test_last_only_sdpa_path(gpu):
+    """Head shapes the flash kernel does not serve take torch SDPA with a per-request key mask at the
+    picked rows; it agrees with the full last layer's is_causal SDPA within bf16 rounding."""
+    print("[case] last-only SDPA path", file=sys.stderr, flush=True)
+    cfg = StackConfig(layers=2, hidden=512, intermediate=1024, heads=8, kv_heads=2, head_dim=64, vocab=4096,
+                      n_options=31)
+    last = W8A8Stack(cfg, device=gpu, seed=31)
+    full = W8A8Stack(cfg, device=gpu, seed=31, last_only=False)
+    ids, rows = _padded_batch(cfg, gpu, [64, 40], 64, seed=32)
+    lo, cnt = last.slices(None, None, 2, gpu)
+    a = last.forward_last(ids, 2, rows, lo, cnt)
+    b = full.forward_last(ids, 2, rows, lo, cnt)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(a[1].cpu().numpy(), b[1].cpu().numpy(), atol=2e-2)
