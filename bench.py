@@ -667,8 +667,9 @@ def serving_latency(torch, dev, st, reps=3):
 # the runs of >= 20 dispatches of one kernel with these names, in this order)
 PMC_WORKLOADS = (
     "gemm_headline_4096x9728x2560", "gemm_qkv_4096x6144x2560", "gemm_o_residual_4096x2560x4096",
-    "gemm_gate_up_silu_4096x19456x2560", "gemm_down_residual_4096x2560x9728", "rmsnorm_quant_T4096",
-    "rmsnorm_quant_T32768", "act_quant_h_4096x9728", "copy_256MiB",
+    "gemm_gate_up_silu_4096x19456x2560", "gemm_down_residual_4096x2560x9728", "gemm_c0_512x9728x2560",
+    "gemm_c3_qkv_32768x6144x2560", "gemm_c3_o_32768x2560x4096", "rmsnorm_quant_T4096", "rmsnorm_quant_T32768",
+    "rmsnorm_quant_3consumers_smoothed_T4096", "act_quant_h_4096x9728", "copy_256MiB",
 )
 
 
@@ -694,8 +695,32 @@ def pmc_workload():
         g = torch.Generator(device="cpu").manual_seed(n + k)
         qw = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
         sw = torch.empty(n).uniform_(1e-3, 1e-2, generator=g).to(dev)
-        out = torch.empty(T, n // 2 if epilogue else n, dtype=torch.bfloat16, device=dev)
+        out = torch.empty(qa_.shape[0], n // 2 if epilogue else n, dtype=torch.bfloat16, device=dev)
         return gemm_launcher(torch, lib, qa_, sa_, qw, sw, out, residual=residual, epilogue=epilogue)
+
+    def activations(m, k, seed):
+        xx, _, _ = synthetic(torch, dev, m, k, 16, seed=seed)
+        return int8_kernels.act_quant(xx)
+
+    def norm3_smoothed(rows):
+        import ctypes
+        P = ctypes.c_void_p
+        g = torch.Generator().manual_seed(rows)
+        hx = torch.randn(rows, HIDDEN, device=dev).to(torch.bfloat16)
+        w = torch.ones(HIDDEN, device=dev).to(torch.bfloat16)
+        invs = [(torch.rand(HIDDEN, generator=g) + 0.5).to(dev) for _ in range(3)]
+        q3 = [torch.empty(rows, HIDDEN, dtype=torch.int8, device=dev) for _ in range(3)]
+        s3 = [torch.empty(rows, dtype=torch.float32, device=dev) for _ in range(3)]
+        keep = (hx, w, invs, q3, s3)
+        ivp, qp = (P * 3)(*[t.data_ptr() for t in invs]), (P * 3)(*[t.data_ptr() for t in q3])
+        sp, ld3 = (P * 3)(*[t.data_ptr() for t in s3]), (ctypes.c_int * 3)(HIDDEN, HIDDEN, HIDDEN)
+        args = (hx.data_ptr(), _lib.BF16, HIDDEN, None, HIDDEN, w.data_ptr(), _lib.BF16, 0.0, 1e-6, 3, ivp, qp, ld3,
+                sp, None, HIDDEN, None, HIDDEN, rows, HIDDEN, 0, st)
+
+        def run(keep=keep):
+            if lib.mica_rmsnorm_quant_multi(*args) != 0:
+                raise RuntimeError("mica_rmsnorm_quant_multi failed")
+        return run
 
     def norm(rows):
         hx = torch.randn(rows, HIDDEN, device=dev).to(torch.bfloat16)
@@ -726,6 +751,10 @@ def pmc_workload():
         "gemm_o_residual_4096x2560x4096": gemm(HIDDEN, O_K, qa, sa, residual=res),
         "gemm_gate_up_silu_4096x19456x2560": gemm(2 * INTER, HIDDEN, qx, sx, epilogue=1),
         "gemm_down_residual_4096x2560x9728": gemm(HIDDEN, INTER, qh, sh, residual=res),
+        "gemm_c0_512x9728x2560": gemm(INTER, HIDDEN, *activations(512, HIDDEN, 1)),
+        "gemm_c3_qkv_32768x6144x2560": gemm(QKV_N, HIDDEN, *activations(32768, HIDDEN, 2)),
+        "gemm_c3_o_32768x2560x4096": gemm(HIDDEN, O_K, *activations(32768, O_K, 3)),
+        "rmsnorm_quant_3consumers_smoothed_T4096": norm3_smoothed(4096),
         "rmsnorm_quant_T4096": norm(4096),
         "rmsnorm_quant_T32768": norm(32768),
         "act_quant_h_4096x9728": requant,

@@ -758,6 +758,10 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
 #define MICA_GEMM_AGPR 1
 #endif
     constexpr bool kAgpr = MICA_GEMM_AGPR != 0;
+#ifndef MICA_GEMM_SMALL
+#define MICA_GEMM_SMALL 1
+#endif
+    constexpr bool kSmall = MICA_GEMM_SMALL != 0;
     constexpr long long kSplit = 4;
     constexpr long long kMinSplitSlabs = 32;
     p.dp_tiles = (int)tiles;
@@ -814,6 +818,21 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
                          (!residual || (long long)kTile * ldr * 4 < (1ll << 31));
     if (wide_ok) {
         if (rem == 0 && cus > 0 && tiles > cus) grid = cus;
+        // Fewer whole tiles than CUs, too many for four quarters each to fit one round (the halves
+        // schedule above): one round of 128 x 160 tiles when they fit it (the AGPR kernel's small tiles,
+        // same bits).  Each CU then streams (128 + 160) rows of operands instead of a half tile's 384.
+        const long long tiles_small = (long long)((M + 127) / 128) * ((N + 159) / 160);
+        const bool small = kAgpr && kSmall && epilogue == MICA_EPI_SCALE && p.half_tiles == tiles && cus > 0 &&
+                           4 * tiles > cus && tiles_small <= cus && K >= 512 &&
+                           (out_dtype == MICA_BF16 || out_dtype == MICA_FP16) && ldc % 8 == 0 && Nout % 8 == 0 &&
+                           (!residual || ldr % 8 == 0);
+        if (small) {
+            p.tiles_m = (M + 127) / 128;
+            p.tiles_n = (N + 159) / 160;
+            p.dp_tiles = (int)tiles_small;
+            p.half_tiles = 0;
+            return agpr_small_launch(p, out_dtype, (int)tiles_small, hb, hr, st);
+        }
         // One partial round of whole tiles with no tail pieces (more than half the CUs busy, e.g.
         // 4096 x 2560: 160 tiles on 256 CUs) runs as 256 x 160 tiles instead when those still fit one
         // round (256 of them there): each costs about 0.65 of a whole tile and more CUs work.

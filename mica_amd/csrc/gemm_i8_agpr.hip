@@ -69,6 +69,13 @@ using QQuart = QCfg<128, 128, 3>;  // waves of 64 x 64 (SCALE tail at most a qua
 // One partial round of 256 x 256 tiles run as 256 x 160 tiles (e.g. N = 2560 at M = 4096: 160 tiles
 // become 256): waves of 64 x 160 stacked along M, 10 x 4 MFMA tiles = 160 accumulators per lane.
 using QNarrow = QCfg<256, 160, 2, 4, 1>;
+// One round of 128 x 160 tiles for launches whose 256 x 256 tiles fill less than a round and are too
+// many for 128 x 128 quarters to fit one (e.g. 512 x 2560 x 9728: 76 tiles, 244 of these): waves of
+// 32 x 160 stacked along M, 2 x 10 MFMA tiles = 80 accumulators per lane, four LDS stages (one tile
+// per workgroup, nothing to prefetch for a successor: three slabs stay in flight, against two with three
+// stages, whose DMA waited on memory latency).  Such a tile is bound by its DMA feed, (128 + 160) rows x
+// K against 384 rows for the 256 x 128 half tile it replaces.
+using QSmall = QCfg<128, 160, 4, 4, 1>;
 
 // LDS: the A stages, the B stages, then (at a fixed place past the largest stage set) two buffers of
 // tile scales (sa, sb, bias: 3 x 256 fp32), for this tile and the next.
@@ -79,7 +86,7 @@ static_assert(kQSmem <= 160 * 1024, "LDS");
 template <class C>
 constexpr bool stages_fit = C::NS * (C::kAHalf + C::kBHalf) <= kQScale;
 static_assert(stages_fit<QFull> && stages_fit<QHalfN> && stages_fit<QHalfM> && stages_fit<QQuart> &&
-                  stages_fit<QNarrow>, "stages");
+                  stages_fit<QNarrow> && stages_fit<QSmall>, "stages");
 
 // This lane's index, computed afresh where it is used (a few VALU operations per tile instead of a
 // register held across the persistent loop).  The wave index lives in an SGPR.
@@ -334,13 +341,15 @@ struct QTile {
         kstep<false, 0, false, -1>(R0, R1, wa[0], xa[0], own);
     }
 
-    // ---- the slabs of a tail piece (C::NS == 3, no next piece to prefetch for): on entry slab 0 is
-    // visible in stage 0 and slabs 1 and 2 are in flight into stages 1 and 2.  Slab s lives in stage
-    // s % 3; after the barrier of B(k) (slab k + 1 landed, slab k read by every wave) slab k + 3 goes
-    // into slab k's stage, so two slabs are in flight while one is read.  Stage offsets beyond the
-    // 16-bit offset of ds_read_b128 ride on the base registers.
-    MICA_DEVICE void run3(const GemmParams &p, int8_t *smem, int wave, int m0, int n0) {
-        static_assert(C::NS == 3, "three stages");
+    // ---- the slabs of a piece with no successor to prefetch for (C::NS >= 3 stages): on entry slab 0 is
+    // visible in stage 0 and slabs 1 .. NS - 1 are in flight into stages 1 .. NS - 1.  Slab s lives in
+    // stage s % NS; after the barrier of B(k) (slab k + 1 landed, slab k read by every wave) slab k + NS
+    // goes into slab k's stage, so NS - 1 slabs are in flight while one is read.  Stage offsets beyond
+    // the 16-bit offset of ds_read_b128 ride on the base registers.
+    MICA_DEVICE void run_deep(const GemmParams &p, int8_t *smem, int wave, int m0, int n0) {
+        constexpr int NS = C::NS;
+        static_assert(NS == 3 || NS == 4, "stages");
+        static_assert((NS - 2) * C::kDma < 64, "vmcnt");
         const int lane = lane_id();
         const int wm = wave / C::WGN, wn = wave % C::WGN;
         const int r16 = lane & 15, kq = lane >> 4;
@@ -356,7 +365,7 @@ struct QTile {
         constexpr int kDMore = C::kDma > kDFirst ? kDFirst : -1;
         Ops R0, R1;
         DmaPlan cont = tile_plan(p, smem, wave, lane, m0, n0, 0, 0, false);
-        // the plan for slab `slab` (stage ST = slab % 3): zero-sized past the last slab, so every wave
+        // the plan for slab `slab` (stage ST = slab % NS): zero-sized past the last slab, so every wave
         // issues the same instructions and the waits below count them
         auto plan = [&](int slab, auto st_c) {
             return tile_plan(p, smem, wave, lane, m0, n0, slab, decltype(st_c)::value, slab < nk);
@@ -371,11 +380,11 @@ struct QTile {
             else
                 kstep<true, 0, false, kDMore>(R1, R0, wa[1] + ST * C::kBHalf, xa[1] + ST * C::kAHalf, cont);
         };
-        // B: slab k + 1 (stage ST + 1) landed, only slab k + 2's instructions may be in flight
+        // B: slab k + 1 (stage ST + 1) landed -- only the NS - 2 slabs after it may be in flight
         auto half_b = [&](auto st_c, const DmaPlan &dp) {
             constexpr int ST = decltype(st_c)::value;
-            constexpr int SN = (ST + 1) % 3;
-            wait_vmcnt<C::kDma>();
+            constexpr int SN = (ST + 1) % NS;
+            wait_vmcnt<(NS - 2) * C::kDma>();
             wait_lgkmcnt0();
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
@@ -387,26 +396,40 @@ struct QTile {
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
         using S2 = std::integral_constant<int, 2>;
+        using S3 = std::integral_constant<int, NS - 1>;   // stage 3 (NS == 4)
         frag_reads<0, NB>(R0.w, wa[0]);
         frag_reads<0, MB>(R0.x, xa[0]);
         half_a(S0{}, T{});
         int k = 0;
-        for (; k + 3 <= nk - 1; k += 3) {
-            half_b(S0{}, plan(k + 3, S0{}));
+        for (; k + NS <= nk - 1; k += NS) {
+            half_b(S0{}, plan(k + NS, S0{}));
             half_a(S1{}, F{});
-            half_b(S1{}, plan(k + 4, S1{}));
+            half_b(S1{}, plan(k + NS + 1, S1{}));
             half_a(S2{}, F{});
-            half_b(S2{}, plan(k + 5, S2{}));
-            half_a(S0{}, F{});
+            if constexpr (NS == 3) {
+                half_b(S2{}, plan(k + 5, S2{}));
+                half_a(S0{}, F{});
+            } else {
+                half_b(S2{}, plan(k + 6, S2{}));
+                half_a(S3{}, F{});
+                half_b(S3{}, plan(k + 7, S3{}));
+                half_a(S0{}, F{});
+            }
         }
-        // the last nk - 1 - k (0 to 2) pairs, from stage 0
+        // the last nk - 1 - k (0 to NS - 1) pairs, from stage 0
         if (k + 1 <= nk - 1) {
-            half_b(S0{}, plan(k + 3, S0{}));
+            half_b(S0{}, plan(k + NS, S0{}));
             half_a(S1{}, F{});
         }
         if (k + 2 <= nk - 1) {
-            half_b(S1{}, plan(k + 4, S1{}));
+            half_b(S1{}, plan(k + NS + 1, S1{}));
             half_a(S2{}, F{});
+        }
+        if constexpr (NS == 4) {
+            if (k + 3 <= nk - 1) {
+                half_b(S2{}, plan(k + 6, S2{}));
+                half_a(S3{}, F{});
+            }
         }
         wait_lgkmcnt0();
         __builtin_amdgcn_sched_barrier(0);
@@ -570,8 +593,9 @@ MICA_DEVICE void run_qphase(const GemmParams &p, int8_t *smem, __amdgpu_buffer_r
     while (h < hend && !piece(h, m0, n0)) h += G;
     if (h >= hend) return;
     Tile t;
-    if constexpr (C::NS == 3) {
-        // tail pieces, each on its own: slabs 0 - 2 out, slab 0 and the scales waited for
+    if constexpr (C::NS >= 3) {
+        // pieces with no successor, each on its own: slabs 0 .. NS - 1 out, slab 0 and the scales
+        // waited for
         for (; h < hend; h += G) {
             if (!piece(h, m0, n0)) continue;
             wait_vmcnt<0>();
@@ -581,9 +605,10 @@ MICA_DEVICE void run_qphase(const GemmParams &p, int8_t *smem, __amdgpu_buffer_r
             Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 0, 0);
             Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 1, 1);
             Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 2, 2);
-            wait_vmcnt<2 * C::kDma>();  // scales and slab 0 landed (slabs 1 and 2 may be in flight)
+            if constexpr (C::NS > 3) Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 3, 3);
+            wait_vmcnt<(C::NS - 1) * C::kDma>();  // scales and slab 0 landed (slabs 1 .. NS - 1 may be in flight)
             __builtin_amdgcn_s_barrier();
-            t.run3(p, smem, wave, m0, n0);
+            t.run_deep(p, smem, wave, m0, n0);
             t.epilogue(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 0, false, 0, 0);
         }
         return;
@@ -690,6 +715,39 @@ __global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_narrow_kernel(GemmP
     wait_vmcnt<0>();
 }
 
+// One round of 128 x 160 tiles (dp_tiles of them over tiles_m x tiles_n, one per workgroup), SCALE
+// epilogue.
+template <int OUT, bool HAS_BIAS, bool HAS_RES>
+__global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_small_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kQSmem];
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, p.M * p.lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, p.N * p.ldb, kBufferFlags);
+    const int tm_n = p.tiles_m, tn_n = p.tiles_n;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    run_qphase<QSmall, MICA_EPI_SCALE, OUT, HAS_BIAS, HAS_RES>(p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, p.dp_tiles,
+                                                              gridDim.x, [&](int h, int &m0, int &n0) {
+                                                                  int tm, tn;
+                                                                  tile_of(h, tm_n, tn_n, tm, tn);
+                                                                  m0 = tm * QSmall::BM;
+                                                                  n0 = tn * QSmall::BN;
+                                                                  return true;
+                                                              });
+    // every store of this workgroup has left before the waves end
+    wait_vmcnt<0>();
+}
+
+template <int OUT>
+int agpr_small_out(const GemmParams &p, int grid, bool has_bias, bool has_res, hipStream_t st) {
+    dim3 g(grid), b(kQThreads);
+#define MICA_QS(B_, R_) hipLaunchKernelGGL((gemm_i8_agpr_small_kernel<OUT, B_, R_>), g, b, 0, st, p)
+    if (has_bias && has_res) MICA_QS(true, true);
+    else if (has_bias) MICA_QS(true, false);
+    else if (has_res) MICA_QS(false, true);
+    else MICA_QS(false, false);
+#undef MICA_QS
+    return mica_err(hipGetLastError());
+}
+
 template <int OUT>
 int agpr_narrow_out(const GemmParams &p, int grid, bool has_bias, bool has_res, hipStream_t st) {
     dim3 g(grid), b(kQThreads);
@@ -741,5 +799,14 @@ int mica_gemm::agpr_narrow_launch(const GemmParams &p, int out_dtype, int grid, 
                                   hipStream_t st) {
     if (out_dtype == MICA_BF16) return agpr_narrow_out<MICA_BF16>(p, grid, has_bias, has_res, st);
     if (out_dtype == MICA_FP16) return agpr_narrow_out<MICA_FP16>(p, grid, has_bias, has_res, st);
+    return MICA_MISS_ARG;
+}
+
+// Launch of the 128 x 160 AGPR kernel for one round of tiles (p.tiles_m / p.tiles_n count 128-row /
+// 160-column tiles; SCALE epilogue, 16-bit outputs; the same conditions as agpr_launch).
+int mica_gemm::agpr_small_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res,
+                                 hipStream_t st) {
+    if (out_dtype == MICA_BF16) return agpr_small_out<MICA_BF16>(p, grid, has_bias, has_res, st);
+    if (out_dtype == MICA_FP16) return agpr_small_out<MICA_FP16>(p, grid, has_bias, has_res, st);
     return MICA_MISS_ARG;
 }

@@ -142,6 +142,7 @@ int wide_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool
 int agpr_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool has_bias, bool has_res,
                 hipStream_t st);
 int agpr_narrow_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res, hipStream_t st);
+int agpr_small_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res, hipStream_t st);
 
 }  // namespace mica_gemm
 

@@ -412,6 +412,37 @@ def test_gemm_narrow_tiles_bit_exact(gpu, m, n, k, epi):
         assert_equal_diag(y.cpu().numpy(), O.epilogue(acc, sa, sb, None, "fp16"), "fp16")
 
 
+@pytest.mark.parametrize("m,n,k,epi", [
+    (512, 9728, 2560, "none"),       # config 0: 76 whole tiles -> one round of 244 tiles of 128 x 160
+    (500, 9696, 2560, "residual"),   # both edges ragged: the last row tile 116 rows, the last column tile 96 wide
+    (768, 6144, 1024, "bias"),       # 72 tiles -> 234 tiles of 128 x 160
+    (640, 6400, 512, "fp16"),        # the shortest K of the AGPR kernels, fp16 output
+])
+def test_gemm_small_tiles_bit_exact(gpu, m, n, k, epi):
+    """Fewer whole 256 x 256 tiles than CUs, too many for four quarters each to fit one round: one round
+    of 128 x 160 tiles.  Bit-exact with the oracle on every output."""
+    note(f"gemm small tiles m={m} n={n} k={k} epi={epi}")
+    rng = np.random.default_rng(m * 3 + n + k)
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    tA, tB, tsa, tsb = (torch.from_numpy(v).cuda() for v in (A, B, sa, sb))
+    acc = O.int_gemm(A, B)
+    if epi == "residual":
+        res = act_bits(rng, (m, n), outliers=0)
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, residual=to_gpu_bf16(res))
+        ref = O.f32_to_bf16(O.bf16_to_f32(O.epilogue(acc, sa, sb)) + O.bf16_to_f32(res))
+        assert_equal_diag(bits_of(y), ref, "bf16 + residual")
+    elif epi == "bias":
+        bias = rng.uniform(-1, 1, n).astype(np.float32)
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, torch.from_numpy(bias).cuda())
+        assert_equal_diag(bits_of(y), O.epilogue(acc, sa, sb, bias), "bf16 + bias")
+    elif epi == "fp16":
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, out_dtype=torch.float16)
+        assert_equal_diag(y.cpu().numpy(), O.epilogue(acc, sa, sb, None, "fp16"), "fp16")
+    else:
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb)
+        assert_equal_diag(bits_of(y), O.epilogue(acc, sa, sb), "bf16")
+
+
 def test_gemm_headline_full_size(gpu):
     """The benchmarked GEMM itself, M=4096 K=2560 N=9728 (every tile, including the partial last round
     of tiles), bit-exact: int32 accumulators and the bf16 output.  Then a size-independent property
