@@ -552,13 +552,15 @@ def stack_prefill(torch, dev, reps=3):
 
 
 def hybrid_prefill(torch, dev, reps=3):
-    """The reference model's hybrid layout at the same shape: 32 layers, every fourth full attention
-    (16 / 4 heads of 256) and the other 24 gated-delta-net layers (16 key / 32 value heads of 128:
-    W8A8 input projections 8192 + 4096 + 32 + 32, conv, chunked scan, gated norm + quant, W8A8
-    out_proj), each followed by the same W8A8 MLP; 8 requests x 2048 tokens, last-position readout."""
+    """The reference model's hybrid layout and attention at the same shape (StackConfig.reference_model):
+    32 layers, every fourth full attention (16 / 4 heads of 256 with the q_proj output gate, per-head
+    q / k RMSNorm and RoPE on 64 dims: QKV N = 10240) and the other 24 gated-delta-net layers (16 key /
+    32 value heads of 128: W8A8 input projections 8192 + 4096 + 32 + 32, conv, chunked scan, gated norm
+    + quant, W8A8 out_proj), each followed by the same W8A8 MLP; 8 requests x 2048 tokens, last-position
+    readout (last layer last-only)."""
     from mica_amd.model import StackConfig, W8A8Stack
 
-    st = W8A8Stack(StackConfig(layers=32, full_attention_interval=4), device=dev, seed=0)
+    st = W8A8Stack(StackConfig.reference_model(), device=dev, seed=0)
     B, S = 8, 2048
     ids = torch.randint(0, st.cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(0)).to(dev)
     st.prefill(ids, B)  # warm-up
@@ -588,8 +590,9 @@ def hybrid_prefill(torch, dev, reps=3):
         single[f"B1_S{S1}"] = {"ms": round(ms1, 2), "tokens_per_s": round(S1 / (ms1 * 1e-3), 1)}
     del st
     torch.cuda.empty_cache()
-    return {"workload": "32 layers (24 gated-delta-net + 8 full attention), hidden 2560, inter 9728; "
-                        "8 requests x 2048 tokens packed; last-position readout over 255 option ids + softmax",
+    return {"workload": "32 layers (24 gated-delta-net + 8 full attention with output gate, q / k head norm and "
+                        "RoPE on 64 dims), hidden 2560, inter 9728; 8 requests x 2048 tokens packed; "
+                        "last-position readout over 255 option ids + softmax",
             "ms_per_prefill": round(ms, 2), "tokens_per_s": round(B * S / (ms * 1e-3), 1),
             "w8a8_linear_TOP": round(ops / 1e12, 2), "probs_valid": ok, "reps": reps, "single_request": single}
 

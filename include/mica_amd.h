@@ -195,6 +195,39 @@ int mica_rope_inplace(void *x, long long ldx, int n_heads, int head_dim, const v
                       int n_pos, const int *pos, int period, int T, mica_stream_t stream);
 
 /*
+ * The q / k head norm and partial rotary embedding of the full-attention layers, in place on the rows
+ * of a fused QKV projection output (replaces the torch ops q_norm / k_norm and rope_one of the
+ * reference's attention, fast_runtime.py:229-236, prefill_engine.py:83-89, 123-130).  Segment q holds
+ * n_q heads at column q_off of each row, segment k n_k heads at k_off; head_dim is a power of two, 16 to
+ * 512.  Each head is first normed when its segment's weight is given (bf16 [head_dim]; NULL: no norm):
+ *   y = bf16((x * (1 / sqrt(sum(x^2) / head_dim + eps))) * (offset + w))
+ * (the reference model's zero-centred RMSNorm: offset 1), then its first rot_dim dims (a power of two,
+ * 16 .. head_dim; 0: none) are rotated as mica_rope_inplace rotates a head of rot_dim dims, the others
+ * passed through: for i < h = rot_dim / 2,
+ *   y[i] = bf16(bf16(y[i] cos[p][i]) + bf16(y[i + h] (-sin[p][i]))),
+ *   y[i + h] = bf16(bf16(y[i + h] cos[p][i]) + bf16(y[i] sin[p][i])),
+ * with cos_tab / sin_tab bf16 [n_pos][rot_dim / 2] and position p of row t = pos[t] (int32, device) or
+ * t % period when pos is NULL (rows whose position is outside the tables: normed, not rotated).
+ */
+int mica_head_norm_rope(void *x, long long ldx, int T, int q_off, int n_q, int k_off, int n_k, int head_dim,
+                        const void *q_norm_w, const void *k_norm_w, float offset, float eps, int rot_dim,
+                        const void *cos_tab, const void *sin_tab, int n_pos, const int *pos, int period,
+                        mica_stream_t stream);
+
+/*
+ * The attention output gate of the full-attention layers fused with o_proj's activation quantizer:
+ *   y = bf16(a * bf16(sigmoid(g)))   (fast_runtime.py:240: o * torch.sigmoid(gate), bf16 ops; the sigmoid
+ *                                     as torch's fp32 1 / (1 + exp(-g)) rounded to bf16)
+ *   s[m] = max(max_k |y[m, k]|, 1e-8) / 127,  q[m, k] = round_half_even(y[m, k] / s[m])
+ *                                    (int8_quant.quant_act, int8_quant.py:64-73)
+ * a, g: bf16 [M, K] with row strides lda / ldg (elements); q int8 [M, K] (ldq), s fp32 [M]; y (optional,
+ * bf16, ldy): the gated rows.  K a multiple of 512, 512 .. 8192; rounding must be MICA_ROUND_EVEN.
+ * No counterpart in the reference's launchers (its gate and act_quant are two torch / Triton steps).
+ */
+int mica_gate_quant(const void *a, long long lda, const void *gate, long long ldg, int8_t *q, long long ldq,
+                    float *s, void *y, long long ldy, int M, int K, int rounding, mica_stream_t stream);
+
+/*
  * Causal grouped-query attention forward, head dim 256, HQ = 4 HK (query head h reads key/value head
  * h / 4), Sq queries over Sk >= Sq keys (the queries are the last Sq positions).  Replaces the
  * reference's attn_fwd (int8_kernels.py:409-481, Triton kernel kernel_src/kernels.py:71-124) and the

@@ -44,6 +44,8 @@ SIGNATURES = {
     "mica_gather_logits": (_I, [_P, _I, _I, _P, _I, _P, _I, _F, _F, _P, _I, _I, _I, _P, _I, _I, _P, _P, _P, _P, _I,
                                 _P]),
     "mica_rope_inplace": (_I, [_P, _LL, _I, _I, _P, _P, _I, _P, _I, _I, _P]),
+    "mica_head_norm_rope": (_I, [_P, _LL, _I, _I, _I, _I, _I, _I, _P, _P, _F, _F, _I, _P, _P, _I, _P, _I, _P]),
+    "mica_gate_quant": (_I, [_P, _LL, _P, _LL, _P, _LL, _P, _P, _LL, _I, _I, _I, _P]),
     "mica_attention_fwd": (_I, [_P, _LL, _LL, _LL, _P, _LL, _LL, _LL, _P, _LL, _LL, _LL, _P, _LL, _LL, _LL, _I, _I,
                                 _I, _I, _I, _I, _F, _I, _P, _LL, _P]),
     "mica_attention_workspace_bytes": (_LL, [_I, _I, _I]),

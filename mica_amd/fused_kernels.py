@@ -208,3 +208,77 @@ def rope_inplace(rows, n_heads: int, head_dim: int, cos_tab, sin_tab, period: in
         raise ValueError(f"rope_inplace: unsupported input ({_lib.status_name(rc)})")
     _launched()
     return rows
+
+
+def head_norm_rope(rows, head_dim: int, q_heads, k_heads, q_norm_w=None, k_norm_w=None, eps: float = 1e-6,
+                   offset: float = 1.0, rot_dim: int = 0, cos_tab=None, sin_tab=None, period: int | None = None,
+                   pos=None):
+    """In place on bf16 rows [T, C] (unit feature stride): the q / k head RMSNorm and partial RoPE of the
+    reference model's full-attention layers (fast_runtime.py:229-236; rope_one, prefill_engine.py:83-89).
+    q_heads = (column offset, head count) of the query heads, k_heads likewise; each head of head_dim
+    values is normed when its segment's weight (bf16 [head_dim]) is given,
+    y = bf16((x * rstd) * (offset + w)) (offset 1: the zero-centred Qwen3.5 RMSNorm), then its first
+    rot_dim dims are rotated (cos_tab / sin_tab bf16 [n_pos, rot_dim / 2]; row t at position pos[t] or
+    t % period).  One launch (mica_head_norm_rope)."""
+    if not rows.is_cuda:
+        raise ValueError("mica_amd head norm + RoPE runs on the GPU only (got a CPU tensor)")
+    if rows.dim() != 2 or rows.dtype != torch.bfloat16 or rows.stride(1) != 1:
+        raise ValueError("head_norm_rope expects bf16 [T, C] rows with unit feature stride")
+    for w in (q_norm_w, k_norm_w):
+        if w is not None and (w.dtype != torch.bfloat16 or w.numel() != head_dim or not w.is_contiguous()
+                              or w.device != rows.device):
+            raise ValueError("norm weights must be contiguous bf16 [head_dim] tensors on the rows' device")
+    if rot_dim:
+        if cos_tab is None or sin_tab is None or cos_tab.dtype != torch.bfloat16 or cos_tab.shape != sin_tab.shape \
+                or cos_tab.shape[1] != rot_dim // 2 or not cos_tab.is_contiguous() or not sin_tab.is_contiguous():
+            raise ValueError("cos / sin tables must be contiguous bf16 [n_pos, rot_dim / 2]")
+        if pos is not None and (pos.dtype != torch.int32 or not pos.is_contiguous() or pos.numel() != rows.shape[0]):
+            raise ValueError("pos must be a contiguous int32 [T] tensor")
+        if pos is None and not period:
+            raise ValueError("give pos or period")
+    dev = rows.device
+    if not _gpu_ok(dev):
+        raise RuntimeError(f"mica_amd kernels need a gfx950 GPU (device {dev})")
+    L = _lib.load()
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = _lib.check(_on(dev, lambda: L.mica_head_norm_rope(
+        rows.data_ptr(), rows.stride(0), rows.shape[0], int(q_heads[0]), int(q_heads[1]), int(k_heads[0]),
+        int(k_heads[1]), head_dim, ptr(q_norm_w), ptr(k_norm_w), float(offset), float(eps), int(rot_dim),
+        ptr(cos_tab), ptr(sin_tab), 0 if cos_tab is None else cos_tab.shape[0], ptr(pos), int(period or 0),
+        _stream(dev))), "mica_head_norm_rope")
+    if rc:
+        raise ValueError(f"head_norm_rope: unsupported input ({_lib.status_name(rc)})")
+    _launched()
+    return rows
+
+
+def gate_quant(a, gate, return_gated: bool = False):
+    """o_proj's input from the attention output: y = bf16(a * bf16(sigmoid(gate))) (the output gate of
+    the full-attention layers, fast_runtime.py:240), quantized per token (int8_quant.quant_act, half even)
+    in the same pass.  a, gate: bf16 [M, K] with unit feature stride (gate may be a strided view of the
+    QKV projection output), K a multiple of 512.  Returns (q int8 [M, K], s fp32 [M]) and, with
+    return_gated, the bf16 gated rows y."""
+    for t in (a, gate):
+        if not t.is_cuda:
+            raise ValueError("mica_amd gate + quant runs on the GPU only (got a CPU tensor)")
+        if t.dim() != 2 or t.dtype != torch.bfloat16 or t.stride(1) != 1:
+            raise ValueError("gate_quant expects bf16 [M, K] tensors with unit feature stride")
+    if a.shape != gate.shape or gate.device != a.device:
+        raise ValueError("a and gate must have one shape and device")
+    M, K = a.shape
+    dev = a.device
+    q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, K), dtype=torch.bfloat16, device=dev) if return_gated else None
+    if not _aligned(a, gate, q, s, *(() if y is None else (y,))):
+        raise ValueError("gate_quant requires 16-byte aligned rows")
+    if not _gpu_ok(dev):
+        raise RuntimeError(f"mica_amd kernels need a gfx950 GPU (device {dev})")
+    L = _lib.load()
+    rc = _lib.check(_on(dev, lambda: L.mica_gate_quant(
+        a.data_ptr(), a.stride(0), gate.data_ptr(), gate.stride(0), q.data_ptr(), K, s.data_ptr(),
+        None if y is None else y.data_ptr(), K, M, K, ROUNDING["even"], _stream(dev))), "mica_gate_quant")
+    if rc:
+        raise ValueError(f"gate_quant: unsupported input ({_lib.status_name(rc)})")
+    _launched()
+    return (q, s, y) if return_gated else (q, s)

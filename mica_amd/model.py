@@ -6,11 +6,14 @@ Shape (the benchmark's synthetic 4B configuration): 36 layers, hidden 2560, MLP 
 weights.  With ``full_attention_interval = k > 0`` the stack is the hybrid layout of the reference's
 model instead (Qwen3.5: three gated-delta-net layers, then one full-attention layer, repeated).
 
-The stack is a synthetic workload with the benchmark's shapes, not the reference model's computation:
-its full-attention layers have no q_proj output gate (o * sigmoid(gate)) and no per-head q / k
-RMSNorm, both of which the reference model's attention layers apply (fast_runtime.py:229-241), and all
-weights are random.  Per full-attention layer (the call pattern of the reference's fork.layer_step,
-v0.5/serving/lib/fork.py:394-422, without those two ops):
+Weights are random.  By default the full-attention layers are the benchmark's plain shape (QKV
+N = 6144, RoPE over the whole head).  StackConfig.reference_model() (or the flags attn_output_gate,
+qk_norm, rotary_dim) gives them the reference model's computation (fast_runtime.py:229-241): q_proj also
+produces an output gate per head (QKV rows [q | gate | k | v], N = 10240), the q and k heads are
+RMSNormed per head (zero-centred weight) and rotated on their first 64 dims (one head_norm_rope launch
+in place of the RoPE), and the attention output is gated, o * sigmoid(gate), in the kernel that quantizes
+it for the O projection (gate_quant, in place of act_quant).  Per full-attention layer (the call pattern
+of the reference's fork.layer_step, v0.5/serving/lib/fork.py:394-422):
   q, s   = rms_norm_quant(h, input_norm)                     1 launch
   qkv    = QKV W8A8 GEMM                                     1 launch
   a      = causal GQA attention per request: RoPE in place on the q / k heads, then the
@@ -43,7 +46,7 @@ import torch.nn.functional as F
 
 from . import int8_kernels as aot
 from .attention import GROUP as _FA_GROUP, HEAD_DIM as _FA_DIM, causal_gqa_attention, key_splits_for
-from .fused_kernels import rms_norm_quant, rope_inplace
+from .fused_kernels import gate_quant, head_norm_rope, rms_norm_quant, rope_inplace
 from .gdn import HEAD_DIM as _GDN_DIM, GDNLayer
 from .int8_runtime import GateUpQLinear, QLinear
 from .readout import LabelReadout
@@ -67,9 +70,29 @@ class StackConfig:
     linear_k_heads: int = 16
     linear_v_heads: int = 32
     conv_width: int = 4
+    # the reference model's full-attention extras (fast_runtime.py:229-241): q_proj's per-head output gate
+    # o * sigmoid(gate), the per-head q / k RMSNorm (zero-centred weights), RoPE on the first rotary_dim
+    # dims of each head (0: all of them)
+    attn_output_gate: bool = False
+    qk_norm: bool = False
+    rotary_dim: int = 0
 
     def is_gdn(self, i: int) -> bool:
         return self.full_attention_interval > 0 and (i + 1) % self.full_attention_interval != 0
+
+    @property
+    def rot_dim(self) -> int:
+        return self.rotary_dim or self.head_dim
+
+    @classmethod
+    def reference_model(cls, **overrides) -> "StackConfig":
+        """The reference model's layer layout and attention (Qwen3.5, as served): 32 layers, every fourth
+        full attention (16 / 4 heads of 256 with the output gate, q / k norm, RoPE on 64 dims, theta 1e7),
+        the others gated-delta-net layers (16 key / 32 value heads of 128), hidden 2560, MLP 9728."""
+        base = dict(layers=32, full_attention_interval=4, attn_output_gate=True, qk_norm=True, rotary_dim=64,
+                    rope_theta=10_000_000.0)
+        base.update(overrides)
+        return cls(**base)
 
 
 _CUS = {}
@@ -101,11 +124,17 @@ class Layer:
         self.cfg = cfg
         self.input_norm = _rand_norm(H, g, device)
         self.post_norm = _rand_norm(H, g, device)
-        self.qkv = _rand_qlinear((cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim, H, g, device)
+        # fused projection rows: [q | gate | k | v] (the gate rows only with attn_output_gate)
+        nq = cfg.heads * cfg.head_dim * (2 if cfg.attn_output_gate else 1)
+        self.qkv = _rand_qlinear(nq + 2 * cfg.kv_heads * cfg.head_dim, H, g, device)
         self.o = _rand_qlinear(H, cfg.heads * cfg.head_dim, g, device)
         _mlp_weights(self, cfg, g, device)
-        # the last-only pass's two projections: views of the fused weight's query rows and K / V rows
-        nq = cfg.heads * cfg.head_dim
+        # the per-head norms' zero-centred weights (the norm multiplies by 1 + w)
+        self.q_norm = self.k_norm = None
+        if cfg.qk_norm:
+            self.q_norm = (torch.randn(cfg.head_dim, generator=g, device=device) * 0.1).to(torch.bfloat16)
+            self.k_norm = (torch.randn(cfg.head_dim, generator=g, device=device) * 0.1).to(torch.bfloat16)
+        # the last-only pass's two projections: views of the fused weight's query (+ gate) rows and K / V rows
         self.q_rows = QLinear.from_quantized(self.qkv.qweight[:nq], self.qkv.wscale[:nq])
         self.kv_rows = QLinear.from_quantized(self.qkv.qweight[nq:], self.qkv.wscale[nq:])
 
@@ -226,11 +255,11 @@ class W8A8Stack:
             size = max(n, 4096 if self._rope is None else 2 * self._rope[0].shape[0])
             if self._rope is not None:
                 self._retired.append(self._rope)
-            self._rope = _rope(size, self.cfg.head_dim, self.cfg.rope_theta, device)
+            self._rope = _rope(size, self.cfg.rot_dim, self.cfg.rope_theta, device)
         cos, sin = self._rope
         return cos[:n], sin[:n]
 
-    def _attention(self, qkv, B, S, past=None, keep=False, pos=None):
+    def _attention(self, qkv, B, S, past=None, keep=False, pos=None, norms=(None, None)):
         """Causal GQA attention per request.  RoPE rotates the q and k heads of the QKV output in place
         (one kernel); the flash-attention kernel (head dim 256, 4 query heads per K/V head) then reads
         [B, S, heads, d] views of it and writes [B, S, heads, d]-contiguous output, i.e. already the O
@@ -240,17 +269,15 @@ class W8A8Stack:
         past: (k, v) of a prefix of P tokens; the S rows are then positions P .. P + S - 1 and attend to
         the prefix's keys too (Sk = P + S keys, the queries being the last S); pos: their int32 RoPE
         positions (PrefixState.positions_for).  keep: also return this call's rotated (k, v),
-        contiguous (batch 1: a prefix being recorded)."""
+        contiguous (batch 1: a prefix being recorded); norms: the layer's (q_norm, k_norm) weights."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        ng = hq if cfg.attn_output_gate else 0          # gate heads between the q and the k heads
         P = 0 if past is None else past[0].shape[1]
-        if P == 0:
-            cos, sin = self._tables(S, qkv.device)
-            rope_inplace(qkv, hq + hk, d, cos, sin, period=S)
-        else:
-            cos, sin = self._tables(P + S, qkv.device)
-            rope_inplace(qkv, hq + hk, d, cos, sin, pos=pos)
-        q, k, v = qkv.view(B, S, hq + 2 * hk, d).split((hq, hk, hk), dim=2)
+        cos, sin = self._tables(P + S, qkv.device)
+        self._rotate(qkv, (0, hq), (ng * d + hq * d, hk), cos, sin, S if P == 0 else None, None if P == 0 else pos,
+                     norms)
+        q, _, k, v = qkv.view(B, S, hq + ng + 2 * hk, d).split((hq, ng, hk, hk), dim=2)
         state = (k.contiguous(), v.contiguous()) if keep else None
         if P:
             k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
@@ -267,7 +294,39 @@ class W8A8Stack:
             a = a.transpose(1, 2).reshape(B * S, hq * d).contiguous()
         return (a, state) if keep else a
 
-    def _attention_rows(self, qr, kv, B, S, rows, past=None, pos=None):
+    def _plain_rope(self) -> bool:
+        """RoPE over whole heads and no head norm: the rope_inplace kernel serves it."""
+        return not self.cfg.qk_norm and self.cfg.rot_dim == self.cfg.head_dim
+
+    def _rotate(self, rows, q_heads, k_heads, cos, sin, period=None, pos=None, norms=(None, None)):
+        """The q / k heads of the projection rows, in place: RoPE (rope_inplace) when the q heads come
+        right before the k heads, the heads are rotated whole and not normed; else the head norm (when
+        configured) and RoPE on the first rot_dim dims in one head_norm_rope launch.  q_heads / k_heads:
+        (column offset, head count); norms: the layer's (q_norm, k_norm) weights or Nones."""
+        cfg = self.cfg
+        d = cfg.head_dim
+        nq, nk = q_heads[1], k_heads[1]
+        if self._plain_rope() and (nq == 0 or nk == 0 or k_heads[0] == q_heads[0] + nq * d):
+            first = q_heads[0] if nq else k_heads[0]
+            view = rows[:, first:] if first else rows
+            rope_inplace(view, nq + nk, d, cos, sin, period=period, pos=pos)
+            return
+        head_norm_rope(rows, d, q_heads, k_heads, norms[0], norms[1], cfg.eps, 1.0, cfg.rot_dim, cos, sin,
+                       period=period, pos=pos)
+
+    def _o_input(self, a, gate, keep_gated=False):
+        """O projection's int8 input (q, s, gated rows or None): the attention output quantized per
+        token, gated first with the output gate when the layers have one (gate_quant; with keep_gated the
+        bf16 gated rows too, for a trace)."""
+        if gate is None:
+            q, s = aot.act_quant(a)
+            return q, s, None
+        if keep_gated:
+            return gate_quant(a, gate, return_gated=True)
+        q, s = gate_quant(a, gate)
+        return q, s, None
+
+    def _attention_rows(self, qr, kv, B, S, rows, past=None, pos=None, norms=(None, None)):
         """Attention of the last-only pass: one query per request, the picked row rows[b] (int32, a row
         of the packed [B * S] batch), over its request's keys.  qr: the picked rows' query projection
         [B, heads * d]; kv: every row's K / V projection [B * S, 2 * kv_heads * d].  RoPE rotates the
@@ -279,17 +338,14 @@ class W8A8Stack:
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
         P = 0 if past is None else past[0].shape[1]
         cos, sin = self._tables(P + S, kv.device)
-        if P == 0:
-            rope_inplace(kv, hk, d, cos, sin, period=S)
-        else:
-            rope_inplace(kv, hk, d, cos, sin, pos=pos)
+        self._rotate(kv, (0, 0), (0, hk), cos, sin, S if P == 0 else None, None if P == 0 else pos, norms)
         qpos = (rows - torch.arange(B, device=rows.device, dtype=torch.int32) * S + P).to(torch.int32)
-        rope_inplace(qr, hq, d, cos, sin, pos=qpos)
+        self._rotate(qr, (0, hq), (0, 0), cos, sin, pos=qpos, norms=norms)
         k, v = kv.view(B, S, 2 * hk, d).split((hk, hk), dim=2)
         if P:
             k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
             v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
-        q = qr.view(B, 1, hq, d)
+        q = qr[:, :hq * d].view(B, 1, hq, d)
         kv_len = (qpos + 1).to(torch.int32)
         if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
             return causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), kv_len=kv_len).view(B, hq * d)
@@ -317,11 +373,12 @@ class W8A8Stack:
             qr = L.q_rows.forward_quantized(q.index_select(0, rows), s.index_select(0, rows))
             if t is not None:
                 t.update(kind="attention_last", h=h, q=q, s=s, y=y, kv=kv.clone(), qr=qr.clone())
-            a = self._attention_rows(qr, kv, B, S, rows, past, pos)
-            r = aot.act_quant(a)
-            h1 = L.o.forward_quantized(*r, residual=h.index_select(0, rows))
+            a = self._attention_rows(qr, kv, B, S, rows, past, pos, (L.q_norm, L.k_norm))
+            nq = cfg.heads * cfg.head_dim
+            qa, sa, gated = self._o_input(a, qr[:, nq:] if cfg.attn_output_gate else None, t is not None)
+            h1 = L.o.forward_quantized(qa, sa, residual=h.index_select(0, rows))
             if t is not None:
-                t.update(kv_rope=kv, qr_rope=qr, a=a, qa=r[0], sa=r[1])
+                t.update(kv_rope=kv, qr_rope=qr, a=a, gated=gated, qa=qa, sa=sa)
         q2, s2, y2 = _norm_quant(h1, L.post_norm, cfg.eps, t is not None)
         g = L.gate_up.forward_quantized(q2, s2)
         qh, sh = aot.act_quant(g)
@@ -354,13 +411,14 @@ class W8A8Stack:
             q, s, y = _norm_quant(h, L.input_norm, cfg.eps, trace is not None)
             qkv = L.qkv.forward_quantized(q, s)
             qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
-            a = self._attention(qkv, B, S, past, keep, pos)
+            a = self._attention(qkv, B, S, past, keep, pos, (L.q_norm, L.k_norm))
             if keep:
                 a, state = a
-            r = aot.act_quant(a)
-            h1 = L.o.forward_quantized(*r, residual=h)
-            t = dict(kind="attention", h=h, q=q, s=s, y=y, qkv=qkv_out, qkv_rope=qkv, a=a, qa=r[0], sa=r[1],
-                     h1=h1) if trace is not None else None
+            nq = cfg.heads * cfg.head_dim
+            qa, sa, gated = self._o_input(a, qkv[:, nq:2 * nq] if cfg.attn_output_gate else None, trace is not None)
+            h1 = L.o.forward_quantized(qa, sa, residual=h)
+            t = dict(kind="attention", h=h, q=q, s=s, y=y, qkv=qkv_out, qkv_rope=qkv, a=a, gated=gated, qa=qa,
+                     sa=sa, h1=h1) if trace is not None else None
         q2, s2, y2 = _norm_quant(h1, L.post_norm, cfg.eps, trace is not None)
         g = L.gate_up.forward_quantized(q2, s2)
         qh, sh = aot.act_quant(g)
@@ -432,7 +490,7 @@ class W8A8Stack:
     def linear_ops_per_token(self):
         """int8 ops per token of the W8A8 linears (2 N K per projection), final readout excluded."""
         c = self.cfg
-        attn = ((c.heads + 2 * c.kv_heads) * c.head_dim * c.hidden    # QKV
+        attn = (((2 if c.attn_output_gate else 1) * c.heads + 2 * c.kv_heads) * c.head_dim * c.hidden  # QKV (+ gate)
                 + c.hidden * c.heads * c.head_dim)                   # O
         hk, hv, D = c.linear_k_heads, c.linear_v_heads, _GDN_DIM
         gdn = ((2 * hk + hv) * D + hv * D + 2 * hv) * c.hidden + c.hidden * hv * D  # in_proj qkv / z / b / a, out

@@ -278,3 +278,34 @@ def causal_gqa_attention(q, k, v, scale: float) -> np.ndarray:
             p = np.exp(s)
             out[b, :, h] = (p / p.sum(1, keepdims=True)) @ v[b, :, h // grp]
     return out
+
+
+# ---------------------------------------------------------------- full-attention extras
+def sigmoid_bf16(g_bits: np.ndarray) -> np.ndarray:
+    """bf16(sigmoid(g)) on bf16 g, torch.sigmoid's fp32 steps for a bf16 tensor: 1 / (1 + exp(-g)) with
+    exp(-g) in float64 rounded once to fp32 (inf past the fp32 range, as the fp32 exp), then the fp32 sum
+    and IEEE quotient, rounded to bf16 (the gate of the full-attention layers, fast_runtime.py:240)."""
+    g = bf16_to_f32(g_bits)
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    return f32_to_bf16(F32(1.0) / (F32(1.0) + e))
+
+
+def gate_mul(a_bits: np.ndarray, g_bits: np.ndarray) -> np.ndarray:
+    """The output gate o * sigmoid(gate) on bf16 tensors (fast_runtime.py:240,
+    prefill_engine.py:331): the fp32 product of o and bf16(sigmoid(g)), rounded to bf16."""
+    return f32_to_bf16(bf16_to_f32(a_bits) * bf16_to_f32(sigmoid_bf16(g_bits)))
+
+
+def head_rms_norm(x_bits: np.ndarray, w, eps: float, offset: float = 1.0) -> np.ndarray:
+    """q_norm / k_norm of the full-attention layers (fast_runtime.py:232-233): the RMSNorm of rms_norm over
+    the last axis (each head of head_dim values), with the zero-centred weight (offset 1)."""
+    return rms_norm(x_bits, w, eps, offset)[0]
+
+
+def rope_partial(x_bits: np.ndarray, cos_bits: np.ndarray, sin_bits: np.ndarray, rot_dim: int) -> np.ndarray:
+    """Partial rotary embedding (rope_one, prefill_engine.py:83-89): rope on the first rot_dim dims of each
+    head, the other dims unchanged.  cos / sin: bf16 bits broadcastable to [..., rot_dim / 2]."""
+    x = np.asarray(x_bits, dtype=np.uint16)
+    rot = rope(x[..., :rot_dim], cos_bits, sin_bits)
+    return np.concatenate([rot, x[..., rot_dim:]], -1)

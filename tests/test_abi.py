@@ -263,3 +263,40 @@ def test_gdn_gate_rejects():
     assert with_(a9=0) == 1               # no heads
     assert with_(a1=16) == 4              # lda < HV
     assert with_(a8=0) == 0               # no tokens
+
+
+def test_head_norm_rope_rejects():
+    lib = _lib.load()
+    base = dict(x=A16, ldx=6144, T=4, qo=0, nq=16, ko=4096, nk=4, d=256, wq=A16, wk=A16, off=1.0, eps=1e-6, rd=64,
+                cs=A16, sn=A16, npos=100, pos=None, period=4)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return lib.mica_head_norm_rope(*a.values(), None)
+
+    assert call(x=None) == 6               # no rows
+    assert call(d=192) == 1                # head_dim not a power of two
+    assert call(rd=512) == 1               # rotary dims beyond the head
+    assert call(rd=48) == 1                # rotary dims not a power of two
+    assert call(cs=None) == 6              # rotation without tables
+    assert call(period=0) == 6             # rotation without positions
+    assert call(ldx=5000) == 4             # k heads past the row
+    assert call(ko=4100) == 4              # unaligned segment
+    assert call(wq=A16 + 4) == 3           # misaligned weight
+    assert call(T=0) == 0
+
+
+def test_gate_quant_rejects():
+    lib = _lib.load()
+    base = dict(a=A16, lda=4096, g=A16, ldg=10240, q=A16, ldq=4096, s=A16, y=None, ldy=0, M=4, K=4096, rnd=0)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return lib.mica_gate_quant(*a.values(), None)
+
+    assert call(g=None) == 6
+    assert call(rnd=1) == 6                # half away is not served
+    assert call(K=1000) == 1               # not a multiple of 512
+    assert call(ldg=2048) == 4             # gate rows shorter than K
+    assert call(s=A16 + 4) == 3
+    assert call(M=0) == 0

@@ -367,3 +367,82 @@ def test_last_only_sdpa_path(gpu):
     b = full.forward_last(ids, 2, rows, lo, cnt)
     torch.cuda.synchronize()
     np.testing.assert_allclose(a[1].cpu().numpy(), b[1].cpu().numpy(), atol=2e-2)
+
+
+def test_reference_attention_layer_stage_by_stage(gpu):
+    """A full-attention layer with the reference model's extras (q_proj output gate, q / k head norm,
+    RoPE on 64 dims; fast_runtime.py:229-241): the gated QKV GEMM bit-exact, head norm + RoPE of the q
+    and k heads within two bf16 ulps of the oracle (the gate and v columns untouched), attention against
+    the float64 oracle, the gated o_proj input (one ulp of the oracle's gate, int8 bit-exact given the
+    kernel's gated row), then O + residual and the MLP as in the other layers."""
+    print("[case] reference attention layer", file=sys.stderr, flush=True)
+    cfg = StackConfig.reference_model(layers=1, full_attention_interval=0, hidden=512, intermediate=1024,
+                                      heads=4, kv_heads=1, vocab=4096, n_options=31)
+    st = W8A8Stack(cfg, device=gpu, seed=51, last_only=False)
+    B, S = 2, 96
+    ids = torch.randint(0, cfg.vocab, (B * S,), generator=torch.Generator().manual_seed(52)).to(gpu)
+    trace = []
+    st.prefill(ids, B, trace=trace)
+    torch.cuda.synchronize()
+    L, t = st.layers[0], trace[0]
+    hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+    q, s = t["q"].cpu().numpy(), t["s"].cpu().numpy()
+    qkv = O.epilogue(O.int_gemm(q, L.qkv.qweight.cpu().numpy()), s, L.qkv.wscale.cpu().numpy())
+    assert qkv.shape[1] == (2 * hq + 2 * hk) * d
+    assert np.array_equal(bits(t["qkv"]), qkv), "gated QKV GEMM"
+    cos, sin = (bits(x) for x in st._tables(S, gpu))
+    pos = np.arange(B * S) % S
+    xr = qkv.reshape(B * S, -1, d)
+    want = xr.copy()
+    for sl, w in ((slice(0, hq), L.q_norm), (slice(2 * hq, 2 * hq + hk), L.k_norm)):
+        want[:, sl] = O.rope_partial(O.head_rms_norm(xr[:, sl], O.bf16_to_f32(bits(w)), cfg.eps, 1.0),
+                                     cos[pos][:, None, :], sin[pos][:, None, :], 64)
+    got = bits(t["qkv_rope"]).reshape(B * S, -1, d)
+    assert np.array_equal(got[:, hq:2 * hq], xr[:, hq:2 * hq]) and np.array_equal(got[:, -hk:], xr[:, -hk:])
+    heads = np.r_[0:hq, 2 * hq:2 * hq + hk]
+    u = np.abs(O.bf16_to_f32(got[:, heads]) - O.bf16_to_f32(want[:, heads])) / O.bf16_ulp(want[:, heads])
+    assert u.max() <= 2.0001 and np.mean(got[:, heads] == want[:, heads]) >= 0.99
+    # attention on the kernel's rotated q / k
+    g4 = got.reshape(B, S, -1, d)
+    a_ref = O.causal_gqa_attention(O.bf16_to_f32(g4[:, :, :hq]), O.bf16_to_f32(g4[:, :, 2 * hq:2 * hq + hk]),
+                                   O.bf16_to_f32(g4[:, :, 2 * hq + hk:]), 1.0 / 16)
+    # row-relative L2 error of each (request, position, head) row <= 0.02: the reference's attention
+    # acceptance criterion (int8_runtime.py:445-488, ATTN_TOL; bf16 probabilities and outputs)
+    ak = O.bf16_to_f32(bits(t["a"])).reshape(B, S, hq, d)
+    rel = np.linalg.norm(ak - a_ref, axis=-1) / np.maximum(np.linalg.norm(a_ref, axis=-1), 1e-30)
+    assert rel.max() <= 0.02, f"attention row error {rel.max():.4f}"
+    # the gated o_proj input
+    gk = bits(t["gated"])
+    gref = O.gate_mul(bits(t["a"]), got[:, hq:2 * hq].reshape(B * S, -1))
+    u = np.abs(O.bf16_to_f32(gk) - O.bf16_to_f32(gref)) / O.bf16_ulp(gref)
+    assert u.max() <= 1.0001 and np.mean(gk == gref) >= 0.999
+    qa, sa = O.quant_act(O.bf16_to_f32(gk))
+    assert np.array_equal(t["qa"].cpu().numpy(), qa) and np.array_equal(t["sa"].cpu().numpy(), sa)
+    h1 = O.epilogue(O.int_gemm(qa, L.o.qweight.cpu().numpy()), sa, L.o.wscale.cpu().numpy())
+    h1 = O.f32_to_bf16(O.bf16_to_f32(h1) + O.bf16_to_f32(bits(t["h"])))
+    assert np.array_equal(bits(t["h1"]), h1), "o_proj + residual"
+    _check_mlp(L, t, cfg, 0)
+
+
+def test_reference_model_last_only_bit_identical(gpu):
+    """The reference model's layout (GDN layers, every fourth full attention with the gate, q / k norm and
+    partial RoPE): last-only equals the full last layer bit for bit, padded requests and a prefix too."""
+    print("[case] reference model last-only", file=sys.stderr, flush=True)
+    cfg = StackConfig.reference_model(layers=4, hidden=512, intermediate=1024, heads=4, kv_heads=1, vocab=4096,
+                                      n_options=31, linear_k_heads=2, linear_v_heads=4)
+    last = W8A8Stack(cfg, device=gpu, seed=61)
+    full = W8A8Stack(cfg, device=gpu, seed=61, last_only=False)
+    assert [type(L).__name__ for L in last.layers] == ["GDNBlock"] * 3 + ["Layer"]
+    ids, rows = _padded_batch(cfg, gpu, [128, 90, 5], 128, seed=62)
+    lo, cnt = last.slices(None, None, 3, gpu)
+    a = last.forward_last(ids, 3, rows, lo, cnt)
+    b = full.forward_last(ids, 3, rows, lo, cnt)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    p = a[1].cpu().numpy()
+    assert np.isfinite(p).all() and np.allclose(p.sum(1), 1.0, atol=1e-5)
+    pre = torch.randint(0, cfg.vocab, (64,), generator=torch.Generator().manual_seed(63)).to(gpu)
+    a = last.forward_last(ids, 3, rows, lo, cnt, prefix=last.prefix_state(pre))
+    b = full.forward_last(ids, 3, rows, lo, cnt, prefix=full.prefix_state(pre))
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

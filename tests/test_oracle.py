@@ -374,3 +374,58 @@ def test_attention_oracle_queries_after_a_prefix():
     p = np.exp(s - s.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
     np.testing.assert_allclose(one[:, 0], np.einsum("bhk,bkhd->bhd", p, np.repeat(v, HQ // HK, axis=2)), rtol=1e-10)
+
+
+# ---------------------------------------------------------------- full-attention extras
+def test_sigmoid_bf16_equals_torch_cpu_on_every_code():
+    """sigmoid_bf16 against torch.sigmoid on bf16 CPU tensors (a library, not the reference), for every
+    finite bf16 code: identical bits.  Plus closed forms: sigmoid(0) = 0.5, sigmoid(g) + sigmoid(-g) = 1
+    within rounding, monotone, 0 / 1 far out."""
+    codes = np.arange(65536, dtype=np.uint16)
+    g = O.bf16_to_f32(codes)
+    fin = np.isfinite(g)
+    s = O.sigmoid_bf16(codes)
+    t = torch.sigmoid(torch.from_numpy(codes.view(np.int16)).view(torch.bfloat16)).view(torch.int16).numpy()
+    assert np.array_equal(s[fin], t.view(np.uint16)[fin])
+    assert O.bf16_to_f32(O.sigmoid_bf16(np.array([0], np.uint16)))[0] == 0.5
+    sv = O.bf16_to_f32(s[fin])
+    order = np.argsort(g[fin], kind="stable")
+    assert np.all(np.diff(sv[order]) >= 0)
+    pos = codes[fin & (g > 0)]
+    neg = pos | np.uint16(0x8000)
+    assert np.all(np.abs(O.bf16_to_f32(O.sigmoid_bf16(pos)) + O.bf16_to_f32(O.sigmoid_bf16(neg)) - 1.0) <= 2 ** -8)
+    assert O.bf16_to_f32(O.sigmoid_bf16(O.f32_to_bf16(np.array([100.0], np.float32))))[0] == 1.0
+
+
+def test_gate_mul_matches_torch_bf16_ops():
+    """o * torch.sigmoid(gate) on bf16 CPU tensors, the reference's op sequence (fast_runtime.py:240)."""
+    rng = np.random.default_rng(40)
+    a = O.f32_to_bf16(rng.standard_normal((64, 512)).astype(np.float32) * 3)
+    gt = O.f32_to_bf16(rng.standard_normal((64, 512)).astype(np.float32) * 4)
+    ta, tg = (torch.from_numpy(x.view(np.int16)).view(torch.bfloat16) for x in (a, gt))
+    ref = (ta * torch.sigmoid(tg)).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.gate_mul(a, gt), ref)
+    # closed form: a gate of 0 halves a exactly (bf16 * 0.5 is exact)
+    assert np.array_equal(O.bf16_to_f32(O.gate_mul(a, np.zeros_like(gt))), O.bf16_to_f32(a) * 0.5)
+
+
+def test_rope_partial_and_head_norm():
+    """rope_partial with rot_dim = head_dim is rope; with rot_dim < head_dim its first rot_dim dims are rope
+    of that slice and the rest pass through; head_rms_norm is rms_norm of each head (zero-centred weight)."""
+    rng = np.random.default_rng(41)
+    x = O.f32_to_bf16(rng.standard_normal((6, 4, 256)).astype(np.float32))
+    ang = rng.uniform(-3, 3, (6, 1, 128)).astype(np.float32)
+    c, s = O.f32_to_bf16(np.cos(ang)), O.f32_to_bf16(np.sin(ang))
+    assert np.array_equal(O.rope_partial(x, c, s, 256), O.rope(x, c, s))
+    y = O.rope_partial(x, c[..., :32], s[..., :32], 64)
+    assert np.array_equal(y[..., 64:], x[..., 64:])
+    assert np.array_equal(y[..., :64], O.rope(x[..., :64], c[..., :32], s[..., :32]))
+    # rotate_half pairs dim i with i + 32 inside the 64 rotated dims: a quarter turn maps (a, b) to (-b, a)
+    quarter_c = O.f32_to_bf16(np.zeros((1, 1, 32), np.float32))
+    quarter_s = O.f32_to_bf16(np.ones((1, 1, 32), np.float32))
+    z = O.bf16_to_f32(O.rope_partial(x, quarter_c, quarter_s, 64))
+    xf = O.bf16_to_f32(x)
+    assert np.array_equal(z[..., :32], -xf[..., 32:64]) and np.array_equal(z[..., 32:64], xf[..., :32])
+    w = rng.normal(0, 0.1, 256).astype(np.float32)
+    wb = O.round_bf16(w)
+    assert np.array_equal(O.head_rms_norm(x, wb, 1e-6), O.rms_norm(x.reshape(-1, 256), wb, 1e-6)[0].reshape(x.shape))
