@@ -1,7 +1,8 @@
 """Requests end to end on the GPU: /v1/systemone request -> rows -> prompts -> tokens -> the prefill
 engine (W8A8 stack, last-position label readout) -> typed answers.
 
-The stack is a small random one, so the probabilities mean nothing; what is checked is the plumbing
+The stack is a small random one with the reference model's layer computation, so the probabilities
+mean nothing; what is checked is the plumbing
 around them: every stored request gets a response with the stored answer ids, types and order; each
 answer is the typed result of that row's own distribution, computed by running its prompt alone
 (batching, padding and duplicate removal do not change a bit); Noul rows read the No / Yes slice and
@@ -31,8 +32,11 @@ def _tokenize(text):
 
 @pytest.fixture(scope="module")
 def judge(gpu):
-    cfg = StackConfig(layers=2, hidden=512, intermediate=1024, heads=4, kv_heads=1, head_dim=256, vocab=4096,
-                      n_options=255, full_attention_interval=2, linear_k_heads=2, linear_v_heads=4)
+    # the reference model's computation at a small size: a GDN layer, then a full-attention layer with the
+    # q_proj output gate, q / k head norm and partial RoPE (StackConfig.reference_model)
+    cfg = StackConfig.reference_model(layers=2, hidden=512, intermediate=1024, heads=4, kv_heads=1, head_dim=256,
+                                      vocab=4096, n_options=255, full_attention_interval=2, linear_k_heads=2,
+                                      linear_v_heads=4)
     st = W8A8Stack(cfg, device=gpu, seed=11)
     return C.EngineJudge(PrefillEngine(st, graph=False), _tokenize, max_length=32768, max_batch=8)
 
