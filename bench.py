@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--summarize", nargs=2, metavar=("ROCPROF_DIR", "OUT_TXT"),
                     help="write a text summary of rocprofv3 CSV output (kernel stats or counters)")
     ap.add_argument("--command", default="", help="with --summarize: the command that produced ROCPROF_DIR")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="rebuild profiles/gemm_i8_m4096_n9728_k2560_traffic.json from a FETCH_SIZE and a WRITE_SIZE "
+                         "pass of --pmc-workload (rocprofv3 output folders) and exit")
     return ap.parse_args()
 
 
@@ -224,21 +227,89 @@ def cpu_baseline(torch, M, K, N):
     return out
 
 
+TRAFFIC_JSON = ROOT / "profiles" / "gemm_i8_m4096_n9728_k2560_traffic.json"
+GEMM_SOURCES = ("gemm_i8.hip", "gemm_i8_agpr.hip", "gemm_i8_wide.hip", "gemm_i8_common.h", "common.h")
+
+
+def gemm_sources_digest() -> str:
+    """First 16 hex digits of the SHA-256 over the GEMM kernels' sources: the traffic figure is valid for
+    the kernels built from exactly these."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in GEMM_SOURCES:
+        h.update((ROOT / "mica_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def traffic_from_profiles():
-    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, if one was recorded."""
-    p = ROOT / "profiles" / "gemm_i8_m4096_n9728_k2560_traffic.json"
-    if p.is_file():
-        try:
-            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            return None
-    return None
+    """(HBM bytes per headline GEMM launch, note) from the committed rocprofv3 counter passes
+    (profiles/gemm_i8_m4096_n9728_k2560_traffic.json, written by --traffic); (None, why) when there is
+    none or it was measured on other GEMM sources than the ones built here."""
+    if not TRAFFIC_JSON.is_file():
+        return None, "no traffic measurement committed"
+    try:
+        d = json.loads(TRAFFIC_JSON.read_text())
+    except (ValueError, OSError) as ex:
+        return None, f"traffic file unreadable: {ex}"[:120]
+    if d.get("sources_sha16") != gemm_sources_digest():
+        return None, "traffic measurement is of other GEMM sources (run the FETCH_SIZE / WRITE_SIZE passes and --traffic)"
+    return d.get("hbm_bytes_per_launch"), ("traffic: " + TRAFFIC_JSON.relative_to(ROOT).as_posix() +
+                                           ", rocprofv3 FETCH_SIZE + WRITE_SIZE passes over --pmc-workload, "
+                                           "scaled by the 256 MiB copy's factors; sources " + d["sources_sha16"])
+
+
+def write_traffic(fetch_dir, write_dir, commands=()):
+    """Rebuild the traffic file from a FETCH_SIZE pass and a WRITE_SIZE pass of --pmc-workload (their
+    rocprofv3 output folders): the headline GEMM's KiB per dispatch, scaled by the factors that make the
+    256 MiB copy of the same run read and write 256 MiB, stamped with the GEMM sources' digest."""
+    import csv
+    import glob
+
+    def per_run(folder, counter):
+        f = sorted(glob.glob(os.path.join(folder, "**", "*counter_collection.csv"), recursive=True))[0]
+        disp = {}
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                disp[int(r["Dispatch_Id"])] = (r["Kernel_Name"], float(r["Counter_Value"]))
+        runs, cur = [], None
+        for i in sorted(disp):
+            k, v = disp[i]
+            if cur is not None and cur[0] == k:
+                cur[1].append(v)
+            else:
+                cur = (k, [v])
+                runs.append(cur)
+        long_runs = [r for r in runs if len(r[1]) >= 20]
+        if len(long_runs) != len(PMC_WORKLOADS):
+            raise SystemExit(f"{folder}: {len(long_runs)} runs of 20 dispatches, expected {len(PMC_WORKLOADS)}")
+        return {name: sum(v) / len(v) for name, (_, v) in zip(PMC_WORKLOADS, long_runs)}
+
+    fetch, write = per_run(fetch_dir, "FETCH_SIZE"), per_run(write_dir, "WRITE_SIZE")
+    copied = 256 << 20
+    ff, wf = copied / (fetch["copy_256MiB"] * 1024), copied / (write["copy_256MiB"] * 1024)
+    head = "gemm_headline_4096x9728x2560"
+    fb, wb = fetch[head] * 1024 * ff, write[head] * 1024 * wf
+    M, K, N = 4096, HIDDEN, INTER
+    out = {"workload": "M=4096 K=2560 N=9728", "sources_sha16": gemm_sources_digest(), "commands": list(commands),
+           "fetch_size_kib_per_dispatch": round(fetch[head], 1), "write_size_kib_per_dispatch": round(write[head], 1),
+           "copy_calibration": {"bytes_copied": copied, "fetch_size_kib": round(fetch["copy_256MiB"], 1),
+                                "write_size_kib": round(write["copy_256MiB"], 1), "fetch_factor": round(ff, 4),
+                                "write_factor": round(wf, 4)},
+           "fetch_bytes_per_launch": int(fb), "write_bytes_per_launch": int(wb), "hbm_bytes_per_launch": int(fb + wb),
+           "algorithmic_bytes_per_launch": M * K + N * K + 2 * M * N + 4 * (M + N),
+           "note": "FETCH_SIZE / WRITE_SIZE count L2 (TCC) traffic to the memory fabric; fetches served by the 256 MB "
+                   "Infinity Cache are included, so this is an upper bound on HBM bytes."}
+    TRAFFIC_JSON.write_text(json.dumps(out, indent=1) + "\n")
+    print(f"wrote {TRAFFIC_JSON}: {out['hbm_bytes_per_launch']} bytes per launch", flush=True)
 
 
 def main():
     args = parse()
     if args.summarize:
         summarize(*args.summarize, command=args.command)
+        return
+    if args.traffic:
+        write_traffic(*args.traffic, commands=[c for c in args.command.split(" ;; ") if c])
         return
     if args.pmc_workload:
         pmc_workload()
@@ -414,6 +485,7 @@ def main():
         result["prefill_tokens_per_s"] = result["stack"]["tokens_per_s"]
     ms = timer.run(gemm_launcher(torch, lib, qx, sx, qw, sw, out), args.steps, args.warmup)
     tops = ops / (ms * 1e-3) / 1e12
+    traffic, traffic_note = traffic_from_profiles()
     head = {
         "metric": METRIC,
         "value": round(tops, 2),
@@ -436,9 +508,9 @@ def main():
                              "(GPU clocks of a busy GPU)"},
         "pct_int8_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(),
+                     "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
                      "note": "INT8 TOP/s (2 M N K per launch / mean launch time); peak = MI355X dense INT8 5.0 "
-                             "POP/s"},
+                             "POP/s; " + traffic_note},
         "device": {**info, "derived_int8_peak_tops": round(info["cu_count"] * info["clock_khz"] * 1e3 * 8192 / 1e12,
                                                            1)},
     }
