@@ -107,17 +107,21 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
 // (kFast: unsmoothed bf16 rows; the row kernels take this path for half-away rounding, and the
 // one-FMA quantizer of common.h for half even) its rounded integer equals the IEEE quotient's for every input
 // (tests/native/quotient_check.c, exhaustive).  For other values (SmoothQuant-scaled rows, fp16 and
-// fp32 activations) the plain product y = x * r is used: it is within 2^-16 of x / s for |x / s| <=
-// 127.5 (r's rounding and y's), so its integer can only differ from the IEEE quotient's near a rounding
-// boundary: lanes whose y lies within 2^-13 of k + 0.5 (|fract(y) - 0.5| <= 2^-13, v_fract_f32)
-// recompute it with the IEEE division (tests/native/guarded_quotient_check.c: 2^28 samples, no
-// mismatch, the slow path on ~5e-5 of the values).
+// fp32 activations) the plain product y = x * r is used.  With |x / s| <= 127.5, the exact product x r
+// is within 127.5 * 2^-24 < 2^-17 of x / s (r = RN(1 / s)), y's rounding adds at most 2^-18, and the
+// IEEE quotient RN(x / s) is within 2^-18 of x / s: so y and RN(x / s) lie within 2^-16 of each other,
+// and their integers can only differ when y is within 2^-16 of a boundary k + 0.5.  Lanes whose y lies
+// within kTieWindow = 2^-15 of one (|fract(y) - 0.5| <= 2^-15, v_fract_f32) recompute the chunk with
+// the IEEE division.  A wave takes that path when any of its 512 values is that close: ~3 % of the
+// chunks of a smoothed row, against ~12 % for a 2^-13 window.
 //
 // Half even without kFast is one step shorter: the exact product x r (one FMA with 1.5 * 2^23) is
-// rounded to an integer directly, and the guard looks at u = fma(x, r, 0.5 + 2^-13): x r within
-// 2^-16 of k + 0.5 puts fract(u) below 2^-12 (|x r - x / s| < 2^-17, u's own rounding < 2^-17), so
-// the lanes whose exact product lies within ~2^-13 of a tie take the IEEE division
-// (tests/native/guarded_quotient_check.c checks this form as well).
+// rounded to an integer directly, and the guard looks at u = RN(x r + 0.5 + 2^-15): x r within 2^-16
+// of k + 0.5 puts u within 2^-15 +- (2^-16 + 2^-18) of the integer k + 1 (|u| < 128, so its rounding
+// is at most 2^-18), i.e. fract(u) in (0, 2^-14), and those lanes take the IEEE division.
+// tests/native/guarded_quotient_check.c checks both forms on 2^28 random pairs and on every x within
+// the window around every boundary k + 0.5 for 2^15 values of s (the computation is invariant under
+// scaling x and s by the same power of two, so s in [1, 2) covers every normal scale).
 //
 // Half even rounds with the 1.5 * 2^23 trick: for |t| < 2^22, t + 12582912 is an integer-valued
 // float (its rounding is the IEEE round-half-even of t), whose low mantissa byte is that integer in
@@ -125,6 +129,8 @@ MICA_DEVICE void load_inv8(const float *inv, int idx, float (&v)[kChunk]) {
 // |x| <= amax and s = RN(max(amax, 1e-8) / 127) give |x / s| <= 127 / (1 - 2^-24) < 127.5, so
 // round(x / s) is already within +-127 (the reference's clamp is the identity on finite rows; a row
 // holding Inf or NaN yields 0 for those elements).
+constexpr float kTieWindow = 0x1p-15f;
+
 template <bool kFast, int RND>
 MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int rounding, int8_t *dst) {
     const int mode = RND == 2 ? rounding : RND;
@@ -134,9 +140,9 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
             b[j] = __float_as_uint(__builtin_fmaf(v[j], r, kMagicRne));
-            low = __builtin_fminf(low, __builtin_amdgcn_fractf(__builtin_fmaf(v[j], r, 0.5f + 0x1p-13f)));
+            low = __builtin_fminf(low, __builtin_amdgcn_fractf(__builtin_fmaf(v[j], r, 0.5f + kTieWindow)));
         }
-        if (low < 0x1p-12f) {
+        if (low < 2.0f * kTieWindow) {
 #pragma unroll
             for (int j = 0; j < kChunk; ++j) b[j] = __float_as_uint(v[j] / s + kMagicRne);
         }
@@ -162,7 +168,7 @@ MICA_DEVICE void quant_store8r(const float (&v)[kChunk], float s, float r, int r
         float gap = 1.0f;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) gap = __builtin_fminf(gap, __builtin_fabsf(__builtin_amdgcn_fractf(t[j]) - 0.5f));
-        const bool near = gap <= 0x1p-13f;
+        const bool near = gap <= kTieWindow;
         if (near) {
 #pragma unroll
             for (int j = 0; j < kChunk; ++j) t[j] = v[j] / s;
@@ -236,9 +242,11 @@ MICA_DEVICE void row16_body(const RowParams &p) {
     // rows of up to 2560 elements with smoothing factors: the workgroup copies every output's factors
     // into LDS once (n_out x K fp32, dynamic shared memory), so the two passes of every row read them
     // there instead of through the vector memory path.  Chunk ch = c * 64 + lane of output o sits at
-    // float4 pair ((o * NCH + c) * 64 + lane) * 2.
+    // float4 X = (o * NCH + c) * 64 + lane (its first 4 factors) and kHalf + X (its last 4): a wave's
+    // 16-byte reads then cover consecutive addresses, free of bank conflicts.
     constexpr bool kInvLds = HAS_INV && NCH <= 5;
     extern __shared__ float4 inv_sh[];
+    const int kHalf = p.n_out * NCH * 64;
     if (kInvLds) {
         for (int o = 0; o < p.n_out; ++o) {
             if (p.inv[o] == nullptr) continue;
@@ -248,8 +256,8 @@ MICA_DEVICE void row16_body(const RowParams &p) {
                     a = ((const float4 *)(p.inv[o] + ch * kChunk))[0];
                     b = ((const float4 *)(p.inv[o] + ch * kChunk))[1];
                 }
-                inv_sh[(o * NCH * 64 + ch) * 2] = a;
-                inv_sh[(o * NCH * 64 + ch) * 2 + 1] = b;
+                inv_sh[o * NCH * 64 + ch] = a;
+                inv_sh[kHalf + o * NCH * 64 + ch] = b;
             }
         }
         __syncthreads();
@@ -353,8 +361,8 @@ MICA_DEVICE void row16_body(const RowParams &p) {
                 if (HAS_INV && inv != nullptr) {
                     float iv[kChunk];
                     if (kInvLds) {
-                        const float4 a = inv_sh[((o * NCH + c) * 64 + lane) * 2];
-                        const float4 b = inv_sh[((o * NCH + c) * 64 + lane) * 2 + 1];
+                        const float4 a = inv_sh[(o * NCH + c) * 64 + lane];
+                        const float4 b = inv_sh[kHalf + (o * NCH + c) * 64 + lane];
                         iv[0] = a.x; iv[1] = a.y; iv[2] = a.z; iv[3] = a.w;
                         iv[4] = b.x; iv[5] = b.y; iv[6] = b.z; iv[7] = b.w;
                     } else if (live(c)) {
@@ -469,15 +477,17 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
     const int row = blockIdx.x * (kSmoothThreads / 64) + (threadIdx.x >> 6);
     const bool on = row < p.M;
     const bool has_res = NORM && p.res != nullptr;
-    // every output's factors go to LDS: chunk ch = c * 64 + lane of output o at float4 pair
-    // ((o * NCH + c) * 64 + lane) * 2; with the norm, the multipliers offset + w (fp32) after them as
-    // output NOUT.  This thread's share is loaded first, the row second: the memory counter retires
+    // every output's factors go to LDS: chunk ch = c * 64 + lane of output o at float4
+    // X = (o * NCH + c) * 64 + lane (its first 4 factors) and kHalf + X (its last 4), so a wave's 16-byte
+    // reads cover consecutive addresses, free of bank conflicts; with the norm, the multipliers
+    // offset + w (fp32) after them as output NOUT.  This thread's share is loaded first, the row second: the memory counter retires
     // loads in issue order, so the LDS fill waits for the factors alone, and the barrier after it waits
     // for LDS only -- each wave then starts on its row as soon as that row has arrived, instead of the
     // whole workgroup waiting for its slowest row (which a full __syncthreads() fence would do).
     extern __shared__ float4 inv_sh[];
     constexpr int kSets = SMOOTH ? NOUT : 0;  // factor sets before the norm's multipliers
     constexpr int kFill = (NCH * 64 + kSmoothThreads - 1) / kSmoothThreads;  // chunks per thread and set
+    constexpr int kHalf = (kSets + (NORM ? 1 : 0)) * NCH * 64;
     float4 fin[kSets > 0 ? kSets : 1][kFill][2];
     u32x4 win[NORM ? kFill : 1];
     // (both loads are issued on every path, idle lanes re-reading the last valid chunk or row, so that
@@ -514,14 +524,14 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
         if (ch < NCH * 64) {
 #pragma unroll
             for (int o = 0; o < kSets; ++o) {
-                inv_sh[(o * NCH * 64 + ch) * 2] = fin[o][i][0];
-                inv_sh[(o * NCH * 64 + ch) * 2 + 1] = fin[o][i][1];
+                inv_sh[o * NCH * 64 + ch] = fin[o][i][0];
+                inv_sh[kHalf + o * NCH * 64 + ch] = fin[o][i][1];
             }
             if (NORM) {
                 float wv[kChunk];
                 unpack8<MICA_BF16>(win[i], wv);
-                inv_sh[(kSets * NCH * 64 + ch) * 2] = float4{p.offset + wv[0], p.offset + wv[1], p.offset + wv[2], p.offset + wv[3]};
-                inv_sh[(kSets * NCH * 64 + ch) * 2 + 1] = float4{p.offset + wv[4], p.offset + wv[5], p.offset + wv[6], p.offset + wv[7]};
+                inv_sh[kSets * NCH * 64 + ch] = float4{p.offset + wv[0], p.offset + wv[1], p.offset + wv[2], p.offset + wv[3]};
+                inv_sh[kHalf + kSets * NCH * 64 + ch] = float4{p.offset + wv[4], p.offset + wv[5], p.offset + wv[6], p.offset + wv[7]};
             }
         }
     }
@@ -551,8 +561,8 @@ __global__ __launch_bounds__(kSmoothThreads) __attribute__((amdgpu_waves_per_eu(
         unpack8<XT>(cur[c], v[c]);
     }
     auto factors = [&](int o, int c, float (&iv)[kChunk]) {
-        const float4 a = inv_sh[((o * NCH + c) * 64 + lane) * 2];
-        const float4 b = inv_sh[((o * NCH + c) * 64 + lane) * 2 + 1];
+        const float4 a = inv_sh[(o * NCH + c) * 64 + lane];
+        const float4 b = inv_sh[kHalf + (o * NCH + c) * 64 + lane];
         iv[0] = a.x; iv[1] = a.y; iv[2] = a.z; iv[3] = a.w;
         iv[4] = b.x; iv[5] = b.y; iv[6] = b.z; iv[7] = b.w;
     };
