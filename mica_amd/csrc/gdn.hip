@@ -191,21 +191,56 @@ struct GdnParams {
 MICA_DEVICE long chunk_id(const GdnParams &p, int b, int h, int c) { return ((long)b * p.HV + h) * p.NT + c; }
 
 // ---- prep: one workgroup per (chunk, value head, sequence) ------------------------------------
-// LDS (bytes): K rows, V rows (64 x 128 bf16, rows padded to 272 B), L (64 x 64 fp32, permuted for
-// the solve), G, exp(G), beta.  T (64 x 64 bf16, rows padded to 144 B) reuses L's space once every
-// wave has finished the solve, and the W staging (64 x 128 bf16) reuses K's once W and U are done:
-// 52 KB, three workgroups per CU.
+// LDS (bytes): K rows, V rows (64 x 128 bf16, rows padded to 272 B), L (64 x 64 fp32, rows padded to
+// 272 B), G, exp(G), beta.  The blocked solve keeps its fp32 blocks of T in L's space (the diagonal
+// blocks in place of L's, the off-diagonal ones in the unused upper triangle); the bf16 T (64 x 64,
+// rows padded to 144 B) then reuses that space once every wave holds its blocks in registers, and the
+// W staging (64 x 128 bf16) reuses K's once W and U are done: 52 KB, three workgroups per CU.
 constexpr int kRowP = 136;          // bf16 elements per padded 128-wide row
 constexpr int kRowC = 72;           // bf16 elements per padded 64-wide row
+constexpr int kLs = 68;             // fp32 elements per padded row of L (A-operand reads free of conflicts)
 constexpr int kPrepK = 0;
 constexpr int kPrepV = kPrepK + kC * kRowP * 2;
 constexpr int kPrepL = kPrepV + kC * kRowP * 2;
 constexpr int kPrepT = kPrepL;                     // after the solve
 constexpr int kPrepW = kPrepK;                     // after W and U
-constexpr int kPrepG = kPrepL + kC * kC * 4;
+constexpr int kPrepG = kPrepL + kC * kLs * 4;
 constexpr int kPrepSmem = kPrepG + 3 * kC * 4;
-static_assert(kC * kRowC * 2 <= kC * kC * 4, "T fits in L's space");
+static_assert(kC * kRowC * 2 <= kC * kLs * 4, "T fits in L's space");
 static_assert(3 * kPrepSmem <= 160 * 1024, "three prep workgroups per CU");
+
+// ---- 16 x 16 fp32 blocks on v_mfma_f32_16x16x4f32 (the blocked solve of T) ----
+// Operand layouts of one k-step (4 of the 16 inner indices): lane i + 16 k holds A[i][k] and
+// B[k][i]; the 16 x 16 result ("C layout"): lane j + 16 g holds rows 4 g .. 4 g + 3 of column j.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+MICA_DEVICE f32x4 mfma16(float a, float b, const f32x4 &c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+// c + A B with both blocks in LDS (row stride kLs)
+MICA_DEVICE f32x4 blk_mm(const float *A, const float *B, f32x4 c, int lane) {
+    const int r = lane & 15, k = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) c = mfma16(A[r * kLs + 4 * s + k], B[(4 * s + k) * kLs + r], c);
+    return c;
+}
+// c + A X with A in LDS and X in this wave's registers in the C layout: k-step s takes the inner
+// indices m = 4 k + s (k = 0..3), whose X rows lane j + 16 k holds in its register s
+MICA_DEVICE f32x4 blk_mm_reg(const float *A, const f32x4 &x, f32x4 c, int lane) {
+    const int r = lane & 15, k = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) c = mfma16(A[r * kLs + 4 * k + s], x[s], c);
+    return c;
+}
+// store a C-layout block at (row 16 bi, column 16 bj) of an fp32 matrix with row stride kLs
+MICA_DEVICE void blk_store(float *M, int bi, int bj, const f32x4 &x, int lane) {
+    const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) M[(16 * bi + 4 * g + v) * kLs + 16 * bj + j] = x[v];
+}
+// the same block as bf16 into T (row stride kRowC)
+MICA_DEVICE void blk_store_bf16(uint16_t *T, int bi, int bj, const f32x4 &x, int lane) {
+    const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) T[(16 * bi + 4 * g + v) * kRowC + 16 * bj + j] = f32_to_bf16(x[v]);
+}
 
 __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
     __shared__ __attribute__((aligned(16))) int8_t smem[kPrepSmem];
@@ -288,55 +323,94 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_prep_kernel(GdnParams p) {
             for (int u = 0; u < 4; ++u) {
                 const int i = i0 + u;
                 const float lv = (ba[u] * acc[4 * r4 + u]) * fexp(ga[u] - gj);
-                const float l = j < i ? lv : 0.0f;
-                // permuted: Lp[i][j % 4][j / 4], so a solving lane reads its 16 values contiguously
-                Lp[i * kC + (j & 3) * 16 + (j >> 2)] = l;
+                Lp[i * kLs + j] = j < i ? lv : 0.0f;
             }
         }
     }
     __syncthreads();
 
-    // ---- T = (I + L)^-1 by forward substitution, four rows at a time: wave w solves columns
-    // 16 w .. 16 w + 15 with four lanes per column; lane (j, q) holds T[4 s + q][j], s = 0..15.
-    // For rows i .. i + 3 (i = 4 s0) the terms m < i of T[r][j] = delta_rj - sum_{m<r} L[r][m] T[m][j]
-    // are summed per lane (m = q mod 4) and over the quad; the terms i <= m < r are then a 4 x 4
-    // substitution done redundantly by all four lanes, which keep row i + q each. ----
+    // ---- T = (I + L)^-1 over 16 x 16 blocks (block (i, j) = rows 16 i.., columns 16 j..).  From
+    // (I + L) T = I: the diagonal blocks D_i = (I + L_ii)^-1 by forward substitution, and below the
+    // diagonal T_ij = -D_i sum_{k=j}^{i-1} L_ik T_kj, in three dependent stages of fp32 MFMA products:
+    //   stage 1: T_10 (wave 0), T_21 (wave 1), T_32 (wave 2), L_30 D_0 (wave 3, kept)
+    //   stage 2: T_20 (wave 0), T_31 (wave 1), + L_31 T_10 (wave 3)
+    //   stage 3: T_30 = -D_3 (L_30 D_0 + L_31 T_10 + L_32 T_20) (wave 3)
+    // D_i replaces L_ii in LDS, and T_10, T_21, T_32, T_20 go to the unused upper blocks (0, 1),
+    // (1, 2), (2, 3), (0, 2) for the waves that read them.  Every wave keeps its own blocks in
+    // registers and writes them as bf16 once no wave reads L any more. ----
     {
-        const int j = wave * 16 + (lane >> 2), q = lane & 3;
-        float t[16];
+        const int jc = lane & 15, gq = lane >> 4;
+        auto blk = [&](int bi, int bj) { return Lp + 16 * bi * kLs + 16 * bj; };
+        // wave w: D_w, lane jc + 16 gq holding rows 4 gq .. 4 gq + 3 of column jc.  Four rows at a
+        // time: the terms of earlier row groups are summed per lane (its own four rows m) and over
+        // the four lane groups, then the 4 x 4 substitution is done redundantly in every lane
+        f32x4 D = {0.0f, 0.0f, 0.0f, 0.0f};
+        {
+            const float *N = blk(wave, wave);
 #pragma unroll
-        for (int s = 0; s < 16; ++s) t[s] = (4 * s + q == j) ? 1.0f : 0.0f;
+            for (int g2 = 0; g2 < 4; ++g2) {
+                float S4[4];
 #pragma unroll
-        for (int s0 = 0; s0 < 16; ++s0) {
-            const int i = 4 * s0;
-            float S4[4];
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const float *row = Lp + (i + a) * kC + q * 16;
-                float p0 = 0.0f, p1 = 0.0f; // two independent FMA chains
-#pragma unroll
-                for (int s4 = 0; s4 < (s0 + 3) / 4; ++s4) {
-                    const float4 lv = *(const float4 *)(row + s4 * 4);
-                    if (s4 * 4 + 0 < s0) p0 = __builtin_fmaf(lv.x, t[s4 * 4 + 0], p0);
-                    if (s4 * 4 + 1 < s0) p1 = __builtin_fmaf(lv.y, t[s4 * 4 + 1], p1);
-                    if (s4 * 4 + 2 < s0) p0 = __builtin_fmaf(lv.z, t[s4 * 4 + 2], p0);
-                    if (s4 * 4 + 3 < s0) p1 = __builtin_fmaf(lv.w, t[s4 * 4 + 3], p1);
+                for (int a = 0; a < 4; ++a) {
+                    float acc = 0.0f;
+                    if (g2 > 0) {
+                        const float4 nv = *(const float4 *)(N + (4 * g2 + a) * kLs + 4 * gq);
+                        acc = __builtin_fmaf(nv.x, D[0], __builtin_fmaf(nv.y, D[1], __builtin_fmaf(nv.z, D[2], nv.w * D[3])));
+                        acc = gq < g2 ? acc : 0.0f;
+                        acc += __shfl_xor(acc, 16, 64);
+                        acc += __shfl_xor(acc, 32, 64);
+                    }
+                    S4[a] = acc;
                 }
-                S4[a] = quad_sum(p0 + p1);
+                const float *nb = N + 4 * g2 * kLs + 4 * g2; // N[4 g2 + a][4 g2 + b] at nb[a * kLs + b]
+                const float n10 = nb[kLs], n20 = nb[2 * kLs], n21 = nb[2 * kLs + 1];
+                const float n30 = nb[3 * kLs], n31 = nb[3 * kLs + 1], n32 = nb[3 * kLs + 2];
+                const int r0 = 4 * g2;
+                const float x0 = (r0 == jc ? 1.0f : 0.0f) - S4[0];
+                const float x1 = (r0 + 1 == jc ? 1.0f : 0.0f) - S4[1] - n10 * x0;
+                const float x2 = (r0 + 2 == jc ? 1.0f : 0.0f) - S4[2] - n20 * x0 - n21 * x1;
+                const float x3 = (r0 + 3 == jc ? 1.0f : 0.0f) - S4[3] - n30 * x0 - n31 * x1 - n32 * x2;
+                if (gq == g2) D = f32x4{x0, x1, x2, x3};
             }
-            // L[i + a][i + b] sits at Lp[(i + a) * 64 + b * 16 + s0]
-            const float *lb = Lp + i * kC + s0;
-            const float l10 = lb[kC], l20 = lb[2 * kC], l21 = lb[2 * kC + 16];
-            const float l30 = lb[3 * kC], l31 = lb[3 * kC + 16], l32 = lb[3 * kC + 32];
-            const float x0 = (i == j ? 1.0f : 0.0f) - S4[0];
-            const float x1 = (i + 1 == j ? 1.0f : 0.0f) - S4[1] - l10 * x0;
-            const float x2 = (i + 2 == j ? 1.0f : 0.0f) - S4[2] - l20 * x0 - l21 * x1;
-            const float x3 = (i + 3 == j ? 1.0f : 0.0f) - S4[3] - l30 * x0 - l31 * x1 - l32 * x2;
-            t[s0] = q == 0 ? x0 : q == 1 ? x1 : q == 2 ? x2 : x3;
+            blk_store(Lp, wave, wave, D, lane); // only this wave read L_ww
         }
-        __syncthreads(); // every wave is done reading L: T takes its place
-#pragma unroll
-        for (int s = 0; s < 16; ++s) Ts[(4 * s + q) * kRowC + j] = f32_to_bf16(t[s]);
+        __syncthreads();
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 Ta = z, Tb = z; // this wave's off-diagonal blocks
+        if (wave < 3) {
+            // T_{w+1, w} = -D_{w+1} (L_{w+1, w} D_w)
+            const f32x4 x = blk_mm(blk(wave + 1, wave), blk(wave, wave), z, lane);
+            Ta = -blk_mm_reg(blk(wave + 1, wave + 1), x, z, lane);
+            blk_store(Lp, wave, wave + 1, Ta, lane);
+        } else {
+            Tb = blk_mm(blk(3, 0), blk(0, 0), z, lane); // L_30 D_0, completed in stages 2 and 3
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // T_20 = -D_2 (L_20 D_0 + L_21 T_10)
+            const f32x4 x = blk_mm(blk(2, 1), blk(0, 1), blk_mm(blk(2, 0), blk(0, 0), z, lane), lane);
+            Tb = -blk_mm_reg(blk(2, 2), x, z, lane);
+            blk_store(Lp, 0, 2, Tb, lane);
+        } else if (wave == 1) {
+            // T_31 = -D_3 (L_31 D_1 + L_32 T_21)
+            const f32x4 x = blk_mm(blk(3, 2), blk(1, 2), blk_mm(blk(3, 1), blk(1, 1), z, lane), lane);
+            Tb = -blk_mm_reg(blk(3, 3), x, z, lane);
+        } else if (wave == 3) {
+            Tb = blk_mm(blk(3, 1), blk(0, 1), Tb, lane); // + L_31 T_10
+        }
+        __syncthreads();
+        if (wave == 3) Ta = -blk_mm_reg(blk(3, 3), blk_mm(blk(3, 2), blk(0, 2), Tb, lane), z, lane); // T_30
+        __syncthreads(); // no wave reads L or the fp32 blocks any more: T (bf16) takes their place
+        // blocks as bf16: D_w on the diagonal, the off-diagonal blocks of each wave, zeros above
+        blk_store_bf16(Ts, wave, wave, D, lane);
+        if (wave < 3) blk_store_bf16(Ts, wave + 1, wave, Ta, lane);
+        if (wave == 0) blk_store_bf16(Ts, 2, 0, Tb, lane);
+        if (wave == 1) blk_store_bf16(Ts, 3, 1, Tb, lane);
+        if (wave == 3) blk_store_bf16(Ts, 3, 0, Ta, lane);
+        // the six zero blocks above the diagonal, two per wave 0-2
+        if (wave == 0) { blk_store_bf16(Ts, 0, 1, z, lane); blk_store_bf16(Ts, 0, 2, z, lane); }
+        if (wave == 1) { blk_store_bf16(Ts, 0, 3, z, lane); blk_store_bf16(Ts, 1, 2, z, lane); }
+        if (wave == 2) { blk_store_bf16(Ts, 1, 3, z, lane); blk_store_bf16(Ts, 2, 3, z, lane); }
     }
     __syncthreads();
 
