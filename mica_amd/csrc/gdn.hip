@@ -522,9 +522,14 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
     const int dvw = blockIdx.z * ((WAVES / 4) * 32 * DVT) + hf * 32 * DVT;
     const long bh = (long)b * p.HV + h;
     const bool w_rows = wr < 2;                    // X rows from W (v_new); otherwise from Q (output)
-    const bool needs_q = wave < 4 || wave >= 6;    // Q tile for P^T (waves 0-3) and/or X (wr = 2, 3)
-    const int mq = wave < 4 ? (wave & 1) : (wave - 6); // that Q tile
-    const int mk = wave >> 1;                      // K tile of this wave's P^T tile (waves 0-3)
+    const bool needs_q = !w_rows;                  // Q tile for X (wr = 2, 3) and the P^T tile
+    const int mq = wr - 2;                         // that Q tile (query rows 32 mq ..)
+    // P^T tiles (key tile mk, query tile mq) on the Q-row waves, which have no v_new to form before
+    // barrier (B): wave 2 (0, 0), wave 3 (0, 1), wave 7 (1, 1); with 4 waves, wave 3 takes (0, 1) and
+    // (1, 1).  Tile (1, 0) -- keys 32-63 against queries 0-31 -- is wholly masked: its zeros are
+    // written once, before the first chunk.
+    const bool p_tile = wave == 2 || wave == 3 || wave == 7;
+    const int mk_lo = wave == 7 ? 1 : 0, mk_hi = (wave == 7 || (WAVES == 4 && wave == 3)) ? 1 : 0;
 
     // state: S[dk = 32 wr + acc_row][dv = 64 hf + 32 dvt + l32]
     f32x16 S[DVT];
@@ -589,6 +594,11 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
     load_k(0);
     if (needs_q) load_q(0);
     if (w_rows) { load_w(0); load_u(0); }
+    // the masked P tile: P[i][j] = 0 for queries i < 32 and keys j >= 32 (read after barrier (B))
+    for (int e = tid; e < 32 * 4; e += kThr) {
+        const int i = e >> 2, j = 32 + (e & 3) * 8;
+        *(u32x4 *)(Ps + i * kRowC + j) = u32x4{0u, 0u, 0u, 0u};
+    }
 
     for (int c = 0; c < p.NT; ++c) {
         const int tbase = c * kC;
@@ -614,7 +624,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
         }
         if (w_rows && more) load_w(c + 1);
         // ---- P^T tile (K rows mk) x (Q rows mq): P[i][j] = (q_i . k_j) exp(G_i - G_j), j <= i ----
-        if (wave < 4) {
+        if (p_tile) for (int mk = mk_lo; mk <= mk_hi; ++mk) {
             f32x16 pt = {};
 #pragma unroll
             for (int s = 0; s < 8; ++s) pt = mfma(ld_frag(Ks + (mk * 32 + l32) * kRowP + s * 16 + kh), qf[s], pt);
@@ -674,6 +684,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
             f32x16 O[DVT] = {};
 #pragma unroll
             for (int s = 0; s < kC / 16; ++s) {
+                if (mo == 0 && s >= 2) break; // keys 32-63 are masked for queries 0-31
                 const bf16x8 a = ld_frag(Ps + (mo * 32 + l32) * kRowC + s * 16 + kh);
 #pragma unroll
                 for (int dvt = 0; dvt < DVT; ++dvt)
