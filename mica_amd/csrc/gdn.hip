@@ -500,7 +500,7 @@ constexpr int kScanVd = kScanVn + kDv * kRowC * 2;
 constexpr int kScanP = kScanVd + kDv * kRowC * 2;
 constexpr int kScanO = kScanP + kC * kRowC * 2;
 constexpr int kScanG = kScanO + 4 * 32 * kRowC * 2;
-constexpr int kScanSmem = kScanG + 2 * kC * 4;
+constexpr int kScanSmem = kScanG + 2 * 3 * kC * 4;  // per buffer: G, exp(G_63 - G), exp(G)
 static_assert(kScanSmem <= 160 * 1024, "scan LDS");
 
 template <int DVT, int WAVES>
@@ -604,13 +604,21 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
         const int tbase = c * kC;
         const bool more = c + 1 < p.NT;
         uint16_t *Ks = (uint16_t *)(smem + kScanK) + (c & 1) * kC * kRowP;
-        float *Gs = (float *)(smem + kScanG) + (c & 1) * kC;
+        float *Gs = (float *)(smem + kScanG) + (c & 1) * 3 * kC;
+        float *Ed = Gs + kC;      // exp(G_63 - G_m): the decay of v_new row m into the state update
+        float *Eg = Ed + kC;      // exp(G_i): the decay of the state into output row i
 #pragma unroll
         for (int i = 0; i < kPieces; ++i) {
             const int piece = tid + i * kThr;
             *(u32x4 *)(Ks + (piece >> 4) * kRowP + (piece & 15) * 8) = kreg[i];
         }
-        if (tid < kC) Gs[tid] = gn;
+        if (tid < kC) {
+            // each token's two decays once per chunk, for every wave that applies them
+            const float glast = __shfl(gn, kC - 1, 64);
+            Gs[tid] = gn;
+            Ed[tid] = fexp(glast - gn);
+            Eg[tid] = fexp(gn);
+        }
         __syncthreads(); // (A) K rows, G and the state S^T visible to every wave
 
         // ---- X = [W; Q] S for this wave's 32 rows and dv half ----
@@ -651,7 +659,6 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
         if (needs_q && more) load_q(c + 1);
         // ---- v_new = U - W S (wr = 0, 1), stored transposed, plain and decayed by exp(G_63 - G_m) ----
         if (w_rows) {
-            const float glast = Gs[kC - 1];
 #pragma unroll
             for (int dvt = 0; dvt < DVT; ++dvt) {
                 const int dv = dvw + dvt * 32 + l32;
@@ -664,9 +671,8 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
                     u32x2 a2, d2;
                     a2[0] = pack_bf16x2(vn[0], vn[1]);
                     a2[1] = pack_bf16x2(vn[2], vn[3]);
-                    const float4 gm = *(const float4 *)(Gs + m0);
-                    const float dec[4] = {vn[0] * fexp(glast - gm.x), vn[1] * fexp(glast - gm.y),
-                                          vn[2] * fexp(glast - gm.z), vn[3] * fexp(glast - gm.w)};
+                    const float4 ed = *(const float4 *)(Ed + m0);
+                    const float dec[4] = {vn[0] * ed.x, vn[1] * ed.y, vn[2] * ed.z, vn[3] * ed.w};
                     d2[0] = pack_bf16x2(dec[0], dec[1]);
                     d2[1] = pack_bf16x2(dec[2], dec[3]);
                     *(u32x2 *)(Vn + dv * kRowC + m0) = a2;
@@ -690,16 +696,16 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
                 for (int dvt = 0; dvt < DVT; ++dvt)
                     O[dvt] = mfma(a, ld_frag(Vn + (dvw + dvt * 32 + l32) * kRowC + s * 16 + kh), O[dvt]);
             }
-            uint16_t *ost = (uint16_t *)(smem + kScanO) + (hf * 2 + mo) * 32 * kRowC;
-            float eg[16]; // exp(G) of this lane's 16 output rows, read and computed before the stores
+            float eg[16]; // exp(G) of this lane's 16 output rows, read before the stores
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const float4 g4 = *(const float4 *)(Gs + mo * 32 + 8 * r4 + 4 * (lane >> 5));
-                eg[4 * r4] = fexp(g4.x);
-                eg[4 * r4 + 1] = fexp(g4.y);
-                eg[4 * r4 + 2] = fexp(g4.z);
-                eg[4 * r4 + 3] = fexp(g4.w);
+                const float4 g4 = *(const float4 *)(Eg + mo * 32 + 8 * r4 + 4 * (lane >> 5));
+                eg[4 * r4] = g4.x;
+                eg[4 * r4 + 1] = g4.y;
+                eg[4 * r4 + 2] = g4.z;
+                eg[4 * r4 + 3] = g4.w;
             }
+            uint16_t *ost = (uint16_t *)(smem + kScanO) + (hf * 2 + mo) * 32 * kRowC;
 #pragma unroll
             for (int dvt = 0; dvt < DVT; ++dvt)
 #pragma unroll
@@ -720,7 +726,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
         }
         // ---- S <- exp(G_63) S + K^T (decayed v_new) ----
         {
-            const float dl = fexp(Gs[kC - 1]);
+            const float dl = Eg[kC - 1];
 #pragma unroll
             for (int dvt = 0; dvt < DVT; ++dvt) S[dvt] *= dl;
             const int dk = wr * 32 + l32;
