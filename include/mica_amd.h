@@ -284,6 +284,27 @@ int mica_attention_fwd_kvlen(const void *q, long long sbq, long long shq, long l
  * 32 ceil(Sq / 32) rows of 1032 bytes (O, m, l); -1 for an invalid argument */
 long long mica_attention_split_workspace_bytes(int B, int Sq, int Sk, int HQ, int HK, int key_splits);
 
+/*
+ * mica_attention_fwd_kvlen (kv_len may be NULL) over keys whose first Pk (a multiple of 32, at most
+ * Sk - Sq) are one prefix shared by every sequence: kp / vp hold the prefix's rows (head j of row t at
+ * ptr + j sh + t ld), k / v each sequence's Sk - Pk keys after it.  The result equals
+ * mica_attention_fwd_kvlen on the concatenated keys bit for bit (same key tiles, same order); the
+ * prefix is neither copied per sequence nor transposed more than once.  Serves several continuations
+ * of one cached prefix (the reference's prefix reuse, prefill_engine.py:283-339 with a recorded
+ * state) without expanding it to every row of the batch.  workspace:
+ * mica_attention_prefix_workspace_bytes(B, Sq, Sk, Pk, HQ, HK, key_splits) bytes, 16-byte aligned.
+ */
+int mica_attention_fwd_prefix(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
+                              long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv,
+                              const void *kp, long long shkp, long long ldkp, const void *vp, long long shvp,
+                              long long ldvp, int Pk, void *o, long long sbo, long long sho, long long ldo, int B,
+                              int Sq, int Sk, int HQ, int HK, int head_dim, float scale, int causal, int key_splits,
+                              const int *kv_len, void *workspace, long long workspace_bytes, mica_stream_t stream);
+
+/* bytes of mica_attention_fwd_prefix workspace: HK x Pk / 32 prefix V^T images of 16 KiB, the
+ * sequences' own images for Sk - Pk keys, the split states as above; -1 for an invalid argument */
+long long mica_attention_prefix_workspace_bytes(int B, int Sq, int Sk, int Pk, int HQ, int HK, int key_splits);
+
 /* ---- gated delta net (GDN) token mixer ------------------------------------------------------- */
 
 /*

@@ -33,7 +33,8 @@ def key_splits_for(B: int, Sq: int, Sk: int, HK: int, cus: int = 256, per_cu: in
     return int(max(1, min(want, most, MAX_KEY_SPLITS)))
 
 
-def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits: int = 1, kv_len=None):
+def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits: int = 1, kv_len=None,
+                  prefix=None):
     """Launch the kernel on q [B, Sq, HQ, 256] / k, v [B, Sk, HK, 256] ('bshd') or q [B, HQ, Sq, 256] /
     k, v [B, HK, Sk, 256] ('bhsd') views with unit feature stride.  Returns o in q's layout
     (contiguous [B, Sq, HQ, 256] memory), or raises ValueError on an unsupported input.
@@ -44,7 +45,12 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
 
     kv_len (int32 [B] on the device, optional): sequence b's key count, clamped to Sq .. Sk; its queries
     are then the last Sq positions of its first kv_len[b] keys (mica_attention_fwd_kvlen), e.g. the last
-    real position of each request of a batch padded to a common width."""
+    real position of each request of a batch padded to a common width.
+
+    prefix ((kp, vp), optional, 'bshd' only): P keys shared by every sequence, [P, HK, 256] or
+    [1, P, HK, 256] views, P a multiple of 32; k / v then hold each sequence's keys after them and the
+    attention runs over the P + Sk keys as if concatenated (mica_attention_fwd_prefix, bit-identical to
+    the concatenated call) without expanding the prefix to the batch."""
     for t in (q, k, v):
         if not t.is_cuda:
             raise ValueError("mica_amd attention runs on the GPU only (got a CPU tensor)")
@@ -61,22 +67,43 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
         st = lambda t: (t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
     if k.shape != v.shape or k.shape[0] != B or HQ != GROUP * HK or Sk < Sq:
         raise ValueError("q / k / v shapes do not match (4 query heads per key/value head, Sk >= Sq)")
+    P = 0
+    if prefix is not None:
+        kp, vp = (t[0] if t.dim() == 4 else t for t in prefix)
+        if q_layout != "bshd":
+            raise ValueError("a key prefix needs the 'bshd' layout")
+        for t in (kp, vp):
+            if (not t.is_cuda or t.device != dev or t.dim() != 3 or t.dtype != torch.bfloat16
+                    or t.shape[1:] != (HK, HEAD_DIM) or t.stride(2) != 1):
+                raise ValueError("prefix keys / values must be bf16 [P, HK, 256] views on q's device")
+        P = kp.shape[0]
+        if vp.shape != kp.shape or P % 32:
+            raise ValueError("the prefix's keys and values must have one length, a multiple of 32")
+        Sk += P
     key_splits = int(key_splits)
     if not 1 <= key_splits <= MAX_KEY_SPLITS:
         raise ValueError(f"key_splits must be 1 .. {MAX_KEY_SPLITS}")
     o = torch.empty((B, Sq, HQ, HEAD_DIM), dtype=torch.bfloat16, device=dev)
     L = _lib.load()
-    nbytes = int(L.mica_attention_split_workspace_bytes(B, Sq, Sk, HQ, HK, key_splits))
+    nbytes = int(L.mica_attention_prefix_workspace_bytes(B, Sq, Sk, P, HQ, HK, key_splits))
     if nbytes < 0:
         raise ValueError("attention: invalid sizes")
     ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=dev)
-    if not _aligned(q, k, v, o, ws):
+    if not _aligned(q, k, v, o, ws, *((kp, vp) if P else ())):
         raise ValueError("attention operands must be 16-byte aligned")
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else float(scale)
     o_st = (o.stride(0), o.stride(2), o.stride(1))
     if kv_len is not None:
         if kv_len.dtype != torch.int32 or kv_len.device != dev or kv_len.numel() != B or not kv_len.is_contiguous():
             raise ValueError("kv_len must be a contiguous int32 [B] tensor on q's device")
+    if P:
+        rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd_prefix(
+            q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v),
+            kp.data_ptr(), kp.stride(1), kp.stride(0), vp.data_ptr(), vp.stride(1), vp.stride(0), P,
+            o.data_ptr(), *o_st, B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, key_splits,
+            None if kv_len is None else kv_len.data_ptr(), ws.data_ptr(), nbytes, _stream(dev))),
+            "mica_attention_fwd_prefix")
+    elif kv_len is not None:
         rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd_kvlen(
             q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), o.data_ptr(), *o_st,
             B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, key_splits, kv_len.data_ptr(), ws.data_ptr(), nbytes,
@@ -96,8 +123,9 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
     return o if q_layout == "bshd" else o.transpose(1, 2)
 
 
-def causal_gqa_attention(q, k, v, scale: float | None = None, key_splits: int = 1, kv_len=None):
+def causal_gqa_attention(q, k, v, scale: float | None = None, key_splits: int = 1, kv_len=None, prefix=None):
     """softmax(scale q k^T, causal) v per sequence and head on [B, S, heads, 256] views (e.g. of the
     fused QKV output); query head h reads key/value head h // 4.  Returns o [B, S, HQ, 256] bf16.
-    With Sk > Sq the queries are the last Sq positions; key_splits and kv_len as in attention_fwd."""
-    return attention_fwd(q, k, v, "bshd", scale, key_splits, kv_len)
+    With Sk > Sq the queries are the last Sq positions; key_splits, kv_len and prefix as in
+    attention_fwd."""
+    return attention_fwd(q, k, v, "bshd", scale, key_splits, kv_len, prefix)

@@ -99,6 +99,12 @@ struct FaParams {
     int nsplit, sq_pad;
     float *part_o, *part_m, *part_l;
     const int *kv_len;                          // [B] per-sequence key counts, or null: Sk for every one
+    // a prefix shared by every sequence: keys 0 .. 32 ntiles_p - 1 are row t of kp (head h at
+    // kp + h shkp + t ldkp) with their V^T images at vtp [HK][ntiles_p][256][32]; keys from there on are
+    // rows t - 32 ntiles_p of k / vt (vt [B][HK][ntiles_k - ntiles_p][256][32]).  ntiles_p = 0: no prefix.
+    const uint16_t *kp; long long shkp, ldkp;
+    const uint16_t *vtp;
+    int ntiles_p;
 };
 
 // ---- V -> V^T tile images: one workgroup per (tile, sequence x head); thread = 8 dims x 4 keys ----
@@ -146,11 +152,17 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
     const int first = SPLIT ? (int)((long long)split * (last + 1) / p.nsplit) : 0;
     const int last_own = SPLIT ? (int)((long long)(split + 1) * (last + 1) / p.nsplit) - 1 : last;
 
-    // operand buffers: K rows of (b, hk) (rows >= Sk read as zeros), the V^T images of (b, hk)
+    // operand buffers: K rows of (b, hk) past the prefix (rows past the keys read as zeros), their V^T
+    // images, and the shared prefix's K rows and V^T images of head hk
+    const int ntp = p.ntiles_p, ntn = p.ntiles_k - ntp, pk = ntp * kBK;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.k + b * p.sbk + hk * p.shk), 0, (int)((long long)p.Sk * p.ldk * 2), kBufferFlags);
+        (void *)(p.k + b * p.sbk + hk * p.shk), 0, (int)((long long)(p.Sk - pk) * p.ldk * 2), kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.vt + ((long long)(b * p.HK + hk) * p.ntiles_k) * kD * kBK), 0, p.ntiles_k * kVBytes, kBufferFlags);
+        (void *)(p.vt + ((long long)(b * p.HK + hk) * ntn) * kD * kBK), 0, ntn * kVBytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rkp = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(ntp ? p.kp + hk * p.shkp : p.k), 0, (int)((long long)pk * p.ldkp * 2), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rvp = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(ntp ? p.vtp + ((long long)hk * ntp) * kD * kBK : p.vt), 0, ntp * kVBytes, kBufferFlags);
     // DMA of key tile j into stage ST.  K: 1 KB block (wave, i) = key rows 2 (4 wave + i) + lane / 32;
     // the lane writes physical chunk l % 32 of its row, which holds logical chunk (l % 32) ^ row.  V^T:
     // block (wave, i) of the tile image.  The per-lane offsets are recomputed at every call from an
@@ -162,16 +174,21 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         int ln = lane;
         __asm__ volatile("" : "+v"(ln));
         const int hi_ = ln >> 5, l32_ = ln & 31;
+        // the tile's segment: the shared prefix (tiles below ntp) or this sequence's own keys
+        const bool pre = j < ntp;
+        const __amdgpu_buffer_rsrc_t rks = pre ? rkp : rk, rvs = pre ? rvp : rv;
+        const int jj = pre ? j : j - ntp;
+        const long long ld = pre ? p.ldkp : p.ldk;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = (wave * 4 + i) * 2 + hi_;
-            const int ko = (int)((long long)(j * kBK + row) * p.ldk * 2 + ((l32_ ^ row) << 4));
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(ks + (wave * 4 + i) * 1024), 16, ko, 0, 0, 0);
+            const int ko = (int)((long long)(jj * kBK + row) * ld * 2 + ((l32_ ^ row) << 4));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rks, (lds_void *)(ks + (wave * 4 + i) * 1024), 16, ko, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16,
-                                                     ln * 16, j * kVBytes + (wave * 4 + i) * 1024, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rvs, (lds_void *)(ks + kKBytes + (wave * 4 + i) * 1024), 16,
+                                                     ln * 16, jj * kVBytes + (wave * 4 + i) * 1024, 0, 0);
     };
 
     // Q fragments (B operand of S^T): lane holds query q0 + l % 32, dims 16 s + 8 (l / 32) .. + 7
@@ -358,59 +375,91 @@ extern "C" long long mica_attention_workspace_bytes(int B, int Sk, int HK) {
     return (long long)B * HK * ((Sk + kBK - 1) / kBK) * kVBytes;
 }
 
+extern "C" long long mica_attention_prefix_workspace_bytes(int B, int Sq, int Sk, int Pk, int HQ, int HK, int key_splits) {
+    if (B < 0 || Sq < 0 || Sk < 0 || Pk < 0 || Pk % kBK || Pk > Sk || HQ <= 0 || HK <= 0 || key_splits < 1 ||
+        key_splits > kMaxKeySplits)
+        return -1;
+    // the prefix's V^T images (one set for every sequence), each sequence's own, the split states
+    long long n = (long long)HK * (Pk / kBK) * kVBytes + mica_attention_workspace_bytes(B, Sk - Pk, HK);
+    if (key_splits > 1) n += (long long)B * HQ * key_splits * ((Sq + kBQ - 1) / kBQ) * kBQ * (kD * 4 + 8);
+    return n;
+}
+
 extern "C" long long mica_attention_split_workspace_bytes(int B, int Sq, int Sk, int HQ, int HK, int key_splits) {
-    if (B < 0 || Sq < 0 || Sk < 0 || HQ <= 0 || HK <= 0 || key_splits < 1 || key_splits > kMaxKeySplits) return -1;
-    const long long vt = mica_attention_workspace_bytes(B, Sk, HK);
-    if (key_splits == 1) return vt;
-    const long long rows = (long long)B * HQ * key_splits * ((Sq + kBQ - 1) / kBQ) * kBQ;
-    return vt + rows * (kD * 4 + 8);
+    return mica_attention_prefix_workspace_bytes(B, Sq, Sk, 0, HQ, HK, key_splits);
 }
 
 namespace {
 
+// kp / vp (optional, Pk > 0 keys, a multiple of 32): a key prefix shared by every sequence, read in
+// place of each sequence's first Pk keys; k / v then hold each sequence's Sk - Pk keys after it.
 int attention_launch(const void *q, long long sbq, long long shq, long long ldq, const void *k, long long sbk,
-                     long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv, void *o,
-                     long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ, int HK, int head_dim,
-                     float scale, int causal, int key_splits, const int *kv_len, void *workspace,
+                     long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv,
+                     const void *kp, long long shkp, long long ldkp, const void *vp, long long shvp, long long ldvp,
+                     int Pk, void *o, long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
+                     int HK, int head_dim, float scale, int causal, int key_splits, const int *kv_len, void *workspace,
                      long long workspace_bytes, mica_stream_t stream) {
     if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || Sq < 0 || Sk < Sq) return MICA_MISS_SHAPE;
+    if (Pk < 0 || Pk % kBK || Pk > Sk - Sq) return MICA_MISS_SHAPE;
     if (!causal || key_splits < 1 || key_splits > kMaxKeySplits) return MICA_MISS_ARG;
     if (B == 0 || Sq == 0) return 0;
     if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || workspace == nullptr) return MICA_MISS_ARG;
-    const long long st[12] = {sbq, shq, ldq, sbk, shk, ldk, sbv, shv, ldv, sbo, sho, ldo};
+    if (Pk > 0 && (kp == nullptr || vp == nullptr)) return MICA_MISS_ARG;
+    const long long st[16] = {sbq, shq, ldq, sbk, shk, ldk, sbv, shv, ldv, sbo, sho, ldo, shkp, ldkp, shvp, ldvp};
     for (long long x : st)
         if (x < 0 || x % 8) return MICA_MISS_STRIDE;
     if (ldq < kD && Sq > 1) return MICA_MISS_STRIDE;
     if (!mica_aligned16(q) || !mica_aligned16(k) || !mica_aligned16(v) || !mica_aligned16(o) ||
-        !mica_aligned16(workspace))
+        !mica_aligned16(workspace) || (Pk > 0 && (!mica_aligned16(kp) || !mica_aligned16(vp))))
         return MICA_MISS_ALIGN;
-    const int ntiles_q = (Sq + kBQ - 1) / kBQ, ntiles_k = (Sk + kBK - 1) / kBK;
+    const int ntiles_q = (Sq + kBQ - 1) / kBQ, ntiles_k = (Sk + kBK - 1) / kBK, ntiles_p = Pk / kBK;
     if ((long long)ntiles_k * kBK * ldk * 2 >= (1LL << 31) || (long long)ntiles_k * kVBytes >= (1LL << 31) ||
-        (long long)ntiles_q * key_splits > 65535 || B > 65535)
+        (long long)Pk * ldkp * 2 >= (1LL << 31) || (long long)ntiles_q * key_splits > 65535 || B > 65535)
         return MICA_MISS_RANGE;
-    if (workspace_bytes < mica_attention_split_workspace_bytes(B, Sq, Sk, HQ, HK, key_splits)) return MICA_MISS_ARG;
+    if (workspace_bytes < mica_attention_prefix_workspace_bytes(B, Sq, Sk, Pk, HQ, HK, key_splits)) return MICA_MISS_ARG;
     FaParams p{};
     p.q = (const uint16_t *)q; p.sbq = sbq; p.shq = shq; p.ldq = ldq;
     p.k = (const uint16_t *)k; p.sbk = sbk; p.shk = shk; p.ldk = ldk;
     p.v = (const uint16_t *)v; p.sbv = sbv; p.shv = shv; p.ldv = ldv;
-    p.vt = (uint16_t *)workspace; p.o = (uint16_t *)o; p.sbo = sbo; p.sho = sho; p.ldo = ldo;
+    p.o = (uint16_t *)o; p.sbo = sbo; p.sho = sho; p.ldo = ldo;
     p.B = B; p.Sq = Sq; p.Sk = Sk; p.HQ = HQ; p.HK = HK; p.ntiles_q = ntiles_q; p.ntiles_k = ntiles_k;
     p.scale_log2 = scale * 1.44269504088896341f;
     p.nsplit = key_splits;
     p.sq_pad = ntiles_q * kBQ;
     p.kv_len = kv_len;
+    // workspace: the prefix's V^T images, then each sequence's, then the split states
+    char *ws = (char *)workspace;
+    p.kp = (const uint16_t *)kp; p.shkp = shkp; p.ldkp = ldkp;
+    p.vtp = (uint16_t *)ws;
+    p.ntiles_p = ntiles_p;
+    ws += (long long)HK * ntiles_p * kVBytes;
+    p.vt = (uint16_t *)ws;
+    ws += mica_attention_workspace_bytes(B, Sk - Pk, HK);
     if (key_splits > 1) {
-        // partial states after the V^T images: O rows (1 KiB each), then m, then l
+        // partial states: O rows (1 KiB each), then m, then l
         const long long rows = (long long)B * HQ * key_splits * p.sq_pad;
-        char *base = (char *)workspace + mica_attention_workspace_bytes(B, Sk, HK);
-        p.part_o = (float *)base;
-        p.part_m = (float *)(base + rows * kD * 4);
+        p.part_o = (float *)ws;
+        p.part_m = (float *)(ws + rows * kD * 4);
         p.part_l = p.part_m + rows;
     }
     hipStream_t stream_ = (hipStream_t)stream;
-    hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles_k, B * HK), dim3(256), 0, stream_, p);
+    // V^T images: each sequence's keys past the prefix, and the prefix's once (as one sequence)
+    FaParams pv = p;
+    pv.Sk = Sk - Pk;
+    pv.ntiles_k = ntiles_k - ntiles_p;
+    hipLaunchKernelGGL(v_transpose_kernel, dim3(pv.ntiles_k, B * HK), dim3(256), 0, stream_, pv);
     int rc = mica_err(hipGetLastError());
     if (rc) return rc;
+    if (ntiles_p > 0) {
+        FaParams pp = p;
+        pp.v = (const uint16_t *)vp; pp.sbv = 0; pp.shv = shvp; pp.ldv = ldvp;
+        pp.Sk = Pk;
+        pp.ntiles_k = ntiles_p;
+        pp.vt = (uint16_t *)p.vtp;  // the prefix images are written here, read-only in the attention kernel
+        hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles_p, HK), dim3(256), 0, stream_, pp);
+        rc = mica_err(hipGetLastError());
+        if (rc) return rc;
+    }
     if (key_splits == 1) {
         hipLaunchKernelGGL(fa_fwd_kernel<false>, dim3(HK, B, ntiles_q), dim3(kFaThreads), 0, stream_, p);
         return mica_err(hipGetLastError());
@@ -431,8 +480,9 @@ extern "C" int mica_attention_fwd(const void *q, long long sbq, long long shq, l
                                   long long ldv, void *o, long long sbo, long long sho, long long ldo, int B, int Sq,
                                   int Sk, int HQ, int HK, int head_dim, float scale, int causal, void *workspace,
                                   long long workspace_bytes, mica_stream_t stream) {
-    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
-                            head_dim, scale, causal, 1, nullptr, workspace, workspace_bytes, stream);
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, nullptr, 0, 0, nullptr, 0, 0, 0, o,
+                            sbo, sho, ldo, B, Sq, Sk, HQ, HK, head_dim, scale, causal, 1, nullptr, workspace,
+                            workspace_bytes, stream);
 }
 
 extern "C" int mica_attention_fwd_split(const void *q, long long sbq, long long shq, long long ldq, const void *k,
@@ -441,8 +491,9 @@ extern "C" int mica_attention_fwd_split(const void *q, long long sbq, long long 
                                         long long ldo, int B, int Sq, int Sk, int HQ, int HK, int head_dim, float scale,
                                         int causal, int key_splits, void *workspace, long long workspace_bytes,
                                         mica_stream_t stream) {
-    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
-                            head_dim, scale, causal, key_splits, nullptr, workspace, workspace_bytes, stream);
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, nullptr, 0, 0, nullptr, 0, 0, 0, o,
+                            sbo, sho, ldo, B, Sq, Sk, HQ, HK, head_dim, scale, causal, key_splits, nullptr, workspace,
+                            workspace_bytes, stream);
 }
 
 extern "C" int mica_attention_fwd_kvlen(const void *q, long long sbq, long long shq, long long ldq, const void *k,
@@ -452,6 +503,20 @@ extern "C" int mica_attention_fwd_kvlen(const void *q, long long sbq, long long 
                                         int causal, int key_splits, const int *kv_len, void *workspace,
                                         long long workspace_bytes, mica_stream_t stream) {
     if (kv_len == nullptr) return MICA_MISS_ARG;
-    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, o, sbo, sho, ldo, B, Sq, Sk, HQ, HK,
-                            head_dim, scale, causal, key_splits, kv_len, workspace, workspace_bytes, stream);
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, nullptr, 0, 0, nullptr, 0, 0, 0, o,
+                            sbo, sho, ldo, B, Sq, Sk, HQ, HK, head_dim, scale, causal, key_splits, kv_len, workspace,
+                            workspace_bytes, stream);
+}
+
+extern "C" int mica_attention_fwd_prefix(const void *q, long long sbq, long long shq, long long ldq, const void *k,
+                                         long long sbk, long long shk, long long ldk, const void *v, long long sbv,
+                                         long long shv, long long ldv, const void *kp, long long shkp, long long ldkp,
+                                         const void *vp, long long shvp, long long ldvp, int Pk, void *o,
+                                         long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
+                                         int HK, int head_dim, float scale, int causal, int key_splits,
+                                         const int *kv_len, void *workspace, long long workspace_bytes,
+                                         mica_stream_t stream) {
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, kp, shkp, ldkp, vp, shvp, ldvp, Pk,
+                            o, sbo, sho, ldo, B, Sq, Sk, HQ, HK, head_dim, scale, causal, key_splits, kv_len,
+                            workspace, workspace_bytes, stream);
 }

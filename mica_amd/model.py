@@ -279,15 +279,20 @@ class W8A8Stack:
                      norms)
         q, _, k, v = qkv.view(B, S, hq + ng + 2 * hk, d).split((hq, ng, hk, hk), dim=2)
         state = (k.contiguous(), v.contiguous()) if keep else None
-        if P:
-            k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
-            v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
         if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
             ks = 1
             if P and self.split_keys:
                 ks = key_splits_for(B, S, P + S, hk, cus=_cu_count(qkv.device))
-            a = causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), key_splits=ks).view(B * S, hq * d)
+            # a tile-aligned prefix's keys are read in place, shared by the batch's rows
+            pre = past if P and P % 32 == 0 else None
+            if P and pre is None:
+                k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
+                v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
+            a = causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), key_splits=ks, prefix=pre).view(B * S, hq * d)
         else:
+            if P:
+                k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
+                v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
             a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
                                                is_causal=P == 0, attn_mask=None if P == 0 else self._mask(S, P, q.device),
                                                scale=1.0 / math.sqrt(d), enable_gqa=True)
@@ -342,13 +347,17 @@ class W8A8Stack:
         qpos = (rows - torch.arange(B, device=rows.device, dtype=torch.int32) * S + P).to(torch.int32)
         self._rotate(qr, (0, hq), (0, 0), cos, sin, pos=qpos, norms=norms)
         k, v = kv.view(B, S, 2 * hk, d).split((hk, hk), dim=2)
-        if P:
-            k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
-            v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
         q = qr[:, :hq * d].view(B, 1, hq, d)
         kv_len = (qpos + 1).to(torch.int32)
         if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
-            return causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), kv_len=kv_len).view(B, hq * d)
+            pre = past if P and P % 32 == 0 else None
+            if P and pre is None:
+                k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
+                v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
+            return causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), kv_len=kv_len, prefix=pre).view(B, hq * d)
+        if P:
+            k = torch.cat((past[0].expand(B, -1, -1, -1), k), dim=1)
+            v = torch.cat((past[1].expand(B, -1, -1, -1), v), dim=1)
         seen = torch.arange(P + S, device=q.device)[None, :] < kv_len[:, None]
         a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
                                            attn_mask=seen[:, None, None, :], scale=1.0 / math.sqrt(d),

@@ -870,6 +870,45 @@ def test_attention_split_keys_matches_oracle(gpu, B, Sq, Sk, HK, splits):
     assert w_split <= 2.0 * w_one + 1e-3
 
 
+@pytest.mark.parametrize("B,P,Sn,Sq,HK,splits,use_len", [
+    (3, 64, 96, 96, 1, 1, False),     # continuations of one prefix: every new row a query
+    (2, 256, 40, 40, 2, 1, False),    # ragged last tile of the new keys
+    (4, 1024, 64, 64, 1, 5, False),   # split keys over the prefix and the new keys
+    (3, 128, 70, 1, 1, 1, True),      # the last-only pass: one query per sequence at kv_len
+    (2, 32, 33, 1, 1, 3, True),       # one prefix tile, split, per-sequence key counts
+])
+def test_attention_shared_prefix_equals_concatenated_keys(gpu, B, P, Sn, Sq, HK, splits, use_len):
+    """mica_attention_fwd_prefix (a key prefix shared by every sequence, read in place) against the same
+    kernel on the prefix expanded and concatenated to every sequence's keys: bit-identical outputs (each
+    query sees the same key tiles in the same order), and the concatenated run against the oracle."""
+    from mica_amd.attention import causal_gqa_attention
+    note(f"attention prefix B={B} P={P} Sn={Sn} Sq={Sq} HK={HK} splits={splits} kv_len={use_len}")
+    HQ, D = 4 * HK, 256
+    g = torch.Generator().manual_seed(B * 100 + P + Sn + Sq)
+    q = (torch.randn(B, Sq, HQ, D, generator=g) * 1.5).to(torch.bfloat16).to(gpu)
+    kvp = (torch.randn(1, P, 2 * HK, D, generator=g) * 1.5).to(torch.bfloat16).to(gpu)
+    kvn = (torch.randn(B, Sn, 2 * HK, D, generator=g) * 1.5).to(torch.bfloat16).to(gpu)
+    kp, vp = kvp[:, :, :HK], kvp[:, :, HK:]
+    kn, vn = kvn[:, :, :HK], kvn[:, :, HK:]
+    kv_len = None
+    if use_len:   # each sequence's query at a different position of its new keys
+        kv_len = torch.tensor([P + Sn - 3 * b for b in range(B)], dtype=torch.int32, device=gpu)
+    o = causal_gqa_attention(q, kn, vn, key_splits=splits, kv_len=kv_len, prefix=(kp, vp))
+    kc = torch.cat((kp.expand(B, -1, -1, -1), kn), dim=1)
+    vc = torch.cat((vp.expand(B, -1, -1, -1), vn), dim=1)
+    oc = causal_gqa_attention(q, kc, vc, key_splits=splits, kv_len=kv_len)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), oc.view(torch.int16)), "shared prefix differs from concatenated keys"
+    # the concatenated run against the oracle (queries at the last Sq of each sequence's kv_len keys)
+    kcf, vcf, qf = kc.float().cpu().numpy(), vc.float().cpu().numpy(), q.float().cpu().numpy()
+    for b in range(B):
+        n = P + Sn if kv_len is None else int(kv_len[b])
+        ref = O.causal_gqa_attention(qf[b:b + 1], kcf[b:b + 1, :n], vcf[b:b + 1, :n], D ** -0.5)[0]
+        got = oc[b].float().cpu().numpy()
+        err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert err <= 1e-2, (b, err)
+
+
 def test_attn_fwd_reference_selftest_cases(gpu):
     """int8_kernels.attn_fwd under the reference's own attention self-test (int8_runtime.py:444-488):
     its shapes (b, n, keys) with prefix keys, q as a transposed [b, n, hq, d] tensor and head-major k / v,
