@@ -305,6 +305,26 @@ int mica_attention_fwd_prefix(const void *q, long long sbq, long long shq, long 
  * sequences' own images for Sk - Pk keys, the split states as above; -1 for an invalid argument */
 long long mica_attention_prefix_workspace_bytes(int B, int Sq, int Sk, int Pk, int HQ, int HK, int key_splits);
 
+/*
+ * mica_attention_fwd_prefix (kv_len NULL; Pk = 0: no prefix) with the rotary embedding of the new rows
+ * folded in: the attention layers' apply_rotary_pos_emb on q and k before the attention (the step
+ * mica_rope_inplace performs as a pass of its own).  Requires Sk = Pk + Sq: row r of sequence b is
+ * query r and key Pk + r, at position pos[b Sq + r] (int32, device) or Pk + r when pos is NULL;
+ * cos_tab / sin_tab are bf16 [n_pos][128] (16-byte aligned), and a row whose position falls outside
+ * them is left unrotated.  k is rotated in place (bit for bit what mica_rope_inplace writes) before the
+ * attention reads it; q is rotated as it is loaded and left as it was in memory; the prefix's keys kp
+ * must already be rotated.  The output equals mica_rope_inplace over q and k followed by
+ * mica_attention_fwd_prefix bit for bit, without the pass over q (its 16 heads are four fifths of the
+ * rotated bytes).  Workspace as mica_attention_fwd_prefix.
+ */
+int mica_attention_fwd_rope(const void *q, long long sbq, long long shq, long long ldq, void *k, long long sbk,
+                            long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv,
+                            const void *kp, long long shkp, long long ldkp, const void *vp, long long shvp,
+                            long long ldvp, int Pk, void *o, long long sbo, long long sho, long long ldo, int B, int Sq,
+                            int Sk, int HQ, int HK, int head_dim, float scale, int causal, int key_splits,
+                            const void *cos_tab, const void *sin_tab, int n_pos, const int *pos, void *workspace,
+                            long long workspace_bytes, mica_stream_t stream);
+
 /* ---- gated delta net (GDN) token mixer ------------------------------------------------------- */
 
 /*

@@ -105,12 +105,36 @@ struct FaParams {
     const uint16_t *kp; long long shkp, ldkp;
     const uint16_t *vtp;
     int ntiles_p;
+    // rotary embedding of the new rows (rcos null: none): row r of sequence b (query r, key Pk + r, with
+    // Sk = Pk + Sq) at position rpos[b Sq + r], or Pk + r without rpos; tables bf16 [rn_pos][128]
+    const uint16_t *rcos, *rsin;
+    const int *rpos;
+    int rn_pos;
 };
 
 // ---- V -> V^T tile images: one workgroup per (tile, sequence x head); thread = 8 dims x 4 keys ----
 __global__ __launch_bounds__(256) void v_transpose_kernel(FaParams p) {
     const int tile = blockIdx.x, bh = blockIdx.y;
     const int b = bh / p.HK, hk = bh % p.HK;
+    if (p.rcos != nullptr) {
+        // the tile's K rows rotated in place (rope_pairs8, as mica_rope_inplace): thread = 8 pairs of
+        // one key, two keys per thread.  Key t is new row t (its V^T image is built below).
+#pragma unroll
+        for (int u2 = 0; u2 < 2; ++u2) {
+            const int item = threadIdx.x + 256 * u2, t = tile * kBK + (item >> 4), i0 = (item & 15) * 8;
+            if (t >= p.Sk) continue;
+            const int pos = p.rpos ? p.rpos[b * p.Sk + t] : p.ntiles_p * kBK + t;
+            if (pos < 0 || pos >= p.rn_pos) continue;       // out-of-table position: left unrotated
+            uint16_t *kr = (uint16_t *)p.k + b * p.sbk + hk * p.shk + (long long)t * p.ldk;
+            const u32x4 a = *(const u32x4 *)(kr + i0), bb = *(const u32x4 *)(kr + kD / 2 + i0);
+            const u32x4 c = *(const u32x4 *)(p.rcos + (long long)pos * (kD / 2) + i0);
+            const u32x4 sn = *(const u32x4 *)(p.rsin + (long long)pos * (kD / 2) + i0);
+            u32x4 ya, yb;
+            rope_pairs8(a, bb, c, sn, ya, yb);
+            *(u32x4 *)(kr + i0) = ya;
+            *(u32x4 *)(kr + kD / 2 + i0) = yb;
+        }
+    }
     const int d0 = (threadIdx.x >> 3) * 8, u = threadIdx.x & 7; // dims d0 .. d0 + 7, keys 4 u .. 4 u + 3
     u32x4 rows[4];
 #pragma unroll
@@ -200,6 +224,21 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
             u32x4 v = {0u, 0u, 0u, 0u};
             if (t < p.Sq) v = *(const u32x4 *)(p.q + b * p.sbq + head * p.shq + (long long)t * p.ldq + s * 16 + hi * 8);
             qf[s] = __builtin_bit_cast(bf16x8, v);
+        }
+        // rotary embedding of the query (rope_pairs8, as mica_rope_inplace): dims d < 128 and d + 128
+        // are fragments s and s + 8 of the same lane
+        const int rp = p.rcos == nullptr || t >= p.Sq ? -1 : p.rpos ? p.rpos[b * p.Sq + t] : p.ntiles_p * kBK + t;
+        if (rp >= 0 && rp < p.rn_pos) {
+            const uint16_t *cs = p.rcos + (long long)rp * (kD / 2) + hi * 8;
+            const uint16_t *sn = p.rsin + (long long)rp * (kD / 2) + hi * 8;
+#pragma unroll
+            for (int s = 0; s < kD / 32; ++s) {
+                u32x4 ya, yb;
+                rope_pairs8(__builtin_bit_cast(u32x4, qf[s]), __builtin_bit_cast(u32x4, qf[s + kD / 32]),
+                            *(const u32x4 *)(cs + s * 16), *(const u32x4 *)(sn + s * 16), ya, yb);
+                qf[s] = __builtin_bit_cast(bf16x8, ya);
+                qf[s + kD / 32] = __builtin_bit_cast(bf16x8, yb);
+            }
         }
     }
     f32x16 O[kD / 32];
@@ -398,13 +437,20 @@ int attention_launch(const void *q, long long sbq, long long shq, long long ldq,
                      const void *kp, long long shkp, long long ldkp, const void *vp, long long shvp, long long ldvp,
                      int Pk, void *o, long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
                      int HK, int head_dim, float scale, int causal, int key_splits, const int *kv_len, void *workspace,
-                     long long workspace_bytes, mica_stream_t stream) {
+                     long long workspace_bytes, mica_stream_t stream, const void *rope_cos = nullptr,
+                     const void *rope_sin = nullptr, int rope_n_pos = 0, const int *rope_pos = nullptr) {
     if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || Sq < 0 || Sk < Sq) return MICA_MISS_SHAPE;
     if (Pk < 0 || Pk % kBK || Pk > Sk - Sq) return MICA_MISS_SHAPE;
     if (!causal || key_splits < 1 || key_splits > kMaxKeySplits) return MICA_MISS_ARG;
     if (B == 0 || Sq == 0) return 0;
     if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || workspace == nullptr) return MICA_MISS_ARG;
     if (Pk > 0 && (kp == nullptr || vp == nullptr)) return MICA_MISS_ARG;
+    if (rope_cos != nullptr) {
+        // the rotated rows are the new ones: every key past the prefix is one, none has its own count
+        if (rope_sin == nullptr || rope_n_pos <= 0 || kv_len != nullptr) return MICA_MISS_ARG;
+        if (Sk != Pk + Sq) return MICA_MISS_SHAPE;
+        if (!mica_aligned16(rope_cos) || !mica_aligned16(rope_sin)) return MICA_MISS_ALIGN;
+    }
     const long long st[16] = {sbq, shq, ldq, sbk, shk, ldk, sbv, shv, ldv, sbo, sho, ldo, shkp, ldkp, shvp, ldvp};
     for (long long x : st)
         if (x < 0 || x % 8) return MICA_MISS_STRIDE;
@@ -427,6 +473,8 @@ int attention_launch(const void *q, long long sbq, long long shq, long long ldq,
     p.nsplit = key_splits;
     p.sq_pad = ntiles_q * kBQ;
     p.kv_len = kv_len;
+    p.rcos = (const uint16_t *)rope_cos; p.rsin = (const uint16_t *)rope_sin; p.rpos = rope_pos;
+    p.rn_pos = rope_n_pos;
     // workspace: the prefix's V^T images, then each sequence's, then the split states
     char *ws = (char *)workspace;
     p.kp = (const uint16_t *)kp; p.shkp = shkp; p.ldkp = ldkp;
@@ -456,6 +504,7 @@ int attention_launch(const void *q, long long sbq, long long shq, long long ldq,
         pp.Sk = Pk;
         pp.ntiles_k = ntiles_p;
         pp.vt = (uint16_t *)p.vtp;  // the prefix images are written here, read-only in the attention kernel
+        pp.rcos = nullptr;          // the prefix's keys come rotated
         hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles_p, HK), dim3(256), 0, stream_, pp);
         rc = mica_err(hipGetLastError());
         if (rc) return rc;
@@ -519,4 +568,18 @@ extern "C" int mica_attention_fwd_prefix(const void *q, long long sbq, long long
     return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, kp, shkp, ldkp, vp, shvp, ldvp, Pk,
                             o, sbo, sho, ldo, B, Sq, Sk, HQ, HK, head_dim, scale, causal, key_splits, kv_len,
                             workspace, workspace_bytes, stream);
+}
+
+extern "C" int mica_attention_fwd_rope(const void *q, long long sbq, long long shq, long long ldq, void *k,
+                                       long long sbk, long long shk, long long ldk, const void *v, long long sbv,
+                                       long long shv, long long ldv, const void *kp, long long shkp, long long ldkp,
+                                       const void *vp, long long shvp, long long ldvp, int Pk, void *o,
+                                       long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
+                                       int HK, int head_dim, float scale, int causal, int key_splits,
+                                       const void *cos_tab, const void *sin_tab, int n_pos, const int *pos,
+                                       void *workspace, long long workspace_bytes, mica_stream_t stream) {
+    if (cos_tab == nullptr) return MICA_MISS_ARG;
+    return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, kp, shkp, ldkp, vp, shvp, ldvp, Pk,
+                            o, sbo, sho, ldo, B, Sq, Sk, HQ, HK, head_dim, scale, causal, key_splits, nullptr,
+                            workspace, workspace_bytes, stream, cos_tab, sin_tab, n_pos, pos);
 }

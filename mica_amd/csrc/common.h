@@ -47,6 +47,23 @@ MICA_DEVICE float silu_bf16(float g) {
     return round_bf16((g * r) * s);
 }
 
+// Rotary embedding of 8 pairs (x[i], x[i + h]) of one head, in bf16 arithmetic as transformers'
+// apply_rotary_pos_emb computes it (q * cos + rotate_half(q) * sin, each product rounded to bf16, then
+// their sum):  ya[i] = bf16(bf16(a[i] c[i]) + bf16(b[i] (-s[i]))),  yb[i] = bf16(bf16(b[i] c[i]) + bf16(a[i] s[i])).
+// a / b: the 8 first-half / second-half elements, c / s: the 8 cos / sin table entries, all packed bf16.
+MICA_DEVICE void rope_pairs8(const u32x4 &a, const u32x4 &b, const u32x4 &c, const u32x4 &s, u32x4 &ya, u32x4 &yb) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float x0l = bf16_lo(a[e]), x0h = bf16_hi(a[e]), x1l = bf16_lo(b[e]), x1h = bf16_hi(b[e]);
+        const float cl = bf16_lo(c[e]), ch = bf16_hi(c[e]), sl = bf16_lo(s[e]), sh = bf16_hi(s[e]);
+        // the four products of both pairs of this word, each pair rounded to bf16 by one conversion
+        const uint32_t pc0 = pack_bf16x2(x0l * cl, x0h * ch), ps1 = pack_bf16x2(x1l * -sl, x1h * -sh);
+        const uint32_t pc1 = pack_bf16x2(x1l * cl, x1h * ch), ps0 = pack_bf16x2(x0l * sl, x0h * sh);
+        ya[e] = pack_bf16x2(bf16_lo(pc0) + bf16_lo(ps1), bf16_hi(pc0) + bf16_hi(ps1));
+        yb[e] = pack_bf16x2(bf16_lo(pc1) + bf16_lo(ps0), bf16_hi(pc1) + bf16_hi(ps0));
+    }
+}
+
 MICA_DEVICE float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // fp32 -> fp16, round to nearest even, of the fp32 value as rounded.  The empty asm keeps the
 // compiler from folding a preceding multiply into the conversion (v_fma_mix*_f16 would round the

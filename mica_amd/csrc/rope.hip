@@ -34,21 +34,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_kernel(RopeParams p) {
     const u32x4 a = *(const u32x4 *)(xh + i0), b = *(const u32x4 *)(xh + h + i0);
     const u32x4 c = *(const u32x4 *)(p.cs + (long)pos * h + i0), s = *(const u32x4 *)(p.sn + (long)pos * h + i0);
     u32x4 ya, yb;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float lo[2], hi[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const float x0 = u ? bf16_hi(a[e]) : bf16_lo(a[e]);
-            const float x1 = u ? bf16_hi(b[e]) : bf16_lo(b[e]);
-            const float cv = u ? bf16_hi(c[e]) : bf16_lo(c[e]);
-            const float sv = u ? bf16_hi(s[e]) : bf16_lo(s[e]);
-            lo[u] = round_bf16(x0 * cv) + round_bf16(x1 * -sv);
-            hi[u] = round_bf16(x1 * cv) + round_bf16(x0 * sv);
-        }
-        ya[e] = pack_bf16x2(lo[0], lo[1]);
-        yb[e] = pack_bf16x2(hi[0], hi[1]);
-    }
+    rope_pairs8(a, b, c, s, ya, yb);
     *(u32x4 *)(xh + i0) = ya;
     *(u32x4 *)(xh + h + i0) = yb;
 }

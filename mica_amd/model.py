@@ -234,6 +234,8 @@ class W8A8Stack:
         # (attention.key_splits_for).  Off by default: the continuation then matches a full run within
         # bf16 rounding instead of bit for bit.
         self.split_keys = split_keys
+        # whole-head RoPE inside the attention kernel (mica_attention_fwd_rope) instead of a pass of its own
+        self.fuse_rope = True
         self.device = torch.device(device)
         g = torch.Generator(device=self.device).manual_seed(seed)
         H = cfg.hidden
@@ -259,7 +261,7 @@ class W8A8Stack:
         cos, sin = self._rope
         return cos[:n], sin[:n]
 
-    def _attention(self, qkv, B, S, past=None, keep=False, pos=None, norms=(None, None)):
+    def _attention(self, qkv, B, S, past=None, keep=False, pos=None, norms=(None, None), fuse_rope=True):
         """Causal GQA attention per request.  RoPE rotates the q and k heads of the QKV output in place
         (one kernel); the flash-attention kernel (head dim 256, 4 query heads per K/V head) then reads
         [B, S, heads, d] views of it and writes [B, S, heads, d]-contiguous output, i.e. already the O
@@ -269,17 +271,32 @@ class W8A8Stack:
         past: (k, v) of a prefix of P tokens; the S rows are then positions P .. P + S - 1 and attend to
         the prefix's keys too (Sk = P + S keys, the queries being the last S); pos: their int32 RoPE
         positions (PrefixState.positions_for).  keep: also return this call's rotated (k, v),
-        contiguous (batch 1: a prefix being recorded); norms: the layer's (q_norm, k_norm) weights."""
+        contiguous (batch 1: a prefix being recorded); norms: the layer's (q_norm, k_norm) weights.
+
+        With whole-head RoPE and no head norm, the kernel applies the rotation itself
+        (mica_attention_fwd_rope: k in place, q as it is loaded, bit-identical to rope_inplace first)
+        unless fuse_rope is False or self.fuse_rope is off; q then stays unrotated in qkv."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
         ng = hq if cfg.attn_output_gate else 0          # gate heads between the q and the k heads
         P = 0 if past is None else past[0].shape[1]
         cos, sin = self._tables(P + S, qkv.device)
-        self._rotate(qkv, (0, hq), (ng * d + hq * d, hk), cos, sin, S if P == 0 else None, None if P == 0 else pos,
-                     norms)
+        mica = self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk
+        # the q heads right before the k heads, rotated whole, keys read in place: the kernel rotates
+        fused = (mica and fuse_rope and self.fuse_rope and self._plain_rope() and ng == 0 and P % 32 == 0
+                 and (P == 0 or pos is not None))
+        if not fused:
+            self._rotate(qkv, (0, hq), (ng * d + hq * d, hk), cos, sin, S if P == 0 else None,
+                         None if P == 0 else pos, norms)
         q, _, k, v = qkv.view(B, S, hq + ng + 2 * hk, d).split((hq, ng, hk, hk), dim=2)
-        state = (k.contiguous(), v.contiguous()) if keep else None
-        if self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk:
+        state = (k.contiguous(), v.contiguous()) if keep and not fused else None
+        if fused:
+            ks = key_splits_for(B, S, P + S, hk, cus=_cu_count(qkv.device)) if P and self.split_keys else 1
+            a = causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), key_splits=ks, prefix=past if P else None,
+                                     rope=(cos, sin, pos if P else None)).view(B * S, hq * d)
+            if keep:
+                state = (k.contiguous(), v.contiguous())
+        elif mica:
             ks = 1
             if P and self.split_keys:
                 ks = key_splits_for(B, S, P + S, hk, cus=_cu_count(qkv.device))
@@ -420,7 +437,8 @@ class W8A8Stack:
             q, s, y = _norm_quant(h, L.input_norm, cfg.eps, trace is not None)
             qkv = L.qkv.forward_quantized(q, s)
             qkv_out = qkv.clone() if trace is not None else None  # RoPE rotates qkv in place
-            a = self._attention(qkv, B, S, past, keep, pos, (L.q_norm, L.k_norm))
+            # a trace keeps the rotated q too: RoPE as a pass of its own there
+            a = self._attention(qkv, B, S, past, keep, pos, (L.q_norm, L.k_norm), fuse_rope=trace is None)
             if keep:
                 a, state = a
             nq = cfg.heads * cfg.head_dim

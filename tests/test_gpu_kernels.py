@@ -909,6 +909,54 @@ def test_attention_shared_prefix_equals_concatenated_keys(gpu, B, P, Sn, Sq, HK,
         assert err <= 1e-2, (b, err)
 
 
+@pytest.mark.parametrize("B,P,S,HK,splits,n_pos,use_pos", [
+    (2, 0, 200, 1, 1, 4096, False),    # plain prefill, ragged last query block
+    (1, 0, 1024, 4, 1, 4096, False),   # the layer's head count
+    (1, 0, 70, 1, 1, 50, False),       # rows past the table stay unrotated
+    (2, 64, 96, 2, 1, 4096, True),     # continuation of a prefix, explicit positions
+    (2, 64, 96, 2, 3, 200, True),      # the same with split keys, some positions off the table
+])
+def test_attention_fused_rope_equals_rope_then_attention(gpu, B, P, S, HK, splits, n_pos, use_pos):
+    """mica_attention_fwd_rope (the rotary embedding folded into the attention) against rope_inplace over
+    the q and k heads of a fused QKV buffer followed by the plain kernel: k is rotated in place to the
+    same bits, q is left as it was in memory, and the outputs are bit-identical."""
+    from mica_amd.attention import causal_gqa_attention
+    from mica_amd.fused_kernels import rope_inplace
+    from mica_amd.model import _rope
+    note(f"attention rope B={B} P={P} S={S} HK={HK} splits={splits} n_pos={n_pos} pos={use_pos}")
+    HQ, D = 4 * HK, 256
+    g = torch.Generator().manual_seed(B * 1000 + P + S + HK)
+    qkv = (torch.randn(B * S, (HQ + 2 * HK) * D, generator=g) * 1.5).to(torch.bfloat16).to(gpu)
+    cos, sin = _rope(n_pos, D, 1e6, gpu)
+    pos = None
+    if use_pos:   # P + (t % S), every tenth row pushed past the table
+        p_ = torch.arange(B * S, dtype=torch.int32) % S + P
+        p_[::10] += n_pos
+        pos = p_.to(gpu)
+    pre = None
+    if P:
+        kvp = (torch.randn(1, P, 2 * HK, D, generator=g) * 1.5).to(torch.bfloat16).to(gpu)
+        pre = (kvp[:, :, :HK], kvp[:, :, HK:])
+
+    def views(buf):
+        q, k, v = buf.view(B, S, HQ + 2 * HK, D).split((HQ, HK, HK), dim=2)
+        return q, k, v
+
+    ref = qkv.clone()
+    rope_inplace(ref, HQ + HK, D, cos, sin, period=None if use_pos else S, pos=pos)
+    rq, rk, rv = views(ref)
+    want = causal_gqa_attention(rq, rk, rv, key_splits=splits, prefix=pre)
+    fused = qkv.clone()
+    fq, fk, fv = views(fused)
+    got = causal_gqa_attention(fq, fk, fv, key_splits=splits, prefix=pre, rope=(cos, sin, pos))
+    torch.cuda.synchronize()
+    assert torch.equal(fk.view(torch.int16), rk.view(torch.int16)), "keys rotated differently"
+    q0 = views(qkv)[0]
+    assert torch.equal(fq.view(torch.int16), q0.view(torch.int16)), "q was modified in memory"
+    assert torch.equal(fv.view(torch.int16), rv.view(torch.int16)), "v was modified"
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), "fused rope attention differs"
+
+
 def test_attn_fwd_reference_selftest_cases(gpu):
     """int8_kernels.attn_fwd under the reference's own attention self-test (int8_runtime.py:444-488):
     its shapes (b, n, keys) with prefix keys, q as a transposed [b, n, hq, d] tensor and head-major k / v,
