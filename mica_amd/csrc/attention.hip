@@ -323,13 +323,22 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         }
         // ---- O^T += V^T P^T: lane's keys for step s are rows 8 s .. 8 s + 7 of the accumulator, i.e.
         // key units 4 s + hi and 4 s + 2 + hi (4 keys each), one 16-byte chunk of the V^T image ----
+        // Step m = 8 s + dt: every dim tile's step 0, then its step 1 (the two MFMAs on one accumulator
+        // 8 apart, in the same order as before); the V^T fragments are read two steps ahead of their MFMA
+        // (left to itself the compiler reads each into one register quad right before its MFMA and waits)
+        auto vfrag = [&](int m) {
+            return __builtin_bit_cast(bf16x8, *(const u32x4 *)(vs + vfoff[m >> 3] + (m & 7) * 32 * (kBK * 2)));
+        };
+        bf16x8 va = vfrag(0), vb = vfrag(1);
 #pragma unroll
-        for (int dt = 0; dt < kD / 32; ++dt) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const u32x4 av = *(const u32x4 *)(vs + vfoff[s] + dt * 32 * (kBK * 2));
-                O[dt] = mfma_bf16(__builtin_bit_cast(bf16x8, av), pb[s], O[dt]);
+        for (int m = 0; m < kD / 16; ++m) {
+            const bf16x8 a = (m & 1) ? vb : va;
+            if (m + 2 < kD / 16) {
+                if (m & 1) vb = vfrag(m + 2);
+                else va = vfrag(m + 2);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            O[m & 7] = mfma_bf16(a, pb[m >> 3], O[m & 7]);
         }
     }
     const float ltot = half_swap_sum(lsum);
