@@ -266,8 +266,15 @@ class SharedNormQLinears(nn.Module):
     """An RMSNorm and the W8A8 linears that consume its output: the reference model's q/k/v
     projections, or its linear-attention in_proj_qkv / in_proj_z / in_proj_a / in_proj_b (each a
     QLinear with its own SmoothQuant factors, int8_runtime.py:124-127, fed by one input_layernorm,
-    fork.py:394-422).  forward(h) normalizes h once, quantizes it for every linear in one kernel
-    (each with that linear's inv_smooth) and runs one GEMM per linear: 1 + len(linears) launches."""
+    fork.py:394-422).  forward(h) normalizes h once and quantizes it for every linear in one kernel
+    (each with that linear's inv_smooth).
+
+    Linears whose factors are the same (both None, or equal vectors) get the same int8 input, so they
+    share it: one quantized copy and one GEMM over their weights stacked along N, whose output columns
+    are each linear's output (a column view of the shared [.., sum N] result; every element's
+    arithmetic is the linear's own, so the values are those of separate GEMMs).  The reference quantizes
+    once per linear (int8_runtime.py:180-186).  The members' buffers become row views of the stacked
+    ones, so the weights are not held twice.  1 + (number of distinct factor sets) launches."""
 
     def __init__(self, norm_weight, eps, linears, offset=1.0):
         super().__init__()
@@ -278,17 +285,76 @@ class SharedNormQLinears(nn.Module):
         self.register_buffer("norm_weight", norm_weight.contiguous())
         self.eps, self.offset = float(eps), float(offset)
         self.linears = nn.ModuleList(linears)
+        self.groups = []      # lists of linear indices that share one int8 input
+        for i, q in enumerate(linears):
+            for grp in self.groups:
+                r = linears[grp[0]]
+                if _same_factors(r.inv_smooth, q.inv_smooth) and r.out_dtype == q.out_dtype and \
+                        (r.bias is None) == (q.bias is None):
+                    grp.append(i)
+                    break
+            else:
+                self.groups.append([i])
+        self._stacked = {}    # group index -> (qweight, wscale, bias) stacked along N
+
+    def _stack(self, gi):
+        """The group's stacked buffers, made on first use (the members may be filled by a loader after
+        construction) and again whenever a member's buffers were replaced since."""
+        grp = [self.linears[i] for i in self.groups[gi]]
+        st = self._stacked.get(gi)
+        if st is not None:
+            qw = st[0]
+            off, ok = 0, True
+            for q in grp:
+                ok = ok and q.qweight.data_ptr() == qw.data_ptr() + off * qw.stride(0)
+                off += q.out_features
+            if ok:
+                return st
+        qw = torch.cat([q.qweight for q in grp]).contiguous()
+        sw = torch.cat([q.wscale for q in grp]).contiguous()
+        b = None if grp[0].bias is None else torch.cat([q.bias for q in grp]).contiguous()
+        off = 0
+        for q in grp:   # the members read row views of the stacked buffers
+            n = q.out_features
+            q.qweight, q.wscale = qw[off:off + n], sw[off:off + n]
+            if b is not None:
+                q.bias = b[off:off + n]
+            off += n
+        self._stacked[gi] = (qw, sw, b)
+        return self._stacked[gi]
 
     def forward(self, h, residual=None):
         """Returns [y_i] for each linear (and the summed input with a residual: ([y_i], h + residual))."""
         _require_gpu(h)
         shape = h.shape
-        r = rms_norm_quant_multi(h, self.norm_weight, self.eps, [q.inv_smooth for q in self.linears],
+        firsts = [self.linears[grp[0]] for grp in self.groups]
+        r = rms_norm_quant_multi(h, self.norm_weight, self.eps, [q.inv_smooth for q in firsts],
                                  residual=residual, offset=self.offset)
         qs, summed = (r, None) if residual is None else r
-        outs = [lin.forward_quantized(qx, sx).reshape(*shape[:-1], lin.out_features)
-                for lin, (qx, sx) in zip(self.linears, qs)]
+        outs = [None] * len(self.linears)
+        for gi, (grp, (qx, sx)) in enumerate(zip(self.groups, qs)):
+            if len(grp) == 1:
+                lin = self.linears[grp[0]]
+                outs[grp[0]] = lin.forward_quantized(qx, sx).reshape(*shape[:-1], lin.out_features)
+                continue
+            qw, sw, b = self._stack(gi)
+            if qx.shape[0] == 0:
+                y = torch.zeros(0, qw.shape[0], dtype=self.linears[grp[0]].out_dtype, device=qx.device)
+            else:
+                y = _hit(aot.mm_i8(qx, sx, qw, sw, b, self.linears[grp[0]].out_dtype), "mm_i8")
+            off = 0
+            for i in grp:
+                n = self.linears[i].out_features
+                outs[i] = y[:, off:off + n].reshape(*shape[:-1], n)
+                off += n
         return outs if residual is None else (outs, summed)
+
+
+def _same_factors(a, b) -> bool:
+    """Two linears' SmoothQuant factors give the same int8 input: both absent, or equal vectors."""
+    if a is None or b is None:
+        return a is None and b is None
+    return a is b or (a.shape == b.shape and a.device == b.device and bool(torch.equal(a, b)))
 
 
 # ---------------------------------------------------------------------------------- checkpoints

@@ -254,6 +254,40 @@ def test_shared_norm_qlinears_match_separate_path(gpu):
         assert np.array_equal(bits_of(o), bits_of(lin(y)))
 
 
+def test_shared_norm_qlinears_share_equal_factors(gpu):
+    """Linears with the same SmoothQuant factors (both None, or equal vectors held separately) share one
+    int8 input and one GEMM over their stacked weights: 1 + (distinct factor sets) launches, each output
+    bit-identical to its own QLinear on the normed rows, the members' weights row views of the stack."""
+    note("shared-norm qlinears, shared inputs")
+    rng = np.random.default_rng(6)
+    T, K = 260, 2560
+    h = to_gpu_bf16(act_bits(rng, (T, K)))
+    nw = to_gpu_bf16(O.f32_to_bf16(O.round_bf16(rng.normal(0.0, 0.1, K).astype(np.float32))))
+    inv = rng.uniform(0.5, 2.0, K).astype(np.float32)
+    for plan, groups in ((((2048, None), (1024, None), (32, None), (32, None)), 1),   # the GDN in_proj shapes
+                         (((512, "a"), (256, None), (512, "a"), (64, None)), 2)):   # equal factors, two copies
+        lins = []
+        for n, fac in plan:
+            qw = torch.from_numpy(rng.integers(-127, 128, (n, K), dtype=np.int8)).cuda()
+            sw = torch.from_numpy(rng.uniform(1e-3, 1e-2, n).astype(np.float32)).cuda()
+            lins.append(int8_runtime.QLinear.from_quantized(
+                qw, sw, inv_smooth=None if fac is None else torch.from_numpy(inv.copy()).cuda()))
+        mod = int8_runtime.SharedNormQLinears(nw, 1e-6, lins)
+        assert len(mod.groups) == groups
+        l0 = int8_kernels.STATS["launch"]
+        outs = mod(h)
+        torch.cuda.synchronize()
+        assert int8_kernels.STATS["launch"] - l0 == 1 + groups
+        y = fused_kernels.rms_norm(h, nw, 1e-6)
+        for lin, o, (n, _) in zip(lins, outs, plan):
+            assert o.shape == (T, n)
+            assert np.array_equal(bits_of(o), bits_of(lin(y)))
+        for gi, grp in enumerate(mod.groups):
+            if len(grp) > 1:
+                base = mod._stacked[gi][0].untyped_storage().data_ptr()
+                assert all(lins[i].qweight.untyped_storage().data_ptr() == base for i in grp)
+
+
 def test_rms_norm_op_matches_reference_surface(gpu):
     """fused_kernels.rms_norm(x, w, eps, residual) -> y / (y, summed), the reference's signature."""
     note("rms_norm op")
