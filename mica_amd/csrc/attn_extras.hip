@@ -28,9 +28,11 @@ struct NormRopeParams {
     const uint16_t *cs, *sn;
     const int *pos;              // int32 [T] positions, or null: t % period
     int period, n_pos;
+    int tpl_log2;                // log2(head_dim / 8): lanes per head
 };
 
 constexpr int kNrThreads = 256;
+constexpr int kNrRows = 4;   // tokens per thread and step
 
 // sum over the `width` lanes of this lane's group (width a power of two <= 64, groups aligned): every
 // lane of the group gets the same bits (a butterfly: lane l adds l ^ m's value, in the same order)
@@ -39,72 +41,87 @@ MICA_DEVICE float group_sum(float v, int width) {
     return v;
 }
 
+// Grid (ceil((n_q + n_k) * lanes per head / 256), min(ceil(T / kNrRows), 65535)): blockIdx.x walks the
+// heads of a token, blockIdx.y its tokens (grid-stride, kNrRows at a time), so a thread's head and dims
+// come from shifts and no 64-bit division runs per thread.
 __global__ __launch_bounds__(kNrThreads) void head_norm_rope_kernel(NormRopeParams p) {
-    const int tpl = p.head_dim >> 3;                       // lanes per head
-    const long long gid = (long long)blockIdx.x * kNrThreads + threadIdx.x;
-    const long long head_id = gid / tpl;                   // (token, head) pair, q heads first
-    const int part = (int)(gid - head_id * tpl);           // this lane's 8 dims: 8 part .. 8 part + 7
+    const int lg = p.tpl_log2;                             // lanes per head = 1 << lg
     const int per_tok = p.n_q + p.n_k;
-    const long long total = (long long)p.T * per_tok;
-    // lanes past the last head keep the group's shuffles company on a valid head, and store nothing
-    const bool live = head_id < total;
-    const long long hid = live ? head_id : total - 1;
-    const long long t = hid / per_tok;
-    const int h = (int)(hid - t * per_tok);
+    const int item = blockIdx.x * kNrThreads + threadIdx.x;
+    // lanes past the token's last head keep the group's shuffles company on a valid head, and store nothing
+    const bool live = item < (per_tok << lg);
+    const int h = live ? item >> lg : per_tok - 1;
+    const int part = item & ((1 << lg) - 1);               // this lane's 8 dims: 8 part .. 8 part + 7
     const bool is_q = h < p.n_q;
     const int col = is_q ? p.q_off + h * p.head_dim : p.k_off + (h - p.n_q) * p.head_dim;
-    uint16_t *xh = p.x + t * p.ldx + col;
     const uint16_t *w = is_q ? p.wq : p.wk;
-    float v[8];
-    {
-        const u32x4 raw = *(const u32x4 *)(xh + 8 * part);
+    // kRows tokens per step, their loads issued before any of them is worked on (one 16-byte load per
+    // token is too little in flight per wave to keep the memory busy)
+    const int G = gridDim.y;
+    for (int t0 = blockIdx.y; t0 < p.T; t0 += kNrRows * G) {
+        u32x4 raws[kNrRows];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[2 * e] = bf16_lo(raw[e]);
-            v[2 * e + 1] = bf16_hi(raw[e]);
+        for (int u = 0; u < kNrRows; ++u) {
+            const int t = t0 + u * G;
+            raws[u] = t < p.T ? *(const u32x4 *)(p.x + (long long)t * p.ldx + col + 8 * part) : u32x4{0u, 0u, 0u, 0u};
         }
-    }
-    // the norm: every lane of a head takes the same branch (w is per segment)
-    if (w != nullptr) {
-        float ss = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
-        ss = group_sum(ss, tpl);
-        const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.head_dim + p.eps);
-        const u32x4 wr = *(const u32x4 *)(w + 8 * part);
+        for (int u = 0; u < kNrRows; ++u) {
+        const int t = t0 + u * G;
+        if (t >= p.T) break;
+        uint16_t *xh = p.x + (long long)t * p.ldx + col;
+        float v[8];
+        {
+            const u32x4 raw = raws[u];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[2 * e] = round_bf16((v[2 * e] * rstd) * (p.offset + bf16_lo(wr[e])));
-            v[2 * e + 1] = round_bf16((v[2 * e + 1] * rstd) * (p.offset + bf16_hi(wr[e])));
-        }
-    }
-    // RoPE on dims < rot_dim: dim i < rot_dim / 2 pairs with i + rot_dim / 2, held by lane part ^ (rot_dim / 16)
-    u32x4 out;
-    if (p.rot_dim > 0) {
-        const int hl = p.rot_dim >> 4;                     // lanes per rotated half
-        float o[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = __shfl_xor(v[e], hl, 64);
-        const int pv = p.pos ? p.pos[t] : (int)(t % p.period);
-        const bool rot = part < 2 * hl && pv >= 0 && pv < p.n_pos;   // out-of-table positions left unrotated
-        if (rot) {
-            const bool upper = part >= hl;
-            const int i0 = (part & (hl - 1)) * 8;          // index into cos / sin (0 .. rot_dim / 2 - 1)
-            const u32x4 c = *(const u32x4 *)(p.cs + (long long)pv * (p.rot_dim >> 1) + i0);
-            const u32x4 s = *(const u32x4 *)(p.sn + (long long)pv * (p.rot_dim >> 1) + i0);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float cv = (e & 1) ? bf16_hi(c[e >> 1]) : bf16_lo(c[e >> 1]);
-                const float sv = (e & 1) ? bf16_hi(s[e >> 1]) : bf16_lo(s[e >> 1]);
-                // lower half: x_i cos_i - x_{i+h} sin_i; upper half: x_{i+h} cos_i + x_i sin_i
-                v[e] = upper ? round_bf16(v[e] * cv) + round_bf16(o[e] * sv)
-                             : round_bf16(v[e] * cv) + round_bf16(o[e] * -sv);
+            for (int e = 0; e < 4; ++e) {
+                v[2 * e] = bf16_lo(raw[e]);
+                v[2 * e + 1] = bf16_hi(raw[e]);
             }
         }
-    }
+        // the norm: every lane of a head takes the same branch (w is per segment)
+        if (w != nullptr) {
+            float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-    if (live) *(u32x4 *)(xh + 8 * part) = out;
+            for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
+            ss = group_sum(ss, 1 << lg);
+            const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.head_dim + p.eps);
+            const u32x4 wr = *(const u32x4 *)(w + 8 * part);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[2 * e] = round_bf16((v[2 * e] * rstd) * (p.offset + bf16_lo(wr[e])));
+                v[2 * e + 1] = round_bf16((v[2 * e + 1] * rstd) * (p.offset + bf16_hi(wr[e])));
+            }
+        }
+        // RoPE on dims < rot_dim: dim i < rot_dim / 2 pairs with i + rot_dim / 2, held by lane part ^ (rot_dim / 16)
+        u32x4 out;
+        if (p.rot_dim > 0) {
+            const int hl = p.rot_dim >> 4;                     // lanes per rotated half
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = __shfl_xor(v[e], hl, 64);
+            const int pv = p.pos ? p.pos[t] : t % p.period;
+            const bool rot = part < 2 * hl && pv >= 0 && pv < p.n_pos;   // out-of-table positions left unrotated
+            if (rot) {
+                const bool upper = part >= hl;
+                const int i0 = (part & (hl - 1)) * 8;          // index into cos / sin (0 .. rot_dim / 2 - 1)
+                const u32x4 c = *(const u32x4 *)(p.cs + (long long)pv * (p.rot_dim >> 1) + i0);
+                const u32x4 s = *(const u32x4 *)(p.sn + (long long)pv * (p.rot_dim >> 1) + i0);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float cv = (e & 1) ? bf16_hi(c[e >> 1]) : bf16_lo(c[e >> 1]);
+                    const float sv = (e & 1) ? bf16_hi(s[e >> 1]) : bf16_lo(s[e >> 1]);
+                    // lower half: x_i cos_i - x_{i+h} sin_i; upper half: x_{i+h} cos_i + x_i sin_i
+                    v[e] = upper ? round_bf16(v[e] * cv) + round_bf16(o[e] * sv)
+                                 : round_bf16(v[e] * cv) + round_bf16(o[e] * -sv);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+        if (live) *(u32x4 *)(xh + 8 * part) = out;
+        }
+    }
 }
 
 // ---- output gate + per-token int8 quantization ---------------------------------------------------
@@ -199,15 +216,18 @@ extern "C" int mica_head_norm_rope(void *x, long long ldx, int T, int q_off, int
         return MICA_MISS_ALIGN;
     const long long heads = (long long)T * (n_q + n_k);
     if (heads == 0) return 0;
-    const long long threads = heads * (head_dim / 8);
-    const long long blocks = (threads + kNrThreads - 1) / kNrThreads;
-    if (blocks >= (1LL << 31) || (long long)T * ldx >= (1LL << 62)) return MICA_MISS_RANGE;
+    const long long per_tok = (long long)(n_q + n_k) * (head_dim / 8);   // (head, 8 dims) items of a token
+    const long long bx = (per_tok + kNrThreads - 1) / kNrThreads;
+    if (bx >= (1LL << 31) || (long long)T * ldx >= (1LL << 62)) return MICA_MISS_RANGE;
     NormRopeParams p{};
     p.x = (uint16_t *)x; p.ldx = ldx; p.T = T; p.q_off = q_off; p.n_q = n_q; p.k_off = k_off; p.n_k = n_k;
     p.head_dim = head_dim; p.wq = (const uint16_t *)q_norm_w; p.wk = (const uint16_t *)k_norm_w;
     p.offset = offset; p.eps = eps; p.rot_dim = rot_dim; p.cs = (const uint16_t *)cos_tab;
     p.sn = (const uint16_t *)sin_tab; p.pos = pos; p.period = period; p.n_pos = n_pos;
-    hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)blocks), dim3(kNrThreads), 0, (hipStream_t)stream, p);
+    p.tpl_log2 = __builtin_ctz((unsigned)(head_dim / 8));
+    const int gy = (T + kNrRows - 1) / kNrRows;
+    hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)bx, (unsigned)(gy < 65535 ? gy : 65535)), dim3(kNrThreads), 0,
+                       (hipStream_t)stream, p);
     return mica_err(hipGetLastError());
 }
 
