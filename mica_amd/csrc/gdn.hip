@@ -619,6 +619,8 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
             Ed[tid] = fexp(glast - gn);
             Eg[tid] = fexp(gn);
         }
+        // the next chunk's K rows and g into the registers just written out: a whole chunk to arrive
+        if (more) load_k(c + 1);
         __syncthreads(); // (A) K rows, G and the state S^T visible to every wave
 
         // ---- X = [W; Q] S for this wave's 32 rows and dv half ----
@@ -682,7 +684,6 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
             if (more) load_u(c + 1);
         }
         __syncthreads(); // (B) v_new, P visible; every wave is done reading S^T and the previous K buffer
-        if (more) load_k(c + 1);
 
         // ---- o = scale (exp(G_i) (Q S)_i + P v_new) for the rows of wr = 2, 3 ----
         if (!w_rows) {
