@@ -306,22 +306,27 @@ int mica_attention_fwd_prefix(const void *q, long long sbq, long long shq, long 
 long long mica_attention_prefix_workspace_bytes(int B, int Sq, int Sk, int Pk, int HQ, int HK, int key_splits);
 
 /*
- * mica_attention_fwd_prefix (kv_len NULL; Pk = 0: no prefix) with the rotary embedding of the new rows
- * folded in: the attention layers' apply_rotary_pos_emb on q and k before the attention (the step
- * mica_rope_inplace performs as a pass of its own).  Requires Sk = Pk + Sq: row r of sequence b is
- * query r and key Pk + r, at position pos[b Sq + r] (int32, device) or Pk + r when pos is NULL;
- * cos_tab / sin_tab are bf16 [n_pos][128] (16-byte aligned), and a row whose position falls outside
- * them is left unrotated.  k is rotated in place (bit for bit what mica_rope_inplace writes) before the
- * attention reads it; q is rotated as it is loaded and left as it was in memory; the prefix's keys kp
- * must already be rotated.  The output equals mica_rope_inplace over q and k followed by
- * mica_attention_fwd_prefix bit for bit, without the pass over q (its 16 heads are four fifths of the
- * rotated bytes).  Workspace as mica_attention_fwd_prefix.
+ * mica_attention_fwd_prefix (kv_len NULL; Pk = 0: no prefix) with the new rows' q / k head norm and rotary
+ * embedding folded in: the attention layers' q_norm / k_norm and apply_rotary_pos_emb before the attention
+ * (the steps mica_head_norm_rope and mica_rope_inplace perform as passes of their own).  Requires
+ * Sk = Pk + Sq: row r of sequence b is query r and key Pk + r.  Each head (256 dims) is first normed when
+ * its weight is given (q_norm_w / k_norm_w, bf16 [256], 16-byte aligned; NULL: no norm):
+ *   y = bf16((x * (1 / sqrt(sum(x^2) / 256 + eps))) * (norm_offset + w)),
+ * then its first rot_dim dims (0, 64, 128 or 256) are rotated as mica_rope_inplace rotates a head of
+ * rot_dim dims, at position pos[b Sq + r] (int32, device) or Pk + r when pos is NULL; cos_tab / sin_tab
+ * are bf16 [n_pos][rot_dim / 2] (16-byte aligned), and a row whose position falls outside them is left
+ * unrotated.  k is treated in place (bit for bit what mica_head_norm_rope writes) before the attention
+ * reads it; q as it is loaded, left as it was in memory; the prefix's keys kp must already be treated.
+ * The output equals mica_head_norm_rope over q and k followed by mica_attention_fwd_prefix bit for bit,
+ * without the pass over q (its 16 heads are four fifths of the treated bytes).  At least one of the
+ * norms or the rotation must be asked for.  Workspace as mica_attention_fwd_prefix.
  */
 int mica_attention_fwd_rope(const void *q, long long sbq, long long shq, long long ldq, void *k, long long sbk,
                             long long shk, long long ldk, const void *v, long long sbv, long long shv, long long ldv,
                             const void *kp, long long shkp, long long ldkp, const void *vp, long long shvp,
                             long long ldvp, int Pk, void *o, long long sbo, long long sho, long long ldo, int B, int Sq,
                             int Sk, int HQ, int HK, int head_dim, float scale, int causal, int key_splits,
+                            const void *q_norm_w, const void *k_norm_w, float norm_offset, float norm_eps, int rot_dim,
                             const void *cos_tab, const void *sin_tab, int n_pos, const int *pos, void *workspace,
                             long long workspace_bytes, mica_stream_t stream);
 

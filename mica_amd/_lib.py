@@ -59,8 +59,8 @@ SIGNATURES = {
                                        _P]),
     "mica_attention_prefix_workspace_bytes": (_LL, [_I, _I, _I, _I, _I, _I, _I]),
     "mica_attention_fwd_rope": (_I, [_P, _LL, _LL, _LL, _P, _LL, _LL, _LL, _P, _LL, _LL, _LL, _P, _LL, _LL, _P, _LL,
-                                     _LL, _I, _P, _LL, _LL, _LL, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _I, _P,
-                                     _P, _LL, _P]),
+                                     _LL, _I, _P, _LL, _LL, _LL, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _F, _F,
+                                     _I, _P, _P, _I, _P, _P, _LL, _P]),
     "mica_causal_conv1d": (_I, [_P, _LL, _I, _P, _P, _I, _I, _P, _P, _P, _LL, _I, _I, _I, _I, _I, _I, _F, _P]),
     "mica_gdn_chunk": (_I, [_P, _LL, _I, _P, _LL, _I, _P, _LL, _I, _P, _P, _I, _P, _P, _P, _F, _I, _I, _I, _I, _P,
                             _LL, _P]),

@@ -34,7 +34,7 @@ def key_splits_for(B: int, Sq: int, Sk: int, HK: int, cus: int = 256, per_cu: in
 
 
 def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits: int = 1, kv_len=None,
-                  prefix=None, rope=None):
+                  prefix=None, rope=None, head_norm=None):
     """Launch the kernel on q [B, Sq, HQ, 256] / k, v [B, Sk, HK, 256] ('bshd') or q [B, HQ, Sq, 256] /
     k, v [B, HK, Sk, 256] ('bhsd') views with unit feature stride.  Returns o in q's layout
     (contiguous [B, Sq, HQ, 256] memory), or raises ValueError on an unsupported input.
@@ -53,11 +53,13 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
     the concatenated call) without expanding the prefix to the batch.
 
     rope ((cos, sin, pos), optional, 'bshd' only, no kv_len): the rotary embedding of the new rows folded
-    in (mica_attention_fwd_rope).  cos / sin: bf16 [n_pos, 128] tables; pos: int32 [B * Sq] positions on
-    the device, or None for P + r (row r after a prefix of P keys).  Needs Sk = Sq (the new rows are the
-    keys past the prefix).  k is rotated in place, exactly as ``fused_kernels.rope_inplace`` rotates it;
-    q is rotated as the kernel loads it and stays unrotated in memory.  The result equals rope_inplace
-    over q and k followed by the plain call, bit for bit."""
+    in (mica_attention_fwd_rope) over their first 2 * cos.shape[1] dims (64, 128 or 256).  cos / sin: bf16
+    [n_pos, rot_dim / 2] tables; pos: int32 [B * Sq] positions on the device, or None for P + r (row r
+    after a prefix of P keys).  Needs Sk = Sq (the new rows are the keys past the prefix).  head_norm
+    ((q_norm_w, k_norm_w, offset, eps), optional, same conditions): each q / k head normed first,
+    bf16((x rstd) (offset + w)), a weight of None skipping that side.  k is treated in place, exactly as
+    ``fused_kernels.rope_inplace`` / ``head_norm_rope`` treat it; q as the kernel loads it, unchanged in
+    memory.  The result equals those passes over q and k followed by the plain call, bit for bit."""
     for t in (q, k, v):
         if not t.is_cuda:
             raise ValueError("mica_amd attention runs on the GPU only (got a CPU tensor)")
@@ -87,19 +89,30 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
         if vp.shape != kp.shape or P % 32:
             raise ValueError("the prefix's keys and values must have one length, a multiple of 32")
         Sk += P
+    fold = rope is not None or head_norm is not None
+    cos = sin = rpos = None
+    rot_dim, qnw, knw, noff, neps = 0, None, None, 0.0, 0.0
+    if fold and (q_layout != "bshd" or kv_len is not None or Sk - P != Sq):
+        raise ValueError("rope / head_norm need the 'bshd' layout, no kv_len, and one key per query row past "
+                         "the prefix")
     if rope is not None:
         cos, sin, rpos = rope
-        if q_layout != "bshd" or kv_len is not None or Sk - P != Sq:
-            raise ValueError("rope needs the 'bshd' layout, no kv_len, and one key per query row past the prefix")
+        rot_dim = 2 * cos.shape[-1] if cos.dim() == 2 else 0
         for t in (cos, sin):
             if (not t.is_cuda or t.device != dev or t.dtype != torch.bfloat16 or t.dim() != 2
-                    or t.shape[1] != HEAD_DIM // 2 or not t.is_contiguous()):
-                raise ValueError("rope tables must be contiguous bf16 [n_pos, 128] tensors on q's device")
+                    or rot_dim not in (64, 128, 256) or not t.is_contiguous()):
+                raise ValueError("rope tables must be contiguous bf16 [n_pos, 32 | 64 | 128] tensors on q's device")
         if cos.shape != sin.shape:
             raise ValueError("rope cos / sin tables differ in shape")
         if rpos is not None and (rpos.dtype != torch.int32 or rpos.device != dev or rpos.numel() != B * Sq
                                  or not rpos.is_contiguous()):
             raise ValueError("rope positions must be a contiguous int32 [B * Sq] tensor on q's device")
+    if head_norm is not None:
+        qnw, knw, noff, neps = head_norm
+        for t in (qnw, knw):
+            if t is not None and (not t.is_cuda or t.device != dev or t.dtype != torch.bfloat16
+                                  or t.numel() != HEAD_DIM or not t.is_contiguous()):
+                raise ValueError("head norm weights must be contiguous bf16 [256] tensors on q's device")
     key_splits = int(key_splits)
     if not 1 <= key_splits <= MAX_KEY_SPLITS:
         raise ValueError(f"key_splits must be 1 .. {MAX_KEY_SPLITS}")
@@ -109,21 +122,24 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
     if nbytes < 0:
         raise ValueError("attention: invalid sizes")
     ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=dev)
-    if not _aligned(q, k, v, o, ws, *((kp, vp) if P else ()), *((rope[0], rope[1]) if rope is not None else ())):
+    extra = [t for t in (cos, sin, qnw, knw) if t is not None]
+    if not _aligned(q, k, v, o, ws, *((kp, vp) if P else ()), *extra):
         raise ValueError("attention operands must be 16-byte aligned")
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else float(scale)
     o_st = (o.stride(0), o.stride(2), o.stride(1))
     if kv_len is not None:
         if kv_len.dtype != torch.int32 or kv_len.device != dev or kv_len.numel() != B or not kv_len.is_contiguous():
             raise ValueError("kv_len must be a contiguous int32 [B] tensor on q's device")
-    if rope is not None:
+    if fold:
         pk = (kp.data_ptr(), kp.stride(1), kp.stride(0), vp.data_ptr(), vp.stride(1), vp.stride(0)) if P else \
             (None, 0, 0, None, 0, 0)
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd_rope(
             q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v), *pk, P,
             o.data_ptr(), *o_st, B, Sq, Sk, HQ, HK, HEAD_DIM, scale, 1, key_splits,
-            cos.data_ptr(), sin.data_ptr(), cos.shape[0], None if rpos is None else rpos.data_ptr(),
-            ws.data_ptr(), nbytes, _stream(dev))), "mica_attention_fwd_rope")
+            ptr(qnw), ptr(knw), float(noff), float(neps), rot_dim, ptr(cos), ptr(sin),
+            0 if cos is None else cos.shape[0], ptr(rpos), ws.data_ptr(), nbytes, _stream(dev))),
+            "mica_attention_fwd_rope")
     elif P:
         rc = _lib.check(_on(dev, lambda: L.mica_attention_fwd_prefix(
             q.data_ptr(), *st(q), k.data_ptr(), *st(k), v.data_ptr(), *st(v),
@@ -152,9 +168,9 @@ def attention_fwd(q, k, v, q_layout: str, scale: float | None = None, key_splits
 
 
 def causal_gqa_attention(q, k, v, scale: float | None = None, key_splits: int = 1, kv_len=None, prefix=None,
-                         rope=None):
+                         rope=None, head_norm=None):
     """softmax(scale q k^T, causal) v per sequence and head on [B, S, heads, 256] views (e.g. of the
     fused QKV output); query head h reads key/value head h // 4.  Returns o [B, S, HQ, 256] bf16.
-    With Sk > Sq the queries are the last Sq positions; key_splits, kv_len, prefix and rope as in
-    attention_fwd."""
-    return attention_fwd(q, k, v, "bshd", scale, key_splits, kv_len, prefix, rope)
+    With Sk > Sq the queries are the last Sq positions; key_splits, kv_len, prefix, rope and head_norm as
+    in attention_fwd."""
+    return attention_fwd(q, k, v, "bshd", scale, key_splits, kv_len, prefix, rope, head_norm)

@@ -105,34 +105,115 @@ struct FaParams {
     const uint16_t *kp; long long shkp, ldkp;
     const uint16_t *vtp;
     int ntiles_p;
-    // rotary embedding of the new rows (rcos null: none): row r of sequence b (query r, key Pk + r, with
-    // Sk = Pk + Sq) at position rpos[b Sq + r], or Pk + r without rpos; tables bf16 [rn_pos][128]
+    // the new rows' q / k head norm and rotary embedding, as mica_head_norm_rope computes them (rows of
+    // sequence b: query r and key Pk + r, with Sk = Pk + Sq).  qnw / knw: bf16 [256] norm weights (null:
+    // no norm), y = bf16((x rstd) (noff + w)); then the first rot_dim dims (0, 64, 128 or 256) rotated at
+    // position rpos[b Sq + r], or Pk + r without rpos, tables bf16 [rn_pos][rot_dim / 2].
+    const uint16_t *qnw, *knw;
+    float noff, neps;
+    int rot_dim;
     const uint16_t *rcos, *rsin;
     const int *rpos;
     int rn_pos;
 };
 
+// RMSNorm of one head of 256 dims held as 32 pieces of 8 (piece 8 i .. 8 i + 7), summed as the 32-lane
+// butterfly of mica_head_norm_rope adds them (each piece's squares in order, then pieces i and i ^ m
+// for m = 1, 2, 4, 8, 16 in turn; every level's pairs are added in either order with the same bits):
+// returns 1 / sqrt(mean + eps) from the level-1 sums l1[i / 2] of this thread's pieces, the rest of the
+// tree being over pieces held elsewhere and combined by the caller.
+MICA_DEVICE float piece_squares(const u32x4 &x) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float a = bf16_lo(x[e]), b = bf16_hi(x[e]);
+        ss = __builtin_fmaf(a, a, ss);
+        ss = __builtin_fmaf(b, b, ss);
+    }
+    return ss;
+}
+// y = bf16((x rstd) (off + w)) of 8 packed values
+MICA_DEVICE u32x4 norm8(const u32x4 &x, float rstd, float off, const u32x4 &w) {
+    u32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        y[e] = pack_bf16x2((bf16_lo(x[e]) * rstd) * (off + bf16_lo(w[e])), (bf16_hi(x[e]) * rstd) * (off + bf16_hi(w[e])));
+    return y;
+}
+
 // ---- V -> V^T tile images: one workgroup per (tile, sequence x head); thread = 8 dims x 4 keys ----
 __global__ __launch_bounds__(256) void v_transpose_kernel(FaParams p) {
     const int tile = blockIdx.x, bh = blockIdx.y;
     const int b = bh / p.HK, hk = bh % p.HK;
-    if (p.rcos != nullptr) {
-        // the tile's K rows rotated in place (rope_pairs8, as mica_rope_inplace): thread = 8 pairs of
-        // one key, two keys per thread.  Key t is new row t (its V^T image is built below).
+    const int rh = p.rot_dim >> 1;    // rotated pairs per head
+    if (p.knw != nullptr) {
+        // the tile's K rows normed and rotated in place (as mica_head_norm_rope): 8 threads per key, thread
+        // sub holding dims 32 sub .. 32 sub + 31 (pieces 4 sub .. 4 sub + 3); all lanes run the shuffles
+        const int key = threadIdx.x >> 3, sub = threadIdx.x & 7, t = tile * kBK + key;
+        const bool live = t < p.Sk;
+        uint16_t *kr = (uint16_t *)p.k + b * p.sbk + hk * p.shk + (long long)(live ? t : 0) * p.ldk + 32 * sub;
+        u32x4 x[4];
+        float ps[4];
 #pragma unroll
-        for (int u2 = 0; u2 < 2; ++u2) {
-            const int item = threadIdx.x + 256 * u2, t = tile * kBK + (item >> 4), i0 = (item & 15) * 8;
+        for (int j = 0; j < 4; ++j) {
+            x[j] = live ? *(const u32x4 *)(kr + 8 * j) : u32x4{0u, 0u, 0u, 0u};
+            ps[j] = piece_squares(x[j]);
+        }
+        float ss = (ps[0] + ps[1]) + (ps[2] + ps[3]);                 // pieces ^ 1, then ^ 2
+        ss += __shfl_xor(ss, 1, 64);                                  // pieces ^ 4
+        ss += __shfl_xor(ss, 2, 64);                                  // ^ 8
+        ss += __shfl_xor(ss, 4, 64);                                  // ^ 16
+        const float rstd = 1.0f / __builtin_sqrtf(ss / (float)kD + p.neps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = norm8(x[j], rstd, p.noff, *(const u32x4 *)(p.knw + 32 * sub + 8 * j));
+        if (rh > 0) {
+            // pairs (d, d + rh): the partner dims are held by thread sub ^ (rh / 32)
+            const int pm = rh >> 5;
+            u32x4 o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[j][e] = __shfl_xor(x[j][e], pm, 64);
+            const int pos = p.rpos ? p.rpos[b * p.Sk + (live ? t : 0)] : p.ntiles_p * kBK + t;
+            if (32 * sub < p.rot_dim && pos >= 0 && pos < p.rn_pos) {
+                const bool upper = (sub & pm) != 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i0 = (32 * sub + 8 * j) & (rh - 1);        // index into cos / sin
+                    const u32x4 c = *(const u32x4 *)(p.rcos + (long long)pos * rh + i0);
+                    const u32x4 sn = *(const u32x4 *)(p.rsin + (long long)pos * rh + i0);
+                    u32x4 ya, yb;
+                    if (upper) {
+                        rope_pairs8(o[j], x[j], c, sn, ya, yb);
+                        x[j] = yb;
+                    } else {
+                        rope_pairs8(x[j], o[j], c, sn, ya, yb);
+                        x[j] = ya;
+                    }
+                }
+            }
+        }
+        if (live) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *(u32x4 *)(kr + 8 * j) = x[j];
+        }
+    } else if (rh > 0) {
+        // the tile's K rows rotated in place (rope_pairs8, as mica_rope_inplace): thread = 8 pairs of
+        // one key.  Key t is new row t (its V^T image is built below).
+        const int groups = rh >> 3;   // 8-pair groups per key
+        for (int item = threadIdx.x; item < kBK * groups; item += 256) {
+            const int t = tile * kBK + item / groups, i0 = (item % groups) * 8;
             if (t >= p.Sk) continue;
             const int pos = p.rpos ? p.rpos[b * p.Sk + t] : p.ntiles_p * kBK + t;
             if (pos < 0 || pos >= p.rn_pos) continue;       // out-of-table position: left unrotated
             uint16_t *kr = (uint16_t *)p.k + b * p.sbk + hk * p.shk + (long long)t * p.ldk;
-            const u32x4 a = *(const u32x4 *)(kr + i0), bb = *(const u32x4 *)(kr + kD / 2 + i0);
-            const u32x4 c = *(const u32x4 *)(p.rcos + (long long)pos * (kD / 2) + i0);
-            const u32x4 sn = *(const u32x4 *)(p.rsin + (long long)pos * (kD / 2) + i0);
+            const u32x4 a = *(const u32x4 *)(kr + i0), bb = *(const u32x4 *)(kr + rh + i0);
+            const u32x4 c = *(const u32x4 *)(p.rcos + (long long)pos * rh + i0);
+            const u32x4 sn = *(const u32x4 *)(p.rsin + (long long)pos * rh + i0);
             u32x4 ya, yb;
             rope_pairs8(a, bb, c, sn, ya, yb);
             *(u32x4 *)(kr + i0) = ya;
-            *(u32x4 *)(kr + kD / 2 + i0) = yb;
+            *(u32x4 *)(kr + rh + i0) = yb;
         }
     }
     const int d0 = (threadIdx.x >> 3) * 8, u = threadIdx.x & 7; // dims d0 .. d0 + 7, keys 4 u .. 4 u + 3
@@ -225,20 +306,53 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
             if (t < p.Sq) v = *(const u32x4 *)(p.q + b * p.sbq + head * p.shq + (long long)t * p.ldq + s * 16 + hi * 8);
             qf[s] = __builtin_bit_cast(bf16x8, v);
         }
-        // rotary embedding of the query (rope_pairs8, as mica_rope_inplace): dims d < 128 and d + 128
-        // are fragments s and s + 8 of the same lane
-        const int rp = p.rcos == nullptr || t >= p.Sq ? -1 : p.rpos ? p.rpos[b * p.Sq + t] : p.ntiles_p * kBK + t;
-        if (rp >= 0 && rp < p.rn_pos) {
-            const uint16_t *cs = p.rcos + (long long)rp * (kD / 2) + hi * 8;
-            const uint16_t *sn = p.rsin + (long long)rp * (kD / 2) + hi * 8;
+        // the query's head norm (as mica_head_norm_rope: fragment s is piece 2 s + hi of the head, its
+        // level-1 partner piece in lane l ^ 32)
+        if (p.qnw != nullptr) {
+            float l1[kD / 16];
 #pragma unroll
-            for (int s = 0; s < kD / 32; ++s) {
-                u32x4 ya, yb;
-                rope_pairs8(__builtin_bit_cast(u32x4, qf[s]), __builtin_bit_cast(u32x4, qf[s + kD / 32]),
-                            *(const u32x4 *)(cs + s * 16), *(const u32x4 *)(sn + s * 16), ya, yb);
-                qf[s] = __builtin_bit_cast(bf16x8, ya);
-                qf[s + kD / 32] = __builtin_bit_cast(bf16x8, yb);
+            for (int s = 0; s < kD / 16; ++s) {
+                const float own = piece_squares(__builtin_bit_cast(u32x4, qf[s]));
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(own), __float_as_uint(own), false, false);
+                l1[s] = own + __uint_as_float(hi ? r[0] : r[1]);     // pieces ^ 1
             }
+#pragma unroll
+            for (int m = 1; m < kD / 16; m <<= 1)                      // pieces ^ 2, ^ 4, ^ 8, ^ 16
+#pragma unroll
+                for (int s = 0; s < kD / 16; ++s)
+                    if (!(s & m)) {
+                        const float v = l1[s] + l1[s | m];
+                        l1[s] = v;
+                        l1[s | m] = v;
+                    }
+            const float rstd = 1.0f / __builtin_sqrtf(l1[0] / (float)kD + p.neps);
+#pragma unroll
+            for (int s = 0; s < kD / 16; ++s)
+                qf[s] = __builtin_bit_cast(bf16x8, norm8(__builtin_bit_cast(u32x4, qf[s]), rstd, p.noff,
+                                                         *(const u32x4 *)(p.qnw + s * 16 + hi * 8)));
+        }
+        // rotary embedding of the query's first rot_dim dims (rope_pairs8, as mica_rope_inplace): dims
+        // d < rot_dim / 2 and d + rot_dim / 2 are fragments s and s + rot_dim / 32 of the same lane
+        const int rq = p.rot_dim >> 1;
+        const int rp = rq == 0 || t >= p.Sq ? -1 : p.rpos ? p.rpos[b * p.Sq + t] : p.ntiles_p * kBK + t;
+        if (rp >= 0 && rp < p.rn_pos) {
+            const uint16_t *cs = p.rcos + (long long)rp * rq + hi * 8;
+            const uint16_t *sn = p.rsin + (long long)rp * rq + hi * 8;
+            // one instance per rot_dim, so that the fragments are indexed by constants
+            auto rotate = [&](auto rq_c) {
+                constexpr int RQ = decltype(rq_c)::value;
+#pragma unroll
+                for (int s = 0; s < RQ / 16; ++s) {
+                    u32x4 ya, yb;
+                    rope_pairs8(__builtin_bit_cast(u32x4, qf[s]), __builtin_bit_cast(u32x4, qf[s + RQ / 16]),
+                                *(const u32x4 *)(cs + s * 16), *(const u32x4 *)(sn + s * 16), ya, yb);
+                    qf[s] = __builtin_bit_cast(bf16x8, ya);
+                    qf[s + RQ / 16] = __builtin_bit_cast(bf16x8, yb);
+                }
+            };
+            if (rq == kD / 2) rotate(std::integral_constant<int, kD / 2>{});
+            else if (rq == kD / 4) rotate(std::integral_constant<int, kD / 4>{});
+            else rotate(std::integral_constant<int, kD / 8>{});
         }
     }
     f32x16 O[kD / 32];
@@ -446,19 +560,25 @@ int attention_launch(const void *q, long long sbq, long long shq, long long ldq,
                      const void *kp, long long shkp, long long ldkp, const void *vp, long long shvp, long long ldvp,
                      int Pk, void *o, long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
                      int HK, int head_dim, float scale, int causal, int key_splits, const int *kv_len, void *workspace,
-                     long long workspace_bytes, mica_stream_t stream, const void *rope_cos = nullptr,
-                     const void *rope_sin = nullptr, int rope_n_pos = 0, const int *rope_pos = nullptr) {
+                     long long workspace_bytes, mica_stream_t stream, const void *q_norm_w = nullptr,
+                     const void *k_norm_w = nullptr, float norm_offset = 0.0f, float norm_eps = 0.0f,
+                     int rot_dim = 0, const void *rope_cos = nullptr, const void *rope_sin = nullptr,
+                     int rope_n_pos = 0, const int *rope_pos = nullptr) {
     if (head_dim != kD || HK <= 0 || HQ != HK * kFaWaves || B < 0 || Sq < 0 || Sk < Sq) return MICA_MISS_SHAPE;
     if (Pk < 0 || Pk % kBK || Pk > Sk - Sq) return MICA_MISS_SHAPE;
     if (!causal || key_splits < 1 || key_splits > kMaxKeySplits) return MICA_MISS_ARG;
     if (B == 0 || Sq == 0) return 0;
     if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || workspace == nullptr) return MICA_MISS_ARG;
     if (Pk > 0 && (kp == nullptr || vp == nullptr)) return MICA_MISS_ARG;
-    if (rope_cos != nullptr) {
-        // the rotated rows are the new ones: every key past the prefix is one, none has its own count
-        if (rope_sin == nullptr || rope_n_pos <= 0 || kv_len != nullptr) return MICA_MISS_ARG;
+    if (rot_dim != 0 || q_norm_w != nullptr || k_norm_w != nullptr) {
+        // the treated rows are the new ones: every key past the prefix is one, none has its own count
+        if (rot_dim != 0 && rot_dim != kD / 4 && rot_dim != kD / 2 && rot_dim != kD) return MICA_MISS_SHAPE;
+        if (rot_dim != 0 && (rope_cos == nullptr || rope_sin == nullptr || rope_n_pos <= 0)) return MICA_MISS_ARG;
+        if (kv_len != nullptr) return MICA_MISS_ARG;
         if (Sk != Pk + Sq) return MICA_MISS_SHAPE;
-        if (!mica_aligned16(rope_cos) || !mica_aligned16(rope_sin)) return MICA_MISS_ALIGN;
+        if ((rot_dim && (!mica_aligned16(rope_cos) || !mica_aligned16(rope_sin))) ||
+            (q_norm_w && !mica_aligned16(q_norm_w)) || (k_norm_w && !mica_aligned16(k_norm_w)))
+            return MICA_MISS_ALIGN;
     }
     const long long st[16] = {sbq, shq, ldq, sbk, shk, ldk, sbv, shv, ldv, sbo, sho, ldo, shkp, ldkp, shvp, ldvp};
     for (long long x : st)
@@ -482,6 +602,8 @@ int attention_launch(const void *q, long long sbq, long long shq, long long ldq,
     p.nsplit = key_splits;
     p.sq_pad = ntiles_q * kBQ;
     p.kv_len = kv_len;
+    p.qnw = (const uint16_t *)q_norm_w; p.knw = (const uint16_t *)k_norm_w;
+    p.noff = norm_offset; p.neps = norm_eps; p.rot_dim = rot_dim;
     p.rcos = (const uint16_t *)rope_cos; p.rsin = (const uint16_t *)rope_sin; p.rpos = rope_pos;
     p.rn_pos = rope_n_pos;
     // workspace: the prefix's V^T images, then each sequence's, then the split states
@@ -513,7 +635,8 @@ int attention_launch(const void *q, long long sbq, long long shq, long long ldq,
         pp.Sk = Pk;
         pp.ntiles_k = ntiles_p;
         pp.vt = (uint16_t *)p.vtp;  // the prefix images are written here, read-only in the attention kernel
-        pp.rcos = nullptr;          // the prefix's keys come rotated
+        pp.knw = nullptr;           // the prefix's keys come normed and rotated
+        pp.rot_dim = 0;
         hipLaunchKernelGGL(v_transpose_kernel, dim3(ntiles_p, HK), dim3(256), 0, stream_, pp);
         rc = mica_err(hipGetLastError());
         if (rc) return rc;
@@ -585,10 +708,13 @@ extern "C" int mica_attention_fwd_rope(const void *q, long long sbq, long long s
                                        const void *vp, long long shvp, long long ldvp, int Pk, void *o,
                                        long long sbo, long long sho, long long ldo, int B, int Sq, int Sk, int HQ,
                                        int HK, int head_dim, float scale, int causal, int key_splits,
-                                       const void *cos_tab, const void *sin_tab, int n_pos, const int *pos,
-                                       void *workspace, long long workspace_bytes, mica_stream_t stream) {
-    if (cos_tab == nullptr) return MICA_MISS_ARG;
+                                       const void *q_norm_w, const void *k_norm_w, float norm_offset, float norm_eps,
+                                       int rot_dim, const void *cos_tab, const void *sin_tab, int n_pos,
+                                       const int *pos, void *workspace, long long workspace_bytes,
+                                       mica_stream_t stream) {
+    if (rot_dim == 0 && q_norm_w == nullptr && k_norm_w == nullptr) return MICA_MISS_ARG;
     return attention_launch(q, sbq, shq, ldq, k, sbk, shk, ldk, v, sbv, shv, ldv, kp, shkp, ldkp, vp, shvp, ldvp, Pk,
                             o, sbo, sho, ldo, B, Sq, Sk, HQ, HK, head_dim, scale, causal, key_splits, nullptr,
-                            workspace, workspace_bytes, stream, cos_tab, sin_tab, n_pos, pos);
+                            workspace, workspace_bytes, stream, q_norm_w, k_norm_w, norm_offset, norm_eps, rot_dim,
+                            cos_tab, sin_tab, n_pos, pos);
 }

@@ -273,17 +273,17 @@ class W8A8Stack:
         positions (PrefixState.positions_for).  keep: also return this call's rotated (k, v),
         contiguous (batch 1: a prefix being recorded); norms: the layer's (q_norm, k_norm) weights.
 
-        With whole-head RoPE and no head norm, the kernel applies the rotation itself
-        (mica_attention_fwd_rope: k in place, q as it is loaded, bit-identical to rope_inplace first)
-        unless fuse_rope is False or self.fuse_rope is off; q then stays unrotated in qkv."""
+        The attention kernel applies the head norm and the rotation itself (mica_attention_fwd_rope: k in
+        place, q as it is loaded, bit-identical to rope_inplace / head_norm_rope first) unless fuse_rope is
+        False or self.fuse_rope is off; q then stays untreated in qkv."""
         cfg = self.cfg
         hq, hk, d = cfg.heads, cfg.kv_heads, cfg.head_dim
         ng = hq if cfg.attn_output_gate else 0          # gate heads between the q and the k heads
         P = 0 if past is None else past[0].shape[1]
         cos, sin = self._tables(P + S, qkv.device)
         mica = self.attention == "mica" and d == _FA_DIM and hq == _FA_GROUP * hk
-        # the q heads right before the k heads, rotated whole, keys read in place: the kernel rotates
-        fused = (mica and fuse_rope and self.fuse_rope and self._plain_rope() and ng == 0 and P % 32 == 0
+        # the keys read in place (no prefix, or a tile-aligned one): the kernel norms and rotates
+        fused = (mica and fuse_rope and self.fuse_rope and cfg.rot_dim in (64, 128, 256) and P % 32 == 0
                  and (P == 0 or pos is not None))
         if not fused:
             self._rotate(qkv, (0, hq), (ng * d + hq * d, hk), cos, sin, S if P == 0 else None,
@@ -292,8 +292,9 @@ class W8A8Stack:
         state = (k.contiguous(), v.contiguous()) if keep and not fused else None
         if fused:
             ks = key_splits_for(B, S, P + S, hk, cus=_cu_count(qkv.device)) if P and self.split_keys else 1
+            hn = (norms[0], norms[1], 1.0, cfg.eps) if cfg.qk_norm else None
             a = causal_gqa_attention(q, k, v, 1.0 / math.sqrt(d), key_splits=ks, prefix=past if P else None,
-                                     rope=(cos, sin, pos if P else None)).view(B * S, hq * d)
+                                     rope=(cos, sin, pos if P else None), head_norm=hn).view(B * S, hq * d)
             if keep:
                 state = (k.contiguous(), v.contiguous())
         elif mica:

@@ -991,6 +991,60 @@ def test_attention_fused_rope_equals_rope_then_attention(gpu, B, P, S, HK, split
     assert torch.equal(got.view(torch.int16), want.view(torch.int16)), "fused rope attention differs"
 
 
+@pytest.mark.parametrize("B,P,S,rot,norms,n_pos,use_pos", [
+    (2, 0, 200, 64, "qk", 4096, False),     # the reference model's layers: both head norms, RoPE on 64 dims
+    (1, 0, 300, 256, "qk", 4096, False),
+    (2, 64, 96, 128, "k", 200, True),       # a prefix continuation, k norm only, some positions off the table
+    (1, 0, 70, 64, "", 50, False),          # partial RoPE alone
+    (2, 0, 100, 0, "qk", 1, False),         # head norms alone
+])
+def test_attention_fused_head_norm_rope_equals_passes(gpu, B, P, S, rot, norms, n_pos, use_pos):
+    """mica_attention_fwd_rope with head norms and partial RoPE against head_norm_rope over the q and k
+    heads of a fused QKV buffer (output gate heads between them) followed by the plain kernel: k treated
+    in place to the same bits, q and the gate heads left as they were, bit-identical outputs."""
+    from mica_amd.attention import causal_gqa_attention
+    from mica_amd.fused_kernels import head_norm_rope
+    from mica_amd.model import _rope
+    note(f"attention head norm rope B={B} P={P} S={S} rot={rot} norms={norms!r} n_pos={n_pos} pos={use_pos}")
+    HK, D = 4, 256
+    HQ = 4 * HK
+    g = torch.Generator().manual_seed(B * 1000 + P + S + rot)
+    cols = 2 * HQ + 2 * HK                      # q, gate, k, v heads
+    qkv = (torch.randn(B * S, cols * D, generator=g) * 1.5).to(torch.bfloat16).to(gpu)
+    qw = (torch.randn(D, generator=g) * 0.1).to(torch.bfloat16).to(gpu) if "q" in norms else None
+    kw = (torch.randn(D, generator=g) * 0.1).to(torch.bfloat16).to(gpu) if "k" in norms else None
+    cos, sin = _rope(n_pos, rot, 1e7, gpu) if rot else (None, None)
+    pos = None
+    if use_pos:
+        p_ = torch.arange(B * S, dtype=torch.int32) % S + P
+        p_[::10] += n_pos
+        pos = p_.to(gpu)
+    pre = None
+    if P:
+        kvp = (torch.randn(1, P, 2 * HK, D, generator=g) * 1.5).to(torch.bfloat16).to(gpu)
+        pre = (kvp[:, :, :HK], kvp[:, :, HK:])
+
+    def views(buf):
+        q, _, k, v = buf.view(B, S, cols, D).split((HQ, HQ, HK, HK), dim=2)
+        return q, k, v
+
+    ref = qkv.clone()
+    head_norm_rope(ref, D, (0, HQ), (2 * HQ * D, HK), qw, kw, 1e-6, 1.0, rot, cos, sin,
+                   period=None if use_pos else S, pos=pos)
+    rq, rk, rv = views(ref)
+    want = causal_gqa_attention(rq, rk, rv, prefix=pre)
+    fused = qkv.clone()
+    fq, fk, fv = views(fused)
+    got = causal_gqa_attention(fq, fk, fv, prefix=pre, rope=(cos, sin, pos) if rot else None,
+                               head_norm=(qw, kw, 1.0, 1e-6))
+    torch.cuda.synchronize()
+    assert torch.equal(fk.view(torch.int16), rk.view(torch.int16)), "keys treated differently"
+    untouched = torch.cat((qkv[:, :2 * HQ * D], qkv[:, (2 * HQ + HK) * D:]), 1)
+    kept = torch.cat((fused[:, :2 * HQ * D], fused[:, (2 * HQ + HK) * D:]), 1)
+    assert torch.equal(kept.view(torch.int16), untouched.view(torch.int16)), "q, gate or v modified in memory"
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), "fused head norm / rope attention differs"
+
+
 def test_attn_fwd_reference_selftest_cases(gpu):
     """int8_kernels.attn_fwd under the reference's own attention self-test (int8_runtime.py:444-488):
     its shapes (b, n, keys) with prefix keys, q as a transposed [b, n, hq, d] tensor and head-major k / v,
