@@ -24,6 +24,12 @@
 // (buffer_load ... lds), 16-byte chunks XOR-swizzled by row so the operand reads are conflict-free;
 // V^T tiles are DMA'd from an image that v_transpose_kernel writes beforehand in exactly the LDS
 // layout.  Two LDS stages: the DMA of tile j + 1 overlaps the MFMAs of tile j.
+//
+// Optionally (mica_attention_fwd_rope) the new rows' q / k head RMSNorm and rotary embedding of the
+// attention layers are folded in: each query as its fragments are loaded (the head's halves are a lane
+// and its partner l ^ 32, the rotation pairs fragments of the same lane), each key in place by
+// v_transpose_kernel before its V^T tile; the arithmetic is that of mica_head_norm_rope /
+// mica_rope_inplace, element for element.
 
 #include <type_traits>
 
@@ -117,11 +123,12 @@ struct FaParams {
     int rn_pos;
 };
 
-// RMSNorm of one head of 256 dims held as 32 pieces of 8 (piece 8 i .. 8 i + 7), summed as the 32-lane
-// butterfly of mica_head_norm_rope adds them (each piece's squares in order, then pieces i and i ^ m
-// for m = 1, 2, 4, 8, 16 in turn; every level's pairs are added in either order with the same bits):
-// returns 1 / sqrt(mean + eps) from the level-1 sums l1[i / 2] of this thread's pieces, the rest of the
-// tree being over pieces held elsewhere and combined by the caller.
+// The head RMSNorm of mica_head_norm_rope on a head of 256 dims held as 32 pieces of 8 (piece i = dims
+// 8 i .. 8 i + 7): each piece's sum of squares in order (piece_squares), then the pieces summed as its
+// 32-lane butterfly adds them -- pieces i and i ^ m for m = 1, 2, 4, 8, 16 in turn, each level adding the
+// same two values in either order, so every holder of the head gets the same bits.  The callers hold
+// the pieces differently (a query: 16 per lane, the other 16 in lane l ^ 32; a key: 4 per thread over 8
+// threads) and run the levels in-lane or across lanes accordingly.
 MICA_DEVICE float piece_squares(const u32x4 &x) {
     float ss = 0.0f;
 #pragma unroll
