@@ -24,7 +24,10 @@ NORM_DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
 
 def _check_row_input(x, weight, residual):
     if not x.is_cuda:
-        raise ValueError("mica_amd RMSNorm runs on the GPU only (got a CPU tensor)")
+        raise ValueError(
+            f"mica_amd RMSNorm runs on the GPU only (got a tensor on {x.device}): this module has no CPU "
+            "compute path; move x to a gfx950 GPU, or norm CPU rows with torch "
+            "(v * rsqrt(mean(v^2) + eps) * (offset + w)) as the reference's rms_norm does there")
     if x.stride(-1) != 1:
         raise ValueError("fused RMSNorm requires unit feature stride")
     if x.dtype not in NORM_DT:
@@ -130,6 +133,10 @@ def rms_norm(x, weight, eps, residual=None, offset=1.0):
 
     Returns y, or (y, v) with a residual (fused_kernels.py:50-82).  offset=1.0 is the reference's
     Qwen3.5 ``(1 + weight)``.
+
+    GPU tensors only: where the reference computes its torch formula for a CPU tensor
+    (fused_kernels.py:51-56), this raises ValueError naming the device, so a CPU caller has to norm
+    its rows itself.
     """
     _check_row_input(x, weight, residual)
     _, _, y, summed = _launch_norm(x, weight, eps, residual, offset, None, False, True, "even")
