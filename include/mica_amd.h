@@ -122,11 +122,16 @@ int mica_rmsnorm_quant_multi(const void *x, int x_dtype, int ldx, const void *re
  *
  * workspace: NULL, or workspace_bytes >= mica_mm_i8_workspace_bytes(device) bytes of device memory,
  * 16-byte aligned, whose first 4 KiB are zero before its first use (every launch leaves them zero
- * again).  With it, when the last round of 256 x 256 tiles would hold at most CUs / 4 tiles,
- * K >= 8192 and either M <= 256 or the SILU_MUL epilogue is asked for (elsewhere 128 x 128 quarter
- * tiles, which need no workspace, serve such a round better), those tiles are split along K over four
- * workgroups each; partial int32 sums go through the workspace and are added exactly, so the result is
- * bit-identical to the unsplit schedule.  Launches that
+ * again).  With it, two schedules split tiles along K:
+ *   - 16-bit outputs (SILU_MUL included), K % 256 == 0, K >= 8192: when the output fits at most CUs / 3
+ *     tiles of 128 x 160 (SCALE) or 128 x 256 (SILU_MUL) -- a short request's down projection, e.g.
+ *     M <= 512 at N = 2560 -- every tile is split into K / 2560 parts (at least 3), one workgroup per
+ *     part, and each tile's last part adds the others' partial sums;
+ *   - int32 / fp32 outputs: when the last round of 256 x 256 tiles would hold at most CUs / 4 tiles,
+ *     K >= 8192 and M <= 256 (elsewhere 128 x 128 quarter tiles, which need no workspace, serve such
+ *     a round better), those tiles are split along K over four workgroups each.
+ * Partial int32 sums go through the workspace and are added exactly, so the result is bit-identical
+ * to the unsplit schedule.  Launches that
  * share a workspace must be ordered (one stream); concurrent launches need one workspace each.
  * The workspace has no counterpart in the reference (its Triton GEMM has no split schedule).
  */
@@ -143,8 +148,9 @@ long long mica_mm_i8_workspace_bytes(int device);
  * arguments, checks, schedule and bits as mica_mm_i8 with a workspace, but the split schedule's
  * workspace is a static device array of the library (mica_mm_i8_noalloc_scratch_bytes() = 32 MiB +
  * 4 KiB per device, held until the process ends), so the call allocates nothing.  Limit: a split
- * round of at most 16 tiles (64 workgroups); a call whose split round would need more returns
- * MICA_MISS_RANGE.  Every call on a device shares that device's scratch: calls that overlap on one
+ * round of 256 x 256 tiles of at most 16 tiles (64 workgroups); a call whose such round would need
+ * more returns MICA_MISS_RANGE (the split of few 128-row tiles takes fewer parts when the scratch
+ * holds too few of them).  Every call on a device shares that device's scratch: calls that overlap on one
  * device (concurrent streams) race, so order them on one stream.  The first call on a device also
  * clears the scratch's counters on its stream.
  */

@@ -737,10 +737,10 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
     // quarters each, and when at most half full, as two 256 x 128 halves (SCALE epilogue; the pieces
     // fill up to one round).  For the SiLU epilogue, whose waves need 128 columns (gate / up pairs), a
     // last round at most half full runs as two 128 x 256 halves along M (measured: 36.2 -> 27.2 us at
-    // 128 x 19456 x 2560, 86.8 -> 73.8 us at M = 1024).  With a workspace, a partial last round of at most cus / kSplit
-    // tiles whose K has at least kSplit * kMinSplitSlabs slabs is instead split along K, kSplit
-    // workgroups per tile, where quarters do not serve better: for the SiLU epilogue, and for M <= 256,
-    // where a tile's lower quarters are mostly or wholly empty.  A split tile costs its last
+    // 128 x 19456 x 2560, 86.8 -> 73.8 us at M = 1024).  With a workspace and int32 / fp32 outputs (the
+    // 16-bit ones have the 128-row split above), a partial last round of at most cus / kSplit tiles
+    // whose K has at least kSplit * kMinSplitSlabs slabs is instead split along K, kSplit workgroups
+    // per tile, for M <= 256, where a tile's lower quarters are mostly or wholly empty.  A split tile costs its last
     // contributor a serial sum of the others' 256 KiB partials plus the partial-sum round trip
     // (measured about 15 us + 3 us per partial), so the split pays only when a quarter of the tile's
     // K still takes longer than that; with more contributors per tile the sum grows faster than
@@ -773,12 +773,54 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
     int grid = (int)tiles;
     int dev = 0;
     const int cus = hipGetDevice(&dev) == hipSuccess ? cu_count(dev) : 0;
+    // Few tiles and a long K (a short request's down projection, e.g. 128 x 2560 x 9728: 16 tiles of
+    // 128 x 160 on 256 CUs): with a workspace, one round of 128-row tiles split along K into `parts`
+    // pieces whose int32 partial sums each tile's last part adds (agpr_split_launch; same bits as every
+    // other schedule).  The hand-off costs ~5 us (the partial sums' write-through, the arrival count,
+    // the read-back, each a round trip to the device's coherence point) plus ~2 us per further part
+    // read back, so it pays only for a long K: measured on MI355X (us, unsplit / 2 / 3 / 4 parts):
+    // 128 x 2560 x 9728: 29.4 / 22.9 / 20.5 / 19.5; 512 x 2560 x 9728: 31.4 / 26.6 / 26.0 / 28.3;
+    // 1024 x 2560 x 9728: 33.6 / 35.3; 128 x 2560 x 4096: 13.4 / 15.1 / 14.8 / 15.8; 128 x 6144 x 2560:
+    // 10.5 / 12.4 / 14.2 / 15.8; SiLU 128 x 19456 x 2560: 21.5 / 26.9 / 36.0.  Hence K >= 8192 and
+    // about one part per 20 slabs of 128 bytes, at least 3 (capped by the CUs and the workspace).
+#ifndef MICA_GEMM_SPLIT_SMALL
+#define MICA_GEMM_SPLIT_SMALL 1
+#endif
+    if (MICA_GEMM_SPLIT_SMALL && workspace != nullptr && cus > 0 && K % 256 == 0 && K >= 8192 &&
+        (epilogue == MICA_EPI_SILU_MUL || out_dtype == MICA_BF16 || out_dtype == MICA_FP16) && ldc % 8 == 0 &&
+        Nout % 8 == 0 && (!residual || ldr % 8 == 0) && (long long)(M + kTile) * lda < (1ll << 31) &&
+        (long long)(N + kTile) * ldb < (1ll << 31) && (long long)kTile * ldc * 4 < (1ll << 31) &&
+        (!residual || (long long)kTile * ldr * 4 < (1ll << 31))) {
+        const int bn = agpr_split_tile_n(epilogue);
+        const long long tiles_s = (long long)((M + 127) / 128) * ((N + bn - 1) / bn);
+        const long long slabs = K / 128;
+        long long parts = slabs / 20;
+#ifdef MICA_GEMM_SPLIT_PARTS
+        parts = MICA_GEMM_SPLIT_PARTS;
+#endif
+        if (parts > cus / tiles_s) parts = cus / tiles_s;
+        if (parts > slabs / 4) parts = slabs / 4;
+        const long long slot = agpr_split_slot_bytes(epilogue);
+        while (parts >= 3 && kCounterBytes + tiles_s * parts * slot > workspace_bytes) --parts;
+        if (parts >= 3 && tiles_s <= kCounterBytes / 4) {
+            p.tiles_m = (M + 127) / 128;
+            p.tiles_n = (N + bn - 1) / bn;
+            p.dp_tiles = 0;
+            p.sk_tiles = (int)tiles_s;
+            p.sk_grid = (int)(tiles_s * parts);
+            p.arrivals = (int *)workspace;
+            p.partials = (v4i *)((char *)workspace + kCounterBytes);
+            return agpr_split_launch(p, epilogue, out_dtype, bias != nullptr, residual != nullptr, st);
+        }
+    }
     const long long nk = (K + BK - 1) / BK;
     const long long rem = cus > 0 ? tiles % cus : 0;
     if (rem != 0 && cus <= 1024) {
         const bool quarters = kQuarters && epilogue == MICA_EPI_SCALE && 4 * rem <= cus;
+        // (16-bit outputs no longer take it: the AGPR kernel's quarter / half tiles and the 128-row split
+        // above serve them faster, e.g. 128 x 2560 x 9728 in 29.4 / 19.5 us against 48.9 us here)
         const bool want_split = workspace != nullptr && rem * kSplit <= cus && nk >= kSplit * kMinSplitSlabs &&
-                                !(quarters && M > 256);
+                                !(quarters && M > 256) && (out_dtype == MICA_INT32 || out_dtype == MICA_FP32);
         // the existing entry point splits with a workspace of mica_mm_i8_workspace_bytes(device); the
         // no-allocation one with the scratch, which holds kScratchGroups split workgroups
         const bool fits = noalloc ? rem * kSplit <= kScratchGroups : workspace_bytes >= workspace_bytes_for(cus);

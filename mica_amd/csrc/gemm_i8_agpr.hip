@@ -25,6 +25,8 @@
 // Schedule: a persistent grid of at most one workgroup per CU walks the whole tiles in the XCD-aware
 // order of gemm_i8_common.h, then the tail tiles as two halves (256 x 128 for the SCALE epilogue,
 // 128 x 256 along M for SiLU, whose waves need their 128 gate / up rows) or four 128 x 128 quarters.
+// Launches of few tiles with a long K run as 128-row tiles split along K over several workgroups
+// (gemm_i8_agpr_split_kernel), whose int32 partial sums the last part of each tile adds.
 // Epilogue order: y = (f32(acc) * sa[m]) * sb[n] (+ bias[n]), rounded to the output type; the residual
 // is added after that rounding (kernel_src/kernels.py:63-68, int8_runtime.py:186-192); SiLU:
 // bf16(bf16(silu(bf16 g)) * bf16 u) (fast_runtime.py:126-132 with the gate / up pairing of
@@ -341,19 +343,19 @@ struct QTile {
         kstep<false, 0, false, -1>(R0, R1, wa[0], xa[0], own);
     }
 
-    // ---- the slabs of a piece with no successor to prefetch for (C::NS >= 3 stages): on entry slab 0 is
-    // visible in stage 0 and slabs 1 .. NS - 1 are in flight into stages 1 .. NS - 1.  Slab s lives in
-    // stage s % NS; after the barrier of B(k) (slab k + 1 landed, slab k read by every wave) slab k + NS
-    // goes into slab k's stage, so NS - 1 slabs are in flight while one is read.  Stage offsets beyond
-    // the 16-bit offset of ds_read_b128 ride on the base registers.
-    MICA_DEVICE void run_deep(const GemmParams &p, int8_t *smem, int wave, int m0, int n0) {
+    // ---- slabs ks0 .. ks0 + nk - 1 of a piece with no successor to prefetch for (C::NS >= 3 stages; nk
+    // at least NS): on entry the range's slab 0 is visible in stage 0 and its slabs 1 .. NS - 1 are in
+    // flight into stages 1 .. NS - 1.  Slab s of the range lives in stage s % NS; after the barrier of
+    // B(k) (slab k + 1 landed, slab k read by every wave) slab k + NS goes into slab k's stage, so NS - 1
+    // slabs are in flight while one is read.  Stage offsets beyond the 16-bit offset of ds_read_b128
+    // ride on the base registers.
+    MICA_DEVICE void run_deep(const GemmParams &p, int8_t *smem, int wave, int m0, int n0, int ks0, int nk) {
         constexpr int NS = C::NS;
         static_assert(NS == 3 || NS == 4, "stages");
         static_assert((NS - 2) * C::kDma < 64, "vmcnt");
         const int lane = lane_id();
         const int wm = wave / C::WGN, wn = wave % C::WGN;
         const int r16 = lane & 15, kq = lane >> 4;
-        const int nk = p.K / QBK;  // even, at least 4
         const uint32_t lds0 = lds_addr(smem);
         uint32_t xa[2], wa[2];
 #pragma unroll
@@ -368,7 +370,7 @@ struct QTile {
         // the plan for slab `slab` (stage ST = slab % NS): zero-sized past the last slab, so every wave
         // issues the same instructions and the waits below count them
         auto plan = [&](int slab, auto st_c) {
-            return tile_plan(p, smem, wave, lane, m0, n0, slab, decltype(st_c)::value, slab < nk);
+            return tile_plan(p, smem, wave, lane, m0, n0, ks0 + slab, decltype(st_c)::value, slab < nk);
         };
         // A: k-step 0 of the slab in stage ST (in R0), its k-step 1 read into R1
         auto half_a = [&](auto st_c, auto first_c) {
@@ -454,6 +456,55 @@ struct QTile {
         const float a0 = f16_to_f32(v & 0xffff), a1 = f16_to_f32(v >> 16);
         const float b0 = f16_to_f32(r & 0xffff), b1 = f16_to_f32(r >> 16);
         return (uint32_t)f32_to_f16(a0 + b0) | ((uint32_t)f32_to_f16(a1 + b1) << 16);
+    }
+
+    // ---- a tile split along K over `parts` workgroups (gemm_i8_agpr_split_kernel), this one being part
+    // `part`: its int32 accumulators go to its slot t * parts + part of p.partials (slot = int32x4 vector
+    // v of thread x at (v * kQThreads + x) * 16), then it counts itself in p.arrivals[t].  The part that
+    // arrives last adds the other parts' slots to its accumulators, re-zeroes the count for the next
+    // launch and returns true (it runs the epilogue); the others return false.  Integer sums are exact
+    // in any order.  Slots move with device-scope (sc1) buffer stores and loads, written through to the
+    // device's coherence point and read from it; the count is a device-scope atomic taken after every
+    // wave's stores were acknowledged (vmcnt 0, then a workgroup barrier).  Nobody waits for another
+    // workgroup, so no co-residency is assumed.
+    static constexpr int kSlotVecs = NB * MB;
+    MICA_DEVICE bool split_fixup(const GemmParams &p, int8_t *smem, int t, int part, int parts) {
+        constexpr int kDeviceScope = 16;  // cache policy bits: sc1
+        const int tid = threadIdx.x;
+        const __amdgpu_buffer_rsrc_t rsrc_p = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)p.partials, 0, p.sk_grid * kSlotVecs * kQThreads * 16, kBufferFlags);
+        auto off = [&](int slot, int v) { return ((slot * kSlotVecs + v) * kQThreads + tid) * 16; };
+        const int mine = t * parts + part;
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                __builtin_amdgcn_raw_buffer_store_b128(acc[j][i], rsrc_p, off(mine, j * MB + i), 0, kDeviceScope);
+        wait_vmcnt<0>();   // this wave's partial sums reached the coherence point ...
+        __syncthreads();   // ... and every wave's, before the arrival is counted
+        int *flag = (int *)(smem + kQScale + kQScaleBuf);  // the second scale buffer (unused by a split tile)
+        if (tid == 0) *flag = __hip_atomic_fetch_add(p.arrivals + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*flag != parts - 1) return false;  // a later part finishes the tile
+        // each read-back is a round trip to the coherence point: a whole chunk of a slot's vectors goes
+        // out before any is added (left to the compiler, the loads of a slot went out a few at a time)
+        constexpr int kChunk = kSlotVecs <= 20 ? kSlotVecs : kSlotVecs / 2;
+        static_assert(kSlotVecs % kChunk == 0, "chunks");
+        for (int o = 0; o < parts; ++o) {
+            if (o == part) continue;
+            const int slot = t * parts + o;
+#pragma unroll
+            for (int c = 0; c < kSlotVecs; c += kChunk) {
+                v4i buf[kChunk];
+#pragma unroll
+                for (int v = 0; v < kChunk; ++v)
+                    buf[v] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_p, off(slot, c + v), 0, kDeviceScope);
+#pragma unroll
+                for (int v = 0; v < kChunk; ++v) acc[(c + v) / MB][(c + v) % MB] += buf[v];
+            }
+        }
+        if (tid == 0) __hip_atomic_store(p.arrivals + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
     }
 
     // ---- epilogue of tile (m0, n0) from acc, with its scales in buffer buf.  With has_next, the next
@@ -608,7 +659,7 @@ MICA_DEVICE void run_qphase(const GemmParams &p, int8_t *smem, __amdgpu_buffer_r
             if constexpr (C::NS > 3) Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 3, 3);
             wait_vmcnt<(C::NS - 1) * C::kDma>();  // scales and slab 0 landed (slabs 1 .. NS - 1 may be in flight)
             __builtin_amdgcn_s_barrier();
-            t.run_deep(p, smem, wave, m0, n0);
+            t.run_deep(p, smem, wave, m0, n0, 0, p.K / QBK);
             t.epilogue(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 0, false, 0, 0);
         }
         return;
@@ -736,6 +787,65 @@ __global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_small_kernel(GemmPa
     wait_vmcnt<0>();
 }
 
+// One round of tiles split along K (few tiles and a long K, e.g. a short request's projections):
+// p.sk_tiles tiles of 128 x 160 (SiLU: 128 x 256) over tiles_m x tiles_n (M-major), each in
+// parts = sk_grid / sk_tiles pieces of K.  Workgroup g is part g % parts of tile g / parts and runs
+// slabs [part nk / parts, (part + 1) nk / parts) of the nk 128-byte slabs (at least 4 of them; the
+// launcher checks), then split_fixup; the last part of each tile runs the epilogue.
+template <int EPI, int OUT, bool HAS_BIAS, bool HAS_RES>
+__global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_split_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kQSmem];
+    using C = std::conditional_t<EPI == MICA_EPI_SILU_MUL, QHalfM, QSmall>;
+    using Tile = QTile<C, EPI, OUT, HAS_BIAS, HAS_RES>;
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, p.M * p.lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, p.N * p.ldb, kBufferFlags);
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int parts = p.sk_grid / p.sk_tiles;
+    const int t = (int)blockIdx.x / parts, part = (int)blockIdx.x - t * parts;
+    const int m0 = (t % p.tiles_m) * C::BM, n0 = (t / p.tiles_m) * C::BN;
+    const int nk = p.K / QBK;
+    const int k0 = part * nk / parts, k1 = (part + 1) * nk / parts;
+    Tile tile;
+    Tile::scales_dma(p, smem, wave, 0, m0, n0);
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) Tile::tile_dma(p, smem, rsrc_a, rsrc_b, wave, m0, n0, k0 + s, s);
+    wait_vmcnt<(C::NS - 1) * C::kDma>();  // scales and slab k0 landed (the next NS - 1 may be in flight)
+    __builtin_amdgcn_s_barrier();
+    tile.run_deep(p, smem, wave, m0, n0, k0, k1 - k0);
+    if (tile.split_fixup(p, smem, t, part, parts))
+        tile.epilogue(p, smem, rsrc_a, rsrc_b, wave, m0, n0, 0, false, 0, 0);
+    // every store of this workgroup has left before the waves end
+    wait_vmcnt<0>();
+}
+
+// Explicit instantiations: hipcc's host pass left the launch stubs of the variants without a residual
+// undefined when they were only instantiated implicitly by the launches below.
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SILU_MUL, MICA_BF16, false, false>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_BF16, false, false>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_BF16, true, false>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_BF16, false, true>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_BF16, true, true>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_FP16, false, false>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_FP16, true, false>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_FP16, false, true>(GemmParams);
+template __global__ void gemm_i8_agpr_split_kernel<MICA_EPI_SCALE, MICA_FP16, true, true>(GemmParams);
+
+template <int EPI, int OUT>
+int agpr_split_out(const GemmParams &p, bool has_bias, bool has_res, hipStream_t st) {
+    dim3 g(p.sk_grid), b(kQThreads);
+#define MICA_QX(B_, R_) hipLaunchKernelGGL((gemm_i8_agpr_split_kernel<EPI, OUT, B_, R_>), g, b, 0, st, p)
+    if constexpr (EPI == MICA_EPI_SILU_MUL) {
+        MICA_QX(false, false);
+    } else {
+        if (has_bias && has_res) MICA_QX(true, true);
+        else if (has_bias) MICA_QX(true, false);
+        else if (has_res) MICA_QX(false, true);
+        else MICA_QX(false, false);
+    }
+#undef MICA_QX
+    return mica_err(hipGetLastError());
+}
+
 template <int OUT>
 int agpr_small_out(const GemmParams &p, int grid, bool has_bias, bool has_res, hipStream_t st) {
     dim3 g(grid), b(kQThreads);
@@ -808,5 +918,31 @@ int mica_gemm::agpr_small_launch(const GemmParams &p, int out_dtype, int grid, b
                                  hipStream_t st) {
     if (out_dtype == MICA_BF16) return agpr_small_out<MICA_BF16>(p, grid, has_bias, has_res, st);
     if (out_dtype == MICA_FP16) return agpr_small_out<MICA_FP16>(p, grid, has_bias, has_res, st);
+    return MICA_MISS_ARG;
+}
+
+// Tile shape of the split schedule: 128 x 160 for the SCALE epilogue, 128 x 256 for SiLU (whose waves
+// need 128 columns of gate / up pairs).
+int mica_gemm::agpr_split_tile_n(int epilogue) { return epilogue == MICA_EPI_SILU_MUL ? QHalfM::BN : QSmall::BN; }
+// Bytes of one part's slot of partial sums.
+long long mica_gemm::agpr_split_slot_bytes(int epilogue) {
+    return epilogue == MICA_EPI_SILU_MUL ? (long long)QHalfM::MB * QHalfM::NB * kQThreads * 16
+                                         : (long long)QSmall::MB * QSmall::NB * kQThreads * 16;
+}
+static_assert(QSmall::BM == 128 && QHalfM::BM == 128, "split tiles are 128 rows");
+
+// Launch of the split schedule in p (tiles_m x tiles_n tiles of 128 x agpr_split_tile_n columns,
+// sk_tiles of them, sk_grid workgroups = sk_tiles x parts, arrivals zero, partials with sk_grid slots).
+// The same conditions as agpr_launch, and K / 128 at least 4 x parts.
+int mica_gemm::agpr_split_launch(const GemmParams &p, int epilogue, int out_dtype, bool has_bias, bool has_res,
+                                 hipStream_t st) {
+    if (p.sk_tiles <= 0 || p.sk_grid % p.sk_tiles != 0 || p.K / QBK < 4 * (p.sk_grid / p.sk_tiles))
+        return MICA_MISS_ARG;
+    if (epilogue == MICA_EPI_SILU_MUL) {
+        if (out_dtype != MICA_BF16 || has_bias || has_res) return MICA_MISS_ARG;
+        return agpr_split_out<MICA_EPI_SILU_MUL, MICA_BF16>(p, false, false, st);
+    }
+    if (out_dtype == MICA_BF16) return agpr_split_out<MICA_EPI_SCALE, MICA_BF16>(p, has_bias, has_res, st);
+    if (out_dtype == MICA_FP16) return agpr_split_out<MICA_EPI_SCALE, MICA_FP16>(p, has_bias, has_res, st);
     return MICA_MISS_ARG;
 }

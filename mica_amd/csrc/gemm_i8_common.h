@@ -143,6 +143,10 @@ int agpr_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool
                 hipStream_t st);
 int agpr_narrow_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res, hipStream_t st);
 int agpr_small_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res, hipStream_t st);
+// the AGPR kernel's split-along-K schedule for few 128-row tiles (gemm_i8_agpr.hip)
+int agpr_split_tile_n(int epilogue);
+long long agpr_split_slot_bytes(int epilogue);
+int agpr_split_launch(const GemmParams &p, int epilogue, int out_dtype, bool has_bias, bool has_res, hipStream_t st);
 
 }  // namespace mica_gemm
 

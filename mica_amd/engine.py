@@ -44,7 +44,7 @@ class PrefillEngine:
         self.device = stack.device
         self.graph = bool(graph) and self.device.type == "cuda"
         self.bucket, self.graph_max = int(bucket), int(graph_max)
-        self.graphs, self.pool = {}, None
+        self.graphs, self.pool, self.side = {}, None, None
         self.captures = 0
         self.header = None           # (token ids [Hc] on the device, PrefixState), Hc = aligned header length
         if header is not None:
@@ -96,14 +96,18 @@ class PrefillEngine:
         fn = lambda: self.stack.forward_last(g.ids, batch, g.rows, g.lo, g.cnt, prefix=prefix)  # noqa: E731
         if self.pool is None:
             self.pool = torch.cuda.graph_pool_handle()
-        side = torch.cuda.Stream(device=self.device)
+        # one side stream for every warm-up and capture: the warm-ups give it the GEMM split workspace
+        # (int8_kernels.gemm_workspace, per stream), which the captured GEMMs then use
+        if self.side is None:
+            self.side = torch.cuda.Stream(device=self.device)
+        side = self.side
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side), torch.no_grad():
             for _ in range(GRAPH_WARMUP):
                 fn()
         torch.cuda.current_stream(self.device).wait_stream(side)
         g.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g.graph, pool=self.pool), torch.no_grad():
+        with torch.cuda.graph(g.graph, pool=self.pool, stream=side), torch.no_grad():
             g.out = fn()
         self.graphs[batch, width, prefix is not None] = g
         self.captures += 1

@@ -175,6 +175,22 @@ def gemm_workspace(dev):
     return ws.data_ptr(), ws.numel()
 
 
+# QLinear's GEMMs give the kernel the split workspace (mm_i8's split=True) when this allows it.
+SPLIT = {"auto": True}
+
+
+def auto_split(dev):
+    """split= for a GEMM on torch's current stream: True eagerly (the first call allocates that stream's
+    workspace), and under HIP-graph capture only when the capturing stream already has one (a
+    workspace cannot be made inside a capture; capture on a stream that ran the same work eagerly
+    first, as engine.PrefillEngine does).  SPLIT["auto"] = False turns the split schedules off."""
+    if not SPLIT["auto"]:
+        return False
+    if torch.cuda.is_current_stream_capturing():
+        return (dev.index, torch.cuda.current_stream(dev).cuda_stream) in _WORKSPACE
+    return True
+
+
 def act_quant(x, inv_smooth=None, rounding="even"):
     """Per-token INT8 quantization of a 2-D activation (int8_kernels.py:325-353)."""
     if x.dim() != 2 or x.device.type != "cuda" or x.dtype not in DT:
@@ -207,10 +223,13 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
     Extensions: ``residual`` ([M, N] of out_dtype) is added after the output rounding;
     ``epilogue='silu_mul'`` treats qw as gate/up rows interleaved in groups of 64
     (int8_runtime.pack_gate_up) and returns bf16(bf16(silu(gate)) * up) of shape [M, N / 2];
-    ``split=True`` lets the kernel split a partial last round of at most CUs / 4 tiles along K over four
-    workgroups each when K >= 8192 and M <= 256 or the epilogue is 'silu_mul' (exact int32 partial sums
-    through a per-stream workspace; same bits as the default schedule, which runs such a round as
-    128 x 128 quarter tiles).  ``requant=True`` returns the per-token int8 quantization (q, s) of the
+    ``split=True`` gives the kernel a per-stream workspace (``gemm_workspace``) for schedules that split
+    tiles along K, with exact int32 partial sums and so the same bits as without it: for 16-bit outputs
+    with K >= 8192 whose output fits at most CUs / 3 tiles of 128 x 160 (128 x 256 for 'silu_mul') -- a
+    short request's down projection -- every tile in K / 2560 parts; for int32 / fp32 outputs a partial
+    last round of at most CUs / 4 tiles of 256 x 256 over four workgroups each when K >= 8192 and
+    M <= 256 (the default schedule runs such a round as 128 x 128 quarter tiles).  ``requant=True``
+    returns the per-token int8 quantization (q, s) of the
     output instead of the output (the next QLinear's input, e.g. h of the MLP for the down projection):
     a second launch, because each row's scale needs the absmax of the whole row, which spans every
     column tile of the GEMM.

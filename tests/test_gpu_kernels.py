@@ -501,11 +501,11 @@ def test_gemm_headline_full_size(gpu):
 
 @pytest.mark.parametrize("m,n,k,epi", [
     (4096, 4352, 8192, "none"),      # 272 tiles: 256 whole, then 16 as 128 x 128 quarters (M > 256)
-    (700, 2560, 9728, "residual"),   # 30 tiles as quarters, residual epilogue
-    (300, 3072, 8192, "silu_mul"),   # 24 tiles split along K over 96 workgroups, then the SiLU epilogue
-    (200, 2560, 8256, "none"),       # M <= 256: split; 129 slabs per tile, so ranges straddle tiles
-    (256, 2560, 9728, "none"),       # M <= 256: split, 4 contributors of 38 slabs per tile
-    (512, 2560, 4096, "none"),       # K below the split threshold: quarters, workspace unused
+    (700, 2560, 9728, "residual"),   # 96 tiles of 128 x 160 leave room for 2 parts only: quarters
+    (300, 3072, 8192, "silu_mul"),   # 36 tiles of 128 x 256 in 3 parts along K, then the SiLU epilogue
+    (200, 2560, 8256, "none"),       # int32: 256 x 256 stream-K split, ranges straddle tiles; bf16: quarters
+    (256, 2560, 9728, "none"),       # 32 tiles of 128 x 160 in 3 parts (the int32 output: stream-K split)
+    (512, 2560, 4096, "none"),       # K below both split thresholds: quarters, workspace unused
 ])
 def test_gemm_split_schedule_bit_exact(gpu, m, n, k, epi):
     """split=True (a workspace: remainder tiles split along K where that serves best, int32 partial sums
@@ -535,6 +535,60 @@ def test_gemm_split_schedule_bit_exact(gpu, m, n, k, epi):
     for rep in range(2):
         y = int8_kernels.mm_i8(tA, tsa, tB, tsb, residual=None if res is None else to_gpu_bf16(res), split=True)
         assert_equal_diag(bits_of(y), ref, f"bf16 (call {rep})")
+
+
+@pytest.mark.parametrize("m,n,k,epi", [
+    (128, 2560, 9728, "residual"),   # one short request's down projection: 16 tiles of 128 x 160, 3 parts
+    (128, 4096, 8192, "silu_mul"),   # SiLU epilogue: 16 tiles of 128 x 256, 3 parts of 21 or 22 slabs
+    (77, 6144, 8192, "none"),        # ragged M (51 empty rows in every tile), 39 tiles, 3 parts
+    (512, 2560, 9728, "bias_fp16"),  # fp16 output with a bias, 64 tiles, 3 parts
+    (64, 2560, 16384, "none"),       # the most parts: 128 slabs in 6 parts, 16 tiles
+])
+def test_gemm_small_m_split_bit_exact(gpu, m, n, k, epi):
+    """Few 128-row tiles and a long K, with a workspace: every tile is split along K over several
+    workgroups whose int32 partial sums the tile's last part adds.  Integer sums are exact in any order,
+    so the output equals the unsplit schedule's bit for bit and the oracle's (the SiLU within the
+    one-ulp bound of its own test), on two calls in a row (the arrival counts come back to zero)."""
+    note(f"gemm small-M split m={m} n={n} k={k} epi={epi}")
+    rng = np.random.default_rng(m + n + k + 7)
+    A, B, sa, sb = _rand_gemm(rng, m, n, k)
+    tA, tB, tsa, tsb = (torch.from_numpy(v).cuda() for v in (A, B, sa, sb))
+    if epi == "silu_mul":
+        n2 = n // 2
+        grp = B.reshape(n // 128, 2, 64, k)
+        sgr = sb.reshape(n // 128, 2, 64)
+        gv = O.epilogue(O.int_gemm(A, grp[:, 0].reshape(n2, k)), sa, sgr[:, 0].reshape(n2))
+        uv = O.epilogue(O.int_gemm(A, grp[:, 1].reshape(n2, k)), sa, sgr[:, 1].reshape(n2))
+        plain = bits_of(int8_kernels.mm_i8(tA, tsa, tB, tsb, epilogue="silu_mul"))
+        assert_within_one_ulp(plain, O.silu_mul(gv, uv))
+        for rep in range(2):
+            got = bits_of(int8_kernels.mm_i8(tA, tsa, tB, tsb, epilogue="silu_mul", split=True))
+            assert np.array_equal(got, plain), f"split SiLU output differs from the unsplit one (call {rep})"
+        return
+    acc = O.int_gemm(A, B)
+    kw, res, bias = {}, None, None
+    if epi == "residual":
+        res = act_bits(rng, (m, n), outliers=0)
+        kw["residual"] = to_gpu_bf16(res)
+        ref = O.f32_to_bf16(O.bf16_to_f32(O.epilogue(acc, sa, sb)) + O.bf16_to_f32(res))
+    elif epi == "bias_fp16":
+        bias = rng.uniform(-1, 1, n).astype(np.float32)
+        kw.update(bias=torch.from_numpy(bias).cuda(), out_dtype=torch.float16)
+        ref = O.epilogue(acc, sa, sb, bias, "fp16")
+    else:
+        ref = O.epilogue(acc, sa, sb)
+
+    def out(**extra):
+        y = int8_kernels.mm_i8(tA, tsa, tB, tsb, kw.get("bias"), kw.get("out_dtype", torch.bfloat16),
+                               residual=kw.get("residual"), **extra)
+        return y.cpu().numpy() if y.dtype == torch.float16 else bits_of(y)
+
+    plain = out()
+    assert_equal_diag(plain, ref, "unsplit")
+    for rep in range(2):
+        got = out(split=True)
+        assert_equal_diag(got, ref, f"split (call {rep})")
+        assert np.array_equal(got.view(np.uint16), plain.view(np.uint16)), f"split != unsplit (call {rep})"
 
 
 @pytest.mark.parametrize("m,n,k", [(32768, 6144, 2560), (32768, 2560, 4096)])

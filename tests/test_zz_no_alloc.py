@@ -71,9 +71,12 @@ def test_scratch_size_is_stated(gpu):
 
 @pytest.mark.parametrize("calls", [
     # (m, n, k, epilogue) per call; the second call of each pair is smaller
-    ((256, 2560, 9728, "scale"), (128, 1280, 8192, "scale")),       # split rounds of 10 then 5 tiles
-    ((200, 2048, 8192, "silu_mul"), (64, 1024, 8192, "silu_mul")),  # SiLU epilogue split, 8 then 4 tiles
-    ((512, 2560, 4096, "scale"), (300, 1000, 2576, "scale")),       # no split: quarter / half tiles
+    # split rounds of 10 then 5 tiles of 256 x 256 (int32), 32 then 8 of 128 x 160 in 3 parts (bf16)
+    ((256, 2560, 9728, "scale"), (128, 1280, 8192, "scale")),
+    # SiLU epilogue: 16 then 4 tiles of 128 x 256 in 3 parts
+    ((200, 2048, 8192, "silu_mul"), (64, 1024, 8192, "silu_mul")),
+    # no split (K below both thresholds): quarter / half tiles
+    ((512, 2560, 4096, "scale"), (300, 1000, 2576, "scale")),
 ])
 def test_noalloc_matches_mica_mm_i8_twice(gpu, calls):
     rng = np.random.default_rng(7)
@@ -95,14 +98,15 @@ def test_noalloc_matches_mica_mm_i8_twice(gpu, calls):
 
 
 def test_noalloc_rejects_a_split_round_beyond_the_scratch(gpu):
-    """24 SiLU tiles at K = 8192 would split over 96 workgroups: more than the scratch holds."""
-    note("noalloc reject m=300 n=3072 k=8192 silu")
+    """17 tiles of 256 x 256 with int32 outputs at K = 8192, M <= 256 would split over 68 workgroups:
+    more than the scratch holds."""
+    note("noalloc reject m=200 n=4352 k=8192 int32")
     rng = np.random.default_rng(3)
-    A, B, sa, sb = _operands(rng, 300, 3072, 8192, gpu)
-    out = torch.empty((300, 1536), dtype=torch.bfloat16, device=gpu)
-    assert _call(True, A, B, sa, sb, out, _lib.BF16, _lib.EPI_SILU_MUL) == 5  # MICA_MISS_RANGE
+    A, B, sa, sb = _operands(rng, 200, 4352, 8192, gpu)
+    out = torch.empty((200, 4352), dtype=torch.int32, device=gpu)
+    assert _call(True, A, B, sa, sb, out, _lib.INT32, _lib.EPI_SCALE) == 5  # MICA_MISS_RANGE
     # the existing entry point serves it (its workspace is sized for every CU)
-    assert _call(False, A, B, sa, sb, out, _lib.BF16, _lib.EPI_SILU_MUL) == 0
+    assert _call(False, A, B, sa, sb, out, _lib.INT32, _lib.EPI_SCALE) == 0
     torch.cuda.synchronize()
 
 
@@ -115,7 +119,7 @@ def _capture_child():
     dev = torch.device("cuda", 0)
     L = _lib.load()
     rng = np.random.default_rng(21)
-    m, n, k = 256, 2560, 9728                    # a split round of 10 tiles
+    m, n, k = 256, 2560, 9728                    # split: 10 tiles of 256 x 256 (int32), 32 of 128 x 160 (bf16)
     A, B, sa, sb = _operands(rng, m, n, k, dev)
     eager_i32 = torch.empty((m, n), dtype=torch.int32, device=dev)
     eager_bf16 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
