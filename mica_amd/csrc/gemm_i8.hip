@@ -863,6 +863,18 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
         // Fewer whole tiles than CUs, too many for four quarters each to fit one round (the halves
         // schedule above): one round of 128 x 160 tiles when they fit it (the AGPR kernel's small tiles,
         // same bits).  Each CU then streams (128 + 160) rows of operands instead of a half tile's 384.
+        // The SiLU epilogue at M <= 128 (a short request's gate+up: the M-halves schedule leaves the
+        // lower halves without rows): one round of 128 x 128 tiles, one gate / up group each, when they
+        // fit one (same bits).
+        const long long tiles_silu = (long long)((M + 127) / 128) * ((N + 127) / 128);
+        if (kAgpr && kSmall && epilogue == MICA_EPI_SILU_MUL && M <= 128 && cus > 0 && tiles < cus &&
+            tiles_silu <= cus && K >= 512 && ldc % 8 == 0 && Nout % 8 == 0) {
+            p.tiles_m = (M + 127) / 128;
+            p.tiles_n = (N + 127) / 128;
+            p.dp_tiles = (int)tiles_silu;
+            p.mhalf_tiles = 0;
+            return agpr_silu_small_launch(p, (int)tiles_silu, st);
+        }
         const long long tiles_small = (long long)((M + 127) / 128) * ((N + 159) / 160);
         const bool small = kAgpr && kSmall && epilogue == MICA_EPI_SCALE && p.half_tiles == tiles && cus > 0 &&
                            4 * tiles > cus && tiles_small <= cus && K >= 512 &&

@@ -78,6 +78,12 @@ using QNarrow = QCfg<256, 160, 2, 4, 1>;
 // stages, whose DMA waited on memory latency).  Such a tile is bound by its DMA feed, (128 + 160) rows x
 // K against 384 rows for the 256 x 128 half tile it replaces.
 using QSmall = QCfg<128, 160, 4, 4, 1>;
+// The SiLU epilogue's counterpart for launches of at most 128 rows (a short request's gate+up): one round
+// of 128 x 128 tiles, each one 64-row group of gate weights and its 64 up rows, on waves of 32 x 128
+// stacked along M (2 x 8 MFMA tiles, 64 accumulators per lane), so every wave pairs gate and up columns
+// in its own lanes.  128 x 19456 x 2560: 152 tiles on 152 CUs, where the 128 x 256 M-halves keep 76
+// busy (and 76 with no rows).
+using QSiluSmall = QCfg<128, 128, 4, 4, 1>;
 
 // LDS: the A stages, the B stages, then (at a fixed place past the largest stage set) two buffers of
 // tile scales (sa, sb, bias: 3 x 256 fp32), for this tile and the next.
@@ -88,7 +94,7 @@ static_assert(kQSmem <= 160 * 1024, "LDS");
 template <class C>
 constexpr bool stages_fit = C::NS * (C::kAHalf + C::kBHalf) <= kQScale;
 static_assert(stages_fit<QFull> && stages_fit<QHalfN> && stages_fit<QHalfM> && stages_fit<QQuart> &&
-                  stages_fit<QNarrow> && stages_fit<QSmall>, "stages");
+                  stages_fit<QNarrow> && stages_fit<QSmall> && stages_fit<QSiluSmall>, "stages");
 
 // This lane's index, computed afresh where it is used (a few VALU operations per tile instead of a
 // register held across the persistent loop).  The wave index lives in an SGPR.
@@ -787,6 +793,26 @@ __global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_small_kernel(GemmPa
     wait_vmcnt<0>();
 }
 
+// One round of 128 x 128 tiles (dp_tiles of them over tiles_m x tiles_n, one per workgroup), SiLU
+// epilogue (bf16 out).
+__global__ __launch_bounds__(kQThreads, 1) void gemm_i8_agpr_silu_small_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kQSmem];
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void *)p.A, 0, p.M * p.lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void *)p.B, 0, p.N * p.ldb, kBufferFlags);
+    const int tm_n = p.tiles_m, tn_n = p.tiles_n;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    run_qphase<QSiluSmall, MICA_EPI_SILU_MUL, MICA_BF16, false, false>(
+        p, smem, rsrc_a, rsrc_b, wave, blockIdx.x, p.dp_tiles, gridDim.x, [&](int h, int &m0, int &n0) {
+            int tm, tn;
+            tile_of(h, tm_n, tn_n, tm, tn);
+            m0 = tm * QSiluSmall::BM;
+            n0 = tn * QSiluSmall::BN;
+            return true;
+        });
+    // every store of this workgroup has left before the waves end
+    wait_vmcnt<0>();
+}
+
 // One round of tiles split along K (few tiles and a long K, e.g. a short request's projections):
 // p.sk_tiles tiles of 128 x 160 (SiLU: 128 x 256) over tiles_m x tiles_n (M-major), each in
 // parts = sk_grid / sk_tiles pieces of K.  Workgroup g is part g % parts of tile g / parts and runs
@@ -919,6 +945,13 @@ int mica_gemm::agpr_small_launch(const GemmParams &p, int out_dtype, int grid, b
     if (out_dtype == MICA_BF16) return agpr_small_out<MICA_BF16>(p, grid, has_bias, has_res, st);
     if (out_dtype == MICA_FP16) return agpr_small_out<MICA_FP16>(p, grid, has_bias, has_res, st);
     return MICA_MISS_ARG;
+}
+
+// Launch of the 128 x 128 SiLU kernel for one round of tiles (p.tiles_m / p.tiles_n count 128-row /
+// 128-column tiles of the gate / up weight rows; bf16 output; the same conditions as agpr_launch).
+int mica_gemm::agpr_silu_small_launch(const GemmParams &p, int grid, hipStream_t st) {
+    hipLaunchKernelGGL(gemm_i8_agpr_silu_small_kernel, dim3(grid), dim3(kQThreads), 0, st, p);
+    return mica_err(hipGetLastError());
 }
 
 // Tile shape of the split schedule: 128 x 160 for the SCALE epilogue, 128 x 256 for SiLU (whose waves

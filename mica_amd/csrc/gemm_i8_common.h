@@ -143,6 +143,7 @@ int agpr_launch(const GemmParams &p, int epilogue, int out_dtype, int grid, bool
                 hipStream_t st);
 int agpr_narrow_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res, hipStream_t st);
 int agpr_small_launch(const GemmParams &p, int out_dtype, int grid, bool has_bias, bool has_res, hipStream_t st);
+int agpr_silu_small_launch(const GemmParams &p, int grid, hipStream_t st);
 // the AGPR kernel's split-along-K schedule for few 128-row tiles (gemm_i8_agpr.hip)
 int agpr_split_tile_n(int epilogue);
 long long agpr_split_slot_bytes(int epilogue);
