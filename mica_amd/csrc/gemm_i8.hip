@@ -863,12 +863,15 @@ int mm_i8_run(const int8_t *A, int lda, const int8_t *B, int ldb, const float *s
         // Fewer whole tiles than CUs, too many for four quarters each to fit one round (the halves
         // schedule above): one round of 128 x 160 tiles when they fit it (the AGPR kernel's small tiles,
         // same bits).  Each CU then streams (128 + 160) rows of operands instead of a half tile's 384.
-        // The SiLU epilogue at M <= 128 (a short request's gate+up: the M-halves schedule leaves the
-        // lower halves without rows): one round of 128 x 128 tiles, one gate / up group each, when they
-        // fit one (same bits).
+        // The SiLU epilogue with fewer whole tiles than CUs: one round of 128 x 128 tiles, one gate / up
+        // group each, when they fit one (same bits).  Each streams 256 rows of operands against the
+        // M-halves' 384, on up to twice as many CUs (M <= 128: the lower halves had no rows).  Measured
+        // on one box (us, M-halves or whole tiles / these): 128 x 19456 x 2560 21.5 / 14.2, 300 x 3072 x
+        // 2560 17.8 / 11.2, 700 x 3072 x 2560 19.1 / 12.7; over more than one round they lose
+        // (256 x 19456 x 2560: 23.2 / 25.4) or tie (512 x 19456 x 2560: 37.7 / 36.6).
         const long long tiles_silu = (long long)((M + 127) / 128) * ((N + 127) / 128);
-        if (kAgpr && kSmall && epilogue == MICA_EPI_SILU_MUL && M <= 128 && cus > 0 && tiles < cus &&
-            tiles_silu <= cus && K >= 512 && ldc % 8 == 0 && Nout % 8 == 0) {
+        if (kAgpr && kSmall && epilogue == MICA_EPI_SILU_MUL && cus > 0 && tiles < cus && tiles_silu <= cus &&
+            K >= 512 && ldc % 8 == 0 && Nout % 8 == 0) {
             p.tiles_m = (M + 127) / 128;
             p.tiles_n = (N + 127) / 128;
             p.dp_tiles = (int)tiles_silu;

@@ -374,9 +374,10 @@ def test_gemm_extreme_accumulators(gpu):
 
 @pytest.mark.parametrize("m", [1, 100, 128, 200, 300, 700])
 def test_gemm_silu_m_halves(gpu, m):
-    """The fused gate+up SiLU epilogue when the last round runs as 128 x 256 halves along M (a lower
-    half wholly past M skipped, one cut by it, or both full) or, at M <= 128, as one round of 128 x 128
-    tiles, within one bf16 ulp of the oracle."""
+    """The fused gate+up SiLU epilogue at N = 3072 runs as one round of 128 x 128 tiles (one gate / up
+    group each; rows past M in the last tile row), within one bf16 ulp of the oracle; with 32768 more
+    weight rows the same columns come from whole tiles and 128 x 256 halves along M (a lower half wholly
+    past M skipped, one cut by it, or both full), with the same bits."""
     note(f"gemm silu m-halves m={m}")
     rng = np.random.default_rng(m + 5)
     n, k = 3072, 2560
@@ -387,13 +388,13 @@ def test_gemm_silu_m_halves(gpu, m):
     uv = O.epilogue(O.int_gemm(A, grp[:, 1].reshape(n // 2, k)), sa, sgr[:, 1].reshape(n // 2))
     y = int8_kernels.mm_i8(*(torch.from_numpy(v).cuda() for v in (A, sa, B, sb)), epilogue="silu_mul")
     assert_within_one_ulp(bits_of(y), O.silu_mul(gv, uv))
-    if m <= 128:
-        # M <= 128 runs as 128 x 128 tiles of one gate / up group each; the same rows inside a 300-row
-        # launch (M-halves) give the same bits: rows are independent
-        A2 = np.concatenate([A, rng.integers(-127, 128, (300 - m, k), dtype=np.int8)])
-        sa2 = np.concatenate([sa, rng.uniform(1e-3, 1e-2, 300 - m).astype(np.float32)])
-        y2 = int8_kernels.mm_i8(*(torch.from_numpy(v).cuda() for v in (A2, sa2, B, sb)), epilogue="silu_mul")
-        assert np.array_equal(bits_of(y2)[:m], bits_of(y)), "128 x 128 SiLU tiles differ from the M-halves"
+    # here every M runs as one round of 128 x 128 tiles of one gate / up group each; with 32768 more
+    # weight rows (more 128 x 128 tiles than CUs: whole tiles, then M-halves or whole tiles for the tail)
+    # the same columns come out with the same bits: rows and column groups are independent
+    B2 = np.concatenate([B, rng.integers(-127, 128, (32768, k), dtype=np.int8)])
+    sb2 = np.concatenate([sb, rng.uniform(1e-3, 1e-2, 32768).astype(np.float32)])
+    y2 = int8_kernels.mm_i8(*(torch.from_numpy(v).cuda() for v in (A, sa, B2, sb2)), epilogue="silu_mul")
+    assert np.array_equal(bits_of(y2)[:, : n // 2], bits_of(y)), "128 x 128 SiLU tiles differ from the other schedules"
 
 
 def test_gemm_requant_output(gpu):
