@@ -132,9 +132,10 @@ def _on(dev, call):
         return call()
 
 
-def _run(dev, name, fn, *args):
-    """Launch through the C ABI on the current stream; returns True, or None on a miss."""
-    rc = _lib.check(_on(dev, lambda: fn(*args, _stream(dev))), name)
+def _run(dev, name, fn, *args, stream=None):
+    """Launch through the C ABI on the current stream (``stream``: its handle, when the caller has it
+    already); returns True, or None on a miss."""
+    rc = _lib.check(_on(dev, lambda: fn(*args, _stream(dev) if stream is None else stream)), name)
     if rc > 0:
         return _miss(_lib.status_name(rc))
     _launched()
@@ -146,16 +147,20 @@ def _gpu_ok(dev):
 
 
 _WORKSPACE = {}
+_WS_PTR = {}     # (device index, stream handle) -> (pointer, bytes) of _WORKSPACE's tensor
 _WS_LOCK = threading.Lock()
 
 
-def gemm_workspace(dev):
-    """The GEMM's split-tile workspace for torch's current stream on ``dev``: allocated (zeroed) once
-    per (device, stream) and kept for the life of the process, so a HIP graph that captured it
-    stays valid; every launch leaves its counters zero again.  Returns (pointer, bytes).  It cannot
-    be first allocated inside a HIP-graph capture (RuntimeError): allocate it on the stream before."""
-    stream = torch.cuda.current_stream(dev)
-    key = (dev.index, stream.cuda_stream)
+def gemm_workspace(dev, stream=None):
+    """The GEMM's split-tile workspace for torch's current stream on ``dev`` (``stream``: its handle,
+    when the caller has it already): allocated (zeroed) once per (device, stream) and kept for the
+    life of the process, so a HIP graph that captured it stays valid; every launch leaves its counters
+    zero again.  Returns (pointer, bytes).  It cannot be first allocated inside a HIP-graph capture
+    (RuntimeError): allocate it on the stream before."""
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream if stream is None else stream)
+    got = _WS_PTR.get(key)
+    if got is not None:
+        return got
     ws = _WORKSPACE.get(key)
     if ws is None:
         if torch.cuda.is_current_stream_capturing():
@@ -172,23 +177,33 @@ def gemm_workspace(dev):
                     raise RuntimeError(f"mica_mm_i8_workspace_bytes({dev.index}) failed: {nbytes}")
                 ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
                 _WORKSPACE[key] = ws
+                _WS_PTR[key] = (ws.data_ptr(), ws.numel())
     return ws.data_ptr(), ws.numel()
 
 
-# QLinear's GEMMs give the kernel the split workspace (mm_i8's split=True) when this allows it.
+# QLinear's GEMMs pass mm_i8(..., split="auto"): the split workspace when this allows it.
 SPLIT = {"auto": True}
 
 
-def auto_split(dev):
-    """split= for a GEMM on torch's current stream: True eagerly (the first call allocates that stream's
-    workspace), and under HIP-graph capture only when the capturing stream already has one (a
-    workspace cannot be made inside a capture; capture on a stream that ran the same work eagerly
-    first, as engine.PrefillEngine does).  SPLIT["auto"] = False turns the split schedules off."""
+def _auto_workspace(dev, stream):
+    """mm_i8's split="auto": the workspace of (dev, stream) -- made by the first such call on an eager
+    stream; under HIP-graph capture only one the capturing stream already has (a workspace cannot be
+    made inside a capture; capture on a stream that ran the same work eagerly first, as
+    engine.PrefillEngine does) -- else none.  SPLIT["auto"] = False turns the split schedules off."""
     if not SPLIT["auto"]:
-        return False
+        return None, 0
+    got = _WS_PTR.get((dev.index, stream))
+    if got is not None:
+        return got
     if torch.cuda.is_current_stream_capturing():
-        return (dev.index, torch.cuda.current_stream(dev).cuda_stream) in _WORKSPACE
-    return True
+        return None, 0
+    return gemm_workspace(dev, stream)
+
+
+def auto_split(dev):
+    """Whether mm_i8(..., split="auto") gives a GEMM on torch's current stream a workspace (making it
+    now on an eager stream that has none)."""
+    return _auto_workspace(_dev(dev), _stream(_dev(dev)))[0] is not None
 
 
 def act_quant(x, inv_smooth=None, rounding="even"):
@@ -223,7 +238,8 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
     Extensions: ``residual`` ([M, N] of out_dtype) is added after the output rounding;
     ``epilogue='silu_mul'`` treats qw as gate/up rows interleaved in groups of 64
     (int8_runtime.pack_gate_up) and returns bf16(bf16(silu(gate)) * up) of shape [M, N / 2];
-    ``split=True`` gives the kernel a per-stream workspace (``gemm_workspace``) for schedules that split
+    ``split=True`` gives the kernel a per-stream workspace (``gemm_workspace``; ``split="auto"``: the one
+    ``_auto_workspace`` allows, the choice of QLinear's GEMMs) for schedules that split
     tiles along K, with exact int32 partial sums and so the same bits as without it: for 16-bit outputs
     with K >= 8192 whose output fits at most CUs / 3 tiles of 128 x 160 (128 x 256 for 'silu_mul') -- a
     short request's down projection -- every tile in K / 2560 parts; for int32 / fp32 outputs a partial
@@ -266,11 +282,16 @@ def mm_i8(qx, sx, qw, sw, bias=None, out_dtype=torch.bfloat16, residual=None, ep
     if not _aligned(qx, qw, sx, sw, out, *extra):
         return _miss("align")
     L = _lib.load()
-    ws, ws_bytes = gemm_workspace(_dev(qx.device)) if split else (None, 0)
+    dev = _dev(qx.device)
+    st = _stream(dev)
+    if split == "auto":
+        ws, ws_bytes = _auto_workspace(dev, st)
+    else:
+        ws, ws_bytes = gemm_workspace(dev, st) if split else (None, 0)
     ok = _run(qx.device, "mica_mm_i8", L.mica_mm_i8, qx.data_ptr(), k, qw.data_ptr(), k, sx.data_ptr(),
               sw.data_ptr(), None if bias is None else bias.data_ptr(),
               None if residual is None else residual.data_ptr(), n_out, out.data_ptr(), n_out, DT[out_dtype],
-              m, n, k, EPILOGUE[epilogue], ws, ws_bytes)
+              m, n, k, EPILOGUE[epilogue], ws, ws_bytes, stream=st)
     if not ok:
         return None
     return act_quant(out) if requant else out

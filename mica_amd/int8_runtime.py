@@ -159,7 +159,7 @@ class QLinear(nn.Module):
 
     def _mm(self, qx, sx, qw, sw, b, residual=None):
         return _hit(aot.mm_i8(qx, sx, qw, sw, b, self.out_dtype, residual=residual,
-                              split=aot.auto_split(qx.device)), "mm_i8")
+                              split="auto"), "mm_i8")
 
     def rows_forward(self, x, ranges):
         """Quantize once, one GEMM per output-row range (int8_runtime.py:153-170)."""
@@ -233,7 +233,7 @@ class GateUpQLinear(nn.Module):
     def forward_quantized(self, qx, sx):
         _require_gpu(qx)
         return _hit(aot.mm_i8(qx, sx, self.qweight, self.wscale, None, torch.bfloat16, epilogue="silu_mul",
-                              split=aot.auto_split(qx.device)), "fused gate+up mm_i8")
+                              split="auto"), "fused gate+up mm_i8")
 
     def forward(self, x):
         _require_gpu(x)
@@ -343,7 +343,7 @@ class SharedNormQLinears(nn.Module):
                 y = torch.zeros(0, qw.shape[0], dtype=self.linears[grp[0]].out_dtype, device=qx.device)
             else:
                 y = _hit(aot.mm_i8(qx, sx, qw, sw, b, self.linears[grp[0]].out_dtype,
-                                   split=aot.auto_split(qx.device)), "mm_i8")
+                                   split="auto"), "mm_i8")
             off = 0
             for i in grp:
                 n = self.linears[i].out_features
