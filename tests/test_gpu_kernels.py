@@ -552,6 +552,7 @@ def test_gemm_split_schedule_bit_exact(gpu, m, n, k, epi):
     (77, 6144, 8192, "none"),        # ragged M (51 empty rows in every tile), 39 tiles, 3 parts
     (512, 2560, 9728, "bias_fp16"),  # fp16 output with a bias, 64 tiles, 3 parts
     (64, 2560, 16384, "none"),       # the most parts: 128 slabs in 6 parts, 16 tiles
+    (256, 2560, 8192, "bias_residual"),  # bias and residual together (bf16), 32 tiles, 3 parts
 ])
 def test_gemm_small_m_split_bit_exact(gpu, m, n, k, epi):
     """Few 128-row tiles and a long K, with a workspace: every tile is split along K over several
@@ -584,6 +585,11 @@ def test_gemm_small_m_split_bit_exact(gpu, m, n, k, epi):
         bias = rng.uniform(-1, 1, n).astype(np.float32)
         kw.update(bias=torch.from_numpy(bias).cuda(), out_dtype=torch.float16)
         ref = O.epilogue(acc, sa, sb, bias, "fp16")
+    elif epi == "bias_residual":
+        bias = rng.uniform(-1, 1, n).astype(np.float32)
+        res = act_bits(rng, (m, n), outliers=0)
+        kw.update(bias=torch.from_numpy(bias).cuda(), residual=to_gpu_bf16(res))
+        ref = O.f32_to_bf16(O.bf16_to_f32(O.epilogue(acc, sa, sb, bias)) + O.bf16_to_f32(res))
     else:
         ref = O.epilogue(acc, sa, sb)
 
