@@ -44,10 +44,11 @@ constexpr int kQWaves = 4, kQThreads = 64 * kQWaves;
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// A BM x BN tile on 4 waves in a WGM (M) x WGN (N) grid, NS LDS stages of one slab each.
-template <int BM_, int BN_, int NS_ = 2, int WGM_ = 2, int WGN_ = 2>
+// A BM x BN tile on 4 waves in a WGM (M) x WGN (N) grid, NS LDS stages of one slab each; CPOL: the
+// cache policy bits of its output stores (0, or 2: nt).
+template <int BM_, int BN_, int NS_ = 2, int WGM_ = 2, int WGN_ = 2, int CPOL_ = 0>
 struct QCfg {
-    static constexpr int BM = BM_, BN = BN_, NS = NS_, WGM = WGM_, WGN = WGN_;
+    static constexpr int BM = BM_, BN = BN_, NS = NS_, WGM = WGM_, WGN = WGN_, CPOL = CPOL_;
     static_assert(WGM * WGN == kQWaves, "wave grid");
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int MB = WM / 16, NB = WN / 16;
@@ -77,7 +78,10 @@ using QNarrow = QCfg<256, 160, 2, 4, 1>;
 // per workgroup, nothing to prefetch for a successor: three slabs stay in flight, against two with three
 // stages, whose DMA waited on memory latency).  Such a tile is bound by its DMA feed, (128 + 160) rows x
 // K against 384 rows for the 256 x 128 half tile it replaces.
-using QSmall = QCfg<128, 160, 4, 4, 1>;
+// Its outputs are stored non-temporally: 512 x 9728 x 2560 16.4 -> 15.5 us (same bits), where whole
+// 256 x 256 tiles lost by it (4096 x 9728 x 2560 86.5 -> 91.7 us, 4096 x 6144 x 2560 57.3 -> 58.6, the
+// 256 x 160 tiles of 4096 x 2560 x 9728 79.0 -> 80.0; interleaved on one box).
+using QSmall = QCfg<128, 160, 4, 4, 1, 2>;
 // The SiLU epilogue's counterpart for launches of at most 128 rows (a short request's gate+up): one round
 // of 128 x 128 tiles, each one 64-row group of gate weights and its 64 up rows, on waves of 32 x 128
 // stacked along M (2 x 8 MFMA tiles, 64 accumulators per lane), so every wave pairs gate and up columns
@@ -631,7 +635,7 @@ struct QTile {
             for (int jp = 0; jp < kS; ++jp) {
                 const int col = col0 + col_of(jp);
                 const int off = opaque_off(col < ncols_out ? (row_of(i) * p.ldc + col) * 2 : kOutOfRange);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, outv[jp]), rsrc_c, off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, outv[jp]), rsrc_c, off, 0, C::CPOL);
             }
             if constexpr (HAS_RES) {
                 if (i + 2 < MB) res_load(i + 2);
