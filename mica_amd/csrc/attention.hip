@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kFaThreads, MICA_FA_OCC) void fa_fwd_kernel(FaParam
         const int row = piece >> 5, c = piece & 31; // 32 pieces of 16 B per 512 B row
         const int t = q0 + row;
         const u32x4 v = *(const u32x4 *)(ost + row * (kD * 2) + c * 16);
-        if (t < p.Sq) *(u32x4 *)(p.o + b * p.sbo + head * p.sho + (long long)t * p.ldo + c * 8) = v;
+        if (t < p.Sq) __builtin_nontemporal_store(v, (u32x4 *)(p.o + b * p.sbo + head * p.sho + (long long)t * p.ldo + c * 8));
     }
 }
 

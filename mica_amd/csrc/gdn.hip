@@ -722,7 +722,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_scan_kernel(GdnParams p) {
                 const int ml = it * kRpi + lane / kLpr, cc = (lane % kLpr) * 8;
                 const int t = tbase + mo * 32 + ml;
                 const u32x4 v = *(const u32x4 *)(ost + ml * kRowC + cc);
-                if (t < p.T) *(u32x4 *)(p.o + (((long)b * p.T + t) * p.HV + h) * kDv + dvw + cc) = v;
+                if (t < p.T) __builtin_nontemporal_store(v, (u32x4 *)(p.o + (((long)b * p.T + t) * p.HV + h) * kDv + dvw + cc));
             }
         }
         // ---- S <- exp(G_63) S + K^T (decayed v_new) ----
