@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
             u32x4 out;
 #pragma unroll
             for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
-            *(u32x4 *)(p.y + b * p.sby + (long)t * p.ldy + c0) = out;
+            __builtin_nontemporal_store(out, (u32x4 *)(p.y + b * p.sby + (long)t * p.ldy + c0));
         }
     }
     // the last W - 1 input rows (history included when T < W - 1) become the next call's initial
