@@ -823,11 +823,11 @@ __global__ __launch_bounds__(64 * kGnWaves) void gated_norm_quant_kernel(GatedNo
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int col = i * 512 + lane * 8;
-        if (p.y) *(u32x4 *)(p.y + (long)row * p.ldy + col) = yr[i];
+        if (p.y) __builtin_nontemporal_store(yr[i], (u32x4 *)(p.y + (long)row * p.ldy + col));
         float x[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = (e & 1) ? bf16_hi(yr[i][e >> 1]) : bf16_lo(yr[i][e >> 1]);
-        *(u32x2 *)(p.q + (long)row * p.ldq + col) = fma_quant8(x, r);
+        __builtin_nontemporal_store(fma_quant8(x, r), (u32x2 *)(p.q + (long)row * p.ldq + col));
     }
     if (lane == 0) p.s[row] = s;
 }
